@@ -1,0 +1,193 @@
+/*
+ * visionhope_hip.h — C ABI of libvisionhope_hip.so, the MI355X (gfx950) kernels
+ * for VisionHOPE's SRNL operator hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are raw device pointers to dense (contiguous) memory
+ *     in the layout stated next to each argument; sizes are int64_t.
+ *   - `stream` is a hipStream_t passed as void*.  Work is enqueued on it
+ *     asynchronously; nothing synchronises, allocates or frees device memory,
+ *     so every call can be recorded into a HIP graph.
+ *   - The caller owns every buffer: outputs and workspaces are allocated by the
+ *     caller (workspace sizes come from the *_workspace_bytes queries).
+ *   - Return value: VH_OK (0) or one of the VH_ERR_* codes below; a message for
+ *     the last failure on the calling thread is available from vh_last_error().
+ *   - io_dtype selects the element type of activation tensors (x, q, y):
+ *     VH_DTYPE_F32, VH_DTYPE_BF16 or VH_DTYPE_F16.  SRNL memories, skips,
+ *     weights and fused outputs are always fp32, as in the reference.
+ *
+ * Each declaration cites the reference interface it replaces (path:line inside
+ * the PSRben/VisionHOPE repository).
+ */
+#ifndef VISIONHOPE_HIP_H
+#define VISIONHOPE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VH_ABI_VERSION 1
+
+enum {
+    VH_OK = 0,
+    VH_ERR_SHAPE = 1,      /* inconsistent or empty shapes */
+    VH_ERR_DTYPE = 2,      /* unsupported element type */
+    VH_ERR_HEAD_DIM = 3,   /* head_dim not in {4, 8, 16, 32, 64} */
+    VH_ERR_WORKSPACE = 4,  /* workspace missing or too small */
+    VH_ERR_ARG = 5,        /* null pointer or out-of-range scalar */
+    VH_ERR_LAUNCH = 6      /* the HIP runtime rejected a launch */
+};
+
+enum { VH_DTYPE_F32 = 0, VH_DTYPE_BF16 = 1, VH_DTYPE_F16 = 2 };
+
+/* Stability constants of the recurrence.  Replaces the text substitution of
+ * __ETA_SCALE__ ... __ETA2ALPHA_FACTOR__ into the CUDA sources
+ * (models/srnl_core/chunk.py:44-49,89-97; fused.py:38-49): here they are
+ * run-time arguments instead of compile-time literals. */
+typedef struct vh_srnl_consts {
+    float step_scale;        /* ETA_SCALE        = VISIONHOPE_STEP_SCALE (0.025) */
+    float min_retention;     /* ALPHA_MIN        = VISIONHOPE_MIN_RETENTION (0) */
+    float retention_bias;    /* ALPHA_BIAS       = VISIONHOPE_RETENTION_BIAS (ln 9) */
+    float injection_margin;  /* STAB_MU          = VISIONHOPE_INJECTION_MARGIN (0.999) */
+    int32_t spectral_clamp;  /* ETA2ALPHA_CLAMP  = SPECTRAL_CLAMP (1) */
+    float spectral_factor;   /* ETA2ALPHA_FACTOR = 2 * VISIONHOPE_SPECTRAL_MARGIN */
+} vh_srnl_consts;
+
+int vh_abi_version(void);
+const char* vh_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * SRNL recurrence.  Every SRNL entry point runs the same two kernels: a scan
+ * over the chunks of each (batch, direction, head) line that writes the
+ * chunk-start content memory of every chunk into the workspace, and a readout
+ * that computes y = M_m^chunk q_hat for every token (and, for the spatial
+ * entries, restores and fuses the four directions).
+ * Memories: M_m/M_v/M_k [R, heads, d, d], M_eta/M_alpha [R, heads, d], fp32,
+ * shared over the batch (chunk.py:193-196).
+ * ------------------------------------------------------------------------- */
+
+/* Workspace for the chunk-start content memories of `lines` lines whose
+ * longest scan has `max_chunks` chunks of head_dim x head_dim fp32. */
+size_t vh_srnl_workspace_bytes(int64_t lines, int64_t max_chunks, int32_t head_dim);
+
+/* Four-direction spatial operator on channels-last activations: x and q are
+ * [B, H, W, C] (q = W_q x + b, computed once per token), out is [B, H, W, C]
+ * fp32 = sum_r dir_weight[r, c] * (y_r + d_skip[r, c] * x).  chunks[r] is the
+ * chunk length of scan r ((W, W, H, H) on the spatial path).
+ * d_skip holds C values (skip_per_direction = 0) or 4*C values (= 1).
+ * Workspace: vh_srnl_workspace_bytes(B*4*heads, max_r ceil(H*W/chunks[r]), d).
+ * Replaces VisionHOPEOperator._forward_fast's serialize/stack + the fused
+ * kernel call (models/operator.py:172-193, models/srnl_core/csrc/fused.cu:307-351)
+ * without materialising the four serialized copies of x and q. */
+int vh_srnl_spatial_forward(
+    const void* x, const void* q, int32_t io_dtype,
+    const float* M_m, const float* M_v, const float* M_k,
+    const float* M_eta, const float* M_alpha,
+    const float* d_skip, int32_t skip_per_direction, const float* dir_weight,
+    float* out, int64_t B, int64_t H, int64_t W, int64_t C, int32_t head_dim,
+    const int64_t chunks[4], const vh_srnl_consts* consts,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* The reference's fused spatial entry with its own argument layout: X and
+ * Q_raw are the serialized stacks [B, 4, H*W, C]; Out is [B, H, W, C] fp32;
+ * chunks are (W, W, H, H).  Replaces srnl_line_forward_seq_noatomic
+ * (models/srnl_core/csrc/fused.cu:307-351, bound at fused.py:70-76). */
+int vh_srnl_line_forward_seq_noatomic(
+    const void* X, const void* Q_raw, int32_t io_dtype,
+    const float* M_m, const float* M_v, const float* M_k,
+    const float* M_eta, const float* M_alpha,
+    const float* d_skip, int32_t skip_per_direction, const float* dir_weight,
+    float* out, int64_t B, int64_t H, int64_t W, int64_t C, int32_t head_dim,
+    const vh_srnl_consts* consts, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Packed sequences: X [B, R, heads, N, d], Q_raw [B, R, N, heads*d] (raw,
+ * normalised per head inside), Out [B, R, heads, N, d] in io_dtype; chunks[r]
+ * per direction (R in {1, 2, 4}); the final chunk is zero-padded.
+ * memories_per_line = 1: the memories hold one state per line, shaped
+ * [B*R*heads, d, d] / [B*R*heads, d] (the reference's 5-D memories,
+ * chunk.py:193-198, chunk.cu:287).
+ * Workspace: vh_srnl_workspace_bytes(B*R*heads, max_r ceil(N/chunks[r]), d).
+ * Replaces srnl_sequence_forward (models/srnl_core/csrc/fused.cu:131-179) and
+ * the forward halves of srnl_forward_qraw (chunk.cu:1106-1131),
+ * srnl_forward_qraw_large / _varline (lines.cu:688-732). */
+int vh_srnl_sequence_forward(
+    const void* X, const void* Q_raw, int32_t io_dtype,
+    const float* M_m, const float* M_v, const float* M_k,
+    const float* M_eta, const float* M_alpha, int32_t memories_per_line,
+    void* out, int64_t B, int64_t R, int64_t heads, int64_t N, int32_t head_dim,
+    const int64_t* chunks, const vh_srnl_consts* consts,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Packed sequences with pre-normalised fp32 queries Q [B, R, heads, N, d]
+ * (used as given).  Replaces the forward half of srnl_forward
+ * (models/srnl_core/csrc/chunk.cu:1083-1104, called at chunk.py:234). */
+int vh_srnl_forward(
+    const void* X, int32_t io_dtype, const float* Q,
+    const float* M_m, const float* M_v, const float* M_k,
+    const float* M_eta, const float* M_alpha, int32_t memories_per_line,
+    void* out, int64_t B, int64_t R, int64_t heads, int64_t N, int32_t head_dim,
+    const int64_t* chunks, const vh_srnl_consts* consts,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Elementwise tail
+ * ------------------------------------------------------------------------- */
+
+/* Direction fusion: Y, X [B, 4, heads, H*W, d] (io_dtype) ->
+ * out [B, C, H, W] fp32 = sum_r scale[r, c] * (y_r + d_skip[r, c] * x_r),
+ * restored to image order; channels_last selects NHWC storage of out.
+ * Replaces visionhope_postprocess_scale_forward
+ * (utils/csrc/direction_fusion.cu:505-575, called at direction_fusion.py:95). */
+int vh_postprocess_scale_forward(
+    const void* Y, const void* X, int32_t io_dtype,
+    const float* d_skip, int32_t skip_per_direction, const float* scale,
+    float* out, int64_t B, int64_t heads, int64_t H, int64_t W, int32_t head_dim,
+    int32_t channels_last, void* stream);
+
+/* Workspace of vh_grn_forward: B * ceil(H*W / rows_per_slab) * C fp32 partial sums. */
+size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W);
+
+/* GRN on channels-last x [B, H, W, C] (io_dtype): gx = ||x||_2 over H*W,
+ * nx = gx / (mean_c gx + eps), y = x (1 + gamma nx) + beta, y fp32 [B, H, W, C];
+ * gx [B, C] and inv_den [B] are written too (the reference saves them for
+ * backward).  Replaces grn_forward_cuda (utils/csrc/grn_cuda.cu:290-320,
+ * called at utils/grn_cuda.py:42). */
+int vh_grn_forward(
+    const void* x, int32_t io_dtype, const float* gamma, const float* beta,
+    float* y, float* gx, float* inv_den, int64_t B, int64_t C, int64_t H, int64_t W,
+    float eps, void* workspace, size_t workspace_bytes, void* stream);
+
+/* LayerNorm over C for every pixel of x [B, C, H, W] (channels_last = 1: NHWC
+ * storage, 0: NCHW storage), biased variance, y fp32 in the same storage
+ * order; mean/rstd [B*H*W] are optional (may be NULL).  Replaces the Triton
+ * _layernorm2d_forward_kernel (utils/layer_norm_cuda.py:31-57,122-147) and the
+ * F.layer_norm call of LayerNorm2d.inference_layout (models/layers.py:18-20). */
+int vh_layernorm2d_forward(
+    const void* x, int32_t io_dtype, const float* weight, const float* bias,
+    float* y, float* mean, float* rstd, int64_t B, int64_t C, int64_t H, int64_t W,
+    float eps, int32_t channels_last, void* stream);
+
+/* Query normalisation + relayout: q_raw [B, R, N, heads*d] (io_dtype) ->
+ * q [B, R, heads, N, d] fp32 = q_raw / max(||q_raw||, 1e-12) per head, and
+ * inv_norm [B, R, heads, N].  Replaces visionhope_qnorm_forward
+ * (utils/csrc/query_normalization.cu:223-265). */
+int vh_qnorm_forward(
+    const void* q_raw, int32_t io_dtype, float* q, float* inv_norm,
+    int64_t B, int64_t R, int64_t N, int64_t heads, int32_t head_dim, void* stream);
+
+/* Residual add on channels-last data: out[i] = residual[i] +
+ * branch[i] * gamma[c] * drop_scale[b] (fp32 out; residual/branch io_dtype
+ * each).  Replaces the Triton _residual_forward_kernel (utils/residual.py:31-52). */
+int vh_residual_add_forward(
+    const void* residual, int32_t residual_dtype, const void* branch, int32_t branch_dtype,
+    const float* gamma, const float* drop_scale, float* out,
+    int64_t total, int64_t channels, int64_t spatial, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VISIONHOPE_HIP_H */

@@ -1,0 +1,129 @@
+"""GPU parity of the elementwise kernels (direction fusion, GRN, LayerNorm2d, qnorm,
+residual) against the CPU oracle, including BASELINE config 2's full B=128 shapes."""
+
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import assert_close, randn
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("channels_last", [False, True])
+@pytest.mark.parametrize("per_direction", [False, True])
+def test_direction_fusion(oracle, device, dtype, channels_last, per_direction):
+    from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
+
+    batch, heads, head_dim, height, width = 2, 3, 16, 6, 9
+    y = randn(batch, 4, heads, height * width, head_dim, seed=1).to(dtype)
+    x = randn(batch, 4, heads, height * width, head_dim, seed=2).to(dtype)
+    skip = randn(*((4, heads, head_dim) if per_direction else (heads, head_dim)), seed=3, scale=0.1)
+    scale = 1 + randn(4, heads * head_dim, seed=4, scale=0.1)
+    out = visionhope_postprocess_scale(y.to(device), x.to(device), skip.to(device), scale.to(device),
+                                       height, width, channels_last)
+    assert out.dtype == torch.float32
+    assert out.is_contiguous(memory_format=torch.channels_last if channels_last else torch.contiguous_format)
+    expected = oracle.direction_fusion(y.float().numpy(), x.float().numpy(), skip.numpy(), scale.numpy(),
+                                       height, width)
+    assert_close(out.cpu().numpy(), expected, FP32_TOL, "fusion")
+
+
+@pytest.mark.parametrize("shape", [(128, 96, 56, 56), (128, 192, 28, 28)])
+def test_config2_full_size(oracle, device, shape):
+    """BASELINE config 2 at full size: fusion, GRN and LN on bf16 activations."""
+    from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
+    from visionhope_amd.utils.grn_cuda import visionhope_grn
+    from visionhope_amd.utils.layer_norm_cuda import visionhope_layernorm2d
+
+    batch, channels, height, width = shape
+    heads, head_dim = channels // 16, 16
+    gen = torch.Generator(device=device).manual_seed(1234)
+    x = torch.randn(batch, height, width, channels, device=device, generator=gen).bfloat16()
+    x_nchw = x.permute(0, 3, 1, 2)
+    gamma = torch.randn(channels, device=device, generator=gen) * 0.1
+    beta = torch.randn(channels, device=device, generator=gen) * 0.1
+    w = 1 + torch.randn(channels, device=device, generator=gen) * 0.1
+    b = torch.randn(channels, device=device, generator=gen) * 0.1
+
+    y = visionhope_grn(x_nchw, gamma, beta, 1e-6)
+    exp = oracle.grn(x_nchw.float().cpu().numpy(), gamma.cpu().numpy(), beta.cpu().numpy())
+    assert_close(y.cpu().numpy(), exp, 1e-5, "GRN config 2")
+    del y, exp
+
+    y = visionhope_layernorm2d(x_nchw, w, b, 1e-6)
+    exp = oracle.layernorm2d(x_nchw.float().cpu().numpy(), w.cpu().numpy(), b.cpu().numpy())
+    assert_close(y.cpu().numpy(), exp, 1e-5, "LN config 2")
+    del y, exp
+
+    ys = torch.randn(batch, 4, heads, height * width, head_dim, device=device, generator=gen).bfloat16()
+    xs = torch.randn(batch, 4, heads, height * width, head_dim, device=device, generator=gen).bfloat16()
+    skip = torch.randn(heads, head_dim, device=device, generator=gen) * 0.1
+    scale = 1 + torch.randn(4, channels, device=device, generator=gen) * 0.1
+    out = visionhope_postprocess_scale(ys, xs, skip, scale, height, width, True)
+    exp = oracle.direction_fusion(ys.float().cpu().numpy(), xs.float().cpu().numpy(), skip.cpu().numpy(),
+                                  scale.cpu().numpy(), height, width)
+    assert_close(out.cpu().numpy(), exp, 1e-5, "fusion config 2")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("channels,height,width", [(96, 7, 5), (256, 14, 14), (7, 3, 3), (2048, 7, 7)])
+@pytest.mark.parametrize("channels_last", [True, False])
+def test_grn(oracle, device, dtype, channels, height, width, channels_last):
+    from visionhope_amd.utils.grn import global_response_norm
+
+    x = randn(3, channels, height, width, seed=5).to(dtype)
+    if channels_last:
+        x = x.contiguous(memory_format=torch.channels_last)
+    gamma = randn(1, channels, 1, 1, seed=6, scale=0.1)
+    beta = randn(1, channels, 1, 1, seed=7, scale=0.1)
+    y = global_response_norm(x.to(device), gamma.to(device), beta.to(device))
+    assert y.dtype == torch.float32
+    expected = oracle.grn(x.float().numpy(), gamma.numpy(), beta.numpy())
+    assert_close(y.cpu().numpy(), expected, 2e-5, "GRN")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("channels", [3, 16, 64, 96, 128, 200, 512, 1024, 4096])
+@pytest.mark.parametrize("channels_last", [True, False])
+def test_layernorm2d(device, dtype, channels, channels_last):
+    """Textbook check: torch.nn.functional.layer_norm on CPU in float64."""
+    from visionhope_amd.utils.layer_norm_cuda import visionhope_layernorm2d
+
+    x = randn(2, channels, 5, 7, seed=8).to(dtype)
+    if channels_last:
+        x = x.contiguous(memory_format=torch.channels_last)
+    w = 1 + randn(channels, seed=9, scale=0.1)
+    b = randn(channels, seed=10, scale=0.1)
+    y = visionhope_layernorm2d(x.to(device), w.to(device), b.to(device), 1e-6)
+    assert y.dtype == torch.float32
+    assert y.is_contiguous(memory_format=torch.channels_last if channels_last else torch.contiguous_format)
+    expected = torch.nn.functional.layer_norm(x.double().permute(0, 2, 3, 1), (channels,), w.double(),
+                                              b.double(), 1e-6).permute(0, 3, 1, 2)
+    assert_close(y.cpu().numpy(), expected.numpy(), 1e-5, "LN")
+
+
+@pytest.mark.parametrize("head_dim", [4, 8, 16, 32, 64])
+def test_qnorm(oracle, device, head_dim):
+    from visionhope_amd.utils.query_normalization import visionhope_qnorm
+
+    heads = 3
+    q = randn(2, 4, 11, heads * head_dim, seed=12).bfloat16()
+    out = visionhope_qnorm(q.to(device), heads, head_dim)
+    expected, _ = oracle.qnorm(q.float().numpy(), heads, head_dim)
+    assert_close(out.cpu().numpy(), expected, 1e-6, "qnorm")
+
+
+def test_residual_add(oracle, device):
+    from visionhope_amd.utils.residual import visionhope_residual_add
+
+    res = randn(3, 32, 5, 6, seed=13).contiguous(memory_format=torch.channels_last)
+    branch = randn(3, 32, 5, 6, seed=14).bfloat16().contiguous(memory_format=torch.channels_last)
+    gamma = randn(32, 1, 1, seed=15, scale=0.1)
+    out = visionhope_residual_add(res.to(device), branch.to(device), gamma.to(device), 0.0, False)
+    expected = oracle.residual_add(res.permute(0, 2, 3, 1).numpy(), branch.float().permute(0, 2, 3, 1).numpy(),
+                                   gamma.numpy(), np.ones(3, np.float32))
+    assert_close(out.permute(0, 2, 3, 1).cpu().numpy(), expected, 1e-6, "residual")

@@ -1,0 +1,477 @@
+// Memory-bound tail of the SRNL operator for gfx950: direction fusion, GRN,
+// LayerNorm over channels, query normalisation and the residual add.
+//
+// All kernels read activations in their storage order with consecutive lanes
+// on consecutive addresses, reduce with wave64 butterflies (__shfl_xor) and
+// write fp32 results once.
+#include <algorithm>
+#include <cmath>
+
+#include "vh_common.h"
+
+namespace vh {
+
+// ---------------------------------------------------------------------------
+// Direction fusion (utils/csrc/direction_fusion.cu:11-65):
+//   out[b, c, h, w] = sum_r scale[r, c] * (y_r[t_r] + skip_r[c] * x_r[t_r])
+// with y, x in the serialized layout [B, 4, heads, L, D].  One thread per
+// output element in output storage order (coalesced writes); the four reads
+// of a pixel hit D-element rows that neighbouring threads share in cache.
+// ---------------------------------------------------------------------------
+struct FusionParams {
+    const void* y;
+    const void* x;
+    const float* skip;
+    int skip_per_dir;
+    const float* scale;
+    float* out;
+    int64_t B, heads, H, W;
+    int channels_last;
+};
+
+template <int D, typename T>
+__global__ __launch_bounds__(256) void direction_fusion_kernel(const FusionParams p) {
+    const int64_t C = p.heads * D;
+    const int64_t L = p.H * p.W;
+    const int64_t total = p.B * C * L;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= total) return;
+    int64_t b, c, h, w;
+    if (p.channels_last) {
+        c = idx % C;
+        w = (idx / C) % p.W;
+        h = (idx / (C * p.W)) % p.H;
+        b = idx / (C * L);
+    } else {
+        w = idx % p.W;
+        h = (idx / p.W) % p.H;
+        c = (idx / L) % C;
+        b = idx / (C * L);
+    }
+    const int64_t head = c / D;
+    const int64_t i = c % D;
+    const T* y = static_cast<const T*>(p.y);
+    const T* x = static_cast<const T*>(p.x);
+    const int64_t base = (b * 4 * p.heads + head) * L * D + i;
+    const int64_t stride_dir = p.heads * L * D;
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t at = base + r * stride_dir + pixel_to_scan(r, h, w, p.H, p.W) * D;
+        const float ds = p.skip[(p.skip_per_dir ? r * C : 0) + c];
+        v[r] = to_f32(y[at]) + ds * to_f32(x[at]);
+    }
+    float out = p.scale[c] * v[0];
+    out += p.scale[C + c] * v[1];
+    out += p.scale[2 * C + c] * v[2];
+    out += p.scale[3 * C + c] * v[3];
+    p.out[idx] = out;
+}
+
+// ---------------------------------------------------------------------------
+// GRN (utils/grn.py:26-38, utils/csrc/grn_cuda.cu:46-124) on channels-last x.
+//   pass 1  partial[b, slab, c] = sum over the slab's pixels of x^2
+//   pass 2  gx[b, c] = sqrt(sum_slab partial), inv_den[b] = 1 / (mean_c gx + eps)
+//   pass 3  y = x * (1 + gamma_c * gx * inv_den) + beta_c
+// ---------------------------------------------------------------------------
+constexpr int kGrnRowsPerSlab = 64;
+
+template <typename T>
+__global__ __launch_bounds__(256) void grn_partial_kernel(const T* __restrict__ x,
+                                                         float* __restrict__ partial, int64_t C,
+                                                         int64_t S, int64_t nslab) {
+    extern __shared__ float red[];
+    const int64_t b = blockIdx.y;
+    const int64_t slab = blockIdx.x;
+    const int64_t s0 = slab * kGrnRowsPerSlab;
+    const int64_t s1 = std::min<int64_t>(S, s0 + kGrnRowsPerSlab);
+    const int ct = static_cast<int>(std::min<int64_t>(C, 256));
+    const int rp = 256 / ct;                       // row phases
+    const int tc = threadIdx.x % ct, tr = threadIdx.x / ct;
+    const T* xb = x + b * S * C;
+    for (int64_t c = tc; c < C; c += ct) {
+        float acc = 0.f;
+        if (tr < rp) {
+            for (int64_t s = s0 + tr; s < s1; s += rp) {
+                const float v = to_f32(xb[s * C + c]);
+                acc += v * v;
+            }
+            red[tr * C + c] = acc;
+        }
+    }
+    __syncthreads();
+    for (int64_t c = threadIdx.x; c < C; c += 256) {
+        float acc = 0.f;
+        for (int q = 0; q < rp; ++q) acc += red[q * C + c];
+        partial[(b * nslab + slab) * C + c] = acc;
+    }
+}
+
+__global__ __launch_bounds__(256) void grn_finalize_kernel(const float* __restrict__ partial,
+                                                          float* __restrict__ gx,
+                                                          float* __restrict__ inv_den, int64_t C,
+                                                          int64_t nslab, float eps) {
+    __shared__ float wsum[4];
+    const int64_t b = blockIdx.x;
+    float local = 0.f;
+    for (int64_t c = threadIdx.x; c < C; c += 256) {
+        float acc = 0.f;
+        for (int64_t s = 0; s < nslab; ++s) acc += partial[(b * nslab + s) * C + c];
+        const float g = sqrtf(acc);
+        gx[b * C + c] = g;
+        local += g;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = local;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+        inv_den[b] = 1.f / (total / static_cast<float>(C) + eps);
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void grn_apply_kernel(const T* __restrict__ x,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta,
+                                                       const float* __restrict__ gx,
+                                                       const float* __restrict__ inv_den,
+                                                       float* __restrict__ y, int64_t C, int64_t S,
+                                                       int64_t total) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
+         idx += stride) {
+        const int64_t c = idx % C;
+        const int64_t b = idx / (S * C);
+        const float nx = gx[b * C + c] * inv_den[b];
+        y[idx] = to_f32(x[idx]) * (1.f + gamma[c] * nx) + beta[c];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm over C per pixel (models/layers.py:25-35; Triton arithmetic of
+// utils/layer_norm_cuda.py:44-57): mean, biased centred variance,
+// y = (x - mean) * rstd * w + b.
+// Channels-last: TPR lanes per pixel row, values kept in registers.
+// ---------------------------------------------------------------------------
+template <typename T, int TPR, int MAXV>
+__global__ __launch_bounds__(256) void layernorm_nhwc_kernel(const T* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            const float* __restrict__ bias,
+                                                            float* __restrict__ y,
+                                                            float* __restrict__ mean_out,
+                                                            float* __restrict__ rstd_out,
+                                                            int64_t rows, int C, float eps) {
+    constexpr int RPB = 256 / TPR;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
+    const int lane = threadIdx.x % TPR;
+    const bool active = row < rows;
+    const T* xr = x + (active ? row : 0) * C;
+    float v[MAXV];
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+        const int c = lane + k * TPR;
+        v[k] = (active && c < C) ? to_f32(xr[c]) : 0.f;
+        sum += v[k];
+    }
+#pragma unroll
+    for (int off = TPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    const float mean = sum / static_cast<float>(C);
+    float sq = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+        const int c = lane + k * TPR;
+        const float d = (c < C) ? v[k] - mean : 0.f;
+        v[k] = d;
+        sq += d * d;
+    }
+#pragma unroll
+    for (int off = TPR / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+    const float rstd = 1.f / sqrtf(sq / static_cast<float>(C) + eps);
+    if (!active) return;
+    float* yr = y + row * C;
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+        const int c = lane + k * TPR;
+        if (c < C) yr[c] = v[k] * rstd * w[c] + bias[c];
+    }
+    if (lane == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = rstd;
+    }
+}
+
+// NCHW storage: one thread per pixel, channel loop (coalesced over pixels).
+template <typename T>
+__global__ __launch_bounds__(256) void layernorm_nchw_kernel(const T* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            const float* __restrict__ bias,
+                                                            float* __restrict__ y,
+                                                            float* __restrict__ mean_out,
+                                                            float* __restrict__ rstd_out,
+                                                            int64_t B, int64_t C, int64_t S,
+                                                            float eps) {
+    const int64_t pix = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (pix >= B * S) return;
+    const int64_t b = pix / S, s = pix % S;
+    const T* xb = x + b * C * S + s;
+    float sum = 0.f;
+    for (int64_t c = 0; c < C; ++c) sum += to_f32(xb[c * S]);
+    const float mean = sum / static_cast<float>(C);
+    float sq = 0.f;
+    for (int64_t c = 0; c < C; ++c) {
+        const float d = to_f32(xb[c * S]) - mean;
+        sq += d * d;
+    }
+    const float rstd = 1.f / sqrtf(sq / static_cast<float>(C) + eps);
+    float* yb = y + b * C * S + s;
+    for (int64_t c = 0; c < C; ++c) yb[c * S] = (to_f32(xb[c * S]) - mean) * rstd * w[c] + bias[c];
+    if (mean_out) mean_out[pix] = mean;
+    if (rstd_out) rstd_out[pix] = rstd;
+}
+
+// ---------------------------------------------------------------------------
+// Query normalisation + relayout (utils/csrc/query_normalization.cu:135-177):
+// [B, R, N, heads*D] -> [B, R, heads, N, D] fp32, inv_norm [B, R, heads, N].
+// ---------------------------------------------------------------------------
+template <int D, typename T>
+__global__ __launch_bounds__(256) void qnorm_kernel(const T* __restrict__ q, float* __restrict__ out,
+                                                   float* __restrict__ inv_norm, int64_t B,
+                                                   int64_t R, int64_t N, int64_t heads) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t total = B * R * N * heads;
+    if (idx >= total) return;
+    const int64_t head = idx % heads;
+    const int64_t t = (idx / heads) % N;
+    const int64_t br = idx / (heads * N);
+    const T* src = q + (br * N + t) * heads * D + head * D;
+    float v[D];
+    float sq = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        v[j] = to_f32(src[j]);
+        sq += v[j] * v[j];
+    }
+    const float inv = 1.f / fmaxf(sqrtf(sq), 1e-12f);
+    float* dst = out + ((br * heads + head) * N + t) * D;
+#pragma unroll
+    for (int j = 0; j < D; ++j) dst[j] = v[j] * inv;
+    inv_norm[(br * heads + head) * N + t] = inv;
+}
+
+// ---------------------------------------------------------------------------
+// Residual add (utils/residual.py:31-52): out = residual + branch * gamma_c * mask_b.
+// ---------------------------------------------------------------------------
+template <typename TR, typename TB>
+__global__ __launch_bounds__(256) void residual_kernel(const TR* __restrict__ res,
+                                                      const TB* __restrict__ br,
+                                                      const float* __restrict__ gamma,
+                                                      const float* __restrict__ mask,
+                                                      float* __restrict__ out, int64_t total,
+                                                      int64_t channels, int64_t spatial) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
+         idx += stride) {
+        const int64_t c = idx % channels;
+        const int64_t b = idx / (channels * spatial);
+        out[idx] = to_f32(res[idx]) + to_f32(br[idx]) * gamma[c] * mask[b];
+    }
+}
+
+namespace {
+
+template <typename F>
+int dispatch_d(int d, F&& f) {
+    switch (d) {
+        case 4: f(std::integral_constant<int, 4>{}); return VH_OK;
+        case 8: f(std::integral_constant<int, 8>{}); return VH_OK;
+        case 16: f(std::integral_constant<int, 16>{}); return VH_OK;
+        case 32: f(std::integral_constant<int, 32>{}); return VH_OK;
+        case 64: f(std::integral_constant<int, 64>{}); return VH_OK;
+    }
+    return set_error(VH_ERR_HEAD_DIM, "head_dim must be one of 4, 8, 16, 32, 64; got %d", d);
+}
+
+template <typename F>
+int dispatch_t(int t, F&& f) {
+    switch (t) {
+        case VH_DTYPE_F32: f(float{}); return VH_OK;
+        case VH_DTYPE_BF16: f(bf16_t{}); return VH_OK;
+        case VH_DTYPE_F16: f(f16_t{}); return VH_OK;
+    }
+    return set_error(VH_ERR_DTYPE, "unsupported dtype code %d", t);
+}
+
+unsigned grid_for(int64_t total, int64_t cap) {
+    return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((total + 255) / 256, cap)));
+}
+
+template <typename T, int TPR>
+void launch_ln_nhwc(const void* x, const float* w, const float* b, float* y, float* mean,
+                    float* rstd, int64_t rows, int C, float eps, hipStream_t s) {
+    const unsigned blocks = static_cast<unsigned>((rows + 256 / TPR - 1) / (256 / TPR));
+    const int per = (C + TPR - 1) / TPR;
+    const T* xp = static_cast<const T*>(x);
+    if (per <= 4)
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 4>), dim3(blocks), dim3(256), 0, s, xp, w, b,
+                           y, mean, rstd, rows, C, eps);
+    else if (per <= 8)
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 8>), dim3(blocks), dim3(256), 0, s, xp, w, b,
+                           y, mean, rstd, rows, C, eps);
+    else if (per <= 16)
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 16>), dim3(blocks), dim3(256), 0, s, xp, w,
+                           b, y, mean, rstd, rows, C, eps);
+    else if (per <= 32)
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 32>), dim3(blocks), dim3(256), 0, s, xp, w,
+                           b, y, mean, rstd, rows, C, eps);
+    else
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 64>), dim3(blocks), dim3(256), 0, s, xp, w,
+                           b, y, mean, rstd, rows, C, eps);
+}
+
+}  // namespace
+}  // namespace vh
+
+using namespace vh;
+
+extern "C" {
+
+int vh_postprocess_scale_forward(const void* Y, const void* X, int32_t io_dtype, const float* d_skip,
+                                 int32_t skip_per_direction, const float* scale, float* out,
+                                 int64_t B, int64_t heads, int64_t H, int64_t W, int32_t head_dim,
+                                 int32_t channels_last, void* stream) {
+    VH_REQUIRE(Y && X && d_skip && scale && out, VH_ERR_ARG, "direction fusion pointers must not be null");
+    VH_REQUIRE(B > 0 && heads > 0 && H > 0 && W > 0, VH_ERR_SHAPE,
+               "Invalid shape for visionhope_postprocess_scale_forward.");
+    VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);
+    FusionParams fp{Y, X, d_skip, skip_per_direction, scale, out, B, heads, H, W, channels_last};
+    const int64_t total = B * heads * head_dim * H * W;
+    const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = dispatch_d(head_dim, [&](auto dc) {
+        constexpr int D = decltype(dc)::value;
+        dispatch_t(io_dtype, [&](auto tv) {
+            hipLaunchKernelGGL((direction_fusion_kernel<D, decltype(tv)>), dim3(blocks), dim3(256), 0,
+                               s, fp);
+        });
+    });
+    if (rc) return rc;
+    return check_launch("direction_fusion_kernel");
+}
+
+size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W) {
+    if (B <= 0 || C <= 0 || H <= 0 || W <= 0) return 0;
+    const int64_t nslab = (H * W + kGrnRowsPerSlab - 1) / kGrnRowsPerSlab;
+    return static_cast<size_t>(B * nslab * C) * sizeof(float);
+}
+
+int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const float* beta, float* y,
+                   float* gx, float* inv_den, int64_t B, int64_t C, int64_t H, int64_t W, float eps,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+    VH_REQUIRE(x && gamma && beta && y && gx && inv_den, VH_ERR_ARG, "GRN pointers must not be null");
+    VH_REQUIRE(B > 0 && C > 0 && H > 0 && W > 0, VH_ERR_SHAPE, "GRN expects nonempty input");
+    VH_REQUIRE(B <= 65535, VH_ERR_SHAPE, "GRN batch must be <= 65535, got %lld", (long long)B);
+    VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "GRN supports FP32, FP16 and BF16 input");
+    const size_t need = vh_grn_workspace_bytes(B, C, H, W);
+    VH_REQUIRE(workspace && workspace_bytes >= need, VH_ERR_WORKSPACE,
+               "GRN workspace needs %zu bytes, got %zu", need, workspace ? workspace_bytes : (size_t)0);
+    const int64_t S = H * W;
+    const int64_t nslab = (S + kGrnRowsPerSlab - 1) / kGrnRowsPerSlab;
+    VH_REQUIRE(nslab <= 65535 * 16, VH_ERR_SHAPE, "GRN spatial size too large");
+    const int ct = static_cast<int>(std::min<int64_t>(C, 256));
+    const size_t lds = static_cast<size_t>(256 / ct) * static_cast<size_t>(C) * sizeof(float);
+    VH_REQUIRE(lds <= 64 * 1024, VH_ERR_SHAPE, "GRN channel count %lld too large", (long long)C);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    float* partial = static_cast<float*>(workspace);
+    const int64_t total = B * S * C;
+    int rc = dispatch_t(io_dtype, [&](auto tv) {
+        using T = decltype(tv);
+        hipLaunchKernelGGL((grn_partial_kernel<T>), dim3(static_cast<unsigned>(nslab), static_cast<unsigned>(B)),
+                           dim3(256), lds, s, static_cast<const T*>(x), partial, C, S, nslab);
+        hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, partial,
+                           gx, inv_den, C, nslab, eps);
+        hipLaunchKernelGGL((grn_apply_kernel<T>), dim3(grid_for(total, 8192)), dim3(256), 0, s,
+                           static_cast<const T*>(x), gamma, beta, gx, inv_den, y, C, S, total);
+    });
+    if (rc) return rc;
+    return check_launch("grn kernels");
+}
+
+int vh_layernorm2d_forward(const void* x, int32_t io_dtype, const float* weight, const float* bias,
+                           float* y, float* mean, float* rstd, int64_t B, int64_t C, int64_t H,
+                           int64_t W, float eps, int32_t channels_last, void* stream) {
+    VH_REQUIRE(x && weight && bias && y, VH_ERR_ARG, "LayerNorm2d pointers must not be null");
+    VH_REQUIRE(B > 0 && C > 0 && H > 0 && W > 0, VH_ERR_SHAPE, "LayerNorm2d expects nonempty input");
+    VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "LayerNorm2d supports FP32, FP16 and BF16 input");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t rows = B * H * W;
+    int rc;
+    if (channels_last) {
+        VH_REQUIRE(C <= 64 * 64, VH_ERR_SHAPE, "LayerNorm2d supports at most 4096 channels, got %lld",
+                   (long long)C);
+        const int c = static_cast<int>(C);
+        rc = dispatch_t(io_dtype, [&](auto tv) {
+            using T = decltype(tv);
+            if (c <= 16) launch_ln_nhwc<T, 4>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+            else if (c <= 32) launch_ln_nhwc<T, 8>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+            else if (c <= 64) launch_ln_nhwc<T, 16>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+            else if (c <= 128) launch_ln_nhwc<T, 32>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+            else launch_ln_nhwc<T, 64>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+        });
+    } else {
+        rc = dispatch_t(io_dtype, [&](auto tv) {
+            using T = decltype(tv);
+            hipLaunchKernelGGL((layernorm_nchw_kernel<T>), dim3(static_cast<unsigned>((rows + 255) / 256)),
+                               dim3(256), 0, s, static_cast<const T*>(x), weight, bias, y, mean, rstd,
+                               B, C, H * W, eps);
+        });
+    }
+    if (rc) return rc;
+    return check_launch("layernorm2d kernel");
+}
+
+int vh_qnorm_forward(const void* q_raw, int32_t io_dtype, float* q, float* inv_norm, int64_t B,
+                     int64_t R, int64_t N, int64_t heads, int32_t head_dim, void* stream) {
+    VH_REQUIRE(q_raw && q && inv_norm, VH_ERR_ARG, "qnorm pointers must not be null");
+    VH_REQUIRE(B > 0 && R > 0 && N > 0 && heads > 0, VH_ERR_SHAPE, "qnorm expects nonempty input");
+    VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);
+    const int64_t total = B * R * N * heads;
+    const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = dispatch_d(head_dim, [&](auto dc) {
+        constexpr int D = decltype(dc)::value;
+        dispatch_t(io_dtype, [&](auto tv) {
+            using T = decltype(tv);
+            hipLaunchKernelGGL((qnorm_kernel<D, T>), dim3(blocks), dim3(256), 0, s,
+                               static_cast<const T*>(q_raw), q, inv_norm, B, R, N, heads);
+        });
+    });
+    if (rc) return rc;
+    return check_launch("qnorm_kernel");
+}
+
+int vh_residual_add_forward(const void* residual, int32_t residual_dtype, const void* branch,
+                            int32_t branch_dtype, const float* gamma, const float* drop_scale,
+                            float* out, int64_t total, int64_t channels, int64_t spatial,
+                            void* stream) {
+    VH_REQUIRE(residual && branch && gamma && drop_scale && out, VH_ERR_ARG,
+               "residual pointers must not be null");
+    VH_REQUIRE(total > 0 && channels > 0 && spatial > 0 && total % (channels * spatial) == 0,
+               VH_ERR_SHAPE, "residual add shape mismatch");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = dispatch_t(residual_dtype, [&](auto rv) {
+        dispatch_t(branch_dtype, [&](auto bv) {
+            using TR = decltype(rv);
+            using TB = decltype(bv);
+            hipLaunchKernelGGL((residual_kernel<TR, TB>), dim3(grid_for(total, 8192)), dim3(256), 0, s,
+                               static_cast<const TR*>(residual), static_cast<const TB*>(branch), gamma,
+                               drop_scale, out, total, channels, spatial);
+        });
+    });
+    if (rc) return rc;
+    return check_launch("residual_kernel");
+}
+
+}  // extern "C"

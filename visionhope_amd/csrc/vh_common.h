@@ -1,0 +1,89 @@
+// Shared helpers for the gfx950 kernels of libvisionhope_hip.so: element
+// conversions, argument checking and the per-thread error message.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "../../include/visionhope_hip.h"
+
+namespace vh {
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting: every entry point returns a status code and
+// leaves a message for vh_last_error() on the calling thread.
+// ---------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+#define VH_REQUIRE(cond, code, ...)                        \
+    do {                                                   \
+        if (!(cond)) return ::vh::set_error((code), __VA_ARGS__); \
+    } while (0)
+
+inline bool valid_head_dim(int d) { return d == 4 || d == 8 || d == 16 || d == 32 || d == 64; }
+inline bool valid_dtype(int t) { return t == VH_DTYPE_F32 || t == VH_DTYPE_BF16 || t == VH_DTYPE_F16; }
+
+// ---------------------------------------------------------------------------
+// Element types.  bf16 and fp16 are carried as raw 16-bit patterns.
+// ---------------------------------------------------------------------------
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+__device__ __forceinline__ float to_f32(f16_t v) {
+    _Float16 h;
+    __builtin_memcpy(&h, &v.bits, 2);
+    return static_cast<float>(h);
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+    // Round to nearest even; quiet NaNs stay NaN.
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t{static_cast<uint16_t>((u >> 16) | 0x40u)};
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return bf16_t{static_cast<uint16_t>(u >> 16)};
+}
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float v) {
+    _Float16 h = static_cast<_Float16>(v);
+    f16_t r;
+    __builtin_memcpy(&r.bits, &h, 2);
+    return r;
+}
+
+// Element size of an io dtype code.
+inline int dtype_bytes(int t) { return t == VH_DTYPE_F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------------------
+// Scan-order maps of the four-direction operator (models/operator.py:79-86;
+// restoration in models/srnl_core/csrc/parallel_line.cuh:16-23).
+//   t0 = h*W + w, t1 = L-1-t0, t2 = w*H + h, t3 = L-1-t2.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t scan_to_pixel(int r, int64_t t, int64_t H, int64_t W) {
+    const int64_t L = H * W;
+    const int64_t orig = (r & 1) ? L - 1 - t : t;
+    return r < 2 ? orig : (orig % H) * W + orig / H;
+}
+__device__ __forceinline__ int64_t pixel_to_scan(int r, int64_t h, int64_t w, int64_t H, int64_t W) {
+    const int64_t L = H * W;
+    const int64_t base = r < 2 ? h * W + w : w * H + h;
+    return (r & 1) ? L - 1 - base : base;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs of MI355X.  Remap the
+// block index so that each XCD receives one contiguous range of work items
+// (neighbouring lines of one image share the XCD's L2).
+__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
+    if (n % 8 != 0) return bid;
+    return (bid % 8) * (n / 8) + bid / 8;
+}
+
+}  // namespace vh

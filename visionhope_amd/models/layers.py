@@ -1,0 +1,128 @@
+"""Normalization, feed-forward, embedding and downsampling layers (mirrors ``models/layers.py``)."""
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from ..utils.grn import GlobalResponseNorm
+from ..utils.layer_norm_cuda import can_fuse_layernorm2d, visionhope_layernorm2d
+
+
+def _layer_norm_result_dtype(x):
+    """dtype F.layer_norm would return: FP32 under CUDA autocast or for FP32 input."""
+    if x.dtype == torch.float32 or (x.is_cuda and torch.is_autocast_enabled("cuda")):
+        return torch.float32
+    return x.dtype
+
+
+class LayerNorm2d(nn.Module):
+    """LayerNorm over channels of an NCHW map (``models/layers.py:9-35``).
+
+    GPU tensors run the native kernel.  In ``inference_layout`` mode the result
+    is channels-last storage with ``F.layer_norm``'s dtype (``layers.py:18-20``);
+    otherwise FP32 in the input's storage order, as the fused reference kernel.
+    """
+
+    def __init__(self, dim, eps=1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.bias = nn.Parameter(torch.zeros(dim))
+        self.eps = eps
+        self.inference_layout = False
+
+    def forward(self, x):
+        if x.is_cuda and can_fuse_layernorm2d(x, self.weight, self.bias):
+            if self.inference_layout:
+                y = visionhope_layernorm2d(x, self.weight, self.bias, self.eps, force_channels_last=True)
+                dtype = _layer_norm_result_dtype(x)
+                return y if dtype == torch.float32 else y.to(dtype)
+            channels_last = x.is_contiguous(memory_format=torch.channels_last)
+            y = visionhope_layernorm2d(x, self.weight, self.bias, self.eps)
+            if channels_last:
+                return y
+            dtype = _layer_norm_result_dtype(x)
+            return y if dtype == torch.float32 else y.to(dtype)
+        if x.is_cuda:
+            raise ValueError(f"LayerNorm2d: unsupported input {tuple(x.shape)} {x.dtype} on {x.device}")
+        # CPU tensors: the reference formula (layers.py:25-35).
+        channels_last = x.is_contiguous(memory_format=torch.channels_last)
+        y = F.layer_norm(x.permute(0, 2, 3, 1), (x.shape[1],), self.weight, self.bias, self.eps)
+        y = y.permute(0, 3, 1, 2)
+        if self.inference_layout:
+            return y
+        return y.contiguous(memory_format=torch.channels_last) if channels_last else y.contiguous()
+
+
+def build_norm(dim, norm_layer="group"):
+    if norm_layer == "group":
+        return nn.GroupNorm(1, dim)
+    if norm_layer == "layernorm2d":
+        return LayerNorm2d(dim)
+    raise ValueError(f"Unsupported norm_layer={norm_layer!r}.")
+
+
+class FeedForwardNetwork(nn.Module):
+    """fc1 -> GELU -> (x + dwconv3(x)) -> GELU -> GRN -> fc2 (``layers.py:38-82``)."""
+
+    def __init__(self, in_features, hidden_features=None, out_features=None, act_layer=nn.GELU,
+                 drop=0.0, use_grn=False, use_dwconv=False):
+        super().__init__()
+        hidden_features = hidden_features or in_features
+        out_features = out_features or in_features
+        self.fc1 = nn.Conv2d(in_features, hidden_features, kernel_size=1)
+        self.act = act_layer()
+        self.use_dwconv = use_dwconv
+        self.dwconv = (
+            nn.Conv2d(hidden_features, hidden_features, kernel_size=3, padding=1, groups=hidden_features)
+            if use_dwconv else nn.Identity())
+        self.dwconv_act = act_layer() if use_dwconv else nn.Identity()
+        self.grn = GlobalResponseNorm(hidden_features) if use_grn else nn.Identity()
+        self.fc2 = nn.Conv2d(hidden_features, out_features, kernel_size=1)
+        self.drop = nn.Dropout(drop)
+
+    def forward(self, x):
+        x = self.fc1(x)
+        x = self.act(x)
+        if self.use_dwconv:
+            x = self.dwconv_act(x + self.dwconv(x))
+        x = self.grn(x)
+        x = self.drop(x)
+        x = self.fc2(x)
+        x = self.drop(x)
+        return x
+
+
+class PatchEmbedding(nn.Module):
+    """Stride-four convolutional stem (``layers.py:85-107``)."""
+
+    def __init__(self, in_chans, embed_dim, patch_size=4):
+        super().__init__()
+        if patch_size != 4:
+            raise ValueError("The VisionHOPE stem requires patch_size=4")
+        widths = [embed_dim // 2, embed_dim // 2, embed_dim, embed_dim]
+        strides = [2, 1, 2, 1]
+        if min(widths) <= 0:
+            raise ValueError("embed_dim is too small for the convolutional stem")
+        layers = []
+        for i, (width, stride) in enumerate(zip(widths, strides)):
+            layers.extend([nn.Conv2d(in_chans, width, 3, stride=stride, padding=1), nn.BatchNorm2d(width)])
+            if i < 3:
+                layers.append(nn.GELU())
+            in_chans = width
+        self.proj = nn.Sequential(*layers)
+        self.norm = nn.Identity()
+
+    def forward(self, x):
+        return self.norm(self.proj(x))
+
+
+class Downsample(nn.Module):
+    """Overlapping stride-two convolution followed by batch normalization (``layers.py:110-119``)."""
+
+    def __init__(self, in_dim, out_dim):
+        super().__init__()
+        self.proj = nn.Conv2d(in_dim, out_dim, 3, stride=2, padding=1, bias=False)
+        self.norm = nn.BatchNorm2d(out_dim)
+
+    def forward(self, x):
+        return self.norm(self.proj(x))

@@ -1,0 +1,61 @@
+"""Native GRN forward on MI355X (replaces ``utils/grn_cuda.py`` + ``utils/csrc/grn_cuda.cu``).
+
+Three launches on the current stream: per-slab partial sums of x^2, per-image
+statistics (gx, 1/(mean gx + eps)), and the FP32 affine output.
+"""
+import torch
+from torch.autograd import Function
+
+from . import hip
+from .autograd import backward_unavailable
+from .cuda import on_tensor_device
+
+
+class _VisionHOPEGRNFunction(Function):
+    @staticmethod
+    @on_tensor_device
+    def forward(ctx, x, gamma, beta, eps):
+        batch, channels, height, width = x.shape
+        if not x.is_contiguous(memory_format=torch.channels_last):
+            x = x.contiguous(memory_format=torch.channels_last)
+        gamma = gamma.detach().reshape(-1).float().contiguous()
+        beta = beta.detach().reshape(-1).float().contiguous()
+        y = torch.empty_like(x, dtype=torch.float32, memory_format=torch.channels_last)
+        gx = torch.empty((batch, channels), device=x.device, dtype=torch.float32)
+        inv_den = torch.empty((batch,), device=x.device, dtype=torch.float32)
+        lib = hip.load_library()
+        nbytes = lib.vh_grn_workspace_bytes(batch, channels, height, width)
+        ws = hip.workspace(nbytes, x.device)
+        hip.check(lib.vh_grn_forward(
+            hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(gamma), hip.ptr(beta), hip.ptr(y),
+            hip.ptr(gx), hip.ptr(inv_den), batch, channels, height, width, float(eps),
+            hip.ptr(ws), ws.numel() * 4, hip.stream_of(x)), "vh_grn_forward")
+        return y
+
+    @staticmethod
+    def backward(ctx, dout):
+        backward_unavailable("GRN")
+
+
+def can_fuse_grn(x, gamma, beta):
+    """Reference eligibility test (``utils/grn_cuda.py:83-98``)."""
+    if x.ndim != 4 or not x.is_cuda or not x.is_contiguous(memory_format=torch.channels_last):
+        return False
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return False
+    channels = x.shape[1]
+    spatial = x.shape[2] * x.shape[3]
+    if x.shape[0] < 1 or x.shape[0] > 65535 or channels < 1 or spatial < 1:
+        return False
+    return (gamma.device == x.device and beta.device == x.device
+            and gamma.dtype == torch.float32 and beta.dtype == torch.float32
+            and gamma.is_contiguous() and beta.is_contiguous()
+            and gamma.numel() == channels and beta.numel() == channels)
+
+
+def visionhope_grn(x, gamma, beta, eps):
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError("GRN supports FP32, FP16 and BF16 input")
+    if x.shape[0] < 1 or x.shape[0] > 65535:
+        raise ValueError("GRN expects nonempty input and batch <= 65535")
+    return _VisionHOPEGRNFunction.apply(x, gamma, beta, eps)
