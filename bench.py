@@ -1,0 +1,299 @@
+"""Benchmark: VisionHOPE-Tiny classification forward, 224x224, B=128, bf16 autocast, on one
+MI355X, plus live roofline figures for the SRNL operator and the memory-bound tail.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Prints ONE JSON line.  ``value`` is images/s of the full forward (HIP graph replay,
+inputs resident in HBM).  ``roofline`` covers the SRNL spatial operator launches
+(scan + readout, ``vh_srnl_spatial_forward``) summed over one forward, timed with
+HIP events on the stream they run on; ``kernels`` breaks it down per stage and adds
+the elementwise kernels of BASELINE config 2.  ``cpu_baseline`` times the same model
+on the host cores with the CPU oracle standing in for SRNL (the reference has no
+CPU SRNL path).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "images/s VisionHOPE-Tiny 224² B=128 bf16; SRNL-scan ms + % of roofline"
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+SEED = 1234
+TINY_STAGES = [  # (grid, mixer channels, depth), head_dim 16 (models/factory.py, hierarchical.py)
+    (56, 32, 3), (28, 64, 4), (14, 128, 18), (7, 256, 4)]
+
+
+def srnl_flops(batch, height, width, channels, head_dim, chunks):
+    """Reference analytic count (analysis/operation_count.py:36-44), FLOP = 2 MAC."""
+    heads = channels // head_dim
+    length = height * width
+    token_cost = 6 * head_dim ** 2 + 20 * head_dim
+    boundary_cost = 3 * head_dim ** 3 + 2 * head_dim ** 2
+    macs = 0
+    for chunk in chunks:
+        boundaries = math.ceil(length / chunk)
+        macs += batch * heads * (boundaries * chunk * token_cost + boundaries * boundary_cost)
+    return 2 * macs
+
+
+def event_time_ms(fn, stream, iters, warmup=2):
+    import torch
+    for _ in range(warmup):
+        fn()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def _perturbed_memories(heads, head_dim, device, gen):
+    """Repo default init for the matrix memories, N(0, 0.1^2) gate vectors so gates vary."""
+    import torch
+    mats = []
+    for _ in range(3):
+        m = torch.empty(4, heads, head_dim, head_dim, device=device)
+        torch.nn.init.trunc_normal_(m, std=0.01, generator=gen)
+        mats.append(m)
+    vecs = [torch.randn(4, heads, head_dim, device=device, generator=gen) * 0.1 for _ in range(2)]
+    return (*mats, *vecs)
+
+
+def measure_srnl_stages(device, batch):
+    """Average duration of one vh_srnl_spatial_forward launch pair per Tiny stage."""
+    import torch
+    from visionhope_amd.models.srnl_core.fused import srnl_spatial_inference
+
+    stream = torch.cuda.current_stream(device)
+    gen = torch.Generator(device=device).manual_seed(SEED)
+    rows, total_flops, total_ms = [], 0.0, 0.0
+    for grid, channels, depth in TINY_STAGES:
+        head_dim = 16
+        heads = channels // head_dim
+        mems = _perturbed_memories(heads, head_dim, device, gen)
+        x = torch.randn(batch, grid, grid, channels, device=device, generator=gen).bfloat16()
+        q = torch.randn(batch, grid, grid, channels, device=device, generator=gen).bfloat16()
+        skip = torch.zeros(channels, device=device)
+        wts = torch.ones(4, channels, device=device)
+        chunks = (grid, grid, grid, grid)
+        ms = event_time_ms(lambda: srnl_spatial_inference(mems, x, q, skip, wts, chunks), stream, 20)
+        flops = srnl_flops(batch, grid, grid, channels, head_dim, chunks)
+        rows.append({"stage": f"{grid}x{grid} C={channels} d={head_dim}", "blocks": depth,
+                     "ms_per_launch": round(ms, 4), "tflops": round(flops / ms / 1e9, 3)})
+        total_flops += flops * depth
+        total_ms += ms * depth
+    return rows, total_flops, total_ms
+
+
+def measure_tail(device):
+    """BASELINE config 2 kernels at full size (B=128): GB/s of compulsory traffic."""
+    import torch
+    from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
+    from visionhope_amd.utils.grn_cuda import visionhope_grn
+    from visionhope_amd.utils.layer_norm_cuda import visionhope_layernorm2d
+
+    stream = torch.cuda.current_stream(device)
+    gen = torch.Generator(device=device).manual_seed(SEED)
+    out = {}
+    for batch, grid, channels in ((128, 56, 96), (128, 28, 192)):
+        heads, head_dim = channels // 16, 16
+        n = batch * grid * grid * channels
+        x = torch.randn(batch, grid, grid, channels, device=device, generator=gen).bfloat16()
+        xc = x.permute(0, 3, 1, 2)
+        gamma = torch.randn(channels, device=device, generator=gen) * 0.1
+        beta = torch.randn(channels, device=device, generator=gen) * 0.1
+        ys = torch.randn(batch, 4, heads, grid * grid, head_dim, device=device, generator=gen).bfloat16()
+        xs = torch.randn(batch, 4, heads, grid * grid, head_dim, device=device, generator=gen).bfloat16()
+        skip = torch.randn(heads, head_dim, device=device, generator=gen) * 0.1
+        scale = 1 + torch.randn(4, channels, device=device, generator=gen) * 0.1
+        tag = f"{grid}x{grid}x{channels}"
+        for name, fn, bytes_per in (
+                ("fusion", lambda: visionhope_postprocess_scale(ys, xs, skip, scale, grid, grid, True), 20),
+                ("grn", lambda: visionhope_grn(xc, gamma, beta, 1e-6), 6),
+                ("layernorm", lambda: visionhope_layernorm2d(xc, gamma, beta, 1e-6), 6)):
+            ms = event_time_ms(fn, stream, 10)
+            gbs = bytes_per * n / ms / 1e6
+            out[f"{name}_{tag}"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+        del x, ys, xs
+    return out
+
+
+def build_tiny(device, channels_last=True):
+    import torch
+    from visionhope_amd.inference.prepare import prepare_for_inference
+    from visionhope_amd.models import create_model
+
+    torch.manual_seed(SEED)
+    model = create_model("visionhope_tiny", drop_path_rate=0.0).to(device)
+    if channels_last:
+        model = model.to(memory_format=torch.channels_last)
+    prepare_for_inference(model)
+    return model
+
+
+def cpu_baseline(sample_batch=8, reps=3):
+    """Tiny forward on the host: PyTorch CPU for convs/linears/norms and the CPU oracle
+    (oracle/liboracle_srnl.so, OpenMP) for the four-direction SRNL operator."""
+    import torch
+    from oracle import oracle
+    from visionhope_amd.models import operator as op_mod
+
+    threads = torch.get_num_threads()
+
+    def oracle_forward(self, x, *, channels_last=None):
+        x_nhwc = x.float().permute(0, 2, 3, 1).contiguous()
+        with torch.no_grad():
+            q = self.W_q(x_nhwc)
+        mems = tuple(m.detach().numpy() for m in self.srnl.initial_memories)
+        out = oracle.operator_forward(x_nhwc.numpy(), q.numpy(), mems, self.d_skip.detach().numpy(),
+                                      self.direction_weights().detach().numpy(), self.head_dim)
+        return torch.from_numpy(out).permute(0, 3, 1, 2)
+
+    model = build_tiny(torch.device("cpu"), channels_last=False)
+    original = op_mod.VisionHOPEOperator.forward
+    op_mod.VisionHOPEOperator.forward = oracle_forward
+    try:
+        # On CPU tensors the blocks take the ordinary branch, which calls operator.forward.
+        gen = torch.Generator().manual_seed(SEED)
+        images = torch.randn(sample_batch, 3, 224, 224, generator=gen)
+        times = []
+        with torch.no_grad():
+            model(images)
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                model(images)
+                times.append(time.perf_counter() - t0)
+    finally:
+        op_mod.VisionHOPEOperator.forward = original
+    sec = statistics.median(times)
+    return {"value": round(sample_batch / sec, 3), "unit": "images/s", "cores": threads,
+            "kind": "port",
+            "sample": f"VisionHOPE-Tiny 224x224 forward, B={sample_batch}, fp32, median of {reps}; "
+                      f"PyTorch CPU ({threads} threads) + C oracle SRNL (OMP_NUM_THREADS="
+                      f"{os.environ.get('OMP_NUM_THREADS', 'unset')}), "
+                      f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}"}
+
+
+def main(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--batch", type=int, default=128)
+    parser.add_argument("--no-graph", action="store_true", help="time eager forwards instead of a HIP graph")
+    parser.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(every GPU box in this build has a single MI355X).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    torch.backends.cuda.matmul.allow_tf32 = True
+    torch.backends.cudnn.allow_tf32 = True
+    model = build_tiny(device)
+    gen = torch.Generator().manual_seed(SEED)
+    images = torch.randn(args.batch, 3, 224, 224, generator=gen).to(device)
+    images = images.contiguous(memory_format=torch.channels_last)
+
+    def forward():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            return model(images)
+
+    with torch.inference_mode():
+        for _ in range(3):
+            out = forward()
+        torch.cuda.synchronize()
+        if not torch.isfinite(out).all():
+            raise FloatingPointError("Tiny forward produced NaN/Inf")
+        execution = "eager"
+        graph = None
+        if not args.no_graph:
+            try:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    graph_out = forward()
+                graph.replay()
+                torch.cuda.synchronize()
+                if not torch.allclose(graph_out.float(), out.float(), atol=1e-2, rtol=1e-2):
+                    raise RuntimeError("graph replay disagrees with eager forward")
+                execution = "hip_graph"
+            except Exception as exc:  # capture unsupported by a library call: time eager
+                print(f"HIP graph capture unavailable ({exc}); timing eager forwards", file=sys.stderr)
+                graph = None
+        step = graph.replay if graph is not None else forward
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(device)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(args.steps):
+            step()
+        end.record(stream)
+        end.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = start.elapsed_time(end) / args.steps
+        del graph
+
+        stage_rows, srnl_flops_total, srnl_ms_total = measure_srnl_stages(device, args.batch)
+        tail = measure_tail(device)
+
+    images_per_s = args.batch * 1000.0 / ms
+    achieved = srnl_flops_total / srnl_ms_total / 1e9  # TFLOP/s
+    result = {
+        "metric": METRIC,
+        "value": round(images_per_s, 2),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "visionhope_tiny_classification_forward", "resolution": 224,
+                   "global_batch": args.batch, "execution": execution, "autocast": "bf16",
+                   "weights": "random-init (repo default init)", "seed": SEED,
+                   "wall_s_timed_region": round(wall, 3)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 5), "traffic": None,
+                     "kernel": "vh_srnl_spatial_forward (srnl_scan_kernel + srnl_fuse_readout_kernel), "
+                               "all 29 Tiny blocks at B=128",
+                     "srnl_ms_per_forward": round(srnl_ms_total, 3),
+                     "algorithmic_gflop_per_forward": round(srnl_flops_total / 1e9, 2)},
+        "kernels": {"srnl_stages": stage_rows, **tail},
+    }
+    if not args.skip_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
