@@ -7,7 +7,7 @@ Prints ONE JSON line.  ``value`` is images/s of the full forward (HIP graph repl
 inputs resident in HBM).  ``roofline`` covers the SRNL spatial operator launches
 (scan + readout, ``vh_srnl_spatial_forward``) summed over one forward, timed with
 HIP events on the stream they run on; ``kernels`` breaks it down per stage and adds
-the elementwise kernels of BASELINE config 2.  ``cpu_baseline`` times the same model
+the fused elementwise workload (B=128 at 56x56x96 and 28x28x192).  ``cpu_baseline`` times the same model
 on the host cores with the CPU oracle standing in for SRNL (the reference has no
 CPU SRNL path).
 """
@@ -102,7 +102,7 @@ def measure_srnl_stages(device, batch):
 
 
 def measure_tail(device):
-    """BASELINE config 2 kernels at full size (B=128): GB/s of compulsory traffic."""
+    """Fusion, GRN and LN at B=128, 56x56x96 and 28x28x192, bf16: GB/s of compulsory traffic."""
     import torch
     from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
     from visionhope_amd.utils.grn_cuda import visionhope_grn

@@ -1,0 +1,122 @@
+"""The C ABI library: it loads, exports every symbol the public header declares, and
+rejects invalid arguments on the host (before any GPU work) with status codes and
+messages.  No kernel runs here: every call below fails validation first."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from visionhope_amd.utils import hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "visionhope_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(vh_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return hip.load_library()
+
+
+def test_header_declares_expected_entry_points():
+    assert set(_declared()) == set(hip.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(hip.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r" T (vh_\w+)$", out, re.M))
+    missing = set(_declared()) - exported
+    assert not missing, missing
+    for name in _declared():
+        assert getattr(lib, name) is not None
+
+
+def test_library_is_gfx950_and_links_one_hip_runtime():
+    out = subprocess.run(["readelf", "-d", str(hip.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    assert "libamdhip64.so" in out
+    blob = hip.LIB_PATH.read_bytes()
+    assert b"gfx950" in blob
+
+
+def test_abi_version_matches_header(lib):
+    version = int(re.search(r"#define VH_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert lib.vh_abi_version() == version
+
+
+def test_workspace_queries(lib):
+    assert lib.vh_srnl_workspace_bytes(10, 7, 16) == 10 * 7 * 16 * 16 * 4
+    assert lib.vh_srnl_workspace_bytes(0, 7, 16) == 0
+    assert lib.vh_grn_workspace_bytes(2, 8, 10, 10) == 2 * 2 * 8 * 4   # 100 pixels -> 2 slabs of 64
+
+
+def _consts():
+    return hip.make_consts(0.025, 0.0, 2.197224577, 0.999, True, 0.999999)
+
+
+def _spatial(lib, head_dim=16, dtype=hip.VH_DTYPE_BF16, workspace=4096, x=1, chunks=(4, 4, 4, 4),
+             consts=None):
+    p = ctypes.c_void_p(0x1000)
+    arr, keep = hip.int64_array(chunks)
+    return lib.vh_srnl_spatial_forward(
+        ctypes.c_void_p(x) if x else None, p, dtype, p, p, p, p, p, p, 0, p, p,
+        2, 4, 4, 2 * head_dim if head_dim else 32, head_dim, arr,
+        consts if consts is not None else _consts(), p, workspace, None)
+
+
+def test_srnl_rejects_bad_head_dim(lib):
+    assert _spatial(lib, head_dim=12) == hip.VH_ERR_HEAD_DIM
+    assert b"head_dim" in lib.vh_last_error()
+
+
+def test_srnl_rejects_bad_dtype(lib):
+    assert _spatial(lib, dtype=7) == hip.VH_ERR_DTYPE
+
+
+def test_srnl_rejects_small_workspace(lib):
+    assert _spatial(lib, workspace=16) == hip.VH_ERR_WORKSPACE
+    assert b"workspace" in lib.vh_last_error()
+
+
+def test_srnl_rejects_null_input(lib):
+    assert _spatial(lib, x=0) == hip.VH_ERR_ARG
+
+
+def test_srnl_rejects_bad_chunks_and_constants(lib):
+    assert _spatial(lib, chunks=(4, 0, 4, 4)) == hip.VH_ERR_ARG
+    bad = hip.make_consts(0.025, 1.5, 2.197224577, 0.999, True, 0.999999)
+    assert _spatial(lib, consts=bad) == hip.VH_ERR_ARG
+    assert b"MIN_RETENTION" in lib.vh_last_error()
+
+
+def test_grn_rejects_missing_workspace(lib):
+    p = ctypes.c_void_p(0x1000)
+    rc = lib.vh_grn_forward(p, hip.VH_DTYPE_BF16, p, p, p, p, p, 2, 8, 4, 4, 1e-6, None, 0, None)
+    assert rc == hip.VH_ERR_WORKSPACE
+
+
+def test_layernorm_rejects_empty(lib):
+    p = ctypes.c_void_p(0x1000)
+    rc = lib.vh_layernorm2d_forward(p, hip.VH_DTYPE_F32, p, p, p, None, None, 0, 8, 4, 4, 1e-6, 1, None)
+    assert rc == hip.VH_ERR_SHAPE
+
+
+def test_check_raises_with_message(lib):
+    assert _spatial(lib, head_dim=12) == hip.VH_ERR_HEAD_DIM
+    with pytest.raises(RuntimeError, match="head_dim"):
+        hip.check(hip.VH_ERR_HEAD_DIM, "vh_srnl_spatial_forward")
+    with pytest.raises(TypeError):
+        hip.check(hip.VH_ERR_DTYPE, "x")
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(hip.NativeLibraryMissing):
+        hip.load_library(tmp_path / "absent.so")

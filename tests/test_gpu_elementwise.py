@@ -1,5 +1,5 @@
 """GPU parity of the elementwise kernels (direction fusion, GRN, LayerNorm2d, qnorm,
-residual) against the CPU oracle, including BASELINE config 2's full B=128 shapes."""
+residual) against the CPU oracle, including the full B=128 elementwise workload."""
 
 import numpy as np
 import pytest
@@ -34,7 +34,7 @@ def test_direction_fusion(oracle, device, dtype, channels_last, per_direction):
 
 @pytest.mark.parametrize("shape", [(128, 96, 56, 56), (128, 192, 28, 28)])
 def test_config2_full_size(oracle, device, shape):
-    """BASELINE config 2 at full size: fusion, GRN and LN on bf16 activations."""
+    """Full-size elementwise workload (B=128, 56x56x96 and 28x28x192): fusion, GRN, LN in bf16."""
     from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
     from visionhope_amd.utils.grn_cuda import visionhope_grn
     from visionhope_amd.utils.layer_norm_cuda import visionhope_layernorm2d

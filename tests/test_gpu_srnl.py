@@ -1,6 +1,6 @@
 """GPU parity of the SRNL kernels (through the C ABI) against the CPU oracle.
 
-Tolerances (from the build's north star): fp32 I/O 1e-4 normwise and
+Tolerances: fp32 I/O 1e-4 normwise and
 elementwise-on-scale; bf16/fp16 I/O 2e-2 with the oracle fed the same rounded
 inputs.
 """
@@ -40,7 +40,7 @@ def test_sequence_forward_fp32_head_dims(oracle, device, head_dim, kind):
 
 
 def test_config1_standalone_srnl(oracle, device):
-    """B=2, 14x14 tokens (L=196), C=64 in 2 heads, chunk 14, fp32."""
+    """Standalone SRNL workload: B=2, 14x14 tokens (L=196), C=64 in 2 heads, chunk 14, fp32."""
     from visionhope_amd.models import SRNL
 
     torch.manual_seed(1234)
@@ -110,7 +110,7 @@ def test_spatial_forward_fp32(oracle, device, height, width, head_dim, heads, sk
 
 
 def test_spatial_forward_bf16_config3_shape(oracle, device):
-    """BASELINE config 3 shape at reduced batch (B=2, 56x56, C=96, 3 heads of 32), bf16."""
+    """Operator workload shape at reduced batch (B=2, 56x56, C=96, 3 heads of 32), bf16."""
     heads, head_dim, hw = 3, 32, 56
     channels = heads * head_dim
     mems = memories(4, heads, head_dim, kind="perturbed", seed=9)
@@ -170,7 +170,7 @@ def test_zero_length_rejected(device):
 
 
 def test_full_config3_properties(device):
-    """Full BASELINE config 3 (B=32, 56x56, C=96, d=32, bf16) is too large for the oracle
+    """Full operator workload (B=32, 56x56, C=96, d=32, bf16) is too large for the oracle
     in seconds; check the closed form that fixes it exactly: with M_k = M_v = 0 and zero
     gate vectors every gain is 0.9^56 I, so y_r of a pixel in chunk c is
     0.9^(56 c) M_m q_hat (first-chunk GEMM, then pure decay)."""
