@@ -45,6 +45,13 @@ struct LineInput {
     int64_t H, W;
 };
 
+// Chunk length of direction r.  Constant indices only: a runtime index into a
+// kernel-argument array makes the compiler copy the whole argument block to
+// scratch memory (and demotes every pointer in it to flat addressing).
+__device__ __forceinline__ int chunk_of(const int (&chunk)[4], int r) {
+    return r == 0 ? chunk[0] : r == 1 ? chunk[1] : r == 2 ? chunk[2] : chunk[3];
+}
+
 template <typename T>
 __device__ __forceinline__ const T* line_ptr(const LineInput& in, int64_t b, int r, int64_t head,
                                              int64_t t) {
@@ -61,29 +68,100 @@ struct ScanParams {
     int64_t max_chunks;
     float* states;  // [lines, max_chunks, D, D]: chunk-start M_m
     int per_line_state;  // 1: memories hold one state per line (chunk.cu:287, StateCount == N)
+    int x_vec;           // input rows are aligned for vector loads
     Consts k;
 };
 
 template <int D>
 struct ScanCfg {
-    static constexpr int NT = 4 * D;             // threads per line
-    static constexpr int E = D / 4;              // G entries per thread (4 lanes per row)
-    static constexpr int TT = D == 64 ? 32 : 64; // tokens per tile
-    static constexpr int SD = D + 1;             // padded LDS row
-    static constexpr int ROWS = 3 * D + 2;       // M_m, M_v, M_k rows, then e, a
-    static constexpr int NOUT = (ROWS * D + NT - 1) / NT;
+    static constexpr int NT = 4 * D;                            // threads per line
+    static constexpr int E = D / 4;                             // G entries per thread (4 lanes per row)
+    static constexpr int TT = D <= 8 ? NT : (D == 64 ? 32 : 64);  // tokens per tile
+    static constexpr int TPT = NT / TT;                         // token-phase threads per token
+    static constexpr int RPT = D / TPT;                         // key/value rows per token-phase thread
+    static constexpr int ROWS = 3 * D + 2;                      // M_m, M_v, M_k rows, then e, a
+    static constexpr int GS = D + 1;                            // padded stride of the gain staging
+    static constexpr int NCOLG = NT / D;                        // refresh column groups
+    static constexpr int NOUT = (ROWS + NCOLG - 1) / NCOLG;     // refresh rows per thread
 };
+
+// Row of D elements starting at p, as fp32.  `vec`: p is 16-byte aligned (8-byte for
+// D = 4 with 16-bit elements) so whole rows move with vector loads.
+template <typename T, int D>
+__device__ __forceinline__ void load_row(const T* p, bool vec, float (&out)[D]) {
+    if (vec) {
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int j = 0; j < D; j += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(p + j);
+                out[j] = v.x; out[j + 1] = v.y; out[j + 2] = v.z; out[j + 3] = v.w;
+            }
+            return;
+        } else if constexpr (D % 8 == 0) {
+#pragma unroll
+            for (int j = 0; j < D; j += 8) {
+                const uint4 v = *reinterpret_cast<const uint4*>(p + j);
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    out[j + 2 * h] = to_f32(T{static_cast<uint16_t>(w[h] & 0xffffu)});
+                    out[j + 2 * h + 1] = to_f32(T{static_cast<uint16_t>(w[h] >> 16)});
+                }
+            }
+            return;
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(p);
+            out[0] = to_f32(T{static_cast<uint16_t>(v.x & 0xffffu)});
+            out[1] = to_f32(T{static_cast<uint16_t>(v.x >> 16)});
+            out[2] = to_f32(T{static_cast<uint16_t>(v.y & 0xffffu)});
+            out[3] = to_f32(T{static_cast<uint16_t>(v.y >> 16)});
+            return;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j) out[j] = to_f32(p[j]);
+}
+
+template <int D>
+__device__ __forceinline__ float dot_lds(const float* row, const float (&x)[D]) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; j += 4) {
+        const float4 s = *reinterpret_cast<const float4*>(row + j);
+        acc += s.x * x[j];
+        acc += s.y * x[j + 1];
+        acc += s.z * x[j + 2];
+        acc += s.w * x[j + 3];
+    }
+    return acc;
+}
+
+// Sum over the N consecutive lanes of a group (N a power of two, N <= 8).
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = 1; off < N; off <<= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Butterfly steps inside a quad of lanes, on the VALU (DPP quad_perm).
+__device__ __forceinline__ float quad_swap1(float v) {  // lanes (1,0,3,2)
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_swap2(float v) {  // lanes (2,3,0,1)
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
 
 template <int D, typename T>
 __global__ __launch_bounds__(4 * D) void srnl_scan_kernel(const ScanParams p) {
     using Cfg = ScanCfg<D>;
-    constexpr int NT = Cfg::NT, E = Cfg::E, TT = Cfg::TT, SD = Cfg::SD, ROWS = Cfg::ROWS;
-    __shared__ float S[ROWS * SD];
-    __shared__ float Gs[D * SD];
-    __shared__ float xs[TT * SD];
-    __shared__ float kk[TT * SD];
-    __shared__ float vd[TT * SD];
-    __shared__ float ep_s[TT], ap_s[TT], al_s[TT], et_s[TT];
+    constexpr int NT = Cfg::NT, E = Cfg::E, TT = Cfg::TT, TPT = Cfg::TPT, RPT = Cfg::RPT;
+    constexpr int ROWS = Cfg::ROWS, GS = Cfg::GS, NCOLG = Cfg::NCOLG, NOUT = Cfg::NOUT;
+    __shared__ __align__(16) float S[ROWS * D];   // state rows
+    __shared__ __align__(16) float Gs[D * GS];    // chunk gain staging
+    __shared__ __align__(16) float kk[TT * D];    // normalised keys of the tile
+    __shared__ __align__(16) float dk[TT * D];    // k - v of the tile
+    __shared__ float al_s[TT], et_s[TT];         // retention, projected step
 
     const int64_t lines = p.B * p.R * p.heads;
     const int64_t line = xcd_remap(blockIdx.x, lines);
@@ -94,27 +172,37 @@ __global__ __launch_bounds__(4 * D) void srnl_scan_kernel(const ScanParams p) {
     const int tid = threadIdx.x;
 
     for (int idx = tid; idx < D * D; idx += NT) {
-        const int row = idx / D, col = idx % D;
-        S[row * SD + col] = p.Mm[s * D * D + idx];
-        S[(D + row) * SD + col] = p.Mv[s * D * D + idx];
-        S[(2 * D + row) * SD + col] = p.Mk[s * D * D + idx];
+        S[idx] = p.Mm[s * D * D + idx];
+        S[D * D + idx] = p.Mv[s * D * D + idx];
+        S[2 * D * D + idx] = p.Mk[s * D * D + idx];
     }
     for (int idx = tid; idx < D; idx += NT) {
-        S[3 * D * SD + idx] = p.Me[s * D + idx];
-        S[(3 * D + 1) * SD + idx] = p.Ma[s * D + idx];
+        S[3 * D * D + idx] = p.Me[s * D + idx];
+        S[(3 * D + 1) * D + idx] = p.Ma[s * D + idx];
     }
 
-    const int C = p.chunk[r];
+    const int C = chunk_of(p.chunk, r);
     const int64_t nc = (p.L + C - 1) / C;
-    const int grow = tid / 4;       // row of G held by this thread
-    const int c0 = (tid % 4) * E;   // first column of G held by this thread
+    const int grow = tid / 4;                 // recurrence: row of G held by this thread
+    const int c0 = (tid % 4) * E;             // recurrence: first column held
+    const int t_loc = tid / TPT;              // token phase: token of this thread
+    const int sub = tid % TPT;                // token phase: row phase of this thread
+    const int gcol = tid % D;                 // refresh: column of G held
+    const int ggrp = tid / D;                 // refresh: row group
     float* out_states = p.states + line * p.max_chunks * D * D;
+    // One wave holds a whole line and owns token t in lane t: gates travel by readlane.
+    constexpr bool kLaneGates = TPT == 1 && NT <= 64;
+    // Registers for the next tile's x rows (skipped where they would spill).
+    constexpr bool kPrefetch = D <= 32;
+    float xnext[D];
+    bool have_next = false;
 
     for (int64_t c = 0; c < nc; ++c) {
         __syncthreads();
-        for (int idx = tid; idx < D * D; idx += NT)
-            out_states[c * D * D + idx] = S[(idx / D) * SD + idx % D];
-        // The last chunk's gain only feeds a refresh no output reads.
+        for (int idx = tid * 4; idx < D * D; idx += NT * 4)
+            *reinterpret_cast<float4*>(out_states + c * D * D + idx) =
+                *reinterpret_cast<const float4*>(S + idx);
+        // The last chunk's gain only feeds a refresh that no output reads.
         if (c == nc - 1) break;
 
         float g[E];
@@ -123,96 +211,511 @@ __global__ __launch_bounds__(4 * D) void srnl_scan_kernel(const ScanParams p) {
 
         for (int base = 0; base < C; base += TT) {
             const int cnt = min(TT, C - base);
-            for (int idx = tid; idx < cnt * D; idx += NT) {
-                const int t = idx / D, j = idx % D;
-                const int64_t tok = c * C + base + t;
-                xs[t * SD + j] = tok < p.L ? to_f32(line_ptr<T>(p.x, b, r, head, tok)[j]) : 0.f;
-            }
-            __syncthreads();
-            // values (rows D..2D-1), raw keys (2D..3D-1), gate pre-activations (3D, 3D+1)
-            for (int idx = tid; idx < (2 * D + 2) * cnt; idx += NT) {
-                const int t = idx / (2 * D + 2), rr = idx % (2 * D + 2);
-                const float* srow = &S[(D + rr) * SD];
-                const float* xt = &xs[t * SD];
-                float acc = 0.f;
+            // ---- token phase: keys, values, gates from the chunk-start state ----
+            float xr[D];
+            if (kPrefetch && have_next) {
 #pragma unroll
-                for (int j = 0; j < D; ++j) acc += srow[j] * xt[j];
-                if (rr < D) vd[t * SD + rr] = acc;
-                else if (rr < 2 * D) kk[t * SD + rr - D] = acc;
-                else if (rr == 2 * D) ep_s[t] = acc;
-                else ap_s[t] = acc;
+                for (int j = 0; j < D; ++j) xr[j] = xnext[j];
+            } else {
+                const int64_t tok = c * C + base + t_loc;
+                if (t_loc < cnt && tok < p.L) load_row<T, D>(line_ptr<T>(p.x, b, r, head, tok), p.x_vec, xr);
+                else {
+#pragma unroll
+                    for (int j = 0; j < D; ++j) xr[j] = 0.f;
+                }
             }
-            __syncthreads();
-            // per-token normalisation and gates
-            for (int t = tid; t < cnt; t += NT) {
+            float my_alpha, my_eff;
+            {
+                float kr[RPT], vr[RPT];
                 float kn = 0.f;
 #pragma unroll
-                for (int j = 0; j < D; ++j) kn += kk[t * SD + j] * kk[t * SD + j];
+                for (int m = 0; m < RPT; ++m) {
+                    const int i = sub + TPT * m;
+                    kr[m] = dot_lds<D>(S + (2 * D + i) * D, xr);
+                    vr[m] = dot_lds<D>(S + (D + i) * D, xr);
+                    kn += kr[m] * kr[m];
+                }
+                kn = group_sum<TPT>(kn);
                 const float den = sqrtf(kn + 1e-6f);
                 float dsq = 0.f, ksq = 0.f;
 #pragma unroll
-                for (int j = 0; j < D; ++j) {
-                    const float kv = kk[t * SD + j] / den;
-                    kk[t * SD + j] = kv;
-                    const float diff = kv - vd[t * SD + j];
-                    vd[t * SD + j] = diff;
-                    dsq += diff * diff;
+                for (int m = 0; m < RPT; ++m) {
+                    const float kv = kr[m] / den;
+                    kr[m] = kv;
+                    vr[m] = kv - vr[m];
+                    dsq += vr[m] * vr[m];
                     ksq += kv * kv;
                 }
-                const float ep = fminf(10.f, fmaxf(-10.f, ep_s[t]));
-                const float ap = fminf(10.f, fmaxf(-10.f, ap_s[t] + p.k.alpha_bias));
+                dsq = group_sum<TPT>(dsq);
+                ksq = group_sum<TPT>(ksq);
+                float ep = dot_lds<D>(S + 3 * D * D, xr);
+                float ap = dot_lds<D>(S + (3 * D + 1) * D, xr);
+                ep = fminf(10.f, fmaxf(-10.f, ep));
+                ap = fminf(10.f, fmaxf(-10.f, ap + p.k.alpha_bias));
                 const float sp = ep > 20.f ? ep : logf(1.f + expf(ep));
                 const float eta = p.k.eta_scale * sp;
                 const float alpha = p.k.alpha_min + (1.f - p.k.alpha_min) * (1.f / (1.f + expf(-ap)));
                 const float dn = sqrtf(dsq + 1e-12f);
                 const float cap = p.k.stab_mu * (1.f - alpha) / (dn + 1e-6f);
                 float eff = cap * (-expm1f(-(eta / cap)));
-                if (p.k.clamp) {
-                    const float lim = nextafterf(p.k.factor * alpha / fmaxf(ksq, 1e-20f), 0.f);
-                    eff = fminf(eff, lim);
+                if (p.k.clamp) eff = fminf(eff, nextafterf(p.k.factor * alpha / fmaxf(ksq, 1e-20f), 0.f));
+                my_alpha = alpha;
+                my_eff = eff;
+                if (t_loc < cnt) {
+#pragma unroll
+                    for (int m = 0; m < RPT; ++m) {
+                        kk[t_loc * D + sub + TPT * m] = kr[m];
+                        dk[t_loc * D + sub + TPT * m] = vr[m];
+                    }
+                    if (!kLaneGates && sub == 0) {
+                        al_s[t_loc] = alpha;
+                        et_s[t_loc] = eff;
+                    }
                 }
-                al_s[t] = alpha;
-                et_s[t] = eff;
+            }
+            // ---- prefetch the x rows of the next tile (the next chunk's first tile
+            //      if this is the last one); their loads overlap the recurrence ----
+            if constexpr (kPrefetch) {
+                int64_t nc_idx = c, nbase = base + TT;
+                if (nbase >= C) { nc_idx = c + 1; nbase = 0; }
+                have_next = nc_idx < nc - 1;
+                if (have_next) {
+                    const int ncnt = min(TT, C - static_cast<int>(nbase));
+                    const int64_t tok = nc_idx * C + nbase + t_loc;
+                    if (t_loc < ncnt && tok < p.L)
+                        load_row<T, D>(line_ptr<T>(p.x, b, r, head, tok), p.x_vec, xnext);
+                    else {
+#pragma unroll
+                        for (int j = 0; j < D; ++j) xnext[j] = 0.f;
+                    }
+                }
             }
             __syncthreads();
-            // serial gain recurrence; rows are independent, 4 lanes per row
-            for (int t = 0; t < cnt; ++t) {
-                const float* kt = &kk[t * SD];
-                float dot = 0.f;
+            // ---- serial gain recurrence: 4 lanes per row of G; operands of the next
+            //      U tokens are read from LDS while the current U are processed ----
+            constexpr int U = 4;
+            float kvb[U][E], dfb[U], alb[U], etb[U];
 #pragma unroll
-                for (int e = 0; e < E; ++e) dot += g[e] * kt[c0 + e];
-                dot += __shfl_xor(dot, 1);
-                dot += __shfl_xor(dot, 2);
-                const float rv = vd[t * SD + grow] + dot;
-                const float alpha = al_s[t];
-                const float coef = et_s[t] * rv;
+            for (int u = 0; u < U; ++u) {
+                const int t = min(u, cnt - 1);
 #pragma unroll
-                for (int e = 0; e < E; ++e) g[e] = alpha * g[e] - coef * kt[c0 + e];
+                for (int e = 0; e < E; ++e) kvb[u][e] = kk[t * D + c0 + e];
+                dfb[u] = dk[t * D + grow];
+                if constexpr (!kLaneGates) {
+                    alb[u] = al_s[t];
+                    etb[u] = et_s[t];
+                }
+            }
+            for (int t0 = 0; t0 < cnt; t0 += U) {
+                float kvn[U][E], dfn[U], aln[U], etn[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int t = min(t0 + U + u, cnt - 1);
+#pragma unroll
+                    for (int e = 0; e < E; ++e) kvn[u][e] = kk[t * D + c0 + e];
+                    dfn[u] = dk[t * D + grow];
+                    if constexpr (!kLaneGates) {
+                        aln[u] = al_s[t];
+                        etn[u] = et_s[t];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    if (t0 + u < cnt) {
+                        float alpha, eta;
+                        if constexpr (kLaneGates) {
+                            // token t0+u was produced by lane t0+u: broadcast to all lanes
+                            alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_alpha), t0 + u));
+                            eta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_eff), t0 + u));
+                        } else {
+                            alpha = alb[u];
+                            eta = etb[u];
+                        }
+                        float dot = 0.f;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) dot += g[e] * kvb[u][e];
+                        dot += quad_swap1(dot);
+                        dot += quad_swap2(dot);
+                        const float coef = eta * (dfb[u] + dot);
+#pragma unroll
+                        for (int e = 0; e < E; ++e) g[e] = alpha * g[e] - coef * kvb[u][e];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) kvb[u][e] = kvn[u][e];
+                    dfb[u] = dfn[u];
+                    alb[u] = aln[u];
+                    etb[u] = etn[u];
+                }
             }
             __syncthreads();
         }
-        // refresh: S <- S G (all 3D+2 rows)
+        // ---- refresh: S <- S G (all 3D+2 rows) ----
 #pragma unroll
-        for (int e = 0; e < E; ++e) Gs[grow * SD + c0 + e] = g[e];
+        for (int e = 0; e < E; ++e) Gs[grow * GS + c0 + e] = g[e];
         __syncthreads();
-        float buf[Cfg::NOUT];
+        float outv[NOUT];
+        if constexpr (D <= 16) {
+            // Column of G in registers, state rows as LDS broadcasts.
+            float gc[D];
 #pragma unroll
-        for (int q = 0; q < Cfg::NOUT; ++q) {
-            const int idx = tid + q * NT;
-            float acc = 0.f;
-            if (idx < ROWS * D) {
-                const int row = idx / D, col = idx % D;
+            for (int l = 0; l < D; ++l) gc[l] = Gs[l * GS + gcol];
 #pragma unroll
-                for (int l = 0; l < D; ++l) acc += S[row * SD + l] * Gs[l * SD + col];
+            for (int m = 0; m < NOUT; ++m) {
+                const int rr = ggrp + NCOLG * m;
+                outv[m] = rr < ROWS ? dot_lds<D>(S + rr * D, gc) : 0.f;
             }
-            buf[q] = acc;
+        } else {
+            // Large heads: both operands from LDS (a register copy of the column spills).
+#pragma unroll
+            for (int m = 0; m < NOUT; ++m) outv[m] = 0.f;
+#pragma unroll 4
+            for (int l = 0; l < D; ++l) {
+                const float gl = Gs[l * GS + gcol];
+#pragma unroll
+                for (int m = 0; m < NOUT; ++m) {
+                    const int rr = ggrp + NCOLG * m;
+                    if (rr < ROWS) outv[m] += S[rr * D + l] * gl;
+                }
+            }
         }
         __syncthreads();
 #pragma unroll
-        for (int q = 0; q < Cfg::NOUT; ++q) {
-            const int idx = tid + q * NT;
-            if (idx < ROWS * D) S[(idx / D) * SD + idx % D] = buf[q];
+        for (int m = 0; m < NOUT; ++m) {
+            const int rr = ggrp + NCOLG * m;
+            if (rr < ROWS) S[rr * D + gcol] = outv[m];
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// head_dim 16: one wave per line, projections and refresh on MFMA.
+//
+// v_mfma_f32_16x16x4_f32 lane layout (wave64): lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; the 16x16 result lands in lane l as rows 4(l/16)..4(l/16)+3 of
+// column l%16.  A K=16 product runs as 4 steps; step s takes logical index
+// 4(l/16)+s from lane l, so every lane reads 4 consecutive values of a row.
+//
+//   token phase  [K~ ; V] (32 x 64 tokens) = [M_k ; M_v] (32 x 16) . X (16 x 64)
+//                -> lane l ends up with rows 4q..4q+3 (q = l/16) of tokens
+//                   16T + l%16, T = 0..3: norms reduce over the 4 lane groups.
+//   refresh      S (64 x 16, 50 rows used) <- S . G
+// The serial gain recurrence stays on the VALU (4 lanes per row of G).
+// ---------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Four consecutive elements of a row as fp32 (8- or 16-byte load when `vec`).
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, bool vec, float (&out)[4]) {
+    if (vec) {
+        if constexpr (sizeof(T) == 4) {
+            const float4 v = *reinterpret_cast<const float4*>(p);
+            out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(p);
+            out[0] = to_f32(T{static_cast<uint16_t>(v.x & 0xffffu)});
+            out[1] = to_f32(T{static_cast<uint16_t>(v.x >> 16)});
+            out[2] = to_f32(T{static_cast<uint16_t>(v.y & 0xffffu)});
+            out[3] = to_f32(T{static_cast<uint16_t>(v.y >> 16)});
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = to_f32(p[j]);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float quad_perm(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ float xor16_32_sum(float v) {
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
+    constexpr int D = 16, TT = 64, ROWS = 3 * D + 2, GS = D + 1;
+    __shared__ __align__(16) float S[64 * D];    // 50 state rows + zero padding rows
+    __shared__ __align__(16) float Gs[D * GS];
+    __shared__ __align__(16) float kk[TT * D];
+    __shared__ __align__(16) float dk[TT * D];
+
+    const int64_t lines = p.B * p.R * p.heads;
+    const int64_t line = xcd_remap(blockIdx.x, lines);
+    const int64_t head = line % p.heads;
+    const int r = static_cast<int>((line / p.heads) % p.R);
+    const int64_t b = line / (p.heads * p.R);
+    const int64_t s = p.per_line_state ? line : r * p.heads + head;
+    const int lane = threadIdx.x;
+    const int i16 = lane & 15, q = lane >> 4;
+
+    for (int idx = lane; idx < D * D; idx += 64) {
+        S[idx] = p.Mm[s * D * D + idx];
+        S[D * D + idx] = p.Mv[s * D * D + idx];
+        S[2 * D * D + idx] = p.Mk[s * D * D + idx];
+    }
+    if (lane < D) {
+        S[3 * D * D + lane] = p.Me[s * D + lane];
+        S[(3 * D + 1) * D + lane] = p.Ma[s * D + lane];
+    }
+    for (int idx = ROWS * D + lane; idx < 64 * D; idx += 64) S[idx] = 0.f;
+
+    const int C = chunk_of(p.chunk, r);
+    const int64_t nc = (p.L + C - 1) / C;
+    const int grow = lane / 4, c0 = (lane % 4) * 4;   // recurrence layout
+    float* out_states = p.states + line * p.max_chunks * D * D;
+
+    // x operands of the next tile (prefetched during the current recurrence)
+    float xn[4][4];
+    bool have_next = false;
+    auto load_tile = [&](int64_t cc, int base, int cnt, float (&xo)[4][4]) {
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) {
+            const int t = 16 * tc + i16;
+            const int64_t tok = cc * C + base + t;
+            if (t < cnt && tok < p.L) load4<T>(line_ptr<T>(p.x, b, r, head, tok) + 4 * q, p.x_vec, xo[tc]);
+            else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xo[tc][j] = 0.f;
+            }
+        }
+    };
+
+    for (int64_t c = 0; c < nc; ++c) {
+        __syncthreads();
+        *reinterpret_cast<float4*>(out_states + c * D * D + lane * 4) =
+            *reinterpret_cast<const float4*>(S + lane * 4);
+        if (c == nc - 1) break;
+
+        float g[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g[e] = (c0 + e == grow) ? 1.f : 0.f;
+        // A operands of the projections (rows of M_k, M_v) and the gate vectors
+        float ak[4], av[4], ev[4], avv[4];
+        {
+            const float4 k4 = *reinterpret_cast<const float4*>(S + (2 * D + i16) * D + 4 * q);
+            const float4 v4 = *reinterpret_cast<const float4*>(S + (D + i16) * D + 4 * q);
+            const float4 e4 = *reinterpret_cast<const float4*>(S + 3 * D * D + 4 * q);
+            const float4 a4 = *reinterpret_cast<const float4*>(S + (3 * D + 1) * D + 4 * q);
+            ak[0] = k4.x; ak[1] = k4.y; ak[2] = k4.z; ak[3] = k4.w;
+            av[0] = v4.x; av[1] = v4.y; av[2] = v4.z; av[3] = v4.w;
+            ev[0] = e4.x; ev[1] = e4.y; ev[2] = e4.z; ev[3] = e4.w;
+            avv[0] = a4.x; avv[1] = a4.y; avv[2] = a4.z; avv[3] = a4.w;
+        }
+
+        for (int base = 0; base < C; base += TT) {
+            const int cnt = min(TT, C - base);
+            float xo[4][4];
+            if (have_next) {
+#pragma unroll
+                for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) xo[tc][j] = xn[tc][j];
+            } else {
+                load_tile(c, base, cnt, xo);
+            }
+            // ---- projections on MFMA, norms per token; then each lane computes the
+            //      gates of its own token (lane l owns token l of the tile) ----
+            float tok_ksq = 0.f, tok_dsq = 0.f, tok_ep = 0.f, tok_ap = 0.f;
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) {
+                if (16 * tc >= cnt) break;   // uniform: no tokens left in this column tile
+                v4f kacc = {0.f, 0.f, 0.f, 0.f}, vacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    kacc = mfma4(ak[st], xo[tc][st], kacc);
+                    vacc = mfma4(av[st], xo[tc][st], vacc);
+                }
+                float pe = 0.f, pa = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    pe += ev[j] * xo[tc][j];
+                    pa += avv[j] * xo[tc][j];
+                }
+                float kn = kacc[0] * kacc[0] + kacc[1] * kacc[1] + kacc[2] * kacc[2] + kacc[3] * kacc[3];
+                kn = xor16_32_sum(kn);
+                const float inv = rsqrtf(kn + 1e-6f);
+                float kv[4], df[4];
+                float dsq = 0.f, ksq = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    kv[j] = kacc[j] * inv;
+                    df[j] = kv[j] - vacc[j];
+                    dsq += df[j] * df[j];
+                    ksq += kv[j] * kv[j];
+                }
+                dsq = xor16_32_sum(dsq);
+                ksq = xor16_32_sum(ksq);
+                pe = xor16_32_sum(pe);
+                pa = xor16_32_sum(pa);
+                if (q == tc) {
+                    tok_ksq = ksq;
+                    tok_dsq = dsq;
+                    tok_ep = pe;
+                    tok_ap = pa;
+                }
+                const int t = 16 * tc + i16;
+                *reinterpret_cast<float4*>(kk + t * D + 4 * q) = make_float4(kv[0], kv[1], kv[2], kv[3]);
+                *reinterpret_cast<float4*>(dk + t * D + 4 * q) = make_float4(df[0], df[1], df[2], df[3]);
+            }
+            float my_alpha, my_eff;
+            {
+                const float ep = fminf(10.f, fmaxf(-10.f, tok_ep));
+                const float ap = fminf(10.f, fmaxf(-10.f, tok_ap + p.k.alpha_bias));
+                const float sp = ep > 20.f ? ep : logf(1.f + expf(ep));
+                const float eta = p.k.eta_scale * sp;
+                const float alpha = p.k.alpha_min + (1.f - p.k.alpha_min) * (1.f / (1.f + expf(-ap)));
+                const float dn = sqrtf(tok_dsq + 1e-12f);
+                const float cap = p.k.stab_mu * (1.f - alpha) / (dn + 1e-6f);
+                float eff = cap * (-expm1f(-(eta / cap)));
+                if (p.k.clamp) eff = fminf(eff, nextafterf(p.k.factor * alpha / fmaxf(tok_ksq, 1e-20f), 0.f));
+                my_alpha = alpha;
+                my_eff = eff;
+            }
+            // ---- prefetch the next tile's x operands ----
+            {
+                int64_t ncc = c;
+                int nbase = base + TT;
+                if (nbase >= C) { ncc = c + 1; nbase = 0; }
+                have_next = ncc < nc - 1;
+                if (have_next) load_tile(ncc, nbase, min(TT, C - nbase), xn);
+            }
+            __syncthreads();
+            // ---- block coefficients: tokens 4u..4u+3 of the tile are the lanes of one
+            //      DPP quad.  With A_j = prod_{s<=j} alpha_s inside the block,
+            //        r_j = A_{j-1} (g.k_j) + delta_j - sum_{s<j} beta_sj r_s
+            //        g  <- A_3 g - sum_s w_s r_s k_s
+            //      beta_sj = (A_{j-1}/A_s) eta_s (k_s.k_j), w_s = (A_3/A_s) eta_s.
+            //      Tokens past the chunk act as the identity (alpha 1, eta 0). ----
+            float cf_a, cf_b1, cf_b2, cf_b3, cf_w, cf_A3;
+            {
+                const bool valid = lane < cnt;
+                const float al_t = valid ? my_alpha : 1.f;
+                const float et_t = valid ? my_eff : 0.f;
+                const int j = lane & 3;
+                const float pa1 = quad_perm<0x90>(al_t), pa2 = quad_perm<0x40>(al_t), pa3 = quad_perm<0x00>(al_t);
+                const float pe1 = quad_perm<0x90>(et_t), pe2 = quad_perm<0x40>(et_t), pe3 = quad_perm<0x00>(et_t);
+                const float na1 = quad_perm<0xF9>(al_t), na2 = quad_perm<0xFE>(al_t), na3 = quad_perm<0xFF>(al_t);
+                // key dots with the 1, 2, 3 previous tokens of the block
+                float kd1 = 0.f, kd2 = 0.f, kd3 = 0.f;
+                {
+                    const int t1 = max(lane - 1, 0), t2 = max(lane - 2, 0), t3 = max(lane - 3, 0);
+#pragma unroll
+                    for (int e = 0; e < D; e += 4) {
+                        const float4 k0 = *reinterpret_cast<const float4*>(kk + lane * D + e);
+                        const float4 k1 = *reinterpret_cast<const float4*>(kk + t1 * D + e);
+                        const float4 k2 = *reinterpret_cast<const float4*>(kk + t2 * D + e);
+                        const float4 k3 = *reinterpret_cast<const float4*>(kk + t3 * D + e);
+                        kd1 += k0.x * k1.x + k0.y * k1.y + k0.z * k1.z + k0.w * k1.w;
+                        kd2 += k0.x * k2.x + k0.y * k2.y + k0.z * k2.z + k0.w * k2.w;
+                        kd3 += k0.x * k3.x + k0.y * k3.y + k0.z * k3.z + k0.w * k3.w;
+                    }
+                }
+                cf_a = 1.f;
+                if (j >= 1) cf_a *= pa1;
+                if (j >= 2) cf_a *= pa2;
+                if (j >= 3) cf_a *= pa3;
+                cf_b1 = pe1 * kd1;
+                cf_b2 = pe2 * kd2 * pa1;
+                cf_b3 = pe3 * kd3 * pa2 * pa1;
+                cf_w = et_t;
+                if (j <= 2) cf_w *= na1;
+                if (j <= 1) cf_w *= na2;
+                if (j == 0) cf_w *= na3;
+                cf_A3 = quad_perm<0x00>(al_t) * quad_perm<0x55>(al_t) * quad_perm<0xAA>(al_t) *
+                        quad_perm<0xFF>(al_t);
+            }
+            // ---- serial recurrence, 4 tokens per step ----
+            float kvb[4][4], dfb[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kvb[u][e] = kk[u * D + c0 + e];
+                dfb[u] = dk[u * D + grow];
+            }
+            for (int t0 = 0; t0 < cnt; t0 += 4) {
+                float kvn[4][4], dfn[4];
+                const int tn = min(t0 + 4, 60);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) kvn[u][e] = kk[(tn + u) * D + c0 + e];
+                    dfn[u] = dk[(tn + u) * D + grow];
+                }
+                const float a1 = readlane_f(cf_a, t0 + 1), a2 = readlane_f(cf_a, t0 + 2),
+                            a3 = readlane_f(cf_a, t0 + 3);
+                const float b01 = readlane_f(cf_b1, t0 + 1), b02 = readlane_f(cf_b2, t0 + 2),
+                            b12 = readlane_f(cf_b1, t0 + 2), b03 = readlane_f(cf_b3, t0 + 3),
+                            b13 = readlane_f(cf_b2, t0 + 3), b23 = readlane_f(cf_b1, t0 + 3);
+                const float w0 = readlane_f(cf_w, t0), w1 = readlane_f(cf_w, t0 + 1),
+                            w2 = readlane_f(cf_w, t0 + 2), w3 = readlane_f(cf_w, t0 + 3);
+                const float A3 = readlane_f(cf_A3, t0);
+                float pdot[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    float d0 = g[0] * kvb[u][0];
+                    d0 += g[1] * kvb[u][1];
+                    d0 += g[2] * kvb[u][2];
+                    d0 += g[3] * kvb[u][3];
+                    d0 += quad_swap1(d0);
+                    d0 += quad_swap2(d0);
+                    pdot[u] = d0;
+                }
+                const float r0 = pdot[0] + dfb[0];
+                const float r1 = a1 * pdot[1] + dfb[1] - b01 * r0;
+                const float r2 = a2 * pdot[2] + dfb[2] - b02 * r0 - b12 * r1;
+                const float r3 = a3 * pdot[3] + dfb[3] - b03 * r0 - b13 * r1 - b23 * r2;
+                const float c0r = w0 * r0, c1r = w1 * r1, c2r = w2 * r2, c3r = w3 * r3;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v = A3 * g[e] - c0r * kvb[0][e];
+                    v -= c1r * kvb[1][e];
+                    v -= c2r * kvb[2][e];
+                    g[e] = v - c3r * kvb[3][e];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) kvb[u][e] = kvn[u][e];
+                    dfb[u] = dfn[u];
+                }
+            }
+            __syncthreads();
+        }
+        // ---- refresh on MFMA: S <- S G ----
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Gs[grow * GS + c0 + e] = g[e];
+        __syncthreads();
+        float bg[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) bg[st] = Gs[(4 * q + st) * GS + i16];
+        v4f acc[4];
+#pragma unroll
+        for (int R = 0; R < 4; ++R) {
+            const float4 a4 = *reinterpret_cast<const float4*>(S + (16 * R + i16) * D + 4 * q);
+            const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+            acc[R] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) acc[R] = mfma4(a[st], bg[st], acc[R]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int R = 0; R < 4; ++R)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) S[(16 * R + 4 * q + j) * D + i16] = acc[R][j];
     }
 }
 
@@ -277,7 +780,7 @@ __global__ __launch_bounds__(256) void srnl_fuse_readout_kernel(const FuseParams
             qinv = 1.f / fmaxf(sqrtf(qn), 1e-12f);
             xval = to_f32(xq[((b * 4 + r) * L + t) * p.C + c]);
         }
-        const int64_t ch = t / p.chunk[r];
+        const int64_t ch = t / chunk_of(p.chunk, r);
         const float* m = p.states + (((b * 4 + r) * p.heads + head) * p.max_chunks + ch) * D * D + i * D;
         float dot = 0.f;
 #pragma unroll
@@ -324,7 +827,7 @@ __global__ __launch_bounds__(256) void srnl_packed_readout_kernel(const PackedPa
         qn += qv[j] * qv[j];
     }
     const float qinv = p.q_raw ? 1.f / fmaxf(sqrtf(qn), 1e-12f) : 1.f;
-    const float* m = p.states + (line * p.max_chunks + t / p.chunk[r]) * D * D + i * D;
+    const float* m = p.states + (line * p.max_chunks + t / chunk_of(p.chunk, r)) * D * D + i * D;
     float dot = 0.f;
 #pragma unroll
     for (int j = 0; j < D; ++j) dot += m[j] * qv[j];
@@ -360,8 +863,12 @@ int check_memories(const float* a, const float* b, const float* c, const float* 
 template <int D, typename T>
 void launch_scan(const ScanParams& sp, hipStream_t stream) {
     const int64_t lines = sp.B * sp.R * sp.heads;
-    hipLaunchKernelGGL((srnl_scan_kernel<D, T>), dim3(static_cast<unsigned>(lines)),
-                       dim3(ScanCfg<D>::NT), 0, stream, sp);
+    if constexpr (D == 16)
+        hipLaunchKernelGGL((srnl_scan16_kernel<T>), dim3(static_cast<unsigned>(lines)), dim3(64), 0,
+                           stream, sp);
+    else
+        hipLaunchKernelGGL((srnl_scan_kernel<D, T>), dim3(static_cast<unsigned>(lines)),
+                           dim3(ScanCfg<D>::NT), 0, stream, sp);
 }
 
 template <typename F>
@@ -429,6 +936,15 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
     sp.max_chunks = mc;
     sp.states = static_cast<float*>(workspace);
     sp.per_line_state = per_line_state;
+    {
+        // Vector loads need every row start aligned: base pointer and all strides.
+        const size_t elem = static_cast<size_t>(dtype_bytes(io_dtype));
+        const size_t align = (elem == 2 && d == 4) ? 8 : 16;
+        const uintptr_t base = reinterpret_cast<uintptr_t>(x.ptr);
+        bool ok = base % align == 0;
+        for (int64_t st : {x.sb, x.sr, x.sh, x.st}) ok = ok && (static_cast<size_t>(st) * elem) % align == 0;
+        sp.x_vec = ok ? 1 : 0;
+    }
     sp.k = make_consts(consts);
     rc = dispatch_d(d, [&](auto dc) {
         constexpr int D = decltype(dc)::value;
