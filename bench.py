@@ -199,6 +199,8 @@ def main(argv=None):
     parser.add_argument("--batch", type=int, default=128)
     parser.add_argument("--no-graph", action="store_true", help="time eager forwards instead of a HIP graph")
     parser.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
+    parser.add_argument("--cudnn-benchmark", action="store_true",
+                        help="let MIOpen search convolution solvers (analysis/benchmark.py:234)")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -211,6 +213,7 @@ def main(argv=None):
     torch.cuda.set_device(device)
     torch.backends.cuda.matmul.allow_tf32 = True
     torch.backends.cudnn.allow_tf32 = True
+    torch.backends.cudnn.benchmark = args.cudnn_benchmark
     model = build_tiny(device)
     gen = torch.Generator().manual_seed(SEED)
     images = torch.randn(args.batch, 3, 224, 224, generator=gen).to(device)
@@ -279,6 +282,7 @@ def main(argv=None):
         "data": "synthetic",
         "config": {"workload": "visionhope_tiny_classification_forward", "resolution": 224,
                    "global_batch": args.batch, "execution": execution, "autocast": "bf16",
+                   "cudnn_benchmark": args.cudnn_benchmark,
                    "weights": "random-init (repo default init)", "seed": SEED,
                    "wall_s_timed_region": round(wall, 3)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,

@@ -151,23 +151,26 @@ int vh_postprocess_scale_forward(
 size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W);
 
 /* GRN on channels-last x [B, H, W, C] (io_dtype): gx = ||x||_2 over H*W,
- * nx = gx / (mean_c gx + eps), y = x (1 + gamma nx) + beta, y fp32 [B, H, W, C];
+ * nx = gx / (mean_c gx + eps), y = x (1 + gamma nx) + beta, y [B, H, W, C] computed
+ * in fp32 and stored as y_dtype (VH_DTYPE_F32 reproduces the reference's output;
+ * a 16-bit y_dtype stores what a following autocast cast would produce);
  * gx [B, C] and inv_den [B] are written too (the reference saves them for
  * backward).  Replaces grn_forward_cuda (utils/csrc/grn_cuda.cu:290-320,
  * called at utils/grn_cuda.py:42). */
 int vh_grn_forward(
     const void* x, int32_t io_dtype, const float* gamma, const float* beta,
-    float* y, float* gx, float* inv_den, int64_t B, int64_t C, int64_t H, int64_t W,
+    void* y, int32_t y_dtype, float* gx, float* inv_den, int64_t B, int64_t C, int64_t H, int64_t W,
     float eps, void* workspace, size_t workspace_bytes, void* stream);
 
 /* LayerNorm over C for every pixel of x [B, C, H, W] (channels_last = 1: NHWC
- * storage, 0: NCHW storage), biased variance, y fp32 in the same storage
- * order; mean/rstd [B*H*W] are optional (may be NULL).  Replaces the Triton
+ * storage, 0: NCHW storage), biased variance, y in the same storage order,
+ * computed in fp32 and stored as y_dtype (VH_DTYPE_F32 is the reference's
+ * output); mean/rstd [B*H*W] are optional (may be NULL).  Replaces the Triton
  * _layernorm2d_forward_kernel (utils/layer_norm_cuda.py:31-57,122-147) and the
  * F.layer_norm call of LayerNorm2d.inference_layout (models/layers.py:18-20). */
 int vh_layernorm2d_forward(
     const void* x, int32_t io_dtype, const float* weight, const float* bias,
-    float* y, float* mean, float* rstd, int64_t B, int64_t C, int64_t H, int64_t W,
+    void* y, int32_t y_dtype, float* mean, float* rstd, int64_t B, int64_t C, int64_t H, int64_t W,
     float eps, int32_t channels_last, void* stream);
 
 /* Query normalisation + relayout: q_raw [B, R, N, heads*d] (io_dtype) ->
@@ -177,6 +180,24 @@ int vh_layernorm2d_forward(
 int vh_qnorm_forward(
     const void* q_raw, int32_t io_dtype, float* q, float* inv_norm,
     int64_t B, int64_t R, int64_t N, int64_t heads, int32_t head_dim, void* stream);
+
+/* Depthwise KxK convolution (K in {3, 5, 7}, stride 1, padding K/2) on a
+ * channels-last x [B, H, W, C] (io_dtype, C % 8 == 0, 16-byte aligned tensors)
+ * with taps [K*K, C] fp32 (taps-major) and bias [C] (or NULL), accumulated in
+ * fp32, with the block's surrounding elementwise work fused:
+ *   epilogue 0: out = conv(x) + b
+ *   epilogue 1: out = x + conv(x) + b                      (block CPE)
+ *   epilogue 2: out = x + sigmoid(aux) * (conv(x) + b)     (gated local conv)
+ *   epilogue 3: out = gelu_erf(x + conv(x) + b)            (FFN dwconv + act)
+ *   epilogue 4: out (fp32, in place) += conv(x) + b        (LePE into SRNL out)
+ * out/aux are [B, H, W, C] in io_dtype except epilogue 4.  No counterpart in
+ * the reference's native code: it runs PyTorch Conv2d plus separate
+ * elementwise ops inside VisionHOPEBlock (models/block.py:63-107,
+ * models/layers.py:73-77); this fuses them on the prepared inference path. */
+int vh_dwconv2d_nhwc_forward(
+    const void* x, int32_t io_dtype, const float* taps, const float* bias, int32_t ksize,
+    int32_t epilogue, const void* aux, void* out, int64_t B, int64_t H, int64_t W, int64_t C,
+    void* stream);
 
 /* Residual add on channels-last data: out[i] = residual[i] +
  * branch[i] * gamma[c] * drop_scale[b] (fp32 out; residual/branch io_dtype

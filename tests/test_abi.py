@@ -99,14 +99,40 @@ def test_srnl_rejects_bad_chunks_and_constants(lib):
 
 def test_grn_rejects_missing_workspace(lib):
     p = ctypes.c_void_p(0x1000)
-    rc = lib.vh_grn_forward(p, hip.VH_DTYPE_BF16, p, p, p, p, p, 2, 8, 4, 4, 1e-6, None, 0, None)
+    rc = lib.vh_grn_forward(p, hip.VH_DTYPE_BF16, p, p, p, hip.VH_DTYPE_F32, p, p, 2, 8, 4, 4, 1e-6, None, 0,
+                            None)
     assert rc == hip.VH_ERR_WORKSPACE
 
 
 def test_layernorm_rejects_empty(lib):
     p = ctypes.c_void_p(0x1000)
-    rc = lib.vh_layernorm2d_forward(p, hip.VH_DTYPE_F32, p, p, p, None, None, 0, 8, 4, 4, 1e-6, 1, None)
+    rc = lib.vh_layernorm2d_forward(p, hip.VH_DTYPE_F32, p, p, p, hip.VH_DTYPE_F32, None, None, 0, 8, 4, 4, 1e-6,
+                                    1, None)
     assert rc == hip.VH_ERR_SHAPE
+
+
+def test_layernorm_and_grn_reject_bad_output_dtype(lib):
+    p = ctypes.c_void_p(0x1000)
+    rc = lib.vh_layernorm2d_forward(p, hip.VH_DTYPE_F32, p, p, p, 9, None, None, 2, 8, 4, 4, 1e-6, 1, None)
+    assert rc == hip.VH_ERR_DTYPE
+    rc = lib.vh_grn_forward(p, hip.VH_DTYPE_BF16, p, p, p, 9, p, p, 2, 8, 4, 4, 1e-6, p, 1 << 20, None)
+    assert rc == hip.VH_ERR_DTYPE
+
+
+def test_dwconv_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(0x1000)
+
+    def call(ksize=3, epilogue=0, aux=None, channels=16, x=p):
+        return lib.vh_dwconv2d_nhwc_forward(x, hip.VH_DTYPE_BF16, p, p, ksize, epilogue, aux, p,
+                                            2, 4, 4, channels, None)
+
+    assert call(ksize=4) == hip.VH_ERR_ARG
+    assert call(epilogue=9) == hip.VH_ERR_ARG
+    assert call(epilogue=2) == hip.VH_ERR_ARG          # gate tensor missing
+    assert call(channels=12) == hip.VH_ERR_SHAPE       # C % 8 != 0
+    assert call(x=None) == hip.VH_ERR_ARG
+    assert call(x=ctypes.c_void_p(0x1008)) == hip.VH_ERR_ARG   # misaligned
+    assert b"aligned" in lib.vh_last_error()
 
 
 def test_check_raises_with_message(lib):

@@ -1,0 +1,175 @@
+"""GPU parity of the fused depthwise kernels and of the fused inference path of a prepared
+VisionHOPE block.
+
+The depthwise kernels are checked against PyTorch's FP64 CPU convolution on the same
+(rounded) inputs.  The fused block is checked against the same block run on the CPU in
+FP32 with the operator computed by the CPU oracle in FP64.
+"""
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+from torch.nn import functional as F
+
+from tests.helpers import assert_close, randn
+
+pytestmark = pytest.mark.gpu
+
+
+def _dw_reference(x, conv, epilogue, gate=None, acc=None):
+    """FP64 CPU composition of the fused epilogues on NCHW ``x``."""
+    from visionhope_amd.utils import dwconv
+
+    x = x.double().cpu()
+    y = F.conv2d(x, conv.weight.detach().double().cpu(),
+                 None if conv.bias is None else conv.bias.detach().double().cpu(),
+                 padding=conv.padding, groups=conv.groups)
+    if epilogue == dwconv.EPI_ADD_INPUT:
+        y = x + y
+    elif epilogue == dwconv.EPI_GATE:
+        y = x + torch.sigmoid(gate.double().cpu()) * y
+    elif epilogue == dwconv.EPI_ADD_GELU:
+        y = F.gelu(x + y)
+    elif epilogue == dwconv.EPI_ACCUM_F32:
+        y = acc.double().cpu().permute(0, 3, 1, 2) + y
+    return y
+
+
+@pytest.mark.parametrize("ksize", [3, 5, 7])
+@pytest.mark.parametrize("epilogue", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
+def test_depthwise_epilogues(device, ksize, epilogue, dtype, tol):
+    from visionhope_amd.utils import dwconv
+
+    channels = 24
+    conv = torch.nn.Conv2d(channels, channels, ksize, padding=ksize // 2, groups=channels)
+    with torch.no_grad():
+        conv.weight.copy_(randn(*conv.weight.shape, seed=11, scale=0.3))
+        conv.bias.copy_(randn(channels, seed=12, scale=0.1))
+    conv = conv.to(device)
+    # Ragged spatial shape: odd height, width not a multiple of anything.
+    x = randn(2, channels, 9, 13, seed=13).to(dtype)
+    gate = randn(2, channels, 9, 13, seed=14).to(dtype)
+    acc = randn(2, 9, 13, channels, seed=15)
+    x_dev = x.to(device).contiguous(memory_format=torch.channels_last)
+    gate_dev = gate.to(device).contiguous(memory_format=torch.channels_last)
+    acc_dev = acc.to(device).contiguous()
+    out = dwconv.depthwise_conv(x_dev, conv, epilogue, aux=gate_dev if epilogue == 2 else None,
+                                out=acc_dev if epilogue == 4 else None)
+    expected = _dw_reference(x, conv, epilogue, gate=gate, acc=acc)
+    if epilogue == dwconv.EPI_ACCUM_F32:
+        assert out is acc_dev and out.dtype == torch.float32
+        got = out.permute(0, 3, 1, 2)
+    else:
+        assert out.dtype == dtype and out.is_contiguous(memory_format=torch.channels_last)
+        got = out
+    assert_close(got.double().cpu().numpy(), expected.numpy(), tol, f"dwconv K={ksize} epi={epilogue}")
+
+
+def test_depthwise_without_bias_and_noncontiguous_input(device):
+    from visionhope_amd.utils import dwconv
+
+    conv = torch.nn.Conv2d(16, 16, 5, padding=2, groups=16, bias=False)
+    with torch.no_grad():
+        conv.weight.copy_(randn(*conv.weight.shape, seed=21, scale=0.3))
+    conv = conv.to(device)
+    x = randn(1, 16, 7, 5, seed=22)
+    out = dwconv.depthwise_conv(x.to(device), conv)       # NCHW input is relaid out
+    assert_close(out.cpu().numpy(), _dw_reference(x, conv, 0).numpy(), 1e-5, "dwconv no bias")
+
+
+def test_depthwise_taps_cache_follows_weight_updates(device):
+    from visionhope_amd.utils import dwconv
+
+    conv = torch.nn.Conv2d(8, 8, 3, padding=1, groups=8).to(device)
+    x = randn(1, 8, 4, 4, seed=31).to(device).contiguous(memory_format=torch.channels_last)
+    first = dwconv.depthwise_conv(x, conv)
+    with torch.no_grad():
+        conv.weight.mul_(2.0)
+    second = dwconv.depthwise_conv(x, conv)
+    bias = conv.bias.detach().view(1, -1, 1, 1)
+    assert_close((second - bias).cpu().numpy(), (2 * (first - bias)).cpu().numpy(), 1e-6, "cache refresh")
+
+
+def _perturb_block(block, seed):
+    gen = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in block.named_parameters():
+            if name.startswith("operator.srnl.M_") and p.ndim == 3:
+                continue                      # keep the reference init for the matrices
+            if name in ("gamma1", "gamma2"):
+                p.copy_(0.5 + 0.5 * torch.rand(p.shape, generator=gen))
+            elif name.startswith("operator.srnl.M_"):
+                p.copy_(torch.randn(p.shape, generator=gen) * 0.1)
+            else:
+                p.add_(torch.randn(p.shape, generator=gen) * (0.05 if p.ndim > 1 else 0.1))
+
+
+def _cpu_block_reference(block, x, oracle):
+    """The prepared block on the CPU in FP32, with the operator from the FP64 CPU oracle."""
+    from visionhope_amd.models import operator as op_mod
+
+    def oracle_forward(self, xin, *, channels_last=None):
+        x_nhwc = xin.permute(0, 2, 3, 1).contiguous()
+        q = self.W_q(x_nhwc)
+        mems = tuple(m.detach().numpy() for m in self.srnl.initial_memories)
+        out = oracle.operator_forward(x_nhwc.numpy(), q.detach().numpy(), mems, self.d_skip.detach().numpy(),
+                                      self.direction_weights().detach().numpy(), self.head_dim,
+                                      dtype=np.float64)
+        return torch.from_numpy(out.astype(np.float32)).permute(0, 3, 1, 2)
+
+    original = op_mod.VisionHOPEOperator.forward
+    op_mod.VisionHOPEOperator.forward = oracle_forward
+    try:
+        with torch.no_grad():
+            return block(x)
+    finally:
+        op_mod.VisionHOPEOperator.forward = original
+
+
+@pytest.mark.parametrize("local_mode", ["gated_dwconv7", "residual_dwconv"])
+@pytest.mark.parametrize("autocast", [False, True])
+def test_fused_block_matches_oracle(oracle, device, local_mode, autocast):
+    from visionhope_amd.inference.prepare import prepare_for_inference
+    from visionhope_amd.models.block import VisionHOPEBlock
+
+    torch.manual_seed(7)
+    block = VisionHOPEBlock(32, head_dim=16, local_mode=local_mode)
+    _perturb_block(block, seed=8)
+    reference = copy.deepcopy(block)
+    prepare_for_inference(reference)
+    gpu = block.to(device).to(memory_format=torch.channels_last)
+    prepare_for_inference(gpu)
+    x = randn(2, 32, 9, 11, seed=9)
+    expected = _cpu_block_reference(reference, x, oracle).numpy()
+
+    x_dev = x.to(device).contiguous(memory_format=torch.channels_last)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        if autocast:
+            x_dev = x_dev.bfloat16()
+        assert gpu._fused_eligible(x_dev)
+        out = gpu(x_dev)
+    assert out.dtype == (torch.bfloat16 if autocast else torch.float32)
+    assert out.is_contiguous(memory_format=torch.channels_last)
+    # FP32 tolerance 1e-4; bf16 autocast tolerance 2e-2, both normwise and elementwise.
+    assert_close(out.double().cpu().numpy(), expected, 2e-2 if autocast else 1e-4,
+                 f"fused block {local_mode} autocast={autocast}")
+
+
+def test_fused_block_falls_back_for_odd_layouts(device):
+    from visionhope_amd.inference.prepare import prepare_for_inference
+    from visionhope_amd.models.block import VisionHOPEBlock
+
+    block = VisionHOPEBlock(32, head_dim=16)
+    _perturb_block(block, seed=10)
+    block = block.to(device)
+    prepare_for_inference(block)
+    x = torch.randn(1, 32, 6, 6, device=device)                 # NCHW storage
+    assert not block._fused_eligible(x)
+    assert block._fused_eligible(x.contiguous(memory_format=torch.channels_last))
+    with torch.no_grad():
+        a = block(x)
+        b = block(x.contiguous(memory_format=torch.channels_last))
+    assert_close(a.cpu().numpy(), b.cpu().numpy(), 1e-4, "fused vs ordinary block")

@@ -131,13 +131,13 @@ __global__ __launch_bounds__(256) void grn_finalize_kernel(const float* __restri
     }
 }
 
-template <typename T>
+template <typename T, typename TO>
 __global__ __launch_bounds__(256) void grn_apply_kernel(const T* __restrict__ x,
                                                        const float* __restrict__ gamma,
                                                        const float* __restrict__ beta,
                                                        const float* __restrict__ gx,
                                                        const float* __restrict__ inv_den,
-                                                       float* __restrict__ y, int64_t C, int64_t S,
+                                                       TO* __restrict__ y, int64_t C, int64_t S,
                                                        int64_t total) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
     for (int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void grn_apply_kernel(const T* __restrict__ x,
         const int64_t c = idx % C;
         const int64_t b = idx / (S * C);
         const float nx = gx[b * C + c] * inv_den[b];
-        y[idx] = to_f32(x[idx]) * (1.f + gamma[c] * nx) + beta[c];
+        y[idx] = from_f32<TO>(to_f32(x[idx]) * (1.f + gamma[c] * nx) + beta[c]);
     }
 }
 
@@ -155,11 +155,11 @@ __global__ __launch_bounds__(256) void grn_apply_kernel(const T* __restrict__ x,
 // y = (x - mean) * rstd * w + b.
 // Channels-last: TPR lanes per pixel row, values kept in registers.
 // ---------------------------------------------------------------------------
-template <typename T, int TPR, int MAXV>
+template <typename T, typename TO, int TPR, int MAXV>
 __global__ __launch_bounds__(256) void layernorm_nhwc_kernel(const T* __restrict__ x,
                                                             const float* __restrict__ w,
                                                             const float* __restrict__ bias,
-                                                            float* __restrict__ y,
+                                                            TO* __restrict__ y,
                                                             float* __restrict__ mean_out,
                                                             float* __restrict__ rstd_out,
                                                             int64_t rows, int C, float eps) {
@@ -191,11 +191,11 @@ __global__ __launch_bounds__(256) void layernorm_nhwc_kernel(const T* __restrict
     for (int off = TPR / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
     const float rstd = 1.f / sqrtf(sq / static_cast<float>(C) + eps);
     if (!active) return;
-    float* yr = y + row * C;
+    TO* yr = y + row * C;
 #pragma unroll
     for (int k = 0; k < MAXV; ++k) {
         const int c = lane + k * TPR;
-        if (c < C) yr[c] = v[k] * rstd * w[c] + bias[c];
+        if (c < C) yr[c] = from_f32<TO>(v[k] * rstd * w[c] + bias[c]);
     }
     if (lane == 0) {
         if (mean_out) mean_out[row] = mean;
@@ -204,11 +204,11 @@ __global__ __launch_bounds__(256) void layernorm_nhwc_kernel(const T* __restrict
 }
 
 // NCHW storage: one thread per pixel, channel loop (coalesced over pixels).
-template <typename T>
+template <typename T, typename TO>
 __global__ __launch_bounds__(256) void layernorm_nchw_kernel(const T* __restrict__ x,
                                                             const float* __restrict__ w,
                                                             const float* __restrict__ bias,
-                                                            float* __restrict__ y,
+                                                            TO* __restrict__ y,
                                                             float* __restrict__ mean_out,
                                                             float* __restrict__ rstd_out,
                                                             int64_t B, int64_t C, int64_t S,
@@ -226,8 +226,8 @@ __global__ __launch_bounds__(256) void layernorm_nchw_kernel(const T* __restrict
         sq += d * d;
     }
     const float rstd = 1.f / sqrtf(sq / static_cast<float>(C) + eps);
-    float* yb = y + b * C * S + s;
-    for (int64_t c = 0; c < C; ++c) yb[c * S] = (to_f32(xb[c * S]) - mean) * rstd * w[c] + bias[c];
+    TO* yb = y + b * C * S + s;
+    for (int64_t c = 0; c < C; ++c) yb[c * S] = from_f32<TO>((to_f32(xb[c * S]) - mean) * rstd * w[c] + bias[c]);
     if (mean_out) mean_out[pix] = mean;
     if (rstd_out) rstd_out[pix] = rstd;
 }
@@ -308,26 +308,27 @@ unsigned grid_for(int64_t total, int64_t cap) {
     return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((total + 255) / 256, cap)));
 }
 
-template <typename T, int TPR>
-void launch_ln_nhwc(const void* x, const float* w, const float* b, float* y, float* mean,
+template <typename T, typename TO, int TPR>
+void launch_ln_nhwc(const void* x, const float* w, const float* b, void* yv, float* mean,
                     float* rstd, int64_t rows, int C, float eps, hipStream_t s) {
     const unsigned blocks = static_cast<unsigned>((rows + 256 / TPR - 1) / (256 / TPR));
     const int per = (C + TPR - 1) / TPR;
     const T* xp = static_cast<const T*>(x);
+    TO* y = static_cast<TO*>(yv);
     if (per <= 4)
-        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 4>), dim3(blocks), dim3(256), 0, s, xp, w, b,
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TO, TPR, 4>), dim3(blocks), dim3(256), 0, s, xp, w, b,
                            y, mean, rstd, rows, C, eps);
     else if (per <= 8)
-        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 8>), dim3(blocks), dim3(256), 0, s, xp, w, b,
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TO, TPR, 8>), dim3(blocks), dim3(256), 0, s, xp, w, b,
                            y, mean, rstd, rows, C, eps);
     else if (per <= 16)
-        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 16>), dim3(blocks), dim3(256), 0, s, xp, w,
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TO, TPR, 16>), dim3(blocks), dim3(256), 0, s, xp, w,
                            b, y, mean, rstd, rows, C, eps);
     else if (per <= 32)
-        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 32>), dim3(blocks), dim3(256), 0, s, xp, w,
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TO, TPR, 32>), dim3(blocks), dim3(256), 0, s, xp, w,
                            b, y, mean, rstd, rows, C, eps);
     else
-        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TPR, 64>), dim3(blocks), dim3(256), 0, s, xp, w,
+        hipLaunchKernelGGL((layernorm_nhwc_kernel<T, TO, TPR, 64>), dim3(blocks), dim3(256), 0, s, xp, w,
                            b, y, mean, rstd, rows, C, eps);
 }
 
@@ -367,13 +368,14 @@ size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W) {
     return static_cast<size_t>(B * nslab * C) * sizeof(float);
 }
 
-int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const float* beta, float* y,
-                   float* gx, float* inv_den, int64_t B, int64_t C, int64_t H, int64_t W, float eps,
-                   void* workspace, size_t workspace_bytes, void* stream) {
+int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const float* beta, void* y,
+                   int32_t y_dtype, float* gx, float* inv_den, int64_t B, int64_t C, int64_t H,
+                   int64_t W, float eps, void* workspace, size_t workspace_bytes, void* stream) {
     VH_REQUIRE(x && gamma && beta && y && gx && inv_den, VH_ERR_ARG, "GRN pointers must not be null");
     VH_REQUIRE(B > 0 && C > 0 && H > 0 && W > 0, VH_ERR_SHAPE, "GRN expects nonempty input");
     VH_REQUIRE(B <= 65535, VH_ERR_SHAPE, "GRN batch must be <= 65535, got %lld", (long long)B);
     VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "GRN supports FP32, FP16 and BF16 input");
+    VH_REQUIRE(valid_dtype(y_dtype), VH_ERR_DTYPE, "unsupported GRN output dtype code %d", y_dtype);
     const size_t need = vh_grn_workspace_bytes(B, C, H, W);
     VH_REQUIRE(workspace && workspace_bytes >= need, VH_ERR_WORKSPACE,
                "GRN workspace needs %zu bytes, got %zu", need, workspace ? workspace_bytes : (size_t)0);
@@ -392,19 +394,24 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
                            dim3(256), lds, s, static_cast<const T*>(x), partial, C, S, nslab);
         hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, partial,
                            gx, inv_den, C, nslab, eps);
-        hipLaunchKernelGGL((grn_apply_kernel<T>), dim3(grid_for(total, 8192)), dim3(256), 0, s,
-                           static_cast<const T*>(x), gamma, beta, gx, inv_den, y, C, S, total);
+        dispatch_t(y_dtype, [&](auto ov) {
+            using TO = decltype(ov);
+            hipLaunchKernelGGL((grn_apply_kernel<T, TO>), dim3(grid_for(total, 8192)), dim3(256), 0, s,
+                               static_cast<const T*>(x), gamma, beta, gx, inv_den, static_cast<TO*>(y),
+                               C, S, total);
+        });
     });
     if (rc) return rc;
     return check_launch("grn kernels");
 }
 
 int vh_layernorm2d_forward(const void* x, int32_t io_dtype, const float* weight, const float* bias,
-                           float* y, float* mean, float* rstd, int64_t B, int64_t C, int64_t H,
-                           int64_t W, float eps, int32_t channels_last, void* stream) {
+                           void* y, int32_t y_dtype, float* mean, float* rstd, int64_t B, int64_t C,
+                           int64_t H, int64_t W, float eps, int32_t channels_last, void* stream) {
     VH_REQUIRE(x && weight && bias && y, VH_ERR_ARG, "LayerNorm2d pointers must not be null");
     VH_REQUIRE(B > 0 && C > 0 && H > 0 && W > 0, VH_ERR_SHAPE, "LayerNorm2d expects nonempty input");
     VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "LayerNorm2d supports FP32, FP16 and BF16 input");
+    VH_REQUIRE(valid_dtype(y_dtype), VH_ERR_DTYPE, "unsupported LayerNorm2d output dtype code %d", y_dtype);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t rows = B * H * W;
     int rc;
@@ -413,19 +420,26 @@ int vh_layernorm2d_forward(const void* x, int32_t io_dtype, const float* weight,
                    (long long)C);
         const int c = static_cast<int>(C);
         rc = dispatch_t(io_dtype, [&](auto tv) {
-            using T = decltype(tv);
-            if (c <= 16) launch_ln_nhwc<T, 4>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
-            else if (c <= 32) launch_ln_nhwc<T, 8>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
-            else if (c <= 64) launch_ln_nhwc<T, 16>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
-            else if (c <= 128) launch_ln_nhwc<T, 32>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
-            else launch_ln_nhwc<T, 64>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+            dispatch_t(y_dtype, [&](auto ov) {
+                using T = decltype(tv);
+                using TO = decltype(ov);
+                if (c <= 16) launch_ln_nhwc<T, TO, 4>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+                else if (c <= 32) launch_ln_nhwc<T, TO, 8>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+                else if (c <= 64) launch_ln_nhwc<T, TO, 16>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+                else if (c <= 128) launch_ln_nhwc<T, TO, 32>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+                else launch_ln_nhwc<T, TO, 64>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
+            });
         });
     } else {
         rc = dispatch_t(io_dtype, [&](auto tv) {
-            using T = decltype(tv);
-            hipLaunchKernelGGL((layernorm_nchw_kernel<T>), dim3(static_cast<unsigned>((rows + 255) / 256)),
-                               dim3(256), 0, s, static_cast<const T*>(x), weight, bias, y, mean, rstd,
-                               B, C, H * W, eps);
+            dispatch_t(y_dtype, [&](auto ov) {
+                using T = decltype(tv);
+                using TO = decltype(ov);
+                hipLaunchKernelGGL((layernorm_nchw_kernel<T, TO>),
+                                   dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0, s,
+                                   static_cast<const T*>(x), weight, bias, static_cast<TO*>(y), mean,
+                                   rstd, B, C, H * W, eps);
+            });
         });
     }
     if (rc) return rc;

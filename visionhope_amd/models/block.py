@@ -6,9 +6,37 @@ from torch.nn import functional as F
 from torch.nn.init import trunc_normal_
 
 from .droppath import DropPath
-from .layers import FeedForwardNetwork, build_norm
+from .layers import FeedForwardNetwork, LayerNorm2d, build_norm
 from .operator import VisionHOPEOperator
+from ..utils import dwconv
+from ..utils.grn import GlobalResponseNorm
+from ..utils.grn_cuda import visionhope_grn
+from ..utils.layer_norm_cuda import can_fuse_layernorm2d, visionhope_layernorm2d
 from ..utils.residual import can_fuse_residual_add, visionhope_residual_add
+
+
+def _cached_linear(module, dtype):
+    """``(weight [out, in], bias)`` of a 1x1 Conv2d or Linear in ``dtype``, cached on the
+    module and refreshed when either parameter changes."""
+    w, b = module.weight, module.bias
+    key = (dtype, w.data_ptr(), w._version, str(w.device),
+           None if b is None else (b.data_ptr(), b._version))
+    cached = getattr(module, "_vh_linear", None)
+    if cached is None or cached[0] != key:
+        weight = w.detach().reshape(w.shape[0], -1).to(dtype).contiguous()
+        bias = None if b is None else b.detach().to(dtype).contiguous()
+        object.__setattr__(module, "_vh_linear", (key, weight, bias))
+        cached = module._vh_linear
+    return cached[1], cached[2]
+
+
+def _is_pointwise(conv):
+    return (isinstance(conv, nn.Conv2d) and conv.kernel_size == (1, 1) and conv.stride == (1, 1)
+            and conv.padding == (0, 0) and conv.groups == 1)
+
+
+def _is_exact_gelu(act):
+    return type(act) is nn.GELU and act.approximate == "none"
 
 
 class VisionHOPEBlock(nn.Module):
@@ -62,6 +90,92 @@ class VisionHOPEBlock(nn.Module):
             self.gamma1 = None
             self.gamma2 = None
 
+    def _fused_eligible(self, x):
+        """Whether ``forward`` may take the fused inference path for ``x``.
+
+        The fused path computes the same block as ``forward`` (same modules, same
+        rounding points under autocast) with the depthwise convolutions and their
+        surrounding elementwise work in single native passes, the 1x1 projections as
+        channels-last GEMMs, LayerNorm/GRN writing the dtype their consumer reads, and
+        the local position encoding accumulated into the operator's FP32 output.
+        """
+        if not self._inference_prepared or self.training or not x.is_cuda or x.ndim != 4:
+            return False
+        if not x.is_contiguous(memory_format=torch.channels_last) or x.data_ptr() % 16:
+            return False
+        autocast = torch.is_autocast_enabled("cuda")
+        if autocast:
+            if torch.get_autocast_dtype("cuda") not in (torch.bfloat16, torch.float16):
+                return False
+        elif x.dtype != torch.float32 or any(p.dtype != torch.float32 for p in self.parameters()):
+            return False
+        ffn = self.ffn
+        if type(ffn) is not FeedForwardNetwork or not _is_exact_gelu(ffn.act):
+            return False
+        if ffn.use_dwconv and not (dwconv.is_depthwise(ffn.dwconv) and _is_exact_gelu(ffn.dwconv_act)):
+            return False
+        if not isinstance(ffn.grn, (GlobalResponseNorm, nn.Identity)):
+            return False
+        if not all(_is_pointwise(c) for c in (self.proj_in, ffn.fc1, ffn.fc2)):
+            return False
+        if self.local_gate is not None and not _is_pointwise(self.local_gate):
+            return False
+        for conv in (self.cpe, self.local_conv, self.local_position):
+            if conv is not None and not dwconv.is_depthwise(conv):
+                return False
+        for norm in (self.norm1, self.norm2):
+            if type(norm) is not LayerNorm2d:
+                return False
+        return (can_fuse_layernorm2d(x, self.norm1.weight, self.norm1.bias)
+                and self.dim % 8 == 0 and self.mixer_dim % 8 == 0 and ffn.fc1.out_channels % 8 == 0)
+
+    def _fused_forward(self, x):
+        """Inference forward of the block on a channels-last map (``_fused_eligible``)."""
+        autocast = torch.is_autocast_enabled("cuda")
+        act = torch.get_autocast_dtype("cuda") if autocast else torch.float32
+
+        def pointwise(t_nhwc, module):
+            weight, bias = _cached_linear(module, act)
+            return F.linear(t_nhwc.to(act), weight, bias)
+
+        def nchw(t_nhwc):
+            return t_nhwc.permute(0, 3, 1, 2)
+
+        if self.cpe is not None:
+            x = dwconv.depthwise_conv(x, self.cpe, dwconv.EPI_ADD_INPUT)
+        # Token-mixer branch.
+        h = visionhope_layernorm2d(x, self.norm1.weight, self.norm1.bias, self.norm1.eps,
+                                   force_channels_last=True, out_dtype=act)
+        inner = pointwise(h.permute(0, 2, 3, 1), self.proj_in)
+        if self.local_mode == "gated_dwconv7":
+            gate = pointwise(inner, self.local_gate)
+            x_local = dwconv.depthwise_conv(nchw(inner), self.local_conv, dwconv.EPI_GATE, aux=nchw(gate))
+        elif self.local_mode == "residual_dwconv":
+            x_local = dwconv.depthwise_conv(nchw(inner), self.local_conv, dwconv.EPI_ADD_INPUT)
+        else:
+            x_local = F.silu(dwconv.depthwise_conv(nchw(inner), self.local_conv))
+        path, _ = self.operator._inference_path(x_local)
+        if path == "ordinary":
+            branch = self._spatial_tail(x_local, True)
+        else:
+            out = self.operator._forward_fast(x_local, path)
+            if self.local_position is not None:
+                dwconv.depthwise_conv(x_local, self.local_position, dwconv.EPI_ACCUM_F32, out=out)
+            branch = nchw(pointwise(out, self.proj_out))
+        x = self._residual_add(x, branch, self.gamma1)
+        # Feed-forward branch.
+        ffn = self.ffn
+        h = visionhope_layernorm2d(x, self.norm2.weight, self.norm2.bias, self.norm2.eps,
+                                   force_channels_last=True, out_dtype=act)
+        f = F.gelu(pointwise(h.permute(0, 2, 3, 1), ffn.fc1))
+        if ffn.use_dwconv:
+            f = dwconv.depthwise_conv(nchw(f), ffn.dwconv, dwconv.EPI_ADD_GELU).permute(0, 2, 3, 1)
+        if isinstance(ffn.grn, GlobalResponseNorm):
+            f = visionhope_grn(nchw(f), ffn.grn.gamma, ffn.grn.beta, ffn.grn.eps,
+                               out_dtype=act).permute(0, 2, 3, 1)
+        branch = nchw(pointwise(f, ffn.fc2))
+        return self._residual_add(x, branch, self.gamma2)
+
     def _local_features(self, x):
         x_inner = self.proj_in(x)
         if self.local_mode == "gated_dwconv7":
@@ -71,7 +185,9 @@ class VisionHOPEBlock(nn.Module):
 
     def spatial_branch(self, x):
         channels_last = x.is_contiguous(memory_format=torch.channels_last)
-        x_local = self._local_features(x)
+        return self._spatial_tail(self._local_features(x), channels_last)
+
+    def _spatial_tail(self, x_local, channels_last):
         if self._inference_prepared:
             path, _ = self.operator._inference_path(x_local)
             if path != "ordinary":
@@ -103,6 +219,8 @@ class VisionHOPEBlock(nn.Module):
     def forward(self, x):
         if self.training and self._inference_prepared:
             raise RuntimeError("A block with folded LayerScale weights cannot be trained")
+        if self._fused_eligible(x):
+            return self._fused_forward(x)
         if self.cpe is not None:
             x = x + self.cpe(x)
         branch = self.spatial_branch(self.norm1(x))

@@ -1,0 +1,96 @@
+"""Fused depthwise convolutions of the VisionHOPE block on channels-last maps.
+
+``depthwise_conv(x, conv, epilogue)`` runs a depthwise ``nn.Conv2d`` (K in {3, 5, 7},
+stride 1, padding K//2) through ``vh_dwconv2d_nhwc_forward`` with the surrounding
+elementwise work of the block fused into the same pass:
+
+=================  =====================================  ==========================
+epilogue           result                                 reference expression
+=================  =====================================  ==========================
+``EPI_PLAIN``      conv(x) + b                            ``conv(x)``
+``EPI_ADD_INPUT``  x + conv(x) + b                        ``x + self.cpe(x)``
+``EPI_GATE``       x + sigmoid(aux) * (conv(x) + b)       ``_local_features``
+``EPI_ADD_GELU``   gelu(x + conv(x) + b)                  ``dwconv_act(x + dwconv(x))``
+``EPI_ACCUM_F32``  out += conv(x) + b  (fp32 NHWC)        ``out + local_position(x)``
+=================  =====================================  ==========================
+
+(``models/block.py:63-107``, ``models/layers.py:73-77``.)  Accumulation is FP32 with
+FP32 taps; the result is rounded once to the activation dtype.
+"""
+
+import torch
+from torch import nn
+
+from . import hip
+from .cuda import on_tensor_device
+
+EPI_PLAIN, EPI_ADD_INPUT, EPI_GATE, EPI_ADD_GELU, EPI_ACCUM_F32 = range(5)
+_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def is_depthwise(conv):
+    """A depthwise Conv2d the fused kernel implements exactly."""
+    if not isinstance(conv, nn.Conv2d):
+        return False
+    k = conv.kernel_size[0]
+    return (conv.groups == conv.in_channels == conv.out_channels and conv.in_channels % 8 == 0
+            and conv.kernel_size == (k, k) and k in (3, 5, 7) and conv.stride == (1, 1)
+            and conv.padding == (k // 2, k // 2) and conv.dilation == (1, 1)
+            and conv.padding_mode == "zeros")
+
+
+def depthwise_taps(conv):
+    """Taps-major FP32 weights ``[K*K, C]`` and FP32 bias of a depthwise Conv2d, cached on
+    the module and refreshed when the weight changes (version counter, device)."""
+    w = conv.weight
+    key = (w.data_ptr(), w._version, str(w.device),
+           None if conv.bias is None else (conv.bias.data_ptr(), conv.bias._version))
+    cached = getattr(conv, "_vh_taps", None)
+    if cached is None or cached[0] != key:
+        taps = w.detach().float().reshape(w.shape[0], -1).t().contiguous()
+        bias = conv.bias.detach().float().contiguous() if conv.bias is not None else None
+        object.__setattr__(conv, "_vh_taps", (key, taps, bias))
+        cached = conv._vh_taps
+    return cached[1], cached[2]
+
+
+def _channels_last(t):
+    if not t.is_contiguous(memory_format=torch.channels_last) or t.data_ptr() % 16:
+        t = t.contiguous(memory_format=torch.channels_last)
+        if t.data_ptr() % 16:
+            t = t.clone(memory_format=torch.channels_last)
+    return t
+
+
+@on_tensor_device
+def depthwise_conv(x, conv, epilogue=EPI_PLAIN, aux=None, out=None):
+    """Run ``conv`` on the channels-last map ``x`` with a fused epilogue (module docstring).
+
+    For ``EPI_ACCUM_F32`` ``out`` is a contiguous FP32 ``[B, H, W, C]`` tensor updated in
+    place; otherwise a new ``x``-dtype channels-last tensor is returned.
+    """
+    if not x.is_cuda or x.dtype not in _DTYPES:
+        raise ValueError("depthwise_conv expects a CUDA FP32/BF16/FP16 tensor")
+    if not is_depthwise(conv):
+        raise ValueError("depthwise_conv needs a depthwise Conv2d with K in {3, 5, 7}, stride 1, same padding")
+    batch, channels, height, width = x.shape
+    if channels != conv.in_channels:
+        raise ValueError("channel count does not match the convolution")
+    taps, bias = depthwise_taps(conv)
+    x = _channels_last(x)
+    if epilogue == EPI_GATE:
+        if aux is None or aux.shape != x.shape:
+            raise ValueError("the gated epilogue needs a gate tensor shaped like x")
+        aux = _channels_last(aux.to(x.dtype))
+    if epilogue == EPI_ACCUM_F32:
+        if (out is None or out.dtype != torch.float32 or tuple(out.shape) != (batch, height, width, channels)
+                or not out.is_contiguous() or out.data_ptr() % 16):
+            raise ValueError("EPI_ACCUM_F32 needs a contiguous FP32 [B, H, W, C] output")
+    else:
+        out = torch.empty_like(x, memory_format=torch.channels_last)
+    lib = hip.load_library()
+    hip.check(lib.vh_dwconv2d_nhwc_forward(
+        hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(taps), hip.ptr(bias), conv.kernel_size[0],
+        int(epilogue), hip.ptr(aux), hip.ptr(out), batch, height, width, channels, hip.stream_of(x)),
+        "vh_dwconv2d_nhwc_forward")
+    return out

@@ -14,13 +14,13 @@ from .cuda import on_tensor_device
 class _VisionHOPEGRNFunction(Function):
     @staticmethod
     @on_tensor_device
-    def forward(ctx, x, gamma, beta, eps):
+    def forward(ctx, x, gamma, beta, eps, out_dtype=torch.float32):
         batch, channels, height, width = x.shape
         if not x.is_contiguous(memory_format=torch.channels_last):
             x = x.contiguous(memory_format=torch.channels_last)
         gamma = gamma.detach().reshape(-1).float().contiguous()
         beta = beta.detach().reshape(-1).float().contiguous()
-        y = torch.empty_like(x, dtype=torch.float32, memory_format=torch.channels_last)
+        y = torch.empty_like(x, dtype=out_dtype, memory_format=torch.channels_last)
         gx = torch.empty((batch, channels), device=x.device, dtype=torch.float32)
         inv_den = torch.empty((batch,), device=x.device, dtype=torch.float32)
         lib = hip.load_library()
@@ -28,7 +28,8 @@ class _VisionHOPEGRNFunction(Function):
         ws = hip.workspace(nbytes, x.device)
         hip.check(lib.vh_grn_forward(
             hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(gamma), hip.ptr(beta), hip.ptr(y),
-            hip.ptr(gx), hip.ptr(inv_den), batch, channels, height, width, float(eps),
+            hip.dtype_code(out_dtype), hip.ptr(gx), hip.ptr(inv_den), batch, channels, height, width,
+            float(eps),
             hip.ptr(ws), ws.numel() * 4, hip.stream_of(x)), "vh_grn_forward")
         return y
 
@@ -53,9 +54,11 @@ def can_fuse_grn(x, gamma, beta):
             and gamma.numel() == channels and beta.numel() == channels)
 
 
-def visionhope_grn(x, gamma, beta, eps):
+def visionhope_grn(x, gamma, beta, eps, out_dtype=torch.float32):
+    """FP32 GRN output (the reference's contract); ``out_dtype`` stores the same values
+    rounded to a 16-bit type when the consumer casts them anyway (autocast)."""
     if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
         raise TypeError("GRN supports FP32, FP16 and BF16 input")
     if x.shape[0] < 1 or x.shape[0] > 65535:
         raise ValueError("GRN expects nonempty input and batch <= 65535")
-    return _VisionHOPEGRNFunction.apply(x, gamma, beta, eps)
+    return _VisionHOPEGRNFunction.apply(x, gamma, beta, eps, out_dtype)

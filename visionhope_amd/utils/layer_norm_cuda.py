@@ -15,7 +15,7 @@ from .cuda import on_tensor_device
 class _VisionHOPELayerNorm2dFunction(Function):
     @staticmethod
     @on_tensor_device
-    def forward(ctx, x, weight, bias, eps, force_channels_last=False):
+    def forward(ctx, x, weight, bias, eps, force_channels_last=False, out_dtype=torch.float32):
         batch, channels, height, width = x.shape
         channels_last = x.is_contiguous(memory_format=torch.channels_last)
         if force_channels_last and not channels_last:
@@ -26,11 +26,12 @@ class _VisionHOPELayerNorm2dFunction(Function):
         fmt = torch.channels_last if channels_last else torch.contiguous_format
         weight = weight.detach().reshape(-1).float().contiguous()
         bias = bias.detach().reshape(-1).float().contiguous()
-        y = torch.empty_like(x, dtype=torch.float32, memory_format=fmt)
+        y = torch.empty_like(x, dtype=out_dtype, memory_format=fmt)
         lib = hip.load_library()
         hip.check(lib.vh_layernorm2d_forward(
             hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(weight), hip.ptr(bias), hip.ptr(y),
-            None, None, batch, channels, height, width, float(eps), int(channels_last),
+            hip.dtype_code(out_dtype), None, None, batch, channels, height, width, float(eps),
+            int(channels_last),
             hip.stream_of(x)), "vh_layernorm2d_forward")
         return y
 
@@ -55,5 +56,7 @@ def can_fuse_layernorm2d(x, weight, bias):
             and weight.numel() == channels and bias.numel() == channels)
 
 
-def visionhope_layernorm2d(x, weight, bias, eps, force_channels_last=False):
-    return _VisionHOPELayerNorm2dFunction.apply(x, weight, bias, eps, force_channels_last)
+def visionhope_layernorm2d(x, weight, bias, eps, force_channels_last=False, out_dtype=torch.float32):
+    """FP32 output (the reference's contract); ``out_dtype`` stores the same values rounded
+    to a 16-bit type when the consumer casts them anyway (autocast)."""
+    return _VisionHOPELayerNorm2dFunction.apply(x, weight, bias, eps, force_channels_last, out_dtype)
