@@ -191,6 +191,37 @@ def cpu_baseline(sample_batch=8, reps=3):
                       f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}"}
 
 
+COPY_CALIBRATION_BYTES = 512 << 20
+
+
+def profile_stages(device, batch):
+    """Per-stage SRNL launches (3 each) then a 512 MiB FP32 scale-by-one copy, whose
+    dispatch reads and writes exactly COPY_CALIBRATION_BYTES, for counter runs."""
+    import torch
+    from visionhope_amd.models.srnl_core.fused import srnl_spatial_inference
+
+    torch.cuda.set_device(device)
+    gen = torch.Generator(device=device).manual_seed(SEED)
+    for grid, channels, _ in TINY_STAGES:
+        heads = channels // 16
+        mems = _perturbed_memories(heads, 16, device, gen)
+        x = torch.randn(batch, grid, grid, channels, device=device, generator=gen).bfloat16()
+        q = torch.randn(batch, grid, grid, channels, device=device, generator=gen).bfloat16()
+        skip = torch.zeros(channels, device=device)
+        wts = torch.ones(4, channels, device=device)
+        for _ in range(3):
+            srnl_spatial_inference(mems, x, q, skip, wts, (grid,) * 4)
+        torch.cuda.synchronize()
+        print(f"stage {grid}x{grid} C={channels}: 3 launches", flush=True)
+        del x, q
+    src = torch.ones(COPY_CALIBRATION_BYTES // 4, device=device)
+    dst = torch.empty_like(src)
+    torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(f"calibration copy: {COPY_CALIBRATION_BYTES} bytes read and written", flush=True)
+    return 0
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -201,6 +232,10 @@ def main(argv=None):
     parser.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     parser.add_argument("--cudnn-benchmark", action="store_true",
                         help="let MIOpen search convolution solvers (analysis/benchmark.py:234)")
+    parser.add_argument("--stages-only", action="store_true",
+                        help="profiling workload for rocprofv3 --pmc: the per-stage SRNL launches and "
+                             "one FP32 copy of COPY_CALIBRATION_BYTES (HBM counter calibration); "
+                             "no model forward, no JSON line")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -208,6 +243,9 @@ def main(argv=None):
         return 2
 
     import torch
+
+    if args.stages_only:
+        return profile_stages(torch.device("cuda:0"), args.batch)
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)

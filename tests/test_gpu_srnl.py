@@ -109,6 +109,35 @@ def test_spatial_forward_fp32(oracle, device, height, width, head_dim, heads, sk
     assert_close(got, expected, FP32_TOL, f"spatial {height}x{width} d={head_dim}")
 
 
+@pytest.mark.parametrize("height,width,heads", [(19, 37, 2), (16, 32, 1), (33, 17, 3), (56, 56, 2)])
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL)])
+def test_spatial_readout_tiles(oracle, device, height, width, heads, dtype, tol):
+    """head_dim 16 with row/column chunks: 16x16 tile readout, full and ragged edge tiles."""
+    channels = heads * 16
+    mems = memories(4, heads, 16, kind="strong", seed=height + width)
+    x = randn(1, height, width, channels, seed=51).to(dtype)
+    q = randn(1, height, width, channels, seed=52).to(dtype)
+    skip = randn(4 * channels, seed=53, scale=0.1)
+    wts = 1 + randn(4, channels, seed=54, scale=0.1)
+    got = _spatial(device, x, q, mems, skip, wts, (width, width, height, height))
+    expected = oracle.operator_forward(x.float().numpy(), q.float().numpy(), mems, skip.numpy(), wts.numpy(), 16)
+    assert_close(got, expected, tol, f"tiled readout {height}x{width} {dtype}")
+
+
+def test_spatial_forward_other_chunks(oracle, device):
+    """Chunk lengths other than the row/column lengths take the per-element readout."""
+    heads, height, width = 2, 6, 9
+    mems = memories(4, heads, 16, kind="perturbed", seed=5)
+    x = randn(2, height, width, 32, seed=61)
+    q = randn(2, height, width, 32, seed=62)
+    skip = randn(32, seed=63, scale=0.1)
+    wts = 1 + randn(4, 32, seed=64, scale=0.1)
+    chunks = (5, 7, 3, 4)
+    got = _spatial(device, x, q, mems, skip, wts, chunks)
+    expected = oracle.operator_forward(x.numpy(), q.numpy(), mems, skip.numpy(), wts.numpy(), 16, chunks)
+    assert_close(got, expected, FP32_TOL, "spatial other chunks")
+
+
 def test_spatial_forward_bf16_config3_shape(oracle, device):
     """Operator workload shape at reduced batch (B=2, 56x56, C=96, 3 heads of 32), bf16."""
     heads, head_dim, hw = 3, 32, 56

@@ -794,6 +794,110 @@ __global__ __launch_bounds__(256) void srnl_fuse_readout_kernel(const FuseParams
 }
 
 // ---------------------------------------------------------------------------
+// Spatial readout + fusion for head_dim 16 with row/column chunks (W, W, H, H).
+//
+// One wave per 16x16-pixel tile of one (image, head).  Every pixel of a tile row
+// reads the same direction-0/1 states (chunks h and H-1-h) and every pixel of a
+// tile column the same direction-2/3 states (chunks w and W-1-w), so each
+// y = M q over 16 pixels is one 16x16x16 product on the matrix cores:
+//   step m of four 16x16x4 MFMAs: lane l = 16g + n supplies A = M[n][4g+m] and
+//   B = q[pixel n][4g+m] (k permuted so both operands are 4-vector loads) and
+//   receives D[4g+j][n], channels 4g..4g+3 of pixel n.
+// Column contributions go through LDS to move pixels onto the row layout; each
+// output is then (c0 + c1) + (c2 + c3) with c_r = w_r (y_r + skip_r x), stored once.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(64) void srnl_readout16_kernel(const FuseParams p, const int64_t tiles_h,
+                                                            const int64_t tiles_w) {
+    constexpr int D = 16, REC = 20;  // 16 channels + 4 padding floats per pixel record
+    __shared__ __align__(16) float col[256 * REC];
+    const int64_t n_tiles = p.B * p.heads * tiles_h * tiles_w;
+    const int64_t tile = xcd_remap(blockIdx.x, n_tiles);
+    const int64_t tw = tile % tiles_w;
+    const int64_t th = (tile / tiles_w) % tiles_h;
+    const int64_t bh = tile / (tiles_w * tiles_h);
+    const int64_t head = bh % p.heads, b = bh / p.heads;
+    const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+    const int64_t H = p.H, W = p.W, C = p.C, L = H * W;
+    const int64_t h0 = th * 16, w0 = tw * 16;
+    const int64_t cbase = head * D + 4 * g;
+    const T* xb = static_cast<const T*>(p.x) + b * L * C + cbase;
+    const T* qb = static_cast<const T*>(p.q) + b * L * C + cbase;
+    const float* st[4];
+    float wt[4][4], sk[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        st[r] = p.states + ((b * 4 + r) * p.heads + head) * p.max_chunks * (D * D) + n * D + 4 * g;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            wt[r][j] = p.wgt[r * C + cbase + j];
+            sk[r][j] = p.skip[(p.skip_per_dir ? r * C : 0) + cbase + j];
+        }
+    }
+
+    // Directions 2 and 3: tile column ww, lane n holds pixel (h0 + n, w0 + ww).
+#pragma unroll 2
+    for (int ww = 0; ww < 16; ++ww) {
+        const int64_t w = w0 + ww;
+        if (w >= W) break;
+        const int64_t h = h0 + n;
+        float qv[4] = {0.f, 0.f, 0.f, 0.f}, xv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (h < H) {
+            load4(qb + (h * W + w) * C, true, qv);
+            load4(xb + (h * W + w) * C, true, xv);
+        }
+        const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] +
+                                                        qv[3] * qv[3])), 1e-12f);
+        const float4 m2 = *reinterpret_cast<const float4*>(st[2] + w * (D * D));
+        const float4 m3 = *reinterpret_cast<const float4*>(st[3] + (W - 1 - w) * (D * D));
+        v4f y2 = {0.f, 0.f, 0.f, 0.f}, y3 = {0.f, 0.f, 0.f, 0.f};
+        y2 = mfma4(m2.x, qv[0], y2); y3 = mfma4(m3.x, qv[0], y3);
+        y2 = mfma4(m2.y, qv[1], y2); y3 = mfma4(m3.y, qv[1], y3);
+        y2 = mfma4(m2.z, qv[2], y2); y3 = mfma4(m3.z, qv[2], y3);
+        y2 = mfma4(m2.w, qv[3], y2); y3 = mfma4(m3.w, qv[3], y3);
+        float* rec = col + (ww * 16 + n) * REC + 4 * g;
+        float c23[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            c23[j] = wt[2][j] * (y2[j] * inv + sk[2][j] * xv[j]) + wt[3][j] * (y3[j] * inv + sk[3][j] * xv[j]);
+        *reinterpret_cast<float4*>(rec) = make_float4(c23[0], c23[1], c23[2], c23[3]);
+    }
+    __syncthreads();
+
+    // Directions 0 and 1: tile row hh, lane n holds pixel (h0 + hh, w0 + n).
+    const int64_t w = w0 + n;
+    const bool wvalid = w < W;
+#pragma unroll 2
+    for (int hh = 0; hh < 16; ++hh) {
+        const int64_t h = h0 + hh;
+        if (h >= H) break;
+        float qv[4] = {0.f, 0.f, 0.f, 0.f}, xv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (wvalid) {
+            load4(qb + (h * W + w) * C, true, qv);
+            load4(xb + (h * W + w) * C, true, xv);
+        }
+        const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] +
+                                                        qv[3] * qv[3])), 1e-12f);
+        const float4 m0 = *reinterpret_cast<const float4*>(st[0] + h * (D * D));
+        const float4 m1 = *reinterpret_cast<const float4*>(st[1] + (H - 1 - h) * (D * D));
+        v4f y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
+        y0 = mfma4(m0.x, qv[0], y0); y1 = mfma4(m1.x, qv[0], y1);
+        y0 = mfma4(m0.y, qv[1], y0); y1 = mfma4(m1.y, qv[1], y1);
+        y0 = mfma4(m0.z, qv[2], y0); y1 = mfma4(m1.z, qv[2], y1);
+        y0 = mfma4(m0.w, qv[3], y0); y1 = mfma4(m1.w, qv[3], y1);
+        const float4 c23 = *reinterpret_cast<const float4*>(col + (n * 16 + hh) * REC + 4 * g);
+        const float c23v[4] = {c23.x, c23.y, c23.z, c23.w};
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            o[j] = (wt[0][j] * (y0[j] * inv + sk[0][j] * xv[j]) + wt[1][j] * (y1[j] * inv + sk[1][j] * xv[j])) +
+                   c23v[j];
+        if (wvalid)
+            *reinterpret_cast<float4*>(p.out + (b * L + h * W + w) * C + cbase) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Packed readout: y[b, r, head, t, :] = M_m^(t / chunk_r) q_hat_t.
 // ---------------------------------------------------------------------------
 struct PackedParams {
@@ -965,6 +1069,20 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
     fp.skip = skip; fp.skip_per_dir = skip_per_dir; fp.wgt = wgt; fp.out = out;
     fp.B = sp.B; fp.H = H; fp.W = W; fp.C = C; fp.heads = sp.heads;
     for (int r = 0; r < 4; ++r) fp.chunk[r] = sp.chunk[r];
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q) |
+                            reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sp.states);
+    if (d == 16 && !per_direction && sp.chunk[0] == W && sp.chunk[1] == W && sp.chunk[2] == H &&
+        sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0) {
+        const int64_t tiles_h = (H + 15) / 16, tiles_w = (W + 15) / 16;
+        const int64_t n_tiles = sp.B * sp.heads * tiles_h * tiles_w;
+        VH_REQUIRE(n_tiles <= 0x7fffffff, VH_ERR_SHAPE, "SRNL readout grid too large");
+        int rc = dispatch_t(io_dtype, [&](auto tv) {
+            hipLaunchKernelGGL((srnl_readout16_kernel<decltype(tv)>), dim3(static_cast<unsigned>(n_tiles)),
+                               dim3(64), 0, stream, fp, tiles_h, tiles_w);
+        });
+        if (rc) return rc;
+        return check_launch("srnl_readout16_kernel");
+    }
     const int64_t total = sp.B * H * W * C;
     const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
     int rc = dispatch_d(d, [&](auto dc) {
