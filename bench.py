@@ -6,10 +6,10 @@ MI355X, plus live roofline figures for the SRNL operator and the memory-bound ta
 Prints ONE JSON line.  ``value`` is images/s of the full forward (HIP graph replay,
 inputs resident in HBM).  ``roofline`` covers the SRNL spatial operator launches
 (scan + readout, ``vh_srnl_spatial_forward``) summed over one forward, timed with
-HIP events on the stream they run on; ``kernels`` breaks it down per stage and adds
-the fused elementwise workload (B=128 at 56x56x96 and 28x28x192).  ``cpu_baseline`` times the same model
-on the host cores with the CPU oracle standing in for SRNL (the reference has no
-CPU SRNL path).
+HIP events on the stream they run on, with their counter-measured HBM traffic;
+``kernels`` breaks it down per stage and adds the fused elementwise workload (B=128 at
+56x56x96 and 28x28x192).  ``cpu_baseline`` times the same model on the host cores with
+the CPU oracle standing in for SRNL (the reference has no CPU SRNL path).
 """
 
 from __future__ import annotations
@@ -33,6 +33,10 @@ FP32_PEAK_TFLOPS = 157.3
 SEED = 1234
 TINY_STAGES = [  # (grid, mixer channels, depth), head_dim 16 (models/factory.py, hierarchical.py)
     (56, 32, 3), (28, 64, 4), (14, 128, 18), (7, 256, 4)]
+# HBM bytes per vh_srnl_spatial_forward launch (scan + readout) at B=128, bf16, from
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of `bench.py --stages-only`, calibrated against a
+# 512 MiB copy (profiles/srnl_stages_b128_traffic.md).  Valid for the kernels measured there.
+SRNL_TRAFFIC_BYTES_B128 = {56: 319.1e6, 28: 213.0e6, 14: 160.1e6, 7: 139.3e6}
 
 
 def srnl_flops(batch, height, width, channels, head_dim, chunks):
@@ -82,7 +86,7 @@ def measure_srnl_stages(device, batch):
 
     stream = torch.cuda.current_stream(device)
     gen = torch.Generator(device=device).manual_seed(SEED)
-    rows, total_flops, total_ms = [], 0.0, 0.0
+    rows, total_flops, total_ms, total_bytes = [], 0.0, 0.0, 0.0
     for grid, channels, depth in TINY_STAGES:
         head_dim = 16
         heads = channels // head_dim
@@ -94,11 +98,15 @@ def measure_srnl_stages(device, batch):
         chunks = (grid, grid, grid, grid)
         ms = event_time_ms(lambda: srnl_spatial_inference(mems, x, q, skip, wts, chunks), stream, 20)
         flops = srnl_flops(batch, grid, grid, channels, head_dim, chunks)
-        rows.append({"stage": f"{grid}x{grid} C={channels} d={head_dim}", "blocks": depth,
-                     "ms_per_launch": round(ms, 4), "tflops": round(flops / ms / 1e9, 3)})
+        row = {"stage": f"{grid}x{grid} C={channels} d={head_dim}", "blocks": depth,
+               "ms_per_launch": round(ms, 4), "tflops": round(flops / ms / 1e9, 3)}
+        if batch == 128:
+            row["hbm_bytes_per_launch"] = SRNL_TRAFFIC_BYTES_B128[grid]
+            total_bytes += SRNL_TRAFFIC_BYTES_B128[grid] * depth
+        rows.append(row)
         total_flops += flops * depth
         total_ms += ms * depth
-    return rows, total_flops, total_ms
+    return rows, total_flops, total_ms, (total_bytes if batch == 128 else None)
 
 
 def measure_tail(device):
@@ -300,7 +308,7 @@ def main(argv=None):
         ms = start.elapsed_time(end) / args.steps
         del graph
 
-        stage_rows, srnl_flops_total, srnl_ms_total = measure_srnl_stages(device, args.batch)
+        stage_rows, srnl_flops_total, srnl_ms_total, srnl_bytes = measure_srnl_stages(device, args.batch)
         tail = measure_tail(device)
 
     images_per_s = args.batch * 1000.0 / ms
@@ -324,9 +332,11 @@ def main(argv=None):
                    "weights": "random-init (repo default init)", "seed": SEED,
                    "wall_s_timed_region": round(wall, 3)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 5), "traffic": None,
-                     "kernel": "vh_srnl_spatial_forward (srnl_scan_kernel + srnl_fuse_readout_kernel), "
-                               "all 29 Tiny blocks at B=128",
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 5), "traffic": srnl_bytes,
+                     "kernel": "vh_srnl_spatial_forward (srnl_scan16_kernel + srnl_readout16_kernel)",
+                     "scope": "sum over the 29 SRNL launches of one forward (3/4/18/4 blocks at "
+                              "56/28/14/7); achieved = reference FLOP count / event-timed duration; "
+                              "traffic = rocprofv3 FETCH_SIZE+WRITE_SIZE bytes, calibrated",
                      "srnl_ms_per_forward": round(srnl_ms_total, 3),
                      "algorithmic_gflop_per_forward": round(srnl_flops_total / 1e9, 2)},
         "kernels": {"srnl_stages": stage_rows, **tail},

@@ -21,8 +21,10 @@
 //     workspace instead of computing y.
 //   * readout kernels — y = M_m^c q_hat for every token, fully parallel.  For
 //     the spatial operator the readout also restores the four scan orders and
-//     fuses sum_r w_r (y_r + skip_r x) per pixel in the reference's summation
-//     order, so no per-direction output ever reaches HBM and no atomics are used.
+//     fuses sum_r w_r (y_r + skip_r x) per pixel, so no per-direction output
+//     ever reaches HBM and no atomics are used.  head_dim 16 with row/column
+//     chunks uses 16x16-pixel MFMA tiles (srnl_readout16_kernel); every other
+//     case one thread per output in the reference's summation order.
 #include <cmath>
 
 #include "vh_common.h"
