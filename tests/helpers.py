@@ -60,3 +60,53 @@ def randn(*shape, seed=SEED, scale=1.0):
 
 def to_dev(arrays, device):
     return tuple(torch.as_tensor(a).to(device) for a in arrays)
+
+
+def perturb_block(block, seed):
+    """Parameters of a VisionHOPE block at scales that exercise every branch: LayerScale
+    in [0.5, 1], gate vectors ~ N(0, 0.1^2), other tensors offset by small noise; the SRNL
+    matrix memories keep their init."""
+    gen = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in block.named_parameters():
+            if name.startswith("operator.srnl.M_") and p.ndim == 3:
+                continue
+            if name in ("gamma1", "gamma2"):
+                p.copy_(0.5 + 0.5 * torch.rand(p.shape, generator=gen))
+            elif name.startswith("operator.srnl.M_"):
+                p.copy_(torch.randn(p.shape, generator=gen) * 0.1)
+            else:
+                p.add_(torch.randn(p.shape, generator=gen) * (0.05 if p.ndim > 1 else 0.1))
+
+
+class oracle_operator:
+    """Context manager: VisionHOPEOperator.forward computed by the FP64 CPU oracle (CPU
+    tensors; the result is returned in the input's dtype, NCHW)."""
+
+    def __init__(self, oracle):
+        self.oracle = oracle
+
+    def __enter__(self):
+        from visionhope_amd.models import operator as op_mod
+
+        oracle = self.oracle
+
+        def forward(op, xin, *, channels_last=None):
+            x_nhwc = xin.permute(0, 2, 3, 1).contiguous()
+            with torch.no_grad():
+                q = op.W_q(x_nhwc)
+            mems = tuple(m.detach().double().numpy() for m in op.srnl.initial_memories)
+            out = oracle.operator_forward(x_nhwc.double().numpy(), q.double().numpy(), mems,
+                                          op.d_skip.detach().double().numpy(),
+                                          op.direction_weights().detach().double().numpy(),
+                                          op.head_dim, dtype=np.float64)
+            return torch.from_numpy(out).to(xin.dtype).permute(0, 3, 1, 2)
+
+        self._module = op_mod
+        self._original = op_mod.VisionHOPEOperator.forward
+        op_mod.VisionHOPEOperator.forward = forward
+        return self
+
+    def __exit__(self, *exc):
+        self._module.VisionHOPEOperator.forward = self._original
+        return False

@@ -8,12 +8,11 @@ FP32 with the operator computed by the CPU oracle in FP64.
 
 import copy
 
-import numpy as np
 import pytest
 import torch
 from torch.nn import functional as F
 
-from tests.helpers import assert_close, randn
+from tests.helpers import assert_close, oracle_operator, perturb_block, randn
 
 pytestmark = pytest.mark.gpu
 
@@ -93,40 +92,10 @@ def test_depthwise_taps_cache_follows_weight_updates(device):
     assert_close((second - bias).cpu().numpy(), (2 * (first - bias)).cpu().numpy(), 1e-6, "cache refresh")
 
 
-def _perturb_block(block, seed):
-    gen = torch.Generator().manual_seed(seed)
-    with torch.no_grad():
-        for name, p in block.named_parameters():
-            if name.startswith("operator.srnl.M_") and p.ndim == 3:
-                continue                      # keep the reference init for the matrices
-            if name in ("gamma1", "gamma2"):
-                p.copy_(0.5 + 0.5 * torch.rand(p.shape, generator=gen))
-            elif name.startswith("operator.srnl.M_"):
-                p.copy_(torch.randn(p.shape, generator=gen) * 0.1)
-            else:
-                p.add_(torch.randn(p.shape, generator=gen) * (0.05 if p.ndim > 1 else 0.1))
-
-
 def _cpu_block_reference(block, x, oracle):
     """The prepared block on the CPU in FP32, with the operator from the FP64 CPU oracle."""
-    from visionhope_amd.models import operator as op_mod
-
-    def oracle_forward(self, xin, *, channels_last=None):
-        x_nhwc = xin.permute(0, 2, 3, 1).contiguous()
-        q = self.W_q(x_nhwc)
-        mems = tuple(m.detach().numpy() for m in self.srnl.initial_memories)
-        out = oracle.operator_forward(x_nhwc.numpy(), q.detach().numpy(), mems, self.d_skip.detach().numpy(),
-                                      self.direction_weights().detach().numpy(), self.head_dim,
-                                      dtype=np.float64)
-        return torch.from_numpy(out.astype(np.float32)).permute(0, 3, 1, 2)
-
-    original = op_mod.VisionHOPEOperator.forward
-    op_mod.VisionHOPEOperator.forward = oracle_forward
-    try:
-        with torch.no_grad():
-            return block(x)
-    finally:
-        op_mod.VisionHOPEOperator.forward = original
+    with oracle_operator(oracle), torch.no_grad():
+        return block(x)
 
 
 @pytest.mark.parametrize("local_mode", ["gated_dwconv7", "residual_dwconv"])
@@ -137,7 +106,7 @@ def test_fused_block_matches_oracle(oracle, device, local_mode, autocast):
 
     torch.manual_seed(7)
     block = VisionHOPEBlock(32, head_dim=16, local_mode=local_mode)
-    _perturb_block(block, seed=8)
+    perturb_block(block, seed=8)
     reference = copy.deepcopy(block)
     prepare_for_inference(reference)
     gpu = block.to(device).to(memory_format=torch.channels_last)
@@ -163,7 +132,7 @@ def test_fused_block_falls_back_for_odd_layouts(device):
     from visionhope_amd.models.block import VisionHOPEBlock
 
     block = VisionHOPEBlock(32, head_dim=16)
-    _perturb_block(block, seed=10)
+    perturb_block(block, seed=10)
     block = block.to(device)
     prepare_for_inference(block)
     x = torch.randn(1, 32, 6, 6, device=device)                 # NCHW storage

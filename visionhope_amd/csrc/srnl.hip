@@ -45,6 +45,7 @@ struct LineInput {
     int64_t sb, sr, sh, st;
     int spatial;
     int64_t H, W;
+    float inv_h;  // 1.0f / H (spatial inputs, H * W < 2^24)
 };
 
 // Chunk length of direction r.  Constant indices only: a runtime index into a
@@ -58,7 +59,7 @@ template <typename T>
 __device__ __forceinline__ const T* line_ptr(const LineInput& in, int64_t b, int r, int64_t head,
                                              int64_t t) {
     const T* base = static_cast<const T*>(in.ptr);
-    if (in.spatial) return base + b * in.sb + scan_to_pixel(r, t, in.H, in.W) * in.st + head * in.sh;
+    if (in.spatial) return base + b * in.sb + scan_to_pixel(r, t, in.H, in.W, in.inv_h) * in.st + head * in.sh;
     return base + b * in.sb + r * in.sr + head * in.sh + t * in.st;
 }
 
@@ -441,19 +442,23 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Sum over lanes l, l^16, l^32, l^48 with the gfx950 row-swap permutes (VALU, no LDS):
+// permlane16_swap(v, v) yields rows (r0, r0, r2, r2) and (r1, r1, r3, r3), so their sum
+// holds the xor-16 pair sums; permlane32_swap does the same for the two halves.
 __device__ __forceinline__ float xor16_32_sum(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
 }
 
 template <typename T>
 __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
-    constexpr int D = 16, TT = 64, ROWS = 3 * D + 2, GS = D + 1;
+    constexpr int D = 16, TT = 64, ROWS = 3 * D + 2, GS = D + 1, DKS = TT + 4;
     __shared__ __align__(16) float S[64 * D];    // 50 state rows + zero padding rows
     __shared__ __align__(16) float Gs[D * GS];
     __shared__ __align__(16) float kk[TT * D];
-    __shared__ __align__(16) float dk[TT * D];
+    __shared__ __align__(16) float dkT[D * DKS];  // (k - v)[row][token], row stride DKS
 
     const int64_t lines = p.B * p.R * p.heads;
     const int64_t line = xcd_remap(blockIdx.x, lines);
@@ -571,7 +576,8 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 }
                 const int t = 16 * tc + i16;
                 *reinterpret_cast<float4*>(kk + t * D + 4 * q) = make_float4(kv[0], kv[1], kv[2], kv[3]);
-                *reinterpret_cast<float4*>(dk + t * D + 4 * q) = make_float4(df[0], df[1], df[2], df[3]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) dkT[(4 * q + j) * DKS + t] = df[j];
             }
             float my_alpha, my_eff;
             {
@@ -640,23 +646,21 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 cf_A3 = quad_perm<0x00>(al_t) * quad_perm<0x55>(al_t) * quad_perm<0xAA>(al_t) *
                         quad_perm<0xFF>(al_t);
             }
-            // ---- serial recurrence, 4 tokens per step ----
-            float kvb[4][4], dfb[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) kvb[u][e] = kk[u * D + c0 + e];
-                dfb[u] = dk[u * D + grow];
-            }
-            for (int t0 = 0; t0 < cnt; t0 += 4) {
-                float kvn[4][4], dfn[4];
-                const int tn = min(t0 + 4, 60);
+            // ---- serial recurrence, 4 tokens per step; the operands of the next step
+            //      are read from LDS while the current one computes (two register
+            //      sets used alternately, so no copies between steps) ----
+            float kA[4][4], dA[4], kB[4][4], dB[4];
+            auto fetch = [&](int t, float (&kv)[4][4], float (&df)[4]) {
+                const int tn = min(t, TT - 4);
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) kvn[u][e] = kk[(tn + u) * D + c0 + e];
-                    dfn[u] = dk[(tn + u) * D + grow];
+                    const float4 k4 = *reinterpret_cast<const float4*>(kk + (tn + u) * D + c0);
+                    kv[u][0] = k4.x; kv[u][1] = k4.y; kv[u][2] = k4.z; kv[u][3] = k4.w;
                 }
+                const float4 d4 = *reinterpret_cast<const float4*>(dkT + grow * DKS + tn);
+                df[0] = d4.x; df[1] = d4.y; df[2] = d4.z; df[3] = d4.w;
+            };
+            auto step = [&](int t0, const float (&kvb)[4][4], const float (&dfb)[4]) {
                 const float a1 = readlane_f(cf_a, t0 + 1), a2 = readlane_f(cf_a, t0 + 2),
                             a3 = readlane_f(cf_a, t0 + 3);
                 const float b01 = readlane_f(cf_b1, t0 + 1), b02 = readlane_f(cf_b2, t0 + 2),
@@ -688,12 +692,28 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                     v -= c2r * kvb[2][e];
                     g[e] = v - c3r * kvb[3][e];
                 }
+            };
+            // Pin freshly read operands in registers once the step between has run, so
+            // the compiler cannot turn them back into LDS reads next to their use.
+            auto pin = [&](float (&kv)[4][4], float (&df)[4]) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) kvb[u][e] = kvn[u][e];
-                    dfb[u] = dfn[u];
+                    for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(kv[u][e]));
+                    asm volatile("" : "+v"(df[u]));
                 }
+            };
+            fetch(0, kA, dA);
+            for (int t0 = 0; t0 < cnt; t0 += 8) {
+                fetch(t0 + 4, kB, dB);
+                __builtin_amdgcn_sched_barrier(0);
+                step(t0, kA, dA);
+                pin(kB, dB);
+                if (t0 + 4 >= cnt) break;
+                fetch(t0 + 8, kA, dA);
+                __builtin_amdgcn_sched_barrier(0);
+                step(t0 + 4, kB, dB);
+                pin(kA, dA);
             }
             __syncthreads();
         }
@@ -1148,8 +1168,10 @@ int vh_srnl_spatial_forward(const void* x, const void* q, int32_t io_dtype, cons
                "head_dim must be one of 4, 8, 16, 32, 64; got %d", head_dim);
     VH_REQUIRE(C % head_dim == 0, VH_ERR_SHAPE, "C=%lld is not a multiple of head_dim=%d",
                (long long)C, head_dim);
+    VH_REQUIRE(H * W < (int64_t(1) << 24), VH_ERR_SHAPE, "spatial SRNL supports H*W < 2^24 pixels, got %lld",
+               (long long)(H * W));
     const int64_t heads = C / head_dim;
-    LineInput xin{x, H * W * C, 0, head_dim, C, 1, H, W};
+    LineInput xin{x, H * W * C, 0, head_dim, C, 1, H, W, 1.0f / static_cast<float>(H)};
     ScanParams sp{};
     hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = run_scan(xin, io_dtype, M_m, M_v, M_k, M_eta, M_alpha, B, 4, heads, H * W, head_dim,
@@ -1176,7 +1198,7 @@ int vh_srnl_line_forward_seq_noatomic(const void* X, const void* Q_raw, int32_t 
     const int64_t heads = C / head_dim;
     const int64_t L = H * W;
     const int64_t chunks[4] = {W, W, H, H};
-    LineInput xin{X, 4 * L * C, L * C, head_dim, C, 0, 0, 0};
+    LineInput xin{X, 4 * L * C, L * C, head_dim, C, 0, 0, 0, 0.f};
     ScanParams sp{};
     hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = run_scan(xin, io_dtype, M_m, M_v, M_k, M_eta, M_alpha, B, 4, heads, L, head_dim,
@@ -1193,14 +1215,14 @@ int vh_srnl_sequence_forward(const void* X, const void* Q_raw, int32_t io_dtype,
                              const int64_t* chunks, const vh_srnl_consts* consts, void* workspace,
                              size_t workspace_bytes, void* stream) {
     const int64_t d = head_dim;
-    LineInput xin{X, R * heads * N * d, heads * N * d, N * d, d, 0, 0, 0};
+    LineInput xin{X, R * heads * N * d, heads * N * d, N * d, d, 0, 0, 0, 0.f};
     ScanParams sp{};
     hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = run_scan(xin, io_dtype, M_m, M_v, M_k, M_eta, M_alpha, B, R, heads, N, head_dim, chunks,
                       consts, workspace, workspace_bytes, s, &sp, memories_per_line ? 1 : 0);
     if (rc) return rc;
     const int64_t C = heads * d;
-    LineInput qin{Q_raw, R * N * C, N * C, d, C, 0, 0, 0};
+    LineInput qin{Q_raw, R * N * C, N * C, d, C, 0, 0, 0, 0.f};
     return run_packed<void>(sp, qin, 1, io_dtype, out, head_dim, s);
 }
 
@@ -1211,13 +1233,13 @@ int vh_srnl_forward(const void* X, int32_t io_dtype, const float* Q, const float
                     const vh_srnl_consts* consts, void* workspace, size_t workspace_bytes,
                     void* stream) {
     const int64_t d = head_dim;
-    LineInput xin{X, R * heads * N * d, heads * N * d, N * d, d, 0, 0, 0};
+    LineInput xin{X, R * heads * N * d, heads * N * d, N * d, d, 0, 0, 0, 0.f};
     ScanParams sp{};
     hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = run_scan(xin, io_dtype, M_m, M_v, M_k, M_eta, M_alpha, B, R, heads, N, head_dim, chunks,
                       consts, workspace, workspace_bytes, s, &sp, memories_per_line ? 1 : 0);
     if (rc) return rc;
-    LineInput qin{Q, R * heads * N * d, heads * N * d, N * d, d, 0, 0, 0};
+    LineInput qin{Q, R * heads * N * d, heads * N * d, N * d, d, 0, 0, 0, 0.f};
     return run_packed<float>(sp, qin, 0, io_dtype, out, head_dim, s);
 }
 

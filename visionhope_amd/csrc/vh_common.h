@@ -67,10 +67,31 @@ inline int dtype_bytes(int t) { return t == VH_DTYPE_F32 ? 4 : 2; }
 // restoration in models/srnl_core/csrc/parallel_line.cuh:16-23).
 //   t0 = h*W + w, t1 = L-1-t0, t2 = w*H + h, t3 = L-1-t2.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int64_t scan_to_pixel(int r, int64_t t, int64_t H, int64_t W) {
+// n / d and n % d for n < 2^24 and d >= 1, with inv_d = 1.0f / d rounded to nearest.
+// float(n) is exact and n * inv_d is within 2/d of n/d, so the truncated quotient is off
+// by at most one (exact for d = 1); one correction step makes it exact.
+__device__ __forceinline__ void divmod24(uint32_t n, uint32_t d, float inv_d, uint32_t& q, uint32_t& rem) {
+    uint32_t qq = static_cast<uint32_t>(static_cast<float>(n) * inv_d);
+    int32_t rr = static_cast<int32_t>(n - qq * d);
+    if (rr < 0) {
+        --qq;
+        rr += static_cast<int32_t>(d);
+    } else if (rr >= static_cast<int32_t>(d)) {
+        ++qq;
+        rr -= static_cast<int32_t>(d);
+    }
+    q = qq;
+    rem = static_cast<uint32_t>(rr);
+}
+
+// Pixel of scan index t of direction r on an H x W image (H*W < 2^24, inv_h = 1.0f / H).
+__device__ __forceinline__ int64_t scan_to_pixel(int r, int64_t t, int64_t H, int64_t W, float inv_h) {
     const int64_t L = H * W;
     const int64_t orig = (r & 1) ? L - 1 - t : t;
-    return r < 2 ? orig : (orig % H) * W + orig / H;
+    if (r < 2) return orig;
+    uint32_t w, h;
+    divmod24(static_cast<uint32_t>(orig), static_cast<uint32_t>(H), inv_h, w, h);
+    return static_cast<int64_t>(h) * W + w;
 }
 __device__ __forceinline__ int64_t pixel_to_scan(int r, int64_t h, int64_t w, int64_t H, int64_t W) {
     const int64_t L = H * W;
