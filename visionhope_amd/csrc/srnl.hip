@@ -26,6 +26,7 @@
 //     chunks uses 16x16-pixel MFMA tiles (srnl_readout16_kernel); every other
 //     case one thread per output in the reference's summation order.
 #include <cmath>
+#include <cstdlib>
 
 #include "vh_common.h"
 
@@ -72,6 +73,7 @@ struct ScanParams {
     float* states;  // [lines, max_chunks, D, D]: chunk-start M_m
     int per_line_state;  // 1: memories hold one state per line (chunk.cu:287, StateCount == N)
     int x_vec;           // input rows are aligned for vector loads
+    int lines_per_wave;  // head_dim 16: lines packed into one wave (1, 2 or 4)
     Consts k;
 };
 
@@ -452,94 +454,147 @@ __device__ __forceinline__ float xor16_32_sum(float v) {
     return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
 }
 
-template <typename T>
+// Element offset of scan token `tok` of direction r from the start of its line.
+template <bool SPATIAL>
+__device__ __forceinline__ int64_t token_offset(const LineInput& in, int r, int64_t tok) {
+    if constexpr (SPATIAL) return scan_to_pixel(r, tok, in.H, in.W, in.inv_h) * in.st;
+    else return tok * in.st;
+}
+
+// NL lines per wave (NL in {1, 2, 4}): the NL lines share (b, r) and take consecutive
+// heads.  Each tile gives every line S = 64/NL token slots; lane l owns slot l % S of
+// line l / S for the per-token work, and MFMA column tile tc (16 slots) belongs to line
+// tc / (4/NL).  G of every line is spread over 64/NL lanes, RL = 4/NL lanes per row,
+// E = 4 NL entries per lane, so a row dot needs log2(RL) DPP steps.  Packing lines lets
+// short chunks (row length 14 or 7) fill the 64 lanes of the token phase.
+template <typename T, int NL, bool SPATIAL>
 __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
     constexpr int D = 16, TT = 64, ROWS = 3 * D + 2, GS = D + 1, DKS = TT + 4;
-    __shared__ __align__(16) float S[64 * D];    // 50 state rows + zero padding rows
-    __shared__ __align__(16) float Gs[D * GS];
-    __shared__ __align__(16) float kk[TT * D];
-    __shared__ __align__(16) float dkT[D * DKS];  // (k - v)[row][token], row stride DKS
+    constexpr int S = TT / NL, TPL = 4 / NL, RL = 4 / NL, E = D / RL, SR = 64 * D;
+    __shared__ __align__(16) float St[NL * SR];       // per line: 50 state rows + zero rows
+    __shared__ __align__(16) float Gs[NL * D * GS];
+    __shared__ __align__(16) float kk[TT * D];        // normalised keys [slot][16]
+    __shared__ __align__(16) float dkT[D * DKS];      // (k - v)[row][slot]
+    __shared__ __align__(16) float cf[TT * 8];        // block coefficients per slot
 
-    const int64_t lines = p.B * p.R * p.heads;
-    const int64_t line = xcd_remap(blockIdx.x, lines);
-    const int64_t head = line % p.heads;
-    const int r = static_cast<int>((line / p.heads) % p.R);
-    const int64_t b = line / (p.heads * p.R);
-    const int64_t s = p.per_line_state ? line : r * p.heads + head;
+    const int64_t groups = p.B * p.R * p.heads / NL;
+    const int64_t line0 = xcd_remap(blockIdx.x, groups) * NL;
+    const int64_t head0 = line0 % p.heads;
+    const int r = static_cast<int>((line0 / p.heads) % p.R);
+    const int64_t b = line0 / (p.heads * p.R);
     const int lane = threadIdx.x;
     const int i16 = lane & 15, q = lane >> 4;
 
-    for (int idx = lane; idx < D * D; idx += 64) {
-        S[idx] = p.Mm[s * D * D + idx];
-        S[D * D + idx] = p.Mv[s * D * D + idx];
-        S[2 * D * D + idx] = p.Mk[s * D * D + idx];
+#pragma unroll
+    for (int lam = 0; lam < NL; ++lam) {
+        const int64_t s = p.per_line_state ? line0 + lam : r * p.heads + head0 + lam;
+        float* Sl = St + lam * SR;
+        for (int idx = lane; idx < D * D; idx += 64) {
+            Sl[idx] = p.Mm[s * D * D + idx];
+            Sl[D * D + idx] = p.Mv[s * D * D + idx];
+            Sl[2 * D * D + idx] = p.Mk[s * D * D + idx];
+        }
+        if (lane < D) {
+            Sl[3 * D * D + lane] = p.Me[s * D + lane];
+            Sl[(3 * D + 1) * D + lane] = p.Ma[s * D + lane];
+        }
+        for (int idx = ROWS * D + lane; idx < SR; idx += 64) Sl[idx] = 0.f;
     }
-    if (lane < D) {
-        S[3 * D * D + lane] = p.Me[s * D + lane];
-        S[(3 * D + 1) * D + lane] = p.Ma[s * D + lane];
-    }
-    for (int idx = ROWS * D + lane; idx < 64 * D; idx += 64) S[idx] = 0.f;
 
     const int C = chunk_of(p.chunk, r);
     const int64_t nc = (p.L + C - 1) / C;
-    const int grow = lane / 4, c0 = (lane % 4) * 4;   // recurrence layout
-    float* out_states = p.states + line * p.max_chunks * D * D;
+    const int lam_g = lane / (16 * RL);                 // recurrence layout
+    const int grow = (lane % (16 * RL)) / RL, c0 = (lane % RL) * E;
+    const int my_slot = lane % S;
+    const T* xcol[4];
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc)
+        xcol[tc] = static_cast<const T*>(p.x.ptr) + b * p.x.sb + r * p.x.sr + (head0 + tc / TPL) * p.x.sh + 4 * q;
 
-    // x operands of the next tile (prefetched during the current recurrence)
-    float xn[4][4];
+    // x operands of a tile move as raw bits: the loads are issued without a branch
+    // (invalid slots read their line's first token) and decoded only where used, so a
+    // prefetch never waits for memory before the work it overlaps.
+    using Raw = typename std::conditional<sizeof(T) == 4, uint4, uint2>::type;
+    Raw xr_next[4];
+    unsigned valid_next = 0;
     bool have_next = false;
-    auto load_tile = [&](int64_t cc, int base, int cnt, float (&xo)[4][4]) {
+    auto issue_tile = [&](int64_t cc, int base, int cnt, Raw (&raw)[4], unsigned& valid) {
+        valid = 0;
 #pragma unroll
         for (int tc = 0; tc < 4; ++tc) {
-            const int t = 16 * tc + i16;
-            const int64_t tok = cc * C + base + t;
-            if (t < cnt && tok < p.L) load4<T>(line_ptr<T>(p.x, b, r, head, tok) + 4 * q, p.x_vec, xo[tc]);
-            else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) xo[tc][j] = 0.f;
+            const int slot = (tc % TPL) * 16 + i16;
+            const int64_t tok = cc * C + base + slot;
+            const bool ok = slot < cnt && tok < p.L;
+            valid |= ok ? (1u << tc) : 0u;
+            const T* src = xcol[tc] + (ok ? token_offset<SPATIAL>(p.x, r, tok) : 0);
+            if (p.x_vec) {
+                raw[tc] = *reinterpret_cast<const Raw*>(src);
+            } else if constexpr (sizeof(T) == 4) {
+                raw[tc] = make_uint4(__float_as_uint(src[0]), __float_as_uint(src[1]), __float_as_uint(src[2]),
+                                     __float_as_uint(src[3]));
+            } else {
+                raw[tc] = make_uint2(static_cast<uint32_t>(src[0].bits) | (static_cast<uint32_t>(src[1].bits) << 16),
+                                     static_cast<uint32_t>(src[2].bits) | (static_cast<uint32_t>(src[3].bits) << 16));
             }
+        }
+    };
+    auto decode_tile = [&](const Raw (&raw)[4], unsigned valid, float (&xo)[4][4]) {
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) {
+            float v[4];
+            if constexpr (sizeof(T) == 4) {
+                v[0] = __uint_as_float(raw[tc].x); v[1] = __uint_as_float(raw[tc].y);
+                v[2] = __uint_as_float(raw[tc].z); v[3] = __uint_as_float(raw[tc].w);
+            } else {
+                v[0] = to_f32(T{static_cast<uint16_t>(raw[tc].x & 0xffffu)});
+                v[1] = to_f32(T{static_cast<uint16_t>(raw[tc].x >> 16)});
+                v[2] = to_f32(T{static_cast<uint16_t>(raw[tc].y & 0xffffu)});
+                v[3] = to_f32(T{static_cast<uint16_t>(raw[tc].y >> 16)});
+            }
+            const bool ok = (valid >> tc) & 1u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xo[tc][j] = ok ? v[j] : 0.f;
         }
     };
 
     for (int64_t c = 0; c < nc; ++c) {
         __syncthreads();
-        *reinterpret_cast<float4*>(out_states + c * D * D + lane * 4) =
-            *reinterpret_cast<const float4*>(S + lane * 4);
+#pragma unroll
+        for (int lam = 0; lam < NL; ++lam)
+            *reinterpret_cast<float4*>(p.states + ((line0 + lam) * p.max_chunks + c) * D * D + lane * 4) =
+                *reinterpret_cast<const float4*>(St + lam * SR + lane * 4);
         if (c == nc - 1) break;
 
-        float g[4];
+        float g[E];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) g[e] = (c0 + e == grow) ? 1.f : 0.f;
-        // A operands of the projections (rows of M_k, M_v) and the gate vectors
-        float ak[4], av[4], ev[4], avv[4];
-        {
-            const float4 k4 = *reinterpret_cast<const float4*>(S + (2 * D + i16) * D + 4 * q);
-            const float4 v4 = *reinterpret_cast<const float4*>(S + (D + i16) * D + 4 * q);
-            const float4 e4 = *reinterpret_cast<const float4*>(S + 3 * D * D + 4 * q);
-            const float4 a4 = *reinterpret_cast<const float4*>(S + (3 * D + 1) * D + 4 * q);
-            ak[0] = k4.x; ak[1] = k4.y; ak[2] = k4.z; ak[3] = k4.w;
-            av[0] = v4.x; av[1] = v4.y; av[2] = v4.z; av[3] = v4.w;
-            ev[0] = e4.x; ev[1] = e4.y; ev[2] = e4.z; ev[3] = e4.w;
-            avv[0] = a4.x; avv[1] = a4.y; avv[2] = a4.z; avv[3] = a4.w;
-        }
+        for (int e = 0; e < E; ++e) g[e] = (c0 + e == grow) ? 1.f : 0.f;
 
-        for (int base = 0; base < C; base += TT) {
-            const int cnt = min(TT, C - base);
+        for (int base = 0; base < C; base += S) {
+            const int cnt = min(S, C - base);
             float xo[4][4];
-            if (have_next) {
-#pragma unroll
-                for (int tc = 0; tc < 4; ++tc)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) xo[tc][j] = xn[tc][j];
-            } else {
-                load_tile(c, base, cnt, xo);
-            }
+            if (!have_next) issue_tile(c, base, cnt, xr_next, valid_next);
+            decode_tile(xr_next, valid_next, xo);
             // ---- projections on MFMA, norms per token; then each lane computes the
-            //      gates of its own token (lane l owns token l of the tile) ----
+            //      gates of its own slot ----
             float tok_ksq = 0.f, tok_dsq = 0.f, tok_ep = 0.f, tok_ap = 0.f;
 #pragma unroll
             for (int tc = 0; tc < 4; ++tc) {
-                if (16 * tc >= cnt) break;   // uniform: no tokens left in this column tile
+                const int t = 16 * tc + i16;
+                if ((tc % TPL) * 16 >= cnt) {
+                    // No tokens in this column tile (uniform): zero keys and differences,
+                    // so the identity slots of the last block read finite values.
+                    *reinterpret_cast<float4*>(kk + t * D + 4 * q) = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) dkT[(4 * q + j) * DKS + t] = 0.f;
+                    continue;
+                }
+                const float* Sl = St + (tc / TPL) * SR;
+                const float4 k4 = *reinterpret_cast<const float4*>(Sl + (2 * D + i16) * D + 4 * q);
+                const float4 v4 = *reinterpret_cast<const float4*>(Sl + (D + i16) * D + 4 * q);
+                const float4 e4 = *reinterpret_cast<const float4*>(Sl + 3 * D * D + 4 * q);
+                const float4 a4 = *reinterpret_cast<const float4*>(Sl + (3 * D + 1) * D + 4 * q);
+                const float ak[4] = {k4.x, k4.y, k4.z, k4.w}, av[4] = {v4.x, v4.y, v4.z, v4.w};
+                const float ev[4] = {e4.x, e4.y, e4.z, e4.w}, aa[4] = {a4.x, a4.y, a4.z, a4.w};
                 v4f kacc = {0.f, 0.f, 0.f, 0.f}, vacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
@@ -550,7 +605,7 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     pe += ev[j] * xo[tc][j];
-                    pa += avv[j] * xo[tc][j];
+                    pa += aa[j] * xo[tc][j];
                 }
                 float kn = kacc[0] * kacc[0] + kacc[1] * kacc[1] + kacc[2] * kacc[2] + kacc[3] * kacc[3];
                 kn = xor16_32_sum(kn);
@@ -574,7 +629,6 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                     tok_ep = pe;
                     tok_ap = pa;
                 }
-                const int t = 16 * tc + i16;
                 *reinterpret_cast<float4*>(kk + t * D + 4 * q) = make_float4(kv[0], kv[1], kv[2], kv[3]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) dkT[(4 * q + j) * DKS + t] = df[j];
@@ -596,28 +650,26 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
             // ---- prefetch the next tile's x operands ----
             {
                 int64_t ncc = c;
-                int nbase = base + TT;
+                int nbase = base + S;
                 if (nbase >= C) { ncc = c + 1; nbase = 0; }
                 have_next = ncc < nc - 1;
-                if (have_next) load_tile(ncc, nbase, min(TT, C - nbase), xn);
+                if (have_next) issue_tile(ncc, nbase, min(S, C - nbase), xr_next, valid_next);
             }
             __syncthreads();
-            // ---- block coefficients: tokens 4u..4u+3 of the tile are the lanes of one
-            //      DPP quad.  With A_j = prod_{s<=j} alpha_s inside the block,
+            // ---- block coefficients: slots 4u..4u+3 of a line are the lanes of one DPP
+            //      quad.  With A_j = prod_{s<=j} alpha_s inside the block,
             //        r_j = A_{j-1} (g.k_j) + delta_j - sum_{s<j} beta_sj r_s
             //        g  <- A_3 g - sum_s w_s r_s k_s
             //      beta_sj = (A_{j-1}/A_s) eta_s (k_s.k_j), w_s = (A_3/A_s) eta_s.
-            //      Tokens past the chunk act as the identity (alpha 1, eta 0). ----
-            float cf_a, cf_b1, cf_b2, cf_b3, cf_w, cf_A3;
+            //      Slots past the chunk act as the identity (alpha 1, eta 0). ----
             {
-                const bool valid = lane < cnt;
+                const bool valid = my_slot < cnt;
                 const float al_t = valid ? my_alpha : 1.f;
                 const float et_t = valid ? my_eff : 0.f;
                 const int j = lane & 3;
                 const float pa1 = quad_perm<0x90>(al_t), pa2 = quad_perm<0x40>(al_t), pa3 = quad_perm<0x00>(al_t);
                 const float pe1 = quad_perm<0x90>(et_t), pe2 = quad_perm<0x40>(et_t), pe3 = quad_perm<0x00>(et_t);
                 const float na1 = quad_perm<0xF9>(al_t), na2 = quad_perm<0xFE>(al_t), na3 = quad_perm<0xFF>(al_t);
-                // key dots with the 1, 2, 3 previous tokens of the block
                 float kd1 = 0.f, kd2 = 0.f, kd3 = 0.f;
                 {
                     const int t1 = max(lane - 1, 0), t2 = max(lane - 2, 0), t3 = max(lane - 3, 0);
@@ -632,112 +684,136 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                         kd3 += k0.x * k3.x + k0.y * k3.y + k0.z * k3.z + k0.w * k3.w;
                     }
                 }
-                cf_a = 1.f;
+                float cf_a = 1.f;
                 if (j >= 1) cf_a *= pa1;
                 if (j >= 2) cf_a *= pa2;
                 if (j >= 3) cf_a *= pa3;
-                cf_b1 = pe1 * kd1;
-                cf_b2 = pe2 * kd2 * pa1;
-                cf_b3 = pe3 * kd3 * pa2 * pa1;
-                cf_w = et_t;
+                const float cf_b1 = pe1 * kd1;
+                const float cf_b2 = pe2 * kd2 * pa1;
+                const float cf_b3 = pe3 * kd3 * pa2 * pa1;
+                float cf_w = et_t;
                 if (j <= 2) cf_w *= na1;
                 if (j <= 1) cf_w *= na2;
                 if (j == 0) cf_w *= na3;
-                cf_A3 = quad_perm<0x00>(al_t) * quad_perm<0x55>(al_t) * quad_perm<0xAA>(al_t) *
-                        quad_perm<0xFF>(al_t);
+                const float cf_A3 = quad_perm<0x00>(al_t) * quad_perm<0x55>(al_t) * quad_perm<0xAA>(al_t) *
+                                    quad_perm<0xFF>(al_t);
+                *reinterpret_cast<float4*>(cf + lane * 8) = make_float4(cf_a, cf_b1, cf_b2, cf_b3);
+                *reinterpret_cast<float4*>(cf + lane * 8 + 4) = make_float4(cf_w, cf_A3, 0.f, 0.f);
             }
+            __syncthreads();
             // ---- serial recurrence, 4 tokens per step; the operands of the next step
-            //      are read from LDS while the current one computes (two register
-            //      sets used alternately, so no copies between steps) ----
-            float kA[4][4], dA[4], kB[4][4], dB[4];
-            auto fetch = [&](int t, float (&kv)[4][4], float (&df)[4]) {
-                const int tn = min(t, TT - 4);
+            //      are read from LDS while the current one computes (two register sets
+            //      used alternately, so no copies between steps) ----
+            struct StepOps {
+                float kv[4][E];
+                float df[4];
+                float c0v[4][4];   // slots 1..3: a, beta_{j-1,j}, beta_{j-2,j}, beta_{j-3,j}
+                float c1v[4][2];   // every slot: w; slot 0: A_3 of the block
+            };
+            StepOps opA, opB;
+            auto fetch = [&](int t, StepOps& o) {
+                const int tn = lam_g * S + min(t, S - 4);
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(kk + (tn + u) * D + c0);
-                    kv[u][0] = k4.x; kv[u][1] = k4.y; kv[u][2] = k4.z; kv[u][3] = k4.w;
+#pragma unroll
+                    for (int e = 0; e < E; e += 4) {
+                        const float4 k4 = *reinterpret_cast<const float4*>(kk + (tn + u) * D + c0 + e);
+                        o.kv[u][e] = k4.x; o.kv[u][e + 1] = k4.y; o.kv[u][e + 2] = k4.z; o.kv[u][e + 3] = k4.w;
+                    }
+                    if (u > 0) {
+                        const float4 a4 = *reinterpret_cast<const float4*>(cf + (tn + u) * 8);
+                        o.c0v[u][0] = a4.x; o.c0v[u][1] = a4.y; o.c0v[u][2] = a4.z; o.c0v[u][3] = a4.w;
+                    }
+                    const float2 w2 = *reinterpret_cast<const float2*>(cf + (tn + u) * 8 + 4);
+                    o.c1v[u][0] = w2.x; o.c1v[u][1] = w2.y;
                 }
                 const float4 d4 = *reinterpret_cast<const float4*>(dkT + grow * DKS + tn);
-                df[0] = d4.x; df[1] = d4.y; df[2] = d4.z; df[3] = d4.w;
+                o.df[0] = d4.x; o.df[1] = d4.y; o.df[2] = d4.z; o.df[3] = d4.w;
             };
-            auto step = [&](int t0, const float (&kvb)[4][4], const float (&dfb)[4]) {
-                const float a1 = readlane_f(cf_a, t0 + 1), a2 = readlane_f(cf_a, t0 + 2),
-                            a3 = readlane_f(cf_a, t0 + 3);
-                const float b01 = readlane_f(cf_b1, t0 + 1), b02 = readlane_f(cf_b2, t0 + 2),
-                            b12 = readlane_f(cf_b1, t0 + 2), b03 = readlane_f(cf_b3, t0 + 3),
-                            b13 = readlane_f(cf_b2, t0 + 3), b23 = readlane_f(cf_b1, t0 + 3);
-                const float w0 = readlane_f(cf_w, t0), w1 = readlane_f(cf_w, t0 + 1),
-                            w2 = readlane_f(cf_w, t0 + 2), w3 = readlane_f(cf_w, t0 + 3);
-                const float A3 = readlane_f(cf_A3, t0);
+            auto step = [&](const StepOps& o) {
                 float pdot[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    float d0 = g[0] * kvb[u][0];
-                    d0 += g[1] * kvb[u][1];
-                    d0 += g[2] * kvb[u][2];
-                    d0 += g[3] * kvb[u][3];
-                    d0 += quad_swap1(d0);
-                    d0 += quad_swap2(d0);
-                    pdot[u] = d0;
-                }
-                const float r0 = pdot[0] + dfb[0];
-                const float r1 = a1 * pdot[1] + dfb[1] - b01 * r0;
-                const float r2 = a2 * pdot[2] + dfb[2] - b02 * r0 - b12 * r1;
-                const float r3 = a3 * pdot[3] + dfb[3] - b03 * r0 - b13 * r1 - b23 * r2;
-                const float c0r = w0 * r0, c1r = w1 * r1, c2r = w2 * r2, c3r = w3 * r3;
+                    float d0 = g[0] * o.kv[u][0];
+                    float d1 = g[1] * o.kv[u][1];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float v = A3 * g[e] - c0r * kvb[0][e];
-                    v -= c1r * kvb[1][e];
-                    v -= c2r * kvb[2][e];
-                    g[e] = v - c3r * kvb[3][e];
+                    for (int e = 2; e < E; e += 2) {
+                        d0 += g[e] * o.kv[u][e];
+                        d1 += g[e + 1] * o.kv[u][e + 1];
+                    }
+                    float d = d0 + d1;
+                    if constexpr (RL >= 2) d += quad_swap1(d);
+                    if constexpr (RL == 4) d += quad_swap2(d);
+                    pdot[u] = d;
+                }
+                const float r0 = pdot[0] + o.df[0];
+                const float r1 = o.c0v[1][0] * pdot[1] + o.df[1] - o.c0v[1][1] * r0;
+                const float r2 = o.c0v[2][0] * pdot[2] + o.df[2] - o.c0v[2][2] * r0 - o.c0v[2][1] * r1;
+                const float r3 = o.c0v[3][0] * pdot[3] + o.df[3] - o.c0v[3][3] * r0 - o.c0v[3][2] * r1 -
+                                 o.c0v[3][1] * r2;
+                const float A3 = o.c1v[0][1];
+                const float c0r = o.c1v[0][0] * r0, c1r = o.c1v[1][0] * r1, c2r = o.c1v[2][0] * r2,
+                            c3r = o.c1v[3][0] * r3;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    float v = A3 * g[e] - c0r * o.kv[0][e];
+                    v -= c1r * o.kv[1][e];
+                    v -= c2r * o.kv[2][e];
+                    g[e] = v - c3r * o.kv[3][e];
                 }
             };
             // Pin freshly read operands in registers once the step between has run, so
             // the compiler cannot turn them back into LDS reads next to their use.
-            auto pin = [&](float (&kv)[4][4], float (&df)[4]) {
+            auto pin = [&](StepOps& o) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(kv[u][e]));
-                    asm volatile("" : "+v"(df[u]));
+                    for (int e = 0; e < E; ++e) asm volatile("" : "+v"(o.kv[u][e]));
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) asm volatile("" : "+v"(o.c0v[u][m]));
+                    asm volatile("" : "+v"(o.c1v[u][0]), "+v"(o.c1v[u][1]), "+v"(o.df[u]));
                 }
             };
-            fetch(0, kA, dA);
+            fetch(0, opA);
             for (int t0 = 0; t0 < cnt; t0 += 8) {
-                fetch(t0 + 4, kB, dB);
+                fetch(t0 + 4, opB);
                 __builtin_amdgcn_sched_barrier(0);
-                step(t0, kA, dA);
-                pin(kB, dB);
+                step(opA);
+                pin(opB);
                 if (t0 + 4 >= cnt) break;
-                fetch(t0 + 8, kA, dA);
+                fetch(t0 + 8, opA);
                 __builtin_amdgcn_sched_barrier(0);
-                step(t0 + 4, kB, dB);
-                pin(kA, dA);
+                step(opB);
+                pin(opA);
             }
             __syncthreads();
         }
-        // ---- refresh on MFMA: S <- S G ----
+        // ---- refresh on MFMA: S <- S G for every line ----
 #pragma unroll
-        for (int e = 0; e < 4; ++e) Gs[grow * GS + c0 + e] = g[e];
+        for (int e = 0; e < E; ++e) Gs[lam_g * D * GS + grow * GS + c0 + e] = g[e];
         __syncthreads();
-        float bg[4];
+        v4f acc[NL][4];
 #pragma unroll
-        for (int st = 0; st < 4; ++st) bg[st] = Gs[(4 * q + st) * GS + i16];
-        v4f acc[4];
+        for (int lam = 0; lam < NL; ++lam) {
+            float bg[4];
 #pragma unroll
-        for (int R = 0; R < 4; ++R) {
-            const float4 a4 = *reinterpret_cast<const float4*>(S + (16 * R + i16) * D + 4 * q);
-            const float a[4] = {a4.x, a4.y, a4.z, a4.w};
-            acc[R] = v4f{0.f, 0.f, 0.f, 0.f};
+            for (int st = 0; st < 4; ++st) bg[st] = Gs[lam * D * GS + (4 * q + st) * GS + i16];
 #pragma unroll
-            for (int st = 0; st < 4; ++st) acc[R] = mfma4(a[st], bg[st], acc[R]);
+            for (int R = 0; R < 4; ++R) {
+                const float4 a4 = *reinterpret_cast<const float4*>(St + lam * SR + (16 * R + i16) * D + 4 * q);
+                const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+                acc[lam][R] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 4; ++st) acc[lam][R] = mfma4(a[st], bg[st], acc[lam][R]);
+            }
         }
         __syncthreads();
 #pragma unroll
-        for (int R = 0; R < 4; ++R)
+        for (int lam = 0; lam < NL; ++lam)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) S[(16 * R + 4 * q + j) * D + i16] = acc[R][j];
+            for (int R = 0; R < 4; ++R)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) St[lam * SR + (16 * R + 4 * q + j) * D + i16] = acc[lam][R][j];
     }
 }
 
@@ -989,10 +1065,26 @@ int check_memories(const float* a, const float* b, const float* c, const float* 
 template <int D, typename T>
 void launch_scan(const ScanParams& sp, hipStream_t stream) {
     const int64_t lines = sp.B * sp.R * sp.heads;
-    if constexpr (D == 16)
-        hipLaunchKernelGGL((srnl_scan16_kernel<T>), dim3(static_cast<unsigned>(lines)), dim3(64), 0,
-                           stream, sp);
-    else
+    if constexpr (D == 16) {
+        const int nl = sp.lines_per_wave;
+        const unsigned grid = static_cast<unsigned>(lines / nl);
+        auto go = [&](auto nlc, auto spc) {
+            hipLaunchKernelGGL((srnl_scan16_kernel<T, decltype(nlc)::value, decltype(spc)::value>), dim3(grid),
+                               dim3(64), 0, stream, sp);
+        };
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        using S4 = std::integral_constant<int, 4>;
+        if (sp.x.spatial) {
+            if (nl == 4) go(S4{}, std::true_type{});
+            else if (nl == 2) go(S2{}, std::true_type{});
+            else go(S1{}, std::true_type{});
+        } else {
+            if (nl == 4) go(S4{}, std::false_type{});
+            else if (nl == 2) go(S2{}, std::false_type{});
+            else go(S1{}, std::false_type{});
+        }
+    } else
         hipLaunchKernelGGL((srnl_scan_kernel<D, T>), dim3(static_cast<unsigned>(lines)),
                            dim3(ScanCfg<D>::NT), 0, stream, sp);
 }
@@ -1026,6 +1118,21 @@ int64_t max_chunk_count(int64_t length, const int64_t* chunks, int64_t R) {
 }
 
 // Shared validation + scan launch for every SRNL entry point.
+// Lines per wave of the head_dim-16 scan.  Packing NL lines multiplies the useful
+// work of the token phase for chunks of at most 64/NL tokens and shortens every row
+// dot, but divides the number of waves: pack only while at least one wave per SIMD
+// (1024 on MI355X) remains.  The lines of a wave share (b, r), so NL divides heads.
+// VH_SCAN_LINES_PER_WAVE = 1, 2 or 4 forces a packing (when heads allows it).
+int scan16_lines_per_wave(int64_t lines, int64_t heads) {
+    if (const char* env = std::getenv("VH_SCAN_LINES_PER_WAVE")) {
+        const int forced = std::atoi(env);
+        if ((forced == 1 || forced == 2 || forced == 4) && heads % forced == 0) return forced;
+    }
+    if (heads % 4 == 0 && lines >= 4 * 1024) return 4;
+    if (heads % 2 == 0 && lines >= 2 * 1024) return 2;
+    return 1;
+}
+
 int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv, const float* Mk,
              const float* Me, const float* Ma, int64_t B, int64_t R, int64_t heads, int64_t L,
              int d, const int64_t* chunks, const vh_srnl_consts* consts, void* workspace,
@@ -1072,6 +1179,7 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
         sp.x_vec = ok ? 1 : 0;
     }
     sp.k = make_consts(consts);
+    sp.lines_per_wave = scan16_lines_per_wave(lines, heads);
     rc = dispatch_d(d, [&](auto dc) {
         constexpr int D = decltype(dc)::value;
         dispatch_t(io_dtype, [&](auto tv) { launch_scan<D, decltype(tv)>(sp, stream); });
