@@ -55,7 +55,8 @@ def test_abi_version_matches_header(lib):
 def test_workspace_queries(lib):
     assert lib.vh_srnl_workspace_bytes(10, 7, 16) == 10 * 7 * 16 * 16 * 4
     assert lib.vh_srnl_workspace_bytes(0, 7, 16) == 0
-    assert lib.vh_grn_workspace_bytes(2, 8, 10, 10) == 2 * 2 * 8 * 4   # 100 pixels -> 2 slabs of 64
+    # 100 pixels, B=2: the statistics pass splits each image into 13 slabs of 8 pixels
+    assert lib.vh_grn_workspace_bytes(2, 8, 10, 10) == 2 * 13 * 8 * 4
 
 
 def _consts():

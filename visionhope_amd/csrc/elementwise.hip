@@ -68,6 +68,45 @@ __global__ __launch_bounds__(256) void direction_fusion_kernel(const FusionParam
     p.out[idx] = out;
 }
 
+// Channels-last output, D >= 8: one thread per (image, pixel, 8-channel group), 16-byte
+// reads of y and x per direction, one 32-byte write.  Same summation order.
+template <int D, typename T>
+__global__ __launch_bounds__(256) void direction_fusion8_kernel(const FusionParams p, const float inv_w,
+                                                               const float inv_g) {
+    constexpr int GD = D / 8;  // channel groups per head
+    const int G = static_cast<int>(p.heads) * GD;
+    const int L = static_cast<int>(p.H * p.W);
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= static_cast<uint32_t>(L * G)) return;
+    const int64_t b = blockIdx.y;
+    uint32_t pix, cg, h, w;
+    divmod24(idx, static_cast<uint32_t>(G), inv_g, pix, cg);
+    divmod24(pix, static_cast<uint32_t>(p.W), inv_w, h, w);
+    const int head = static_cast<int>(cg) / GD, i0 = (static_cast<int>(cg) % GD) * 8;
+    const int C = G * 8, c0 = static_cast<int>(cg) * 8;
+    const T* y = static_cast<const T*>(p.y);
+    const T* x = static_cast<const T*>(p.x);
+    const int64_t base = (b * 4 * p.heads + head) * static_cast<int64_t>(L) * D + i0;
+    const int64_t stride_dir = p.heads * static_cast<int64_t>(L) * D;
+    float out[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t at = base + r * stride_dir + pixel_to_scan(r, h, w, p.H, p.W) * D;
+        float yv[8], xv[8];
+        load8<T>(y + at, yv);
+        load8<T>(x + at, xv);
+        const float* sk = p.skip + (p.skip_per_dir ? r * C : 0) + c0;
+        const float* sc = p.scale + r * C + c0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float v = yv[j] + sk[j] * xv[j];
+            out[j] = r == 0 ? sc[j] * v : out[j] + sc[j] * v;
+        }
+    }
+    const float z[8] = {out[0], out[1], out[2], out[3], out[4], out[5], out[6], out[7]};
+    store8<float>(p.out + (b * L + pix) * static_cast<int64_t>(C) + c0, z);
+}
+
 // ---------------------------------------------------------------------------
 // GRN (utils/grn.py:26-38, utils/csrc/grn_cuda.cu:46-124) on channels-last x.
 //   pass 1  partial[b, slab, c] = sum over the slab's pixels of x^2
@@ -149,6 +188,65 @@ __global__ __launch_bounds__(256) void grn_apply_kernel(const T* __restrict__ x,
     }
 }
 
+// Vectorised GRN for C % 8 == 0, C <= 2048 and 16-byte aligned tensors: each thread
+// owns 8 consecutive channels of a pixel (one 16-byte load of bf16/fp16), a block is
+// G = C/8 channel groups x R = 256/G pixel rows, so every thread keeps the same channels
+// for the whole block and no index arithmetic runs per element.
+template <typename T>
+__global__ __launch_bounds__(256) void grn_partial8_kernel(const T* __restrict__ x, float* __restrict__ partial,
+                                                          int C, int S, int rows_per_slab, int nslab) {
+    extern __shared__ float red[];  // [R][C]
+    const int G = C / 8, R = static_cast<int>(blockDim.x) / G;
+    const int g = static_cast<int>(threadIdx.x) % G, rr = static_cast<int>(threadIdx.x) / G;
+    const int b = blockIdx.y, slab = blockIdx.x;
+    const int s0 = slab * rows_per_slab, s1 = min(S, s0 + rows_per_slab);
+    const T* xb = x + static_cast<int64_t>(b) * S * C + g * 8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = s0 + rr; s < s1; s += R) {
+        float v[8];
+        load8<T>(xb + static_cast<int64_t>(s) * C, v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += v[j] * v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) red[rr * C + g * 8 + j] = acc[j];
+    __syncthreads();
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float t = 0.f;
+        for (int q = 0; q < R; ++q) t += red[q * C + c];
+        partial[(static_cast<int64_t>(b) * nslab + slab) * C + c] = t;
+    }
+}
+
+template <typename T, typename TO>
+__global__ __launch_bounds__(256) void grn_apply8_kernel(const T* __restrict__ x, const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta,
+                                                        const float* __restrict__ gx,
+                                                        const float* __restrict__ inv_den, TO* __restrict__ y,
+                                                        int C, int S, int rows_per_block) {
+    const int G = C / 8, R = static_cast<int>(blockDim.x) / G;
+    const int g = static_cast<int>(threadIdx.x) % G, rr = static_cast<int>(threadIdx.x) / G;
+    const int b = blockIdx.y;
+    const int s0 = blockIdx.x * rows_per_block, s1 = min(S, s0 + rows_per_block);
+    const float inv = inv_den[b];
+    float sc[8], bt[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = g * 8 + j;
+        const float nx = gx[static_cast<int64_t>(b) * C + c] * inv;
+        sc[j] = 1.f + gamma[c] * nx;
+        bt[j] = beta[c];
+    }
+    const int64_t base = static_cast<int64_t>(b) * S * C + g * 8;
+    for (int s = s0 + rr; s < s1; s += R) {
+        float v[8];
+        load8<T>(x + base + static_cast<int64_t>(s) * C, v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = v[j] * sc[j] + bt[j];
+        store8<TO>(y + base + static_cast<int64_t>(s) * C, v);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // LayerNorm over C per pixel (models/layers.py:25-35; Triton arithmetic of
 // utils/layer_norm_cuda.py:44-57): mean, biased centred variance,
@@ -196,6 +294,56 @@ __global__ __launch_bounds__(256) void layernorm_nhwc_kernel(const T* __restrict
     for (int k = 0; k < MAXV; ++k) {
         const int c = lane + k * TPR;
         if (c < C) yr[c] = from_f32<TO>(v[k] * rstd * w[c] + bias[c]);
+    }
+    if (lane == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = rstd;
+    }
+}
+
+// Channels-last, C % 8 == 0: LPR = 2^lpr_log2 lanes per pixel row, each lane GP groups
+// of 8 channels (group k*LPR + lane), 16-byte loads and stores.
+template <typename T, typename TO, int GP>
+__global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restrict__ x, const float* __restrict__ w,
+                                                             const float* __restrict__ bias, TO* __restrict__ y,
+                                                             float* __restrict__ mean_out,
+                                                             float* __restrict__ rstd_out, int64_t rows, int C,
+                                                             int lpr_log2, float eps) {
+    const int LPR = 1 << lpr_log2;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 >> lpr_log2) + (threadIdx.x >> lpr_log2);
+    const int lane = threadIdx.x & (LPR - 1);
+    const bool active = row < rows;
+    const T* xr = x + (active ? row : 0) * C;
+    float v[GP][8];
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+        load8<T>(xr + (k * LPR + lane) * 8, v[k]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum += v[k][j];
+    }
+    for (int off = LPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    const float mean = sum / static_cast<float>(C);
+    float sq = 0.f;
+#pragma unroll
+    for (int k = 0; k < GP; ++k)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[k][j] -= mean;
+            sq += v[k][j] * v[k][j];
+        }
+    for (int off = LPR / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+    const float rstd = 1.f / sqrtf(sq / static_cast<float>(C) + eps);
+    if (!active) return;
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+        const int c = (k * LPR + lane) * 8;
+        float wv[8], bv[8], o[8];
+        load8<float>(w + c, wv);
+        load8<float>(bias + c, bv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = v[k][j] * rstd * wv[j] + bv[j];
+        store8<TO>(y + row * C + c, o);
     }
     if (lane == 0) {
         if (mean_out) mean_out[row] = mean;
@@ -308,6 +456,33 @@ unsigned grid_for(int64_t total, int64_t cap) {
     return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((total + 255) / 256, cap)));
 }
 
+// Vectorised channels-last LayerNorm when C % 8 == 0 and every tensor is 16-byte aligned:
+// LPR = largest power of two (<= 32) dividing C/8, GP = C/8/LPR groups per lane.
+template <typename T, typename TO>
+bool launch_ln_nhwc8(const void* x, const float* w, const float* b, void* yv, float* mean, float* rstd,
+                     int64_t rows, int C, float eps, hipStream_t s) {
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                            reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(yv);
+    if (C % 8 != 0 || align % 16 != 0) return false;
+    const int ng = C / 8;
+    int lg = 0;
+    while (lg < 5 && ng % (2 << lg) == 0) ++lg;
+    const int gp = ng >> lg;
+    const unsigned blocks = static_cast<unsigned>((rows + (256 >> lg) - 1) / (256 >> lg));
+    const T* xp = static_cast<const T*>(x);
+    TO* y = static_cast<TO*>(yv);
+    switch (gp) {
+#define VH_LN8(G)                                                                                        \
+    case G:                                                                                              \
+        hipLaunchKernelGGL((layernorm_nhwc8_kernel<T, TO, G>), dim3(blocks), dim3(256), 0, s, xp, w, b, y, \
+                           mean, rstd, rows, C, lg, eps);                                                \
+        return true;
+        VH_LN8(1) VH_LN8(2) VH_LN8(3) VH_LN8(4) VH_LN8(5) VH_LN8(6) VH_LN8(7) VH_LN8(8)
+#undef VH_LN8
+    }
+    return false;
+}
+
 template <typename T, typename TO, int TPR>
 void launch_ln_nhwc(const void* x, const float* w, const float* b, void* yv, float* mean,
                     float* rstd, int64_t rows, int C, float eps, hipStream_t s) {
@@ -351,6 +526,26 @@ int vh_postprocess_scale_forward(const void* Y, const void* X, int32_t io_dtype,
     const int64_t total = B * heads * head_dim * H * W;
     const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(Y) | reinterpret_cast<uintptr_t>(X) |
+                            reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(d_skip) |
+                            reinterpret_cast<uintptr_t>(scale);
+    const int64_t groups = H * W * heads * (head_dim / 8);
+    if (channels_last && head_dim >= 8 && align % 16 == 0 && groups < (int64_t(1) << 24)) {
+        const dim3 grid(static_cast<unsigned>((groups + 255) / 256), static_cast<unsigned>(B));
+        const float inv_w = 1.0f / static_cast<float>(W);
+        const float inv_g = 1.0f / static_cast<float>(heads * (head_dim / 8));
+        int rc = dispatch_d(head_dim, [&](auto dc) {
+            constexpr int D = decltype(dc)::value;
+            if constexpr (D >= 8) {
+                dispatch_t(io_dtype, [&](auto tv) {
+                    hipLaunchKernelGGL((direction_fusion8_kernel<D, decltype(tv)>), grid, dim3(256), 0, s, fp,
+                                       inv_w, inv_g);
+                });
+            }
+        });
+        if (rc) return rc;
+        return check_launch("direction_fusion8_kernel");
+    }
     int rc = dispatch_d(head_dim, [&](auto dc) {
         constexpr int D = decltype(dc)::value;
         dispatch_t(io_dtype, [&](auto tv) {
@@ -362,9 +557,23 @@ int vh_postprocess_scale_forward(const void* Y, const void* X, int32_t io_dtype,
     return check_launch("direction_fusion_kernel");
 }
 
+// Slab length of the vectorised GRN statistics: enough slabs for >= ~2048 blocks.
+static int64_t grn_rows_per_slab(int64_t B, int64_t S) {
+    const int64_t want = std::max<int64_t>(1, 2048 / std::max<int64_t>(B, 1));
+    const int64_t nslab = std::min<int64_t>(std::max<int64_t>(1, (S + 7) / 8), want);
+    return (S + nslab - 1) / nslab;
+}
+
+static bool grn_vectorised(int64_t C, const void* x, const void* y) {
+    return C % 8 == 0 && C / 8 <= 256 &&
+           (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16 == 0;
+}
+
 size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W) {
-    if (B <= 0 || C <= 0 || H <= 0 || W <= 0) return 0;
-    const int64_t nslab = (H * W + kGrnRowsPerSlab - 1) / kGrnRowsPerSlab;
+    // Enough for either the vectorised or the scalar slab count.
+    const int64_t S = H * W;
+    const int64_t rows = grn_rows_per_slab(B, S);
+    const int64_t nslab = std::max<int64_t>((S + rows - 1) / rows, (S + kGrnRowsPerSlab - 1) / kGrnRowsPerSlab);
     return static_cast<size_t>(B * nslab * C) * sizeof(float);
 }
 
@@ -388,6 +597,31 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
     hipStream_t s = static_cast<hipStream_t>(stream);
     float* partial = static_cast<float*>(workspace);
     const int64_t total = B * S * C;
+    if (grn_vectorised(C, x, y) && B * S * C < (int64_t(1) << 31)) {
+        const int G = static_cast<int>(C / 8);
+        const int R = std::max(1, 256 / G);
+        const int rows = static_cast<int>(grn_rows_per_slab(B, S));
+        const int vslab = static_cast<int>((S + rows - 1) / rows);
+        const size_t red = static_cast<size_t>(R) * static_cast<size_t>(C) * sizeof(float);
+        const int apply_rows = std::max(R, static_cast<int>(std::min<int64_t>(S, 4 * R)));
+        const unsigned apply_blocks = static_cast<unsigned>((S + apply_rows - 1) / apply_rows);
+        int rc = dispatch_t(io_dtype, [&](auto tv) {
+            using T = decltype(tv);
+            hipLaunchKernelGGL((grn_partial8_kernel<T>), dim3(static_cast<unsigned>(vslab), static_cast<unsigned>(B)),
+                               dim3(G * R), red, s, static_cast<const T*>(x), partial, static_cast<int>(C),
+                               static_cast<int>(S), rows, vslab);
+            hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, partial,
+                               gx, inv_den, C, static_cast<int64_t>(vslab), eps);
+            dispatch_t(y_dtype, [&](auto ov) {
+                using TO = decltype(ov);
+                hipLaunchKernelGGL((grn_apply8_kernel<T, TO>), dim3(apply_blocks, static_cast<unsigned>(B)),
+                                   dim3(G * R), 0, s, static_cast<const T*>(x), gamma, beta, gx, inv_den,
+                                   static_cast<TO*>(y), static_cast<int>(C), static_cast<int>(S), apply_rows);
+            });
+        });
+        if (rc) return rc;
+        return check_launch("grn vectorised kernels");
+    }
     int rc = dispatch_t(io_dtype, [&](auto tv) {
         using T = decltype(tv);
         hipLaunchKernelGGL((grn_partial_kernel<T>), dim3(static_cast<unsigned>(nslab), static_cast<unsigned>(B)),
@@ -423,6 +657,7 @@ int vh_layernorm2d_forward(const void* x, int32_t io_dtype, const float* weight,
             dispatch_t(y_dtype, [&](auto ov) {
                 using T = decltype(tv);
                 using TO = decltype(ov);
+                if (launch_ln_nhwc8<T, TO>(x, weight, bias, y, mean, rstd, rows, c, eps, s)) return;
                 if (c <= 16) launch_ln_nhwc<T, TO, 4>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
                 else if (c <= 32) launch_ln_nhwc<T, TO, 8>(x, weight, bias, y, mean, rstd, rows, c, eps, s);
                 else if (c <= 64) launch_ln_nhwc<T, TO, 16>(x, weight, bias, y, mean, rstd, rows, c, eps, s);

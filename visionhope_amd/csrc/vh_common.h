@@ -59,6 +59,41 @@ template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float v) {
     return r;
 }
 
+// Eight consecutive elements as fp32 (16-byte load of 16-bit types, two of fp32);
+// the address must be 16-byte aligned.
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
+    if constexpr (sizeof(T) == 4) {
+        const float4 a = *reinterpret_cast<const float4*>(p);
+        const float4 b = *reinterpret_cast<const float4*>(p + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const uint4 u = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            v[2 * h] = to_f32(T{static_cast<uint16_t>(w[h] & 0xffffu)});
+            v[2 * h + 1] = to_f32(T{static_cast<uint16_t>(w[h] >> 16)});
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
+    if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+            w[h] = static_cast<uint32_t>(from_f32<T>(v[2 * h]).bits) |
+                   (static_cast<uint32_t>(from_f32<T>(v[2 * h + 1]).bits) << 16);
+        *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 // Element size of an io dtype code.
 inline int dtype_bytes(int t) { return t == VH_DTYPE_F32 ? 4 : 2; }
 
