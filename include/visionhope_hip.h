@@ -190,7 +190,9 @@ int vh_qnorm_forward(
  *   epilogue 2: out = x + sigmoid(aux) * (conv(x) + b)     (gated local conv)
  *   epilogue 3: out = gelu_erf(x + conv(x) + b)            (FFN dwconv + act)
  *   epilogue 4: out (fp32, in place) += conv(x) + b        (LePE into SRNL out)
- * out/aux are [B, H, W, C] in io_dtype except epilogue 4.  No counterpart in
+ *   epilogue 5: out = aux + conv(x) + b, aux fp32          (LePE + SRNL out -> io dtype)
+ * out/aux are [B, H, W, C] in io_dtype except the fp32 out of epilogue 4 and the fp32
+ * aux of epilogue 5.  No counterpart in
  * the reference's native code: it runs PyTorch Conv2d plus separate
  * elementwise ops inside VisionHOPEBlock (models/block.py:63-107,
  * models/layers.py:73-77); this fuses them on the prepared inference path. */

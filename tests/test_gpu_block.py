@@ -31,13 +31,13 @@ def _dw_reference(x, conv, epilogue, gate=None, acc=None):
         y = x + torch.sigmoid(gate.double().cpu()) * y
     elif epilogue == dwconv.EPI_ADD_GELU:
         y = F.gelu(x + y)
-    elif epilogue == dwconv.EPI_ACCUM_F32:
+    elif epilogue in (dwconv.EPI_ACCUM_F32, dwconv.EPI_ADD_F32_AUX):
         y = acc.double().cpu().permute(0, 3, 1, 2) + y
     return y
 
 
 @pytest.mark.parametrize("ksize", [3, 5, 7])
-@pytest.mark.parametrize("epilogue", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("epilogue", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
 def test_depthwise_epilogues(device, ksize, epilogue, dtype, tol):
     from visionhope_amd.utils import dwconv
@@ -55,8 +55,8 @@ def test_depthwise_epilogues(device, ksize, epilogue, dtype, tol):
     x_dev = x.to(device).contiguous(memory_format=torch.channels_last)
     gate_dev = gate.to(device).contiguous(memory_format=torch.channels_last)
     acc_dev = acc.to(device).contiguous()
-    out = dwconv.depthwise_conv(x_dev, conv, epilogue, aux=gate_dev if epilogue == 2 else None,
-                                out=acc_dev if epilogue == 4 else None)
+    aux = gate_dev if epilogue == 2 else acc_dev if epilogue == 5 else None
+    out = dwconv.depthwise_conv(x_dev, conv, epilogue, aux=aux, out=acc_dev if epilogue == 4 else None)
     expected = _dw_reference(x, conv, epilogue, gate=gate, acc=acc)
     if epilogue == dwconv.EPI_ACCUM_F32:
         assert out is acc_dev and out.dtype == torch.float32

@@ -192,3 +192,23 @@ def test_layernorm2d_cpu_matches_oracle(oracle):
     assert y.is_contiguous(memory_format=torch.channels_last)
     expected = oracle.layernorm2d(x.numpy(), ln.weight.detach().numpy(), ln.bias.detach().numpy())
     np.testing.assert_allclose(y.detach().numpy(), expected, rtol=1e-5, atol=1e-5)
+
+
+def test_parameter_caches_follow_updates():
+    from visionhope_amd.utils.cached_params import contiguous_fp32, linear_weights
+
+    p = torch.nn.Parameter(torch.randn(4, 2, 3, 3)).to(memory_format=torch.channels_last)
+    c1 = contiguous_fp32(p)
+    assert c1.is_contiguous() and torch.equal(c1, p.detach())
+    assert contiguous_fp32(p) is c1                 # cached while unchanged
+    with torch.no_grad():
+        p.mul_(2)
+    c2 = contiguous_fp32(p)
+    assert torch.equal(c2, p.detach()) and c2 is not c1
+    lin = torch.nn.Linear(3, 5)
+    w, b = linear_weights(lin, torch.bfloat16)
+    assert w.dtype == torch.bfloat16 and torch.equal(w, lin.weight.detach().bfloat16())
+    with torch.no_grad():
+        lin.bias.add_(1)
+    _, b2 = linear_weights(lin, torch.bfloat16)
+    assert torch.equal(b2, lin.bias.detach().bfloat16())

@@ -4,7 +4,8 @@
 // Reference composition (models/block.py:63-107, models/layers.py:73-77):
 //   cpe     x + dwconv3(x)                                   (block.py:102-103)
 //   local   x + sigmoid(gate) * dwconv7(x)                   (block.py:63-66)
-//   lepe    out + dwconv5(x_local)   (out: SRNL NHWC fp32)   (block.py:77-78)
+//   lepe    out + dwconv5(x_local)   (out: SRNL NHWC fp32)   (block.py:77-78),
+//           accumulated in place (fp32) or written in the io dtype for proj_out
 //   ffn     gelu(h + dwconv3(h))                             (layers.py:76-77)
 // Each thread computes 8 consecutive channels of one pixel with fp32 accumulation;
 // taps are stored taps-major ([K*K][C], fp32) so one tap is two float4 loads.
@@ -14,13 +15,13 @@
 
 namespace vh {
 
-enum DwEpilogue { DW_PLAIN = 0, DW_ADD_INPUT = 1, DW_GATE = 2, DW_ADD_GELU = 3, DW_ACCUM_F32 = 4 };
+enum DwEpilogue { DW_PLAIN = 0, DW_ADD_INPUT = 1, DW_GATE = 2, DW_ADD_GELU = 3, DW_ACCUM_F32 = 4, DW_ADD_F32_AUX = 5 };
 
 struct DwParams {
     const void* x;
     const float* taps;   // [K*K, C]
     const float* bias;   // [C] or null
-    const void* aux;     // gate for DW_GATE
+    const void* aux;     // gate for DW_GATE (io dtype); fp32 addend for DW_ADD_F32_AUX
     void* out;           // io dtype, or fp32 for DW_ACCUM_F32
     int64_t B, H, W, C;
 };
@@ -79,7 +80,12 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p) {
         store8<float>(o, acc);
         return;
     } else {
-        if constexpr (EPI != DW_PLAIN) {
+        if constexpr (EPI == DW_ADD_F32_AUX) {
+            float a[8];
+            load8<float>(static_cast<const float*>(p.aux) + at, a);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = a[j] + acc[j];
+        } else if constexpr (EPI != DW_PLAIN) {
             float xin[8];
             load8<T>(x + at, xin);
             if constexpr (EPI == DW_GATE) {
@@ -109,6 +115,7 @@ void launch_dw(int epi, const DwParams& dp, unsigned blocks, hipStream_t s) {
         case DW_GATE: hipLaunchKernelGGL((dwconv_nhwc_kernel<K, DW_GATE, T>), dim3(blocks), dim3(256), 0, s, dp); break;
         case DW_ADD_GELU: hipLaunchKernelGGL((dwconv_nhwc_kernel<K, DW_ADD_GELU, T>), dim3(blocks), dim3(256), 0, s, dp); break;
         case DW_ACCUM_F32: hipLaunchKernelGGL((dwconv_nhwc_kernel<K, DW_ACCUM_F32, T>), dim3(blocks), dim3(256), 0, s, dp); break;
+        case DW_ADD_F32_AUX: hipLaunchKernelGGL((dwconv_nhwc_kernel<K, DW_ADD_F32_AUX, T>), dim3(blocks), dim3(256), 0, s, dp); break;
     }
 }
 
@@ -125,8 +132,9 @@ extern "C" int vh_dwconv2d_nhwc_forward(const void* x, int32_t io_dtype, const f
     VH_REQUIRE(B > 0 && H > 0 && W > 0 && C > 0, VH_ERR_SHAPE, "depthwise conv expects nonempty NHWC input");
     VH_REQUIRE(C % 8 == 0, VH_ERR_SHAPE, "depthwise conv needs C %% 8 == 0, got %lld", (long long)C);
     VH_REQUIRE(ksize == 3 || ksize == 5 || ksize == 7, VH_ERR_ARG, "kernel size must be 3, 5 or 7, got %d", ksize);
-    VH_REQUIRE(epilogue >= DW_PLAIN && epilogue <= DW_ACCUM_F32, VH_ERR_ARG, "unknown epilogue %d", epilogue);
-    VH_REQUIRE(epilogue != DW_GATE || aux != nullptr, VH_ERR_ARG, "gated epilogue needs the gate tensor");
+    VH_REQUIRE(epilogue >= DW_PLAIN && epilogue <= DW_ADD_F32_AUX, VH_ERR_ARG, "unknown epilogue %d", epilogue);
+    VH_REQUIRE((epilogue != DW_GATE && epilogue != DW_ADD_F32_AUX) || aux != nullptr, VH_ERR_ARG,
+               "epilogue %d needs the aux tensor", epilogue);
     VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);
     const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
                             reinterpret_cast<uintptr_t>(taps) | reinterpret_cast<uintptr_t>(bias) |

@@ -9,25 +9,11 @@ from .droppath import DropPath
 from .layers import FeedForwardNetwork, LayerNorm2d, build_norm
 from .operator import VisionHOPEOperator
 from ..utils import dwconv
+from ..utils.cached_params import linear_weights
 from ..utils.grn import GlobalResponseNorm
 from ..utils.grn_cuda import visionhope_grn
 from ..utils.layer_norm_cuda import can_fuse_layernorm2d, visionhope_layernorm2d
 from ..utils.residual import can_fuse_residual_add, visionhope_residual_add
-
-
-def _cached_linear(module, dtype):
-    """``(weight [out, in], bias)`` of a 1x1 Conv2d or Linear in ``dtype``, cached on the
-    module and refreshed when either parameter changes."""
-    w, b = module.weight, module.bias
-    key = (dtype, w.data_ptr(), w._version, str(w.device),
-           None if b is None else (b.data_ptr(), b._version))
-    cached = getattr(module, "_vh_linear", None)
-    if cached is None or cached[0] != key:
-        weight = w.detach().reshape(w.shape[0], -1).to(dtype).contiguous()
-        bias = None if b is None else b.detach().to(dtype).contiguous()
-        object.__setattr__(module, "_vh_linear", (key, weight, bias))
-        cached = module._vh_linear
-    return cached[1], cached[2]
 
 
 def _is_pointwise(conv):
@@ -135,7 +121,7 @@ class VisionHOPEBlock(nn.Module):
         act = torch.get_autocast_dtype("cuda") if autocast else torch.float32
 
         def pointwise(t_nhwc, module):
-            weight, bias = _cached_linear(module, act)
+            weight, bias = linear_weights(module, act)
             return F.linear(t_nhwc.to(act), weight, bias)
 
         def nchw(t_nhwc):
@@ -160,7 +146,10 @@ class VisionHOPEBlock(nn.Module):
         else:
             out = self.operator._forward_fast(x_local, path)
             if self.local_position is not None:
-                dwconv.depthwise_conv(x_local, self.local_position, dwconv.EPI_ACCUM_F32, out=out)
+                # The position encoding is added to the FP32 operator output and the sum is
+                # rounded once to the compute dtype, the input dtype of proj_out.
+                out = dwconv.depthwise_conv(x_local, self.local_position, dwconv.EPI_ADD_F32_AUX,
+                                            aux=out).permute(0, 2, 3, 1)
             branch = nchw(pointwise(out, self.proj_out))
         x = self._residual_add(x, branch, self.gamma1)
         # Feed-forward branch.

@@ -2,9 +2,11 @@
 
 import torch
 from torch import nn
+from torch.nn import functional as F
 from torch.nn.init import trunc_normal_
 
 from .srnl import SRNL
+from ..utils.cached_params import linear_weights
 from ..utils.cuda import on_tensor_device
 from ..utils.direction_fusion import visionhope_postprocess_scale
 
@@ -166,7 +168,13 @@ class VisionHOPEOperator(nn.Module):
         from .srnl_core.fused import srnl_spatial_inference
 
         x_nhwc = x.permute(0, 2, 3, 1)
-        q_nhwc = self.W_q(x_nhwc)
+        if torch.is_autocast_enabled("cuda"):
+            # What autocast's linear computes, with the weight cast once instead of per call.
+            dtype = torch.get_autocast_dtype("cuda")
+            weight, bias = linear_weights(self.W_q, dtype)
+            q_nhwc = F.linear(x_nhwc.to(dtype), weight, bias)
+        else:
+            q_nhwc = self.W_q(x_nhwc)
         if self.direction_merge == "softmax":
             weights = 4.0 * torch.softmax(self.direction_logits.detach().float(), dim=0)
         else:

@@ -15,13 +15,14 @@ import torch
 
 from .chunk import srnl_consts, srnl_packed_forward
 from ...utils import hip
+from ...utils.cached_params import contiguous_fp32
 from ...utils.cuda import on_tensor_device
 
 _IO_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
 def _fp32_states(states):
-    return tuple(state.detach().contiguous().float().contiguous() for state in states)
+    return tuple(contiguous_fp32(state) for state in states)
 
 
 @on_tensor_device

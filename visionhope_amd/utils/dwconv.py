@@ -12,6 +12,7 @@ epilogue           result                                 reference expression
 ``EPI_GATE``       x + sigmoid(aux) * (conv(x) + b)       ``_local_features``
 ``EPI_ADD_GELU``   gelu(x + conv(x) + b)                  ``dwconv_act(x + dwconv(x))``
 ``EPI_ACCUM_F32``  out += conv(x) + b  (fp32 NHWC)        ``out + local_position(x)``
+``EPI_ADD_F32_AUX`` aux + conv(x) + b (aux fp32 NHWC)      ``out + local_position(x)``
 =================  =====================================  ==========================
 
 (``models/block.py:63-107``, ``models/layers.py:73-77``.)  Accumulation is FP32 with
@@ -24,7 +25,7 @@ from torch import nn
 from . import hip
 from .cuda import on_tensor_device
 
-EPI_PLAIN, EPI_ADD_INPUT, EPI_GATE, EPI_ADD_GELU, EPI_ACCUM_F32 = range(5)
+EPI_PLAIN, EPI_ADD_INPUT, EPI_GATE, EPI_ADD_GELU, EPI_ACCUM_F32, EPI_ADD_F32_AUX = range(6)
 _DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
@@ -67,7 +68,8 @@ def depthwise_conv(x, conv, epilogue=EPI_PLAIN, aux=None, out=None):
     """Run ``conv`` on the channels-last map ``x`` with a fused epilogue (module docstring).
 
     For ``EPI_ACCUM_F32`` ``out`` is a contiguous FP32 ``[B, H, W, C]`` tensor updated in
-    place; otherwise a new ``x``-dtype channels-last tensor is returned.
+    place; otherwise a new ``x``-dtype channels-last tensor is returned (for
+    ``EPI_ADD_F32_AUX``, ``aux`` is the FP32 ``[B, H, W, C]`` addend).
     """
     if not x.is_cuda or x.dtype not in _DTYPES:
         raise ValueError("depthwise_conv expects a CUDA FP32/BF16/FP16 tensor")
@@ -82,6 +84,10 @@ def depthwise_conv(x, conv, epilogue=EPI_PLAIN, aux=None, out=None):
         if aux is None or aux.shape != x.shape:
             raise ValueError("the gated epilogue needs a gate tensor shaped like x")
         aux = _channels_last(aux.to(x.dtype))
+    if epilogue == EPI_ADD_F32_AUX:
+        if (aux is None or aux.dtype != torch.float32 or tuple(aux.shape) != (batch, height, width, channels)
+                or not aux.is_contiguous() or aux.data_ptr() % 16):
+            raise ValueError("EPI_ADD_F32_AUX needs a contiguous FP32 [B, H, W, C] addend")
     if epilogue == EPI_ACCUM_F32:
         if (out is None or out.dtype != torch.float32 or tuple(out.shape) != (batch, height, width, channels)
                 or not out.is_contiguous() or out.data_ptr() % 16):
