@@ -173,6 +173,16 @@ int vh_layernorm2d_forward(
     void* y, int32_t y_dtype, float* mean, float* rstd, int64_t B, int64_t C, int64_t H, int64_t W,
     float eps, int32_t channels_last, void* stream);
 
+/* Residual add followed by LayerNorm over C, on channels-last tensors: x_sum = x + r
+ * rounded to io_dtype (written), y = LayerNorm(x_sum) computed in fp32 and stored as
+ * y_dtype.  C % 8 == 0, 16-byte aligned tensors.  No counterpart in the reference's native
+ * code: it fuses the residual add of VisionHOPEBlock.forward (models/block.py:105-106,
+ * gamma folded by prepare_for_inference) with the following norm2 call. */
+int vh_add_layernorm2d_forward(
+    const void* x, const void* r, int32_t io_dtype, const float* weight, const float* bias,
+    void* x_sum, void* y, int32_t y_dtype, int64_t B, int64_t C, int64_t H, int64_t W, float eps,
+    void* stream);
+
 /* Query normalisation + relayout: q_raw [B, R, N, heads*d] (io_dtype) ->
  * q [B, R, heads, N, d] fp32 = q_raw / max(||q_raw||, 1e-12) per head, and
  * inv_norm [B, R, heads, N].  Replaces visionhope_qnorm_forward

@@ -127,3 +127,24 @@ def test_residual_add(oracle, device):
     expected = oracle.residual_add(res.permute(0, 2, 3, 1).numpy(), branch.float().permute(0, 2, 3, 1).numpy(),
                                    gamma.numpy(), np.ones(3, np.float32))
     assert_close(out.permute(0, 2, 3, 1).cpu().numpy(), expected, 1e-6, "residual")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("channels", [64, 96, 512])
+def test_add_layernorm2d(device, dtype, channels):
+    """Residual add + LayerNorm2d in one pass: the sum equals torch's add in the same dtype
+    bit for bit; the norm matches F.layer_norm (float64) of that sum."""
+    from visionhope_amd.utils.layer_norm_cuda import can_fuse_add_layernorm2d, visionhope_add_layernorm2d
+
+    fmt = torch.channels_last
+    x = randn(2, channels, 5, 7, seed=21).to(dtype).to(device).contiguous(memory_format=fmt)
+    r = randn(2, channels, 5, 7, seed=22).to(dtype).to(device).contiguous(memory_format=fmt)
+    w = (1 + randn(channels, seed=23, scale=0.1)).to(device)
+    b = randn(channels, seed=24, scale=0.1).to(device)
+    assert can_fuse_add_layernorm2d(x, r, w, b)
+    s, y = visionhope_add_layernorm2d(x, r, w, b, 1e-6, out_dtype=torch.float32)
+    assert torch.equal(s, x + r)
+    assert y.is_contiguous(memory_format=fmt)
+    expected = torch.nn.functional.layer_norm(s.double().cpu().permute(0, 2, 3, 1), (channels,), w.double().cpu(),
+                                              b.double().cpu(), 1e-6).permute(0, 3, 1, 2)
+    assert_close(y.cpu().numpy(), expected.numpy(), 1e-5, "add+LN")

@@ -154,8 +154,18 @@ __global__ __launch_bounds__(256) void grn_finalize_kernel(const float* __restri
     const int64_t b = blockIdx.x;
     float local = 0.f;
     for (int64_t c = threadIdx.x; c < C; c += 256) {
-        float acc = 0.f;
-        for (int64_t s = 0; s < nslab; ++s) acc += partial[(b * nslab + s) * C + c];
+        // Four independent partial sums keep four loads in flight.
+        const float* pc = partial + b * nslab * C + c;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        int64_t s = 0;
+        for (; s + 4 <= nslab; s += 4) {
+            a0 += pc[s * C];
+            a1 += pc[(s + 1) * C];
+            a2 += pc[(s + 2) * C];
+            a3 += pc[(s + 3) * C];
+        }
+        for (; s < nslab; ++s) a0 += pc[s * C];
+        const float acc = (a0 + a1) + (a2 + a3);
         const float g = sqrtf(acc);
         gx[b * C + c] = g;
         local += g;
@@ -303,12 +313,16 @@ __global__ __launch_bounds__(256) void layernorm_nhwc_kernel(const T* __restrict
 
 // Channels-last, C % 8 == 0: LPR = 2^lpr_log2 lanes per pixel row, each lane GP groups
 // of 8 channels (group k*LPR + lane), 16-byte loads and stores.
-template <typename T, typename TO, int GP>
+// ADD: the normalised row is x + r rounded to T (a residual add), which is also stored
+// to x_sum, so the sum is read once instead of being written by one kernel and read by
+// the next.
+template <typename T, typename TO, int GP, bool ADD = false>
 __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                              const float* __restrict__ bias, TO* __restrict__ y,
                                                              float* __restrict__ mean_out,
                                                              float* __restrict__ rstd_out, int64_t rows, int C,
-                                                             int lpr_log2, float eps) {
+                                                             int lpr_log2, float eps, const T* __restrict__ r = nullptr,
+                                                             T* __restrict__ x_sum = nullptr) {
     const int LPR = 1 << lpr_log2;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 >> lpr_log2) + (threadIdx.x >> lpr_log2);
     const int lane = threadIdx.x & (LPR - 1);
@@ -319,6 +333,13 @@ __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restric
 #pragma unroll
     for (int k = 0; k < GP; ++k) {
         load8<T>(xr + (k * LPR + lane) * 8, v[k]);
+        if constexpr (ADD) {
+            float rv[8];
+            load8<T>(r + (active ? row : 0) * C + (k * LPR + lane) * 8, rv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[k][j] = to_f32(from_f32<T>(v[k][j] + rv[j]));
+            if (active) store8<T>(x_sum + row * C + (k * LPR + lane) * 8, v[k]);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) sum += v[k][j];
     }
@@ -483,6 +504,34 @@ bool launch_ln_nhwc8(const void* x, const float* w, const float* b, void* yv, fl
     return false;
 }
 
+template <typename T, typename TO>
+bool launch_add_ln_nhwc8(const void* x, const void* r, const float* w, const float* b, void* x_sum, void* yv,
+                         int64_t rows, int C, float eps, hipStream_t s) {
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(r) |
+                            reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b) |
+                            reinterpret_cast<uintptr_t>(x_sum) | reinterpret_cast<uintptr_t>(yv);
+    if (C % 8 != 0 || align % 16 != 0) return false;
+    const int ng = C / 8;
+    int lg = 0;
+    while (lg < 5 && ng % (2 << lg) == 0) ++lg;
+    const int gp = ng >> lg;
+    const unsigned blocks = static_cast<unsigned>((rows + (256 >> lg) - 1) / (256 >> lg));
+    const T* xp = static_cast<const T*>(x);
+    const T* rp = static_cast<const T*>(r);
+    T* sp = static_cast<T*>(x_sum);
+    TO* y = static_cast<TO*>(yv);
+    switch (gp) {
+#define VH_ALN8(G)                                                                                      \
+    case G:                                                                                             \
+        hipLaunchKernelGGL((layernorm_nhwc8_kernel<T, TO, G, true>), dim3(blocks), dim3(256), 0, s, xp, w, \
+                           b, y, nullptr, nullptr, rows, C, lg, eps, rp, sp);                           \
+        return true;
+        VH_ALN8(1) VH_ALN8(2) VH_ALN8(3) VH_ALN8(4) VH_ALN8(5) VH_ALN8(6) VH_ALN8(7) VH_ALN8(8)
+#undef VH_ALN8
+    }
+    return false;
+}
+
 template <typename T, typename TO, int TPR>
 void launch_ln_nhwc(const void* x, const float* w, const float* b, void* yv, float* mean,
                     float* rstd, int64_t rows, int C, float eps, hipStream_t s) {
@@ -637,6 +686,33 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
     });
     if (rc) return rc;
     return check_launch("grn kernels");
+}
+
+int vh_add_layernorm2d_forward(const void* x, const void* r, int32_t io_dtype, const float* weight,
+                               const float* bias, void* x_sum, void* y, int32_t y_dtype, int64_t B, int64_t C,
+                               int64_t H, int64_t W, float eps, void* stream) {
+    VH_REQUIRE(x && r && weight && bias && x_sum && y, VH_ERR_ARG, "add + LayerNorm2d pointers must not be null");
+    VH_REQUIRE(B > 0 && C > 0 && H > 0 && W > 0, VH_ERR_SHAPE, "add + LayerNorm2d expects nonempty input");
+    VH_REQUIRE(valid_dtype(io_dtype) && valid_dtype(y_dtype), VH_ERR_DTYPE, "unsupported dtype code");
+    VH_REQUIRE(C % 8 == 0 && C <= 64 * 64, VH_ERR_SHAPE, "add + LayerNorm2d needs C %% 8 == 0 and C <= 4096");
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(r) |
+                            reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
+                            reinterpret_cast<uintptr_t>(x_sum) | reinterpret_cast<uintptr_t>(y);
+    VH_REQUIRE(align % 16 == 0, VH_ERR_ARG, "add + LayerNorm2d tensors must be 16-byte aligned");
+    const int64_t ng = C / 8;
+    int64_t lg = 0;
+    while (lg < 5 && ng % (int64_t(2) << lg) == 0) ++lg;
+    VH_REQUIRE((ng >> lg) <= 8, VH_ERR_SHAPE, "add + LayerNorm2d: unsupported channel count %lld", (long long)C);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t rows = B * H * W;
+    int rc = dispatch_t(io_dtype, [&](auto tv) {
+        dispatch_t(y_dtype, [&](auto ov) {
+            launch_add_ln_nhwc8<decltype(tv), decltype(ov)>(x, r, weight, bias, x_sum, y, rows, static_cast<int>(C),
+                                                            eps, s);
+        });
+    });
+    if (rc) return rc;
+    return check_launch("add + layernorm2d kernel");
 }
 
 int vh_layernorm2d_forward(const void* x, int32_t io_dtype, const float* weight, const float* bias,

@@ -12,7 +12,8 @@ from ..utils import dwconv
 from ..utils.cached_params import linear_weights
 from ..utils.grn import GlobalResponseNorm
 from ..utils.grn_cuda import visionhope_grn
-from ..utils.layer_norm_cuda import can_fuse_layernorm2d, visionhope_layernorm2d
+from ..utils.layer_norm_cuda import (can_fuse_add_layernorm2d, can_fuse_layernorm2d, visionhope_add_layernorm2d,
+                                     visionhope_layernorm2d)
 from ..utils.residual import can_fuse_residual_add, visionhope_residual_add
 
 
@@ -151,11 +152,15 @@ class VisionHOPEBlock(nn.Module):
                 out = dwconv.depthwise_conv(x_local, self.local_position, dwconv.EPI_ADD_F32_AUX,
                                             aux=out).permute(0, 2, 3, 1)
             branch = nchw(pointwise(out, self.proj_out))
-        x = self._residual_add(x, branch, self.gamma1)
-        # Feed-forward branch.
+        # Feed-forward branch (the residual add fused into norm2 when LayerScale is folded).
         ffn = self.ffn
-        h = visionhope_layernorm2d(x, self.norm2.weight, self.norm2.bias, self.norm2.eps,
-                                   force_channels_last=True, out_dtype=act)
+        if self.gamma1 is None and can_fuse_add_layernorm2d(x, branch, self.norm2.weight, self.norm2.bias):
+            x, h = visionhope_add_layernorm2d(x, branch, self.norm2.weight, self.norm2.bias, self.norm2.eps,
+                                              out_dtype=act)
+        else:
+            x = self._residual_add(x, branch, self.gamma1)
+            h = visionhope_layernorm2d(x, self.norm2.weight, self.norm2.bias, self.norm2.eps,
+                                       force_channels_last=True, out_dtype=act)
         f = F.gelu(pointwise(h.permute(0, 2, 3, 1), ffn.fc1))
         if ffn.use_dwconv:
             f = dwconv.depthwise_conv(nchw(f), ffn.dwconv, dwconv.EPI_ADD_GELU).permute(0, 2, 3, 1)

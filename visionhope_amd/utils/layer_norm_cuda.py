@@ -60,3 +60,42 @@ def visionhope_layernorm2d(x, weight, bias, eps, force_channels_last=False, out_
     """FP32 output (the reference's contract); ``out_dtype`` stores the same values rounded
     to a 16-bit type when the consumer casts them anyway (autocast)."""
     return _VisionHOPELayerNorm2dFunction.apply(x, weight, bias, eps, force_channels_last, out_dtype)
+
+
+def can_fuse_add_layernorm2d(x, r, weight, bias):
+    """x + r followed by LayerNorm2d in one pass: channels-last CUDA tensors of one dtype,
+    C % 8 == 0 with at most 8 groups of 8 channels per lane, 16-byte aligned."""
+    if x.ndim != 4 or not x.is_cuda or r.shape != x.shape or r.dtype != x.dtype:
+        return False
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return False
+    fmt = torch.channels_last
+    if not (x.is_contiguous(memory_format=fmt) and r.is_contiguous(memory_format=fmt)):
+        return False
+    channels = x.shape[1]
+    if channels % 8 or channels > 4096:
+        return False
+    groups, lanes = channels // 8, 1
+    while lanes < 32 and groups % (2 * lanes) == 0:   # lanes per pixel row, as the kernel picks
+        lanes *= 2
+    if groups // lanes > 8:
+        return False
+    tensors = (x, r, weight, bias)
+    return (all(t.data_ptr() % 16 == 0 for t in tensors) and weight.dtype == torch.float32
+            and bias.dtype == torch.float32 and weight.is_contiguous() and bias.is_contiguous()
+            and weight.numel() == channels and bias.numel() == channels)
+
+
+@on_tensor_device
+def visionhope_add_layernorm2d(x, r, weight, bias, eps, out_dtype=torch.float32):
+    """``s = x + r`` (rounded to x's dtype) and ``LayerNorm2d(s)`` in one pass on
+    channels-last maps; returns ``(s, y)`` with y stored as ``out_dtype``."""
+    batch, channels, height, width = x.shape
+    x_sum = torch.empty_like(x, memory_format=torch.channels_last)
+    y = torch.empty_like(x, dtype=out_dtype, memory_format=torch.channels_last)
+    lib = hip.load_library()
+    hip.check(lib.vh_add_layernorm2d_forward(
+        hip.ptr(x), hip.ptr(r), hip.dtype_code(x.dtype), hip.ptr(weight), hip.ptr(bias), hip.ptr(x_sum),
+        hip.ptr(y), hip.dtype_code(out_dtype), batch, channels, height, width, float(eps), hip.stream_of(x)),
+        "vh_add_layernorm2d_forward")
+    return x_sum, y
