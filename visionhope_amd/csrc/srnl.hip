@@ -74,6 +74,7 @@ struct ScanParams {
     int per_line_state;  // 1: memories hold one state per line (chunk.cu:287, StateCount == N)
     int x_vec;           // input rows are aligned for vector loads
     int lines_per_wave;  // head_dim 16: lines packed into one wave (1, 2 or 4)
+    int aligned;         // spatial input with chunks (W, W, H, H): chunk c of scan r is a row/column
     Consts k;
 };
 
@@ -526,7 +527,21 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
             const int64_t tok = cc * C + base + slot;
             const bool ok = slot < cnt && tok < p.L;
             valid |= ok ? (1u << tc) : 0u;
-            const T* src = xcol[tc] + (ok ? token_offset<SPATIAL>(p.x, r, tok) : 0);
+            int64_t off;
+            if (SPATIAL && p.aligned) {
+                // Row/column chunks: token i of chunk cc is pixel (cc, i) of scans 0/1 and
+                // (i, cc) of scans 2/3, mirrored for the reverse scans; no division.
+                const int64_t i = base + slot;
+                const int64_t W = p.x.W, H = p.x.H;
+                const int64_t pix = r == 0 ? cc * W + i
+                                  : r == 1 ? (H - 1 - cc) * W + (W - 1 - i)
+                                  : r == 2 ? i * W + cc
+                                           : (H - 1 - i) * W + (W - 1 - cc);
+                off = pix * p.x.st;
+            } else {
+                off = token_offset<SPATIAL>(p.x, r, tok);
+            }
+            const T* src = xcol[tc] + (ok ? off : 0);
             if (p.x_vec) {
                 raw[tc] = *reinterpret_cast<const Raw*>(src);
             } else if constexpr (sizeof(T) == 4) {
@@ -576,63 +591,75 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
             decode_tile(xr_next, valid_next, xo);
             // ---- projections on MFMA, norms per token; then each lane computes the
             //      gates of its own slot ----
-            float tok_ksq = 0.f, tok_dsq = 0.f, tok_ep = 0.f, tok_ap = 0.f;
+            // All four column tiles at once (no control flow between them), so their
+            // MFMA chains and reductions overlap instead of running back to back.  A
+            // column tile without tokens sees x = 0 and yields zero keys and differences.
+            float ak[TPL == 4 ? 1 : 4][4], av[TPL == 4 ? 1 : 4][4], ev[TPL == 4 ? 1 : 4][4], aa[TPL == 4 ? 1 : 4][4];
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
-                const int t = 16 * tc + i16;
-                if ((tc % TPL) * 16 >= cnt) {
-                    // No tokens in this column tile (uniform): zero keys and differences,
-                    // so the identity slots of the last block read finite values.
-                    *reinterpret_cast<float4*>(kk + t * D + 4 * q) = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) dkT[(4 * q + j) * DKS + t] = 0.f;
-                    continue;
-                }
-                const float* Sl = St + (tc / TPL) * SR;
+            for (int u = 0; u < (TPL == 4 ? 1 : 4); ++u) {
+                const float* Sl = St + (u / TPL) * SR;
                 const float4 k4 = *reinterpret_cast<const float4*>(Sl + (2 * D + i16) * D + 4 * q);
                 const float4 v4 = *reinterpret_cast<const float4*>(Sl + (D + i16) * D + 4 * q);
                 const float4 e4 = *reinterpret_cast<const float4*>(Sl + 3 * D * D + 4 * q);
                 const float4 a4 = *reinterpret_cast<const float4*>(Sl + (3 * D + 1) * D + 4 * q);
-                const float ak[4] = {k4.x, k4.y, k4.z, k4.w}, av[4] = {v4.x, v4.y, v4.z, v4.w};
-                const float ev[4] = {e4.x, e4.y, e4.z, e4.w}, aa[4] = {a4.x, a4.y, a4.z, a4.w};
-                v4f kacc = {0.f, 0.f, 0.f, 0.f}, vacc = {0.f, 0.f, 0.f, 0.f};
+                ak[u][0] = k4.x; ak[u][1] = k4.y; ak[u][2] = k4.z; ak[u][3] = k4.w;
+                av[u][0] = v4.x; av[u][1] = v4.y; av[u][2] = v4.z; av[u][3] = v4.w;
+                ev[u][0] = e4.x; ev[u][1] = e4.y; ev[u][2] = e4.z; ev[u][3] = e4.w;
+                aa[u][0] = a4.x; aa[u][1] = a4.y; aa[u][2] = a4.z; aa[u][3] = a4.w;
+            }
+            v4f kacc[4], vacc[4];
+            float pe[4], pa[4];
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) {
+                const int u = TPL == 4 ? 0 : tc;
+                kacc[tc] = v4f{0.f, 0.f, 0.f, 0.f};
+                vacc[tc] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    kacc = mfma4(ak[st], xo[tc][st], kacc);
-                    vacc = mfma4(av[st], xo[tc][st], vacc);
+                    kacc[tc] = mfma4(ak[u][st], xo[tc][st], kacc[tc]);
+                    vacc[tc] = mfma4(av[u][st], xo[tc][st], vacc[tc]);
                 }
-                float pe = 0.f, pa = 0.f;
+                pe[tc] = ev[u][0] * xo[tc][0] + ev[u][1] * xo[tc][1] + ev[u][2] * xo[tc][2] + ev[u][3] * xo[tc][3];
+                pa[tc] = aa[u][0] * xo[tc][0] + aa[u][1] * xo[tc][1] + aa[u][2] * xo[tc][2] + aa[u][3] * xo[tc][3];
+            }
+            float kn[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    pe += ev[j] * xo[tc][j];
-                    pa += aa[j] * xo[tc][j];
-                }
-                float kn = kacc[0] * kacc[0] + kacc[1] * kacc[1] + kacc[2] * kacc[2] + kacc[3] * kacc[3];
-                kn = xor16_32_sum(kn);
-                const float inv = rsqrtf(kn + 1e-6f);
+            for (int tc = 0; tc < 4; ++tc) {
+                kn[tc] = kacc[tc][0] * kacc[tc][0] + kacc[tc][1] * kacc[tc][1] + kacc[tc][2] * kacc[tc][2] +
+                         kacc[tc][3] * kacc[tc][3];
+                kn[tc] = xor16_32_sum(kn[tc]);
+                pe[tc] = xor16_32_sum(pe[tc]);
+                pa[tc] = xor16_32_sum(pa[tc]);
+            }
+            float dsq[4], ksq[4];
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) {
+                const float inv = rsqrtf(kn[tc] + 1e-6f);
                 float kv[4], df[4];
-                float dsq = 0.f, ksq = 0.f;
+                dsq[tc] = 0.f;
+                ksq[tc] = 0.f;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    kv[j] = kacc[j] * inv;
-                    df[j] = kv[j] - vacc[j];
-                    dsq += df[j] * df[j];
-                    ksq += kv[j] * kv[j];
+                    kv[j] = kacc[tc][j] * inv;
+                    df[j] = kv[j] - vacc[tc][j];
+                    dsq[tc] += df[j] * df[j];
+                    ksq[tc] += kv[j] * kv[j];
                 }
-                dsq = xor16_32_sum(dsq);
-                ksq = xor16_32_sum(ksq);
-                pe = xor16_32_sum(pe);
-                pa = xor16_32_sum(pa);
-                if (q == tc) {
-                    tok_ksq = ksq;
-                    tok_dsq = dsq;
-                    tok_ep = pe;
-                    tok_ap = pa;
-                }
+                const int t = 16 * tc + i16;
                 *reinterpret_cast<float4*>(kk + t * D + 4 * q) = make_float4(kv[0], kv[1], kv[2], kv[3]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) dkT[(4 * q + j) * DKS + t] = df[j];
             }
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) {
+                dsq[tc] = xor16_32_sum(dsq[tc]);
+                ksq[tc] = xor16_32_sum(ksq[tc]);
+            }
+            // Lane 16 tc + i16 owns the token of column i16 of tile tc.
+            const float tok_ksq = q == 0 ? ksq[0] : q == 1 ? ksq[1] : q == 2 ? ksq[2] : ksq[3];
+            const float tok_dsq = q == 0 ? dsq[0] : q == 1 ? dsq[1] : q == 2 ? dsq[2] : dsq[3];
+            const float tok_ep = q == 0 ? pe[0] : q == 1 ? pe[1] : q == 2 ? pe[2] : pe[3];
+            const float tok_ap = q == 0 ? pa[0] : q == 1 ? pa[1] : q == 2 ? pa[2] : pa[3];
             float my_alpha, my_eff;
             {
                 const float ep = fminf(10.f, fmaxf(-10.f, tok_ep));
@@ -1180,6 +1207,8 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
     }
     sp.k = make_consts(consts);
     sp.lines_per_wave = scan16_lines_per_wave(lines, heads);
+    sp.aligned = x.spatial && R == 4 && chunks[0] == x.W && chunks[1] == x.W && chunks[2] == x.H &&
+                 chunks[3] == x.H;
     rc = dispatch_d(d, [&](auto dc) {
         constexpr int D = decltype(dc)::value;
         dispatch_t(io_dtype, [&](auto tv) { launch_scan<D, decltype(tv)>(sp, stream); });
