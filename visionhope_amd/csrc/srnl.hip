@@ -27,6 +27,7 @@
 //     case one thread per output in the reference's summation order.
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 #include "vh_common.h"
 
@@ -416,6 +417,38 @@ __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// bf16 matrix cores for bf16 activations.  v_mfma_f32_16x16x16_bf16 takes from lane l
+// the 4 consecutive k values 4(l/16)..4(l/16)+3 of A row l%16 and of B column l%16 (the
+// same operands one lane gives the four 16x16x4 fp32 steps above) and accumulates in
+// fp32.  An fp32 operand v enters as hi + lo, hi = bf16(v), lo = bf16(v - hi), which
+// leaves |v - hi - lo| <= 2^-16 |v|; bf16 activations enter exactly.
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4f mfma_bf16(v4s a, v4s b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+typedef float v4fl __attribute__((ext_vector_type(4)));
+
+// Hardware round-to-nearest-even conversions (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ void split_bf16(const float (&v)[4], v4s& hi, v4s& lo) {
+    const v4fl f = {v[0], v[1], v[2], v[3]};
+    const v4bf h = __builtin_convertvector(f, v4bf);
+    const v4bf l = __builtin_convertvector(f - __builtin_convertvector(h, v4fl), v4bf);
+    hi = __builtin_bit_cast(v4s, h);
+    lo = __builtin_bit_cast(v4s, l);
+}
+
+__device__ __forceinline__ v4s bf16x4_bits(uint2 r) {
+    v4s s;
+    s[0] = static_cast<short>(r.x & 0xffffu);
+    s[1] = static_cast<short>(r.x >> 16);
+    s[2] = static_cast<short>(r.y & 0xffffu);
+    s[3] = static_cast<short>(r.y >> 16);
+    return s;
+}
+
 // Four consecutive elements of a row as fp32 (8- or 16-byte load when `vec`).
 template <typename T>
 __device__ __forceinline__ void load4(const T* p, bool vec, float (&out)[4]) {
@@ -609,15 +642,33 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
             }
             v4f kacc[4], vacc[4];
             float pe[4], pa[4];
+            constexpr int NU = TPL == 4 ? 1 : 4;
+            [[maybe_unused]] v4s akh[NU], akl[NU], avh[NU], avl[NU];
+            if constexpr (std::is_same<T, bf16_t>::value) {
+#pragma unroll
+                for (int u = 0; u < NU; ++u) {
+                    split_bf16(ak[u], akh[u], akl[u]);
+                    split_bf16(av[u], avh[u], avl[u]);
+                }
+            }
 #pragma unroll
             for (int tc = 0; tc < 4; ++tc) {
                 const int u = TPL == 4 ? 0 : tc;
                 kacc[tc] = v4f{0.f, 0.f, 0.f, 0.f};
                 vacc[tc] = v4f{0.f, 0.f, 0.f, 0.f};
+                if constexpr (std::is_same<T, bf16_t>::value) {
+                    // x is bf16 (exact); M_k, M_v enter as hi + lo.  xr_next still holds this tile.
+                    const v4s xs = ((valid_next >> tc) & 1u) ? bf16x4_bits(xr_next[tc]) : v4s{0, 0, 0, 0};
+                    kacc[tc] = mfma_bf16(akh[u], xs, kacc[tc]);
+                    vacc[tc] = mfma_bf16(avh[u], xs, vacc[tc]);
+                    kacc[tc] = mfma_bf16(akl[u], xs, kacc[tc]);
+                    vacc[tc] = mfma_bf16(avl[u], xs, vacc[tc]);
+                } else {
 #pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    kacc[tc] = mfma4(ak[u][st], xo[tc][st], kacc[tc]);
-                    vacc[tc] = mfma4(av[u][st], xo[tc][st], vacc[tc]);
+                    for (int st = 0; st < 4; ++st) {
+                        kacc[tc] = mfma4(ak[u][st], xo[tc][st], kacc[tc]);
+                        vacc[tc] = mfma4(av[u][st], xo[tc][st], vacc[tc]);
+                    }
                 }
                 pe[tc] = ev[u][0] * xo[tc][0] + ev[u][1] * xo[tc][1] + ev[u][2] * xo[tc][2] + ev[u][3] * xo[tc][3];
                 pa[tc] = aa[u][0] * xo[tc][0] + aa[u][1] * xo[tc][1] + aa[u][2] * xo[tc][2] + aa[u][3] * xo[tc][3];
@@ -967,8 +1018,15 @@ __global__ __launch_bounds__(64) void srnl_readout16_kernel(const FuseParams p, 
         if (w >= W) break;
         const int64_t h = h0 + n;
         float qv[4] = {0.f, 0.f, 0.f, 0.f}, xv[4] = {0.f, 0.f, 0.f, 0.f};
+        uint2 qraw = make_uint2(0u, 0u);
         if (h < H) {
-            load4(qb + (h * W + w) * C, true, qv);
+            if constexpr (std::is_same<T, bf16_t>::value) {
+                qraw = *reinterpret_cast<const uint2*>(qb + (h * W + w) * C);
+                qv[0] = __uint_as_float(qraw.x << 16); qv[1] = __uint_as_float(qraw.x & 0xffff0000u);
+                qv[2] = __uint_as_float(qraw.y << 16); qv[3] = __uint_as_float(qraw.y & 0xffff0000u);
+            } else {
+                load4(qb + (h * W + w) * C, true, qv);
+            }
             load4(xb + (h * W + w) * C, true, xv);
         }
         const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] +
@@ -976,10 +1034,20 @@ __global__ __launch_bounds__(64) void srnl_readout16_kernel(const FuseParams p, 
         const float4 m2 = *reinterpret_cast<const float4*>(st[2] + w * (D * D));
         const float4 m3 = *reinterpret_cast<const float4*>(st[3] + (W - 1 - w) * (D * D));
         v4f y2 = {0.f, 0.f, 0.f, 0.f}, y3 = {0.f, 0.f, 0.f, 0.f};
-        y2 = mfma4(m2.x, qv[0], y2); y3 = mfma4(m3.x, qv[0], y3);
-        y2 = mfma4(m2.y, qv[1], y2); y3 = mfma4(m3.y, qv[1], y3);
-        y2 = mfma4(m2.z, qv[2], y2); y3 = mfma4(m3.z, qv[2], y3);
-        y2 = mfma4(m2.w, qv[3], y2); y3 = mfma4(m3.w, qv[3], y3);
+        if constexpr (std::is_same<T, bf16_t>::value) {
+            const v4s qs = bf16x4_bits(qraw);
+            const float a2[4] = {m2.x, m2.y, m2.z, m2.w}, a3[4] = {m3.x, m3.y, m3.z, m3.w};
+            v4s h2, l2, h3, l3;
+            split_bf16(a2, h2, l2);
+            split_bf16(a3, h3, l3);
+            y2 = mfma_bf16(h2, qs, y2); y3 = mfma_bf16(h3, qs, y3);
+            y2 = mfma_bf16(l2, qs, y2); y3 = mfma_bf16(l3, qs, y3);
+        } else {
+            y2 = mfma4(m2.x, qv[0], y2); y3 = mfma4(m3.x, qv[0], y3);
+            y2 = mfma4(m2.y, qv[1], y2); y3 = mfma4(m3.y, qv[1], y3);
+            y2 = mfma4(m2.z, qv[2], y2); y3 = mfma4(m3.z, qv[2], y3);
+            y2 = mfma4(m2.w, qv[3], y2); y3 = mfma4(m3.w, qv[3], y3);
+        }
         float* rec = col + (ww * 16 + n) * REC + 4 * g;
         float c23[4];
 #pragma unroll
@@ -997,8 +1065,15 @@ __global__ __launch_bounds__(64) void srnl_readout16_kernel(const FuseParams p, 
         const int64_t h = h0 + hh;
         if (h >= H) break;
         float qv[4] = {0.f, 0.f, 0.f, 0.f}, xv[4] = {0.f, 0.f, 0.f, 0.f};
+        uint2 qraw = make_uint2(0u, 0u);
         if (wvalid) {
-            load4(qb + (h * W + w) * C, true, qv);
+            if constexpr (std::is_same<T, bf16_t>::value) {
+                qraw = *reinterpret_cast<const uint2*>(qb + (h * W + w) * C);
+                qv[0] = __uint_as_float(qraw.x << 16); qv[1] = __uint_as_float(qraw.x & 0xffff0000u);
+                qv[2] = __uint_as_float(qraw.y << 16); qv[3] = __uint_as_float(qraw.y & 0xffff0000u);
+            } else {
+                load4(qb + (h * W + w) * C, true, qv);
+            }
             load4(xb + (h * W + w) * C, true, xv);
         }
         const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] +
@@ -1006,10 +1081,20 @@ __global__ __launch_bounds__(64) void srnl_readout16_kernel(const FuseParams p, 
         const float4 m0 = *reinterpret_cast<const float4*>(st[0] + h * (D * D));
         const float4 m1 = *reinterpret_cast<const float4*>(st[1] + (H - 1 - h) * (D * D));
         v4f y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
-        y0 = mfma4(m0.x, qv[0], y0); y1 = mfma4(m1.x, qv[0], y1);
-        y0 = mfma4(m0.y, qv[1], y0); y1 = mfma4(m1.y, qv[1], y1);
-        y0 = mfma4(m0.z, qv[2], y0); y1 = mfma4(m1.z, qv[2], y1);
-        y0 = mfma4(m0.w, qv[3], y0); y1 = mfma4(m1.w, qv[3], y1);
+        if constexpr (std::is_same<T, bf16_t>::value) {
+            const v4s qs = bf16x4_bits(qraw);
+            const float a0[4] = {m0.x, m0.y, m0.z, m0.w}, a1[4] = {m1.x, m1.y, m1.z, m1.w};
+            v4s h0, l0, h1, l1;
+            split_bf16(a0, h0, l0);
+            split_bf16(a1, h1, l1);
+            y0 = mfma_bf16(h0, qs, y0); y1 = mfma_bf16(h1, qs, y1);
+            y0 = mfma_bf16(l0, qs, y0); y1 = mfma_bf16(l1, qs, y1);
+        } else {
+            y0 = mfma4(m0.x, qv[0], y0); y1 = mfma4(m1.x, qv[0], y1);
+            y0 = mfma4(m0.y, qv[1], y0); y1 = mfma4(m1.y, qv[1], y1);
+            y0 = mfma4(m0.z, qv[2], y0); y1 = mfma4(m1.z, qv[2], y1);
+            y0 = mfma4(m0.w, qv[3], y0); y1 = mfma4(m1.w, qv[3], y1);
+        }
         const float4 c23 = *reinterpret_cast<const float4*>(col + (n * 16 + hh) * REC + 4 * g);
         const float c23v[4] = {c23.x, c23.y, c23.z, c23.w};
         float o[4];
