@@ -152,11 +152,13 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 // Butterfly steps inside a quad of lanes, on the VALU (DPP quad_perm).
+// Quad permutes read only lanes of the same quad, so bound_ctrl never applies; setting
+// it lets the compiler fold the move into the consuming add (v_add_f32_dpp).
 __device__ __forceinline__ float quad_swap1(float v) {  // lanes (1,0,3,2)
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float quad_swap2(float v) {  // lanes (2,3,0,1)
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
 }
 
 template <int D, typename T>
@@ -471,7 +473,7 @@ __device__ __forceinline__ void load4(const T* p, bool vec, float (&out)[4]) {
 
 template <int CTRL>
 __device__ __forceinline__ float quad_perm(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
 __device__ __forceinline__ float readlane_f(float v, int lane) {
@@ -552,37 +554,52 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
     Raw xr_next[4];
     unsigned valid_next = 0;
     bool have_next = false;
+    // Row/column chunks (the spatial operator): token i of chunk cc of scan r is pixel
+    // pa*cc + pb*i + pc, an affine map with per-scan constants (no division, no branch).
+    // 32-bit: the host enables row/column addressing only when H*W*pixel_stride < 2^31.
+    int pa = 0, pb = 0, pc = 0, pst = 0;
+    if constexpr (SPATIAL) {
+        const int W = static_cast<int>(p.x.W), L = static_cast<int>(p.x.H * p.x.W);
+        pa = r == 0 ? W : r == 1 ? -W : r == 2 ? 1 : -1;
+        pb = r == 0 ? 1 : r == 1 ? -1 : r == 2 ? W : -W;
+        pc = (r & 1) ? L - 1 : 0;
+        pst = static_cast<int>(p.x.st);
+    }
     auto issue_tile = [&](int64_t cc, int base, int cnt, Raw (&raw)[4], unsigned& valid) {
         valid = 0;
+        int64_t offs[4];
+        if (SPATIAL && p.aligned) {
 #pragma unroll
-        for (int tc = 0; tc < 4; ++tc) {
-            const int slot = (tc % TPL) * 16 + i16;
-            const int64_t tok = cc * C + base + slot;
-            const bool ok = slot < cnt && tok < p.L;
-            valid |= ok ? (1u << tc) : 0u;
-            int64_t off;
-            if (SPATIAL && p.aligned) {
-                // Row/column chunks: token i of chunk cc is pixel (cc, i) of scans 0/1 and
-                // (i, cc) of scans 2/3, mirrored for the reverse scans; no division.
-                const int64_t i = base + slot;
-                const int64_t W = p.x.W, H = p.x.H;
-                const int64_t pix = r == 0 ? cc * W + i
-                                  : r == 1 ? (H - 1 - cc) * W + (W - 1 - i)
-                                  : r == 2 ? i * W + cc
-                                           : (H - 1 - i) * W + (W - 1 - cc);
-                off = pix * p.x.st;
-            } else {
-                off = token_offset<SPATIAL>(p.x, r, tok);
+            for (int tc = 0; tc < 4; ++tc) {
+                const int slot = (tc % TPL) * 16 + i16;
+                const bool ok = slot < cnt && cc * C + base + slot < p.L;
+                valid |= ok ? (1u << tc) : 0u;
+                offs[tc] = ok ? (pa * static_cast<int>(cc) + pb * (base + slot) + pc) * pst : 0;
             }
-            const T* src = xcol[tc] + (ok ? off : 0);
-            if (p.x_vec) {
-                raw[tc] = *reinterpret_cast<const Raw*>(src);
-            } else if constexpr (sizeof(T) == 4) {
-                raw[tc] = make_uint4(__float_as_uint(src[0]), __float_as_uint(src[1]), __float_as_uint(src[2]),
-                                     __float_as_uint(src[3]));
-            } else {
-                raw[tc] = make_uint2(static_cast<uint32_t>(src[0].bits) | (static_cast<uint32_t>(src[1].bits) << 16),
-                                     static_cast<uint32_t>(src[2].bits) | (static_cast<uint32_t>(src[3].bits) << 16));
+        } else {
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) {
+                const int slot = (tc % TPL) * 16 + i16;
+                const int64_t tok = cc * C + base + slot;
+                const bool ok = slot < cnt && tok < p.L;
+                valid |= ok ? (1u << tc) : 0u;
+                offs[tc] = ok ? token_offset<SPATIAL>(p.x, r, tok) : 0;   // invalid: the line's first token
+            }
+        }
+        if (p.x_vec) {
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) raw[tc] = *reinterpret_cast<const Raw*>(xcol[tc] + offs[tc]);
+        } else {
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) {
+                const T* src = xcol[tc] + offs[tc];
+                if constexpr (sizeof(T) == 4) {
+                    raw[tc] = make_uint4(__float_as_uint(src[0]), __float_as_uint(src[1]), __float_as_uint(src[2]),
+                                         __float_as_uint(src[3]));
+                } else {
+                    raw[tc] = make_uint2(static_cast<uint32_t>(src[0].bits) | (static_cast<uint32_t>(src[1].bits) << 16),
+                                         static_cast<uint32_t>(src[2].bits) | (static_cast<uint32_t>(src[3].bits) << 16));
+                }
             }
         }
     };
@@ -812,14 +829,21 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 float pdot[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    float d0 = g[0] * o.kv[u][0];
-                    float d1 = g[1] * o.kv[u][1];
+                    float d;
+                    if constexpr (E <= 4) {
+                        d = g[0] * o.kv[u][0];
 #pragma unroll
-                    for (int e = 2; e < E; e += 2) {
-                        d0 += g[e] * o.kv[u][e];
-                        d1 += g[e + 1] * o.kv[u][e + 1];
+                        for (int e = 1; e < E; ++e) d += g[e] * o.kv[u][e];
+                    } else {
+                        float d0 = g[0] * o.kv[u][0];
+                        float d1 = g[1] * o.kv[u][1];
+#pragma unroll
+                        for (int e = 2; e < E; e += 2) {
+                            d0 += g[e] * o.kv[u][e];
+                            d1 += g[e + 1] * o.kv[u][e + 1];
+                        }
+                        d = d0 + d1;
                     }
-                    float d = d0 + d1;
                     if constexpr (RL >= 2) d += quad_swap1(d);
                     if constexpr (RL == 4) d += quad_swap2(d);
                     pdot[u] = d;
@@ -1293,7 +1317,7 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
     sp.k = make_consts(consts);
     sp.lines_per_wave = scan16_lines_per_wave(lines, heads);
     sp.aligned = x.spatial && R == 4 && chunks[0] == x.W && chunks[1] == x.W && chunks[2] == x.H &&
-                 chunks[3] == x.H;
+                 chunks[3] == x.H && x.H * x.W * x.st < (int64_t(1) << 31);
     rc = dispatch_d(d, [&](auto dc) {
         constexpr int D = decltype(dc)::value;
         dispatch_t(io_dtype, [&](auto tv) { launch_scan<D, decltype(tv)>(sp, stream); });
