@@ -91,6 +91,25 @@ int vh_srnl_spatial_forward(
     const int64_t chunks[4], const vh_srnl_consts* consts,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* The two halves of vh_srnl_spatial_forward, for callers that overlap other work with
+ * the scan (the readout needs q; the scan does not).  vh_srnl_spatial_scan writes the
+ * chunk-start memories of every line into the workspace; vh_srnl_spatial_readout reads
+ * them (same workspace, same chunks, ordered after the scan) and writes out [B, H, W, C]
+ * = sum_r dir_weight[r, c] (y_r + d_skip[r, c] x) + aux, with aux an optional io-dtype
+ * [B, H, W, C] addend (NULL: none) and out stored as out_dtype (fp32 or io_dtype).  No
+ * counterpart in the reference (its fused kernel does both, fused.cu:307-351); the
+ * prepared block uses aux for the local position encoding (models/block.py:77-78). */
+int vh_srnl_spatial_scan(
+    const void* x, int32_t io_dtype, const float* M_m, const float* M_v, const float* M_k,
+    const float* M_eta, const float* M_alpha, int64_t B, int64_t H, int64_t W, int64_t C,
+    int32_t head_dim, const int64_t chunks[4], const vh_srnl_consts* consts,
+    void* workspace, size_t workspace_bytes, void* stream);
+int vh_srnl_spatial_readout(
+    const void* x, const void* q, int32_t io_dtype, const float* d_skip, int32_t skip_per_direction,
+    const float* dir_weight, const void* aux, void* out, int32_t out_dtype, int64_t B, int64_t H,
+    int64_t W, int64_t C, int32_t head_dim, const int64_t chunks[4], const void* workspace,
+    size_t workspace_bytes, void* stream);
+
 /* The reference's fused spatial entry with its own argument layout: X and
  * Q_raw are the serialized stacks [B, 4, H*W, C]; Out is [B, H, W, C] fp32;
  * chunks are (W, W, H, H).  Replaces srnl_line_forward_seq_noatomic

@@ -931,12 +931,13 @@ struct FuseParams {
     const float* skip;
     int skip_per_dir;
     const float* wgt;
-    float* out;
+    void* out;          // [B, H, W, C], fp32 or the io dtype (see the kernel's TO)
+    const void* aux;    // optional [B, H, W, C] io-dtype addend of the fused result
     int64_t B, H, W, C, heads;
     int chunk[4];
 };
 
-template <int D, typename T>
+template <int D, typename T, typename TO>
 __global__ __launch_bounds__(256) void srnl_fuse_readout_kernel(const FuseParams p) {
     const int64_t L = p.H * p.W;
     const int64_t total = p.B * L * p.C;
@@ -990,7 +991,8 @@ __global__ __launch_bounds__(256) void srnl_fuse_readout_kernel(const FuseParams
         const float weighted = p.wgt[r * p.C + c] * contrib;
         acc = r == 0 ? weighted : acc + weighted;
     }
-    p.out[idx] = acc;
+    if (p.aux) acc += to_f32(static_cast<const T*>(p.aux)[idx]);
+    static_cast<TO*>(p.out)[idx] = from_f32<TO>(acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -1006,7 +1008,7 @@ __global__ __launch_bounds__(256) void srnl_fuse_readout_kernel(const FuseParams
 // Column contributions go through LDS to move pixels onto the row layout; each
 // output is then (c0 + c1) + (c2 + c3) with c_r = w_r (y_r + skip_r x), stored once.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, typename TO>
 __global__ __launch_bounds__(64) void srnl_readout16_kernel(const FuseParams p, const int64_t tiles_h,
                                                             const int64_t tiles_w) {
     constexpr int D = 16, REC = 20;  // 16 channels + 4 padding floats per pixel record
@@ -1126,8 +1128,24 @@ __global__ __launch_bounds__(64) void srnl_readout16_kernel(const FuseParams p, 
         for (int j = 0; j < 4; ++j)
             o[j] = (wt[0][j] * (y0[j] * inv + sk[0][j] * xv[j]) + wt[1][j] * (y1[j] * inv + sk[1][j] * xv[j])) +
                    c23v[j];
-        if (wvalid)
-            *reinterpret_cast<float4*>(p.out + (b * L + h * W + w) * C + cbase) = make_float4(o[0], o[1], o[2], o[3]);
+        if (wvalid) {
+            const int64_t at = (b * L + h * W + w) * C + cbase;
+            if (p.aux) {
+                float a[4];
+                load4(static_cast<const T*>(p.aux) + at, true, a);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] += a[j];
+            }
+            if constexpr (sizeof(TO) == 4) {
+                *reinterpret_cast<float4*>(static_cast<float*>(p.out) + at) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+                const uint32_t lo = static_cast<uint32_t>(from_f32<TO>(o[0]).bits) |
+                                    (static_cast<uint32_t>(from_f32<TO>(o[1]).bits) << 16);
+                const uint32_t hi = static_cast<uint32_t>(from_f32<TO>(o[2]).bits) |
+                                    (static_cast<uint32_t>(from_f32<TO>(o[3]).bits) << 16);
+                *reinterpret_cast<uint2*>(static_cast<TO*>(p.out) + at) = make_uint2(lo, hi);
+            }
+        }
     }
 }
 
@@ -1328,25 +1346,35 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
 }
 
 int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_direction, int io_dtype,
-             const float* skip, int skip_per_dir, const float* wgt, float* out, int64_t H,
-             int64_t W, int64_t C, int d, hipStream_t stream) {
+             const float* skip, int skip_per_dir, const float* wgt, void* out, int64_t H,
+             int64_t W, int64_t C, int d, hipStream_t stream, const void* aux = nullptr,
+             int out_dtype = VH_DTYPE_F32) {
     VH_REQUIRE(skip && wgt && out && q, VH_ERR_ARG, "SRNL fusion arguments must not be null");
+    VH_REQUIRE(out_dtype == VH_DTYPE_F32 || out_dtype == io_dtype, VH_ERR_DTYPE,
+               "SRNL fused output must be fp32 or the io dtype");
     FuseParams fp{};
     fp.x = x; fp.q = q; fp.per_direction = per_direction;
     fp.states = sp.states; fp.max_chunks = sp.max_chunks;
-    fp.skip = skip; fp.skip_per_dir = skip_per_dir; fp.wgt = wgt; fp.out = out;
+    fp.skip = skip; fp.skip_per_dir = skip_per_dir; fp.wgt = wgt; fp.out = out; fp.aux = aux;
     fp.B = sp.B; fp.H = H; fp.W = W; fp.C = C; fp.heads = sp.heads;
     for (int r = 0; r < 4; ++r) fp.chunk[r] = sp.chunk[r];
     const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q) |
-                            reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sp.states);
+                            reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sp.states) |
+                            reinterpret_cast<uintptr_t>(aux);
+    const bool out_f32 = out_dtype == VH_DTYPE_F32;
     if (d == 16 && !per_direction && sp.chunk[0] == W && sp.chunk[1] == W && sp.chunk[2] == H &&
         sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0) {
         const int64_t tiles_h = (H + 15) / 16, tiles_w = (W + 15) / 16;
         const int64_t n_tiles = sp.B * sp.heads * tiles_h * tiles_w;
         VH_REQUIRE(n_tiles <= 0x7fffffff, VH_ERR_SHAPE, "SRNL readout grid too large");
         int rc = dispatch_t(io_dtype, [&](auto tv) {
-            hipLaunchKernelGGL((srnl_readout16_kernel<decltype(tv)>), dim3(static_cast<unsigned>(n_tiles)),
-                               dim3(64), 0, stream, fp, tiles_h, tiles_w);
+            using T = decltype(tv);
+            if (out_f32)
+                hipLaunchKernelGGL((srnl_readout16_kernel<T, float>), dim3(static_cast<unsigned>(n_tiles)),
+                                   dim3(64), 0, stream, fp, tiles_h, tiles_w);
+            else
+                hipLaunchKernelGGL((srnl_readout16_kernel<T, T>), dim3(static_cast<unsigned>(n_tiles)),
+                                   dim3(64), 0, stream, fp, tiles_h, tiles_w);
         });
         if (rc) return rc;
         return check_launch("srnl_readout16_kernel");
@@ -1356,8 +1384,11 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
     int rc = dispatch_d(d, [&](auto dc) {
         constexpr int D = decltype(dc)::value;
         dispatch_t(io_dtype, [&](auto tv) {
-            hipLaunchKernelGGL((srnl_fuse_readout_kernel<D, decltype(tv)>), dim3(blocks), dim3(256),
-                               0, stream, fp);
+            using T = decltype(tv);
+            if (out_f32)
+                hipLaunchKernelGGL((srnl_fuse_readout_kernel<D, T, float>), dim3(blocks), dim3(256), 0, stream, fp);
+            else
+                hipLaunchKernelGGL((srnl_fuse_readout_kernel<D, T, T>), dim3(blocks), dim3(256), 0, stream, fp);
         });
     });
     if (rc) return rc;
@@ -1425,6 +1456,50 @@ int vh_srnl_spatial_forward(const void* x, const void* q, int32_t io_dtype, cons
     if (rc) return rc;
     return run_fuse(sp, x, q, 0, io_dtype, d_skip, skip_per_direction, dir_weight, out, H, W, C,
                     head_dim, s);
+}
+
+int vh_srnl_spatial_scan(const void* x, int32_t io_dtype, const float* M_m, const float* M_v, const float* M_k,
+                         const float* M_eta, const float* M_alpha, int64_t B, int64_t H, int64_t W, int64_t C,
+                         int32_t head_dim, const int64_t chunks[4], const vh_srnl_consts* consts, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+    VH_REQUIRE(H > 0 && W > 0 && C > 0 && B > 0, VH_ERR_SHAPE, "spatial SRNL needs nonempty [B,H,W,C]");
+    VH_REQUIRE(valid_head_dim(head_dim), VH_ERR_HEAD_DIM,
+               "head_dim must be one of 4, 8, 16, 32, 64; got %d", head_dim);
+    VH_REQUIRE(C % head_dim == 0, VH_ERR_SHAPE, "C=%lld is not a multiple of head_dim=%d",
+               (long long)C, head_dim);
+    VH_REQUIRE(H * W < (int64_t(1) << 24), VH_ERR_SHAPE, "spatial SRNL supports H*W < 2^24 pixels, got %lld",
+               (long long)(H * W));
+    LineInput xin{x, H * W * C, 0, head_dim, C, 1, H, W, 1.0f / static_cast<float>(H)};
+    ScanParams sp{};
+    return run_scan(xin, io_dtype, M_m, M_v, M_k, M_eta, M_alpha, B, 4, C / head_dim, H * W, head_dim, chunks,
+                    consts, workspace, workspace_bytes, static_cast<hipStream_t>(stream), &sp);
+}
+
+int vh_srnl_spatial_readout(const void* x, const void* q, int32_t io_dtype, const float* d_skip,
+                            int32_t skip_per_direction, const float* dir_weight, const void* aux, void* out,
+                            int32_t out_dtype, int64_t B, int64_t H, int64_t W, int64_t C, int32_t head_dim,
+                            const int64_t chunks[4], const void* workspace, size_t workspace_bytes,
+                            void* stream) {
+    VH_REQUIRE(x && q && workspace && chunks, VH_ERR_ARG, "spatial SRNL readout pointers must not be null");
+    VH_REQUIRE(H > 0 && W > 0 && C > 0 && B > 0, VH_ERR_SHAPE, "spatial SRNL needs nonempty [B,H,W,C]");
+    VH_REQUIRE(valid_head_dim(head_dim), VH_ERR_HEAD_DIM,
+               "head_dim must be one of 4, 8, 16, 32, 64; got %d", head_dim);
+    VH_REQUIRE(C % head_dim == 0, VH_ERR_SHAPE, "C=%lld is not a multiple of head_dim=%d",
+               (long long)C, head_dim);
+    VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);
+    for (int r = 0; r < 4; ++r)
+        VH_REQUIRE(chunks[r] > 0 && chunks[r] <= (int64_t)1 << 30, VH_ERR_ARG, "invalid chunk length %lld",
+                   (long long)chunks[r]);
+    ScanParams sp{};
+    sp.B = B; sp.R = 4; sp.heads = C / head_dim; sp.L = H * W;
+    for (int r = 0; r < 4; ++r) sp.chunk[r] = static_cast<int>(chunks[r]);
+    sp.max_chunks = max_chunk_count(H * W, chunks, 4);
+    const size_t need = vh_srnl_workspace_bytes(B * 4 * sp.heads, sp.max_chunks, head_dim);
+    VH_REQUIRE(workspace_bytes >= need, VH_ERR_WORKSPACE, "SRNL workspace needs %zu bytes, got %zu", need,
+               workspace_bytes);
+    sp.states = const_cast<float*>(static_cast<const float*>(workspace));
+    return run_fuse(sp, x, q, 0, io_dtype, d_skip, skip_per_direction, dir_weight, out, H, W, C, head_dim,
+                    static_cast<hipStream_t>(stream), aux, out_dtype);
 }
 
 int vh_srnl_line_forward_seq_noatomic(const void* X, const void* Q_raw, int32_t io_dtype,

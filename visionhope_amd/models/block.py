@@ -8,6 +8,7 @@ from torch.nn.init import trunc_normal_
 from .droppath import DropPath
 from .layers import FeedForwardNetwork, LayerNorm2d, build_norm
 from .operator import VisionHOPEOperator
+from .srnl_core.fused import srnl_spatial_readout, srnl_spatial_scan
 from ..utils import dwconv
 from ..utils.cached_params import linear_weights
 from ..utils.grn import GlobalResponseNorm
@@ -15,6 +16,17 @@ from ..utils.grn_cuda import visionhope_grn
 from ..utils.layer_norm_cuda import (can_fuse_add_layernorm2d, can_fuse_layernorm2d, visionhope_add_layernorm2d,
                                      visionhope_layernorm2d)
 from ..utils.residual import can_fuse_residual_add, visionhope_residual_add
+
+
+_SIDE_STREAMS = {}
+
+
+def _side_stream(device):
+    """One default-priority side stream per device for work overlapped with the scan."""
+    stream = _SIDE_STREAMS.get(device.index)
+    if stream is None:
+        stream = _SIDE_STREAMS[device.index] = torch.cuda.Stream(device=device)
+    return stream
 
 
 def _is_pointwise(conv):
@@ -144,6 +156,8 @@ class VisionHOPEBlock(nn.Module):
         path, _ = self.operator._inference_path(x_local)
         if path == "ordinary":
             branch = self._spatial_tail(x_local, True)
+        elif path == "spatial" and x_local.dtype == act:
+            branch = nchw(pointwise(self._spatial_overlapped(x_local), self.proj_out))
         else:
             out = self.operator._forward_fast(x_local, path)
             if self.local_position is not None:
@@ -169,6 +183,43 @@ class VisionHOPEBlock(nn.Module):
                                out_dtype=act).permute(0, 2, 3, 1)
         branch = nchw(pointwise(f, ffn.fc2))
         return self._residual_add(x, branch, self.gamma2)
+
+    def _spatial_overlapped(self, x_local):
+        """Operator output plus local position encoding, ``[B, H, W, C]`` in x_local's dtype.
+
+        The scan needs only x_local, so the query projection and the position encoding
+        run on a side stream while it runs; the readout then fuses the four directions,
+        adds the encoding and rounds once (``operator.py:159-193`` + ``block.py:77-78``).
+        """
+        op = self.operator
+        dev = x_local.device
+        memories = op.srnl._validate_memories(dev)
+        skip_shape = (op.num_heads, op.head_dim) if op.share_direction_skip else (4, op.num_heads, op.head_dim)
+        if op.d_skip.shape != skip_shape or op.d_skip.device != dev:
+            raise ValueError("Directional skip has an invalid shape or device")
+        if op.direction_merge == "softmax":
+            weights = 4.0 * torch.softmax(op.direction_logits.detach().float(), dim=0)
+        else:
+            weights = op.direction_weights().detach().float()
+        batch, channels, height, width = x_local.shape
+        chunks = (width, width, height, height)
+        x_nhwc = x_local.permute(0, 2, 3, 1)
+        q = torch.empty_like(x_nhwc)
+        lepe = None if self.local_position is None else torch.empty_like(x_local, memory_format=torch.channels_last)
+        main = torch.cuda.current_stream(dev)
+        side = _side_stream(dev)
+        side.wait_stream(main)
+        with torch.cuda.stream(side), torch.autocast("cuda", enabled=False):
+            # Operands already in the compute dtype: the product autocast would run.
+            weight, bias = linear_weights(op.W_q, x_local.dtype)
+            torch.addmm(bias, x_nhwc.reshape(-1, channels), weight.t(), out=q.view(-1, channels))
+            if lepe is not None:
+                dwconv.depthwise_conv(x_local, self.local_position, dwconv.EPI_PLAIN, out=lepe)
+        ws = srnl_spatial_scan(memories, x_nhwc, chunks)
+        main.wait_stream(side)
+        return srnl_spatial_readout(ws, x_nhwc, q, op.d_skip, weights, chunks, op.head_dim,
+                                    aux=None if lepe is None else lepe.permute(0, 2, 3, 1),
+                                    out_dtype=x_local.dtype)
 
     def _local_features(self, x):
         x_inner = self.proj_in(x)

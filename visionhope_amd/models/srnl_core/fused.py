@@ -60,6 +60,56 @@ def srnl_spatial_inference(states, x_nhwc, q_nhwc, d_skip, weights, chunks):
     return out
 
 
+def _chunk_array(chunks):
+    return hip.int64_array([int(c) for c in chunks])
+
+
+@on_tensor_device
+def srnl_spatial_scan(states, x_nhwc, chunks):
+    """First half of ``srnl_spatial_inference``: the four scans of x_nhwc ``[B, H, W, C]``.
+    Returns the workspace holding every chunk-start content memory, for
+    ``srnl_spatial_readout`` on the same stream."""
+    batch, height, width, channels = x_nhwc.shape
+    head_dim = states[0].shape[-1]
+    mems = _fp32_states(states)
+    x_c = x_nhwc.contiguous()
+    lib = hip.load_library()
+    max_chunks = max(math.ceil(height * width / int(c)) for c in chunks)
+    ws = hip.workspace(lib.vh_srnl_workspace_bytes(batch * 4 * (channels // head_dim), max_chunks, head_dim),
+                       x_nhwc.device)
+    chunk_ptr, _keep = _chunk_array(chunks)
+    hip.check(lib.vh_srnl_spatial_scan(
+        hip.ptr(x_c), hip.dtype_code(x_c.dtype), *[hip.ptr(m) for m in mems], batch, height, width, channels,
+        head_dim, chunk_ptr, srnl_consts(), hip.ptr(ws), ws.numel() * 4, hip.stream_of(x_c)),
+        "vh_srnl_spatial_scan")
+    return ws
+
+
+@on_tensor_device
+def srnl_spatial_readout(workspace, x_nhwc, q_nhwc, d_skip, weights, chunks, head_dim, *, aux=None,
+                         out_dtype=torch.float32):
+    """Second half: sum_r w_r (y_r + skip_r x) (+ aux) as ``[B, H, W, C]`` ``out_dtype``
+    (FP32 or x's dtype); aux is an optional x-dtype ``[B, H, W, C]`` addend."""
+    batch, height, width, channels = x_nhwc.shape
+    if q_nhwc.shape != x_nhwc.shape or q_nhwc.dtype != x_nhwc.dtype:
+        raise ValueError("Spatial SRNL expects x and queries with the same [B, H, W, C] shape and dtype")
+    if aux is not None and (aux.shape != x_nhwc.shape or aux.dtype != x_nhwc.dtype):
+        raise ValueError("The readout addend must match x's shape and dtype")
+    skip = d_skip.detach().float().contiguous()
+    wts = weights.detach().float().contiguous()
+    x_c, q_c = x_nhwc.contiguous(), q_nhwc.contiguous()
+    aux_c = None if aux is None else aux.contiguous()
+    out = torch.empty((batch, height, width, channels), device=x_nhwc.device, dtype=out_dtype)
+    lib = hip.load_library()
+    chunk_ptr, _keep = _chunk_array(chunks)
+    hip.check(lib.vh_srnl_spatial_readout(
+        hip.ptr(x_c), hip.ptr(q_c), hip.dtype_code(x_c.dtype), hip.ptr(skip), int(skip.numel() == 4 * channels),
+        hip.ptr(wts), hip.ptr(aux_c), hip.ptr(out), hip.dtype_code(out_dtype), batch, height, width, channels,
+        head_dim, chunk_ptr, hip.ptr(workspace), workspace.numel() * 4, hip.stream_of(x_c)),
+        "vh_srnl_spatial_readout")
+    return out
+
+
 class FusedSRNLOps:
     """The functions of the reference's ``load_fused_cuda`` module (``fused.py:70-76``)."""
 

@@ -68,7 +68,8 @@ def depthwise_conv(x, conv, epilogue=EPI_PLAIN, aux=None, out=None):
     """Run ``conv`` on the channels-last map ``x`` with a fused epilogue (module docstring).
 
     For ``EPI_ACCUM_F32`` ``out`` is a contiguous FP32 ``[B, H, W, C]`` tensor updated in
-    place; otherwise a new ``x``-dtype channels-last tensor is returned (for
+    place; otherwise the result is written to ``out`` when given (channels-last, x's dtype)
+    or to a new ``x``-dtype channels-last tensor (for
     ``EPI_ADD_F32_AUX``, ``aux`` is the FP32 ``[B, H, W, C]`` addend).
     """
     if not x.is_cuda or x.dtype not in _DTYPES:
@@ -92,6 +93,10 @@ def depthwise_conv(x, conv, epilogue=EPI_PLAIN, aux=None, out=None):
         if (out is None or out.dtype != torch.float32 or tuple(out.shape) != (batch, height, width, channels)
                 or not out.is_contiguous() or out.data_ptr() % 16):
             raise ValueError("EPI_ACCUM_F32 needs a contiguous FP32 [B, H, W, C] output")
+    elif out is not None:
+        if (out.dtype != x.dtype or out.shape != x.shape or not out.is_contiguous(memory_format=torch.channels_last)
+                or out.data_ptr() % 16):
+            raise ValueError("out must be a channels-last tensor shaped and typed like x")
     else:
         out = torch.empty_like(x, memory_format=torch.channels_last)
     lib = hip.load_library()
