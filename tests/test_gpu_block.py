@@ -67,6 +67,29 @@ def test_depthwise_epilogues(device, ksize, epilogue, dtype, tol):
     assert_close(got.double().cpu().numpy(), expected.numpy(), tol, f"dwconv K={ksize} epi={epilogue}")
 
 
+@pytest.mark.parametrize("ksize,epilogue", [(3, 3), (7, 2), (5, 5)])
+def test_depthwise_split_launches_match_one_launch(device, monkeypatch, ksize, epilogue):
+    """Inputs above the per-launch buffer limit go in several launches of whole images;
+    the result is bit-identical to one launch (the limit is lowered to one image here)."""
+    from visionhope_amd.utils import dwconv
+
+    channels, h, w = 16, 6, 11
+    conv = torch.nn.Conv2d(channels, channels, ksize, padding=ksize // 2, groups=channels)
+    with torch.no_grad():
+        conv.weight.copy_(randn(*conv.weight.shape, seed=41, scale=0.3))
+        conv.bias.copy_(randn(channels, seed=42, scale=0.1))
+    conv = conv.to(device)
+    x = randn(5, channels, h, w, seed=43).bfloat16().to(device).contiguous(memory_format=torch.channels_last)
+    gate = randn(5, channels, h, w, seed=44).bfloat16().to(device).contiguous(memory_format=torch.channels_last)
+    acc = randn(5, h, w, channels, seed=45).to(device)
+    aux = gate if epilogue == dwconv.EPI_GATE else acc if epilogue == dwconv.EPI_ADD_F32_AUX else None
+    whole = dwconv.depthwise_conv(x, conv, epilogue, aux=aux)
+    monkeypatch.setenv("VH_DW_LAUNCH_BYTES", str(h * w * channels * 2 + 7))
+    split = dwconv.depthwise_conv(x, conv, epilogue, aux=aux)
+    torch.cuda.synchronize()
+    assert torch.equal(split, whole)
+
+
 def test_depthwise_without_bias_and_noncontiguous_input(device):
     from visionhope_amd.utils import dwconv
 

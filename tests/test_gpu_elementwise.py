@@ -148,3 +148,19 @@ def test_add_layernorm2d(device, dtype, channels):
     expected = torch.nn.functional.layer_norm(s.double().cpu().permute(0, 2, 3, 1), (channels,), w.double().cpu(),
                                               b.double().cpu(), 1e-6).permute(0, 3, 1, 2)
     assert_close(y.cpu().numpy(), expected.numpy(), 1e-5, "add+LN")
+
+
+@pytest.mark.parametrize("channels", [64, 96])
+def test_layernorm2d_bf16_store_is_round_to_nearest_even(device, channels):
+    """The kernels store bf16 through the hardware conversion: the bf16 output is the FP32
+    output rounded by torch's conversion (nearest even), bit for bit, over a wide range of
+    magnitudes (large |w| and tiny |b| put values at every exponent)."""
+    from visionhope_amd.utils.layer_norm_cuda import visionhope_layernorm2d
+
+    x = randn(4, channels, 6, 7, seed=31).to(device).contiguous(memory_format=torch.channels_last)
+    w = (randn(channels, seed=32) * torch.logspace(-20, 20, channels)).to(device)
+    b = (randn(channels, seed=33) * 1e-3).to(device)
+    y32 = visionhope_layernorm2d(x, w, b, 1e-6)
+    y16 = visionhope_layernorm2d(x, w, b, 1e-6, out_dtype=torch.bfloat16)
+    assert y16.dtype == torch.bfloat16
+    assert torch.equal(y16.view(torch.int16), y32.to(torch.bfloat16).view(torch.int16))

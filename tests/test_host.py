@@ -212,3 +212,28 @@ def test_parameter_caches_follow_updates():
         lin.bias.add_(1)
     _, b2 = linear_weights(lin, torch.bfloat16)
     assert torch.equal(b2, lin.bias.detach().bfloat16())
+
+
+def test_invariant_divisor_multiplication_is_exact():
+    """The depthwise kernels divide thread indices by launch-invariant divisors with one
+    multiplication: m = ceil(2^(32+l) / d), l = ceil(log2 d), floor(n/d) = (n*m) >> (32+l)
+    for every n < 2^31.  Brute force over small divisors and dividends, and the extremes
+    (the largest dividends, divisors at and around powers of two)."""
+    rng = np.random.default_rng(5)
+
+    def magic(d):
+        l = (d - 1).bit_length()
+        return -(-(1 << (32 + l)) // d), 32 + l
+
+    divisors = list(range(1, 600)) + [(1 << k) + e for k in range(10, 31) for e in (-1, 0, 1)] + [(1 << 31) - 1]
+    top = (1 << 31) - 1
+    for d in divisors:
+        m, shift = magic(d)
+        assert m < (1 << 33) + 1
+        ns = np.concatenate([np.arange(0, min(4 * d + 3, top), max(1, d // 7)), rng.integers(0, top, 200),
+                             [top, top - 1, top - (top % d), top - (top % d) - 1]]).astype(object)
+        for n in ns:
+            n = int(n)
+            assert 0 <= n <= top
+            assert (n * m) >> shift == n // d, (n, d)
+            assert n * m < (1 << 64)

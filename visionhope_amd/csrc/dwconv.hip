@@ -9,6 +9,7 @@
 //   ffn     gelu(h + dwconv3(h))                             (layers.py:76-77)
 // Each thread computes 8 consecutive channels of a row segment of pixels with fp32
 // accumulation; taps are stored taps-major ([K*K][C], fp32) so one tap is two float4 loads.
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 
@@ -27,67 +28,76 @@ struct DwParams {
     int64_t B, H, W, C;
 };
 
-__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.f + erff(v * 0.70710678118654752f)); }
+// Launch geometry: thread index -> (image, row, segment, channel group), with the
+// divisions done by multiplication (all indices < 2^31, checked on the host).
+struct DwGrid {
+    uint32_t total;            // B * H * segs * G threads
+    FastDiv G, segs, H;
+};
 
-// Epilogue of one output vector (8 channels of pixel `at`) from the fp32 conv sum.
-template <int EPI, typename T>
-__device__ __forceinline__ void dw_epilogue(const DwParams& p, int64_t at, float (&acc)[8]) {
-    const T* x = static_cast<const T*>(p.x);
-    if constexpr (EPI == DW_ACCUM_F32) {
-        float* o = static_cast<float*>(p.out) + at;
-        float prev[8];
-        load8<float>(o, prev);
+// Eight consecutive channels at byte offset `off` of a buffer as raw 32-bit words; an
+// offset past the buffer's range reads zeros (buffer addressing returns 0 out of range),
+// so padding needs no branch and every load of a window can be in flight at once.
+template <typename T>
+struct Raw8 {
+    static constexpr int N = sizeof(T) == 4 ? 2 : 1;   // 16-byte loads per 8 elements
+    uint32_t w[4 * N];
+};
+template <typename T>
+__device__ __forceinline__ Raw8<T> buffer_load8(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
+    Raw8<T> r;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = prev[j] + acc[j];
-        store8<float>(o, acc);
-        return;
+    for (int n = 0; n < Raw8<T>::N; ++n) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(off + 16 * n), 0, 0);
+        r.w[4 * n] = v[0]; r.w[4 * n + 1] = v[1]; r.w[4 * n + 2] = v[2]; r.w[4 * n + 3] = v[3];
+    }
+    return r;
+}
+template <typename T>
+__device__ __forceinline__ void decode8(const Raw8<T>& r, float (&v)[8]) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(r.w[j]);
     } else {
-        if constexpr (EPI == DW_ADD_F32_AUX) {
-            float a[8];
-            load8<float>(static_cast<const float*>(p.aux) + at, a);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = a[j] + acc[j];
-        } else if constexpr (EPI != DW_PLAIN) {
-            float xin[8];
-            load8<T>(x + at, xin);
-            if constexpr (EPI == DW_GATE) {
-                float gv[8];
-                load8<T>(static_cast<const T*>(p.aux) + at, gv);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] = xin[j] + (1.f / (1.f + expf(-gv[j]))) * acc[j];
-            } else if constexpr (EPI == DW_ADD_GELU) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] = gelu_erf(xin[j] + acc[j]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] = xin[j] + acc[j];
-            }
+        for (int h = 0; h < 4; ++h) {
+            v[2 * h] = to_f32(T{static_cast<uint16_t>(r.w[h] & 0xffffu)});
+            v[2 * h + 1] = to_f32(T{static_cast<uint16_t>(r.w[h] >> 16)});
         }
-        store8<T>(static_cast<T*>(p.out) + at, acc);
     }
 }
 
 // One thread per (image, row, segment of P pixels, 8 channels): each kernel row loads
 // the P+K-1 input vectors of the segment once and reuses them for all K horizontal
 // taps of the P outputs, so a K x K window costs (P+K-1)/P input loads per tap row
-// instead of K.  Consecutive lanes take consecutive channel groups (coalesced).
+// instead of K.  Consecutive lanes take consecutive channel groups (coalesced), and
+// consecutive blocks of one XCD take consecutive rows, so the rows above and below a
+// block's own are read through the same L2.  The input is addressed as one buffer of
+// `x_bytes` bytes (< 2^31): positions outside the image read zeros.
 template <int K, int EPI, typename T, int P>
-__global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, const int segs) {
+__global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, const DwGrid g, const uint32_t x_bytes) {
     constexpr int R = K / 2, NI = P + K - 1;
-    const int G = static_cast<int>(p.C / 8);
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= p.B * p.H * segs * G) return;
-    const int cg = static_cast<int>(idx % G);
-    int64_t t = idx / G;
-    const int seg = static_cast<int>(t % segs);
-    t /= segs;
-    const int h = static_cast<int>(t % p.H);
-    const int64_t b = t / p.H;
-    const int W = static_cast<int>(p.W), H = static_cast<int>(p.H);
-    const int w0 = seg * P;
-    const int64_t c = cg * 8;
-    const T* x = static_cast<const T*>(p.x);
-    const int64_t img = b * p.H * p.W;
+    constexpr uint32_t OUTSIDE = 0x80000000u;
+    const uint32_t idx = xcd_remap_any(blockIdx.x, gridDim.x) * 256u + threadIdx.x;
+    if (idx >= g.total) return;
+    const uint32_t t0 = fast_div(idx, g.G);
+    const uint32_t cg = idx - t0 * g.G.d;
+    const uint32_t t1 = fast_div(t0, g.segs);
+    const uint32_t seg = t0 - t1 * g.segs.d;
+    const uint32_t b = fast_div(t1, g.H);
+    const int h = static_cast<int>(t1 - b * g.H.d);
+    const int W = static_cast<int>(p.W), H = static_cast<int>(p.H), C = static_cast<int>(p.C);
+    const int w0 = static_cast<int>(seg) * P;
+    const int c = static_cast<int>(cg) * 8;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.x), 0, x_bytes, 0x00020000);
+    // Byte offset of (row hh, column ww) of this image and channel group.
+    const uint32_t row0 = static_cast<uint32_t>(b) * H;
+    auto offset = [&](int hh, int ww) -> uint32_t {
+        const bool ok = (static_cast<uint32_t>(hh) < static_cast<uint32_t>(H)) &
+                        (static_cast<uint32_t>(ww) < static_cast<uint32_t>(W));
+        const uint32_t off = (((row0 + hh) * static_cast<uint32_t>(W) + ww) * static_cast<uint32_t>(C) + c) * sizeof(T);
+        return ok ? off : OUTSIDE;
+    };
 
     float acc[P][8];
     {
@@ -100,35 +110,90 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
             for (int px = 0; px < P; ++px) acc[px][j] = bj;
         }
     }
+    [[maybe_unused]] float center[P][8];
+    auto load_row = [&](int hh, Raw8<T> (&r)[NI]) {
 #pragma unroll
-    for (int dy = 0; dy < K; ++dy) {
-        const int hh = h + dy - R;
-        if (hh < 0 || hh >= H) continue;  // uniform per thread
-        float in[NI][8];
+        for (int i = 0; i < NI; ++i) r[i] = buffer_load8<T>(xr, offset(hh, w0 - R + i));
+    };
+    // Each input vector is decoded once and applied to every output of the segment
+    // that it touches.
+    auto compute_row = [&](int dy, const Raw8<T> (&r)[NI]) {
+        float tp[K][8];
+#pragma unroll
+        for (int dx = 0; dx < K; ++dx) load8<float>(p.taps + (dy * K + dx) * C + c, tp[dx]);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const int ww = w0 - R + i;
-            if (ww >= 0 && ww < W) {
-                load8<T>(x + ((img + static_cast<int64_t>(hh) * W + ww) * p.C) + c, in[i]);
-            } else {
+            float v[8];
+            decode8<T>(r[i], v);
+            if constexpr (EPI == DW_ADD_INPUT || EPI == DW_GATE || EPI == DW_ADD_GELU) {
+                if (i >= R && i < R + P && dy == R) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) in[i][j] = 0.f;
+                    for (int j = 0; j < 8; ++j) center[i - R][j] = v[j];
+                }
+            }
+#pragma unroll
+            for (int dx = 0; dx < K; ++dx) {
+                const int px = i - dx;
+                if (px >= 0 && px < P) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[px][j] += v[j] * tp[dx][j];
+                }
             }
         }
+    };
+    if constexpr (K == 3) {
+        // Every load of the 3 x (P+2) window in flight at once.
+        Raw8<T> raw[K][NI];
 #pragma unroll
-        for (int dx = 0; dx < K; ++dx) {
-            float tp[8];
-            load8<float>(p.taps + (dy * K + dx) * p.C + c, tp);
+        for (int dy = 0; dy < K; ++dy) load_row(h + dy - R, raw[dy]);
 #pragma unroll
-            for (int px = 0; px < P; ++px)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[px][j] += in[px + dx][j] * tp[j];
+        for (int dy = 0; dy < K; ++dy) compute_row(dy, raw[dy]);
+    } else {
+        // Larger windows: rows pipelined in two register sets (row dy+1 loads while
+        // row dy computes), which keeps the register count within one wave's budget.
+        Raw8<T> ra[NI], rb[NI];
+        load_row(h - R, ra);
+#pragma unroll 1
+        for (int dy = 0; dy < K; dy += 2) {
+            load_row(h + dy + 1 - R, rb);
+            compute_row(dy, ra);
+            if (dy + 1 == K) break;
+            load_row(h + dy + 2 - R, ra);
+            compute_row(dy + 1, rb);
         }
     }
+    const int64_t pix0 = (static_cast<int64_t>(row0) + h) * W + w0;
 #pragma unroll
     for (int px = 0; px < P; ++px) {
         if (w0 + px >= W) break;
-        dw_epilogue<EPI, T>(p, (img + static_cast<int64_t>(h) * W + w0 + px) * p.C + c, acc[px]);
+        const int64_t at = (pix0 + px) * C + c;
+        if constexpr (EPI == DW_ACCUM_F32) {
+            float* o = static_cast<float*>(p.out) + at;
+            float prev[8];
+            load8<float>(o, prev);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[px][j] = prev[j] + acc[px][j];
+            store8<float>(o, acc[px]);
+        } else {
+            if constexpr (EPI == DW_ADD_F32_AUX) {
+                float a[8];
+                load8<float>(static_cast<const float*>(p.aux) + at, a);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[px][j] = a[j] + acc[px][j];
+            } else if constexpr (EPI == DW_GATE) {
+                float gv[8];
+                load8<T>(static_cast<const T*>(p.aux) + at, gv);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[px][j] = center[px][j] + sigmoid_fast(gv[j]) * acc[px][j];
+            } else if constexpr (EPI == DW_ADD_GELU) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[px][j] = gelu_fast(center[px][j] + acc[px][j]);
+            } else if constexpr (EPI == DW_ADD_INPUT) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[px][j] = center[px][j] + acc[px][j];
+            }
+            store8<T>(static_cast<T*>(p.out) + at, acc[px]);
+        }
     }
 }
 
@@ -136,26 +201,48 @@ namespace {
 
 // Pixels per thread (register blocking along W).  VH_DW_PIXELS = 1, 2, 4 or 8 overrides
 // the default for measurements.
-// Measured on MI355X at the Tiny shapes (B=128; W = 56 and 14): 2 pixels for 3x3,
-// 4 for 5x5 on wide maps and 2 on narrow ones, 4 for 7x7.
+// Measured on MI355X at the Tiny shapes (B=128; W = 56, 14 and 7): 8 pixels for 3x3,
+// 4 for 5x5, 2 for 7x7 on wide maps and 8 on narrow ones.
 inline int dw_default_pixels(int K, int64_t W) {
-    if (K == 3) return 2;
-    if (K == 5) return W >= 28 ? 4 : 2;
-    return 4;
+    if (K == 3) return 8;
+    if (K == 5) return 4;
+    return W >= 28 ? 2 : 8;
 }
 
 template <int K, typename T, int P>
 void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
-    const int segs = static_cast<int>((dp.W + P - 1) / P);
-    const int64_t total = dp.B * dp.H * segs * (dp.C / 8);
-    const dim3 grid(static_cast<unsigned>((total + 255) / 256));
-    switch (epi) {
-#define VH_DW(E)                                                                                   \
-    case E: hipLaunchKernelGGL((dwconv_nhwc_kernel<K, E, T, P>), grid, dim3(256), 0, s, dp, segs); \
+    // The input of one launch is addressed as one buffer below 2^31 bytes: large batches
+    // go in several launches of whole images.
+    // VH_DW_LAUNCH_BYTES lowers the per-launch limit (tests use it to exercise the split).
+    int64_t limit = (int64_t(1) << 31) - 1;
+    if (const char* env = std::getenv("VH_DW_LAUNCH_BYTES")) limit = std::min(limit, std::max<int64_t>(1, std::atoll(env)));
+    const int64_t image_elems = dp.H * dp.W * dp.C;
+    const int64_t per_launch = std::max<int64_t>(1, limit / (image_elems * int64_t(sizeof(T))));
+    const int64_t segs = (dp.W + P - 1) / P;
+    const size_t out_size = epi == DW_ACCUM_F32 ? sizeof(float) : sizeof(T);
+    const size_t aux_size = epi == DW_ADD_F32_AUX ? sizeof(float) : sizeof(T);
+    for (int64_t b0 = 0; b0 < dp.B; b0 += per_launch) {
+        DwParams q = dp;
+        q.B = std::min(per_launch, dp.B - b0);
+        const int64_t skip = b0 * image_elems;
+        q.x = static_cast<const char*>(dp.x) + skip * sizeof(T);
+        q.out = static_cast<char*>(dp.out) + skip * out_size;
+        if (dp.aux) q.aux = static_cast<const char*>(dp.aux) + skip * aux_size;
+        DwGrid g;
+        g.total = static_cast<uint32_t>(q.B * q.H * segs * (q.C / 8));
+        g.G = make_fastdiv(static_cast<uint32_t>(q.C / 8));
+        g.segs = make_fastdiv(static_cast<uint32_t>(segs));
+        g.H = make_fastdiv(static_cast<uint32_t>(q.H));
+        const uint32_t x_bytes = static_cast<uint32_t>(q.B * image_elems * int64_t(sizeof(T)));
+        const dim3 grid((g.total + 255) / 256);
+        switch (epi) {
+#define VH_DW(E)                                                                                         \
+    case E: hipLaunchKernelGGL((dwconv_nhwc_kernel<K, E, T, P>), grid, dim3(256), 0, s, q, g, x_bytes); \
         break;
-        VH_DW(DW_PLAIN) VH_DW(DW_ADD_INPUT) VH_DW(DW_GATE) VH_DW(DW_ADD_GELU) VH_DW(DW_ACCUM_F32)
-        VH_DW(DW_ADD_F32_AUX)
+            VH_DW(DW_PLAIN) VH_DW(DW_ADD_INPUT) VH_DW(DW_GATE) VH_DW(DW_ADD_GELU) VH_DW(DW_ACCUM_F32)
+            VH_DW(DW_ADD_F32_AUX)
 #undef VH_DW
+        }
     }
 }
 
@@ -195,7 +282,8 @@ extern "C" int vh_dwconv2d_nhwc_forward(const void* x, int32_t io_dtype, const f
                             reinterpret_cast<uintptr_t>(taps) | reinterpret_cast<uintptr_t>(bias) |
                             reinterpret_cast<uintptr_t>(aux);
     VH_REQUIRE(align % 16 == 0, VH_ERR_ARG, "depthwise conv tensors must be 16-byte aligned");
-    VH_REQUIRE(H < (int64_t(1) << 30) && W < (int64_t(1) << 30), VH_ERR_SHAPE, "depthwise conv image too large");
+    VH_REQUIRE(H * W * C * dtype_bytes(io_dtype) < (int64_t(1) << 31), VH_ERR_SHAPE,
+               "depthwise conv image too large (one image must be below 2 GiB)");
     DwParams dp{x, taps, bias, aux, out, B, H, W, C};
     hipStream_t s = static_cast<hipStream_t>(stream);
     auto go = [&](auto tv) {

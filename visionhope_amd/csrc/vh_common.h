@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <type_traits>
 
 #include "../../include/visionhope_hip.h"
 
@@ -46,11 +47,8 @@ __device__ __forceinline__ float to_f32(f16_t v) {
 template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
-    // Round to nearest even; quiet NaNs stay NaN.
-    uint32_t u = __float_as_uint(v);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t{static_cast<uint16_t>((u >> 16) | 0x40u)};
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return bf16_t{static_cast<uint16_t>(u >> 16)};
+    // v_cvt_pk_bf16_f32: round to nearest even; NaNs stay NaN (quieted).
+    return bf16_t{__builtin_bit_cast(uint16_t, static_cast<__bf16>(v))};
 }
 template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float v) {
     _Float16 h = static_cast<_Float16>(v);
@@ -79,11 +77,23 @@ __device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
     }
 }
 
+typedef __bf16 vh_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float vh_f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats as one packed bf16 pair (one v_cvt_pk_bf16_f32), low half first.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const vh_f32x2 f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, vh_bf16x2));
+}
+
 template <typename T>
 __device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
     if constexpr (sizeof(T) == 4) {
         *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
         *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else if constexpr (std::is_same<T, bf16_t>::value) {
+        *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                  pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
     } else {
         uint32_t w[4];
 #pragma unroll
@@ -140,6 +150,68 @@ __device__ __forceinline__ int64_t pixel_to_scan(int r, int64_t h, int64_t w, in
 __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
     if (n % 8 != 0) return bid;
     return (bid % 8) * (n / 8) + bid / 8;
+}
+
+// The same for any grid size n: XCD x receives the n/8 (+1 for x < n%8) blocks
+// x, x+8, ... and maps them to one contiguous range starting at x*(n/8) + min(x, n%8).
+__device__ __forceinline__ uint32_t xcd_remap_any(uint32_t bid, uint32_t n) {
+    const uint32_t q = n / 8, r = n % 8, x = bid % 8;
+    return x * q + (x < r ? x : r) + bid / 8;
+}
+
+// ---------------------------------------------------------------------------
+// Division by a launch-invariant divisor d >= 1 for dividends n < 2^31, by one
+// multiplication (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994).  With l = ceil(log2 d) and m = ceil(2^(32+l) / d),
+// n*m / 2^(32+l) = n/d + n*e/2^(32+l) with 0 <= e < 1, and n*e*d < 2^(32+l), so
+// the error never reaches the next integer: floor(n/d) = (n*m) >> (32+l).
+// n*m < 2^31 * (2^33 + 1) fits 64 bits.
+// ---------------------------------------------------------------------------
+struct FastDiv {
+    uint64_t m;
+    uint32_t d;
+    uint32_t shift;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((uint64_t(1) << l) < d) ++l;
+    const unsigned __int128 num = static_cast<unsigned __int128>(1) << (32 + l);
+    const uint64_t m = static_cast<uint64_t>((num + d - 1) / d);
+    return FastDiv{m, d, 32 + l};
+}
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
+    return static_cast<uint32_t>((static_cast<uint64_t>(n) * f.m) >> f.shift);
+}
+
+// ---------------------------------------------------------------------------
+// Activations on the hardware exp2 / reciprocal (v_exp_f32, v_rcp_f32, about one ulp
+// each), branch-free.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sigmoid_fast(float v) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.44269504088896341f * v));
+}
+
+// GELU in its exact form x * Phi(x), Phi(x) = erfc(-x/sqrt(2)) / 2.  erfc(z), z >= 0, is
+// the Chebyshev fit t * exp(-z^2 + P(t)), t = 1 / (1 + z/2), of Press, Teukolsky,
+// Vetterling and Flannery, Numerical Recipes, 2nd ed., section 6.2 (fractional error
+// below 1.2e-7 for every z >= 0).  Evaluating the tail x < 0 through erfc keeps the
+// small outputs relatively accurate; in fp32 the result is within 2e-5 (relative) of
+// x * Phi(x) over the whole real line.
+__device__ __forceinline__ float gelu_fast(float x) {
+    const float z = fabsf(x) * 0.70710678118654752f;
+    const float t = __builtin_amdgcn_rcpf(1.f + 0.5f * z);
+    float p = 0.17087277f;
+    p = p * t - 0.82215223f;
+    p = p * t + 1.48851587f;
+    p = p * t - 1.13520398f;
+    p = p * t + 0.27886807f;
+    p = p * t - 0.18628806f;
+    p = p * t + 0.09678418f;
+    p = p * t + 0.37409196f;
+    p = p * t + 1.00002368f;
+    p = p * t - 1.26551223f;
+    const float half_erfc = 0.5f * t * __builtin_amdgcn_exp2f(1.44269504088896341f * (p - z * z));
+    return x * (x < 0.f ? half_erfc : 1.f - half_erfc);
 }
 
 }  // namespace vh
