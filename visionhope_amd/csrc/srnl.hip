@@ -998,129 +998,157 @@ __global__ __launch_bounds__(256) void srnl_fuse_readout_kernel(const FuseParams
 // ---------------------------------------------------------------------------
 // Spatial readout + fusion for head_dim 16 with row/column chunks (W, W, H, H).
 //
-// One wave per 16x16-pixel tile of one (image, head).  Every pixel of a tile row
-// reads the same direction-0/1 states (chunks h and H-1-h) and every pixel of a
-// tile column the same direction-2/3 states (chunks w and W-1-w), so each
-// y = M q over 16 pixels is one 16x16x16 product on the matrix cores:
+// One workgroup of four waves per 16x16-pixel tile of one (image, head).  Every
+// pixel of a tile row reads the same direction-0/1 states (chunks h and H-1-h) and
+// every pixel of a tile column the same direction-2/3 states (chunks w and W-1-w),
+// so each y = M q over 16 pixels is one 16x16x16 product on the matrix cores:
 //   step m of four 16x16x4 MFMAs: lane l = 16g + n supplies A = M[n][4g+m] and
 //   B = q[pixel n][4g+m] (k permuted so both operands are 4-vector loads) and
 //   receives D[4g+j][n], channels 4g..4g+3 of pixel n.
-// Column contributions go through LDS to move pixels onto the row layout; each
-// output is then (c0 + c1) + (c2 + c3) with c_r = w_r (y_r + skip_r x), stored once.
+// Wave v takes tile columns 4v..4v+3 (directions 2, 3) and then tile rows 4v..4v+3
+// (directions 0, 1); column contributions go through LDS to move pixels onto the
+// row layout; each output is then (c0 + c1) + (c2 + c3) with c_r = w_r (y_r +
+// skip_r x), stored once.  Loads are branch-free (positions past the image edge
+// read the edge pixel and are never stored), so every load of a wave's four
+// columns or rows is in flight at once, and the row loads are issued before the
+// column work.
 // ---------------------------------------------------------------------------
+template <typename T>
+struct Pix4 {   // 4 channels of one pixel as raw bits
+    using Raw = typename std::conditional<sizeof(T) == 4, uint4, uint2>::type;
+    Raw q, x;
+};
+
+template <typename T>
+__device__ __forceinline__ void raw4_to_f32(const typename Pix4<T>::Raw& r, float (&v)[4]) {
+    if constexpr (sizeof(T) == 4) {
+        v[0] = __uint_as_float(r.x); v[1] = __uint_as_float(r.y); v[2] = __uint_as_float(r.z); v[3] = __uint_as_float(r.w);
+    } else {
+        v[0] = to_f32(T{static_cast<uint16_t>(r.x & 0xffffu)});
+        v[1] = to_f32(T{static_cast<uint16_t>(r.x >> 16)});
+        v[2] = to_f32(T{static_cast<uint16_t>(r.y & 0xffffu)});
+        v[3] = to_f32(T{static_cast<uint16_t>(r.y >> 16)});
+    }
+}
+
+// y = M q~ for 16 pixels (lane n: pixel n, channels 4g..4g+3 of the result); q~ raw bits.
+template <typename T>
+__device__ __forceinline__ v4f readout_mfma(const float4& m, const typename Pix4<T>::Raw& qr, const float (&qv)[4]) {
+    v4f y = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        const v4s qs = bf16x4_bits(qr);
+        const float a[4] = {m.x, m.y, m.z, m.w};
+        v4s hi, lo;
+        split_bf16(a, hi, lo);
+        y = mfma_bf16(hi, qs, y);
+        y = mfma_bf16(lo, qs, y);
+    } else {
+        y = mfma4(m.x, qv[0], y);
+        y = mfma4(m.y, qv[1], y);
+        y = mfma4(m.z, qv[2], y);
+        y = mfma4(m.w, qv[3], y);
+    }
+    return y;
+}
+
 template <typename T, typename TO>
-__global__ __launch_bounds__(64) void srnl_readout16_kernel(const FuseParams p, const int64_t tiles_h,
-                                                            const int64_t tiles_w) {
-    constexpr int D = 16, REC = 20;  // 16 channels + 4 padding floats per pixel record
+__global__ __launch_bounds__(256) void srnl_readout16_kernel(const FuseParams p, const int64_t tiles_h,
+                                                             const int64_t tiles_w) {
+    constexpr int D = 16, REC = 20, PER = 4;   // 16 channels + 4 padding floats per pixel record
+    using Raw = typename Pix4<T>::Raw;
     __shared__ __align__(16) float col[256 * REC];
-    const int64_t n_tiles = p.B * p.heads * tiles_h * tiles_w;
-    const int64_t tile = xcd_remap(blockIdx.x, n_tiles);
-    const int64_t tw = tile % tiles_w;
-    const int64_t th = (tile / tiles_w) % tiles_h;
-    const int64_t bh = tile / (tiles_w * tiles_h);
-    const int64_t head = bh % p.heads, b = bh / p.heads;
-    const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
-    const int64_t H = p.H, W = p.W, C = p.C, L = H * W;
-    const int64_t h0 = th * 16, w0 = tw * 16;
+    // Tile indices fit 32 bits (the host checks the grid size).
+    const uint32_t thw = static_cast<uint32_t>(tiles_h * tiles_w), ntw = static_cast<uint32_t>(tiles_w);
+    const uint32_t tile = xcd_remap_any(blockIdx.x, gridDim.x);
+    const uint32_t bh = tile / thw, in_img = tile - bh * thw;
+    const uint32_t th = in_img / ntw, tw = in_img - th * ntw;
+    const uint32_t heads = static_cast<uint32_t>(p.heads);
+    const int64_t head = bh % heads, b = bh / heads;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
+    const int H = static_cast<int>(p.H), W = static_cast<int>(p.W);
+    const int64_t C = p.C, L = p.H * p.W;
+    const int h0 = static_cast<int>(th) * 16, w0 = static_cast<int>(tw) * 16;
     const int64_t cbase = head * D + 4 * g;
     const T* xb = static_cast<const T*>(p.x) + b * L * C + cbase;
     const T* qb = static_cast<const T*>(p.q) + b * L * C + cbase;
     const float* st[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        st[r] = p.states + ((b * 4 + r) * p.heads + head) * p.max_chunks * (D * D) + n * D + 4 * g;
+    auto load_pix = [&](int h, int w) {
+        Pix4<T> v;
+        const int64_t at = (static_cast<int64_t>(h) * W + w) * C;
+        v.q = *reinterpret_cast<const Raw*>(qb + at);
+        v.x = *reinterpret_cast<const Raw*>(xb + at);
+        return v;
+    };
+
+    // Row pass operands (directions 0, 1): tile row hh = 4 wv + k, lane n holds pixel
+    // (h0 + hh, w0 + n).  Issued first; consumed after the column pass.
+    const int wr = min(w0 + n, W - 1);
+    Pix4<T> rp[PER];
+    float4 m0[PER], m1[PER];
+    [[maybe_unused]] Raw ra[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int h = min(h0 + 4 * wv + k, H - 1);
+        rp[k] = load_pix(h, wr);
+        m0[k] = *reinterpret_cast<const float4*>(st[0] + h * (D * D));
+        m1[k] = *reinterpret_cast<const float4*>(st[1] + (H - 1 - h) * (D * D));
+        if (p.aux) ra[k] = *reinterpret_cast<const Raw*>(static_cast<const T*>(p.aux) + (b * L + static_cast<int64_t>(h) * W + wr) * C + cbase);
+    }
+
+    // Column pass (directions 2, 3): tile column ww = 4 wv + k, lane n holds pixel
+    // (h0 + n, w0 + ww).
     float wt[4][4], sk[4][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        st[r] = p.states + ((b * 4 + r) * p.heads + head) * p.max_chunks * (D * D) + n * D + 4 * g;
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             wt[r][j] = p.wgt[r * C + cbase + j];
             sk[r][j] = p.skip[(p.skip_per_dir ? r * C : 0) + cbase + j];
         }
-    }
-
-    // Directions 2 and 3: tile column ww, lane n holds pixel (h0 + n, w0 + ww).
-#pragma unroll 2
-    for (int ww = 0; ww < 16; ++ww) {
-        const int64_t w = w0 + ww;
-        if (w >= W) break;
-        const int64_t h = h0 + n;
-        float qv[4] = {0.f, 0.f, 0.f, 0.f}, xv[4] = {0.f, 0.f, 0.f, 0.f};
-        uint2 qraw = make_uint2(0u, 0u);
-        if (h < H) {
-            if constexpr (std::is_same<T, bf16_t>::value) {
-                qraw = *reinterpret_cast<const uint2*>(qb + (h * W + w) * C);
-                qv[0] = __uint_as_float(qraw.x << 16); qv[1] = __uint_as_float(qraw.x & 0xffff0000u);
-                qv[2] = __uint_as_float(qraw.y << 16); qv[3] = __uint_as_float(qraw.y & 0xffff0000u);
-            } else {
-                load4(qb + (h * W + w) * C, true, qv);
-            }
-            load4(xb + (h * W + w) * C, true, xv);
-        }
-        const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] +
-                                                        qv[3] * qv[3])), 1e-12f);
-        const float4 m2 = *reinterpret_cast<const float4*>(st[2] + w * (D * D));
-        const float4 m3 = *reinterpret_cast<const float4*>(st[3] + (W - 1 - w) * (D * D));
-        v4f y2 = {0.f, 0.f, 0.f, 0.f}, y3 = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (std::is_same<T, bf16_t>::value) {
-            const v4s qs = bf16x4_bits(qraw);
-            const float a2[4] = {m2.x, m2.y, m2.z, m2.w}, a3[4] = {m3.x, m3.y, m3.z, m3.w};
-            v4s h2, l2, h3, l3;
-            split_bf16(a2, h2, l2);
-            split_bf16(a3, h3, l3);
-            y2 = mfma_bf16(h2, qs, y2); y3 = mfma_bf16(h3, qs, y3);
-            y2 = mfma_bf16(l2, qs, y2); y3 = mfma_bf16(l3, qs, y3);
-        } else {
-            y2 = mfma4(m2.x, qv[0], y2); y3 = mfma4(m3.x, qv[0], y3);
-            y2 = mfma4(m2.y, qv[1], y2); y3 = mfma4(m3.y, qv[1], y3);
-            y2 = mfma4(m2.z, qv[2], y2); y3 = mfma4(m3.z, qv[2], y3);
-            y2 = mfma4(m2.w, qv[3], y2); y3 = mfma4(m3.w, qv[3], y3);
-        }
-        float* rec = col + (ww * 16 + n) * REC + 4 * g;
-        float c23[4];
+    {
+        const int hc = min(h0 + n, H - 1);
+        Pix4<T> cp[PER];
+        float4 m2[PER], m3[PER];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            c23[j] = wt[2][j] * (y2[j] * inv + sk[2][j] * xv[j]) + wt[3][j] * (y3[j] * inv + sk[3][j] * xv[j]);
-        *reinterpret_cast<float4*>(rec) = make_float4(c23[0], c23[1], c23[2], c23[3]);
+        for (int k = 0; k < PER; ++k) {
+            const int w = min(w0 + 4 * wv + k, W - 1);
+            cp[k] = load_pix(hc, w);
+            m2[k] = *reinterpret_cast<const float4*>(st[2] + w * (D * D));
+            m3[k] = *reinterpret_cast<const float4*>(st[3] + (W - 1 - w) * (D * D));
+        }
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            float qv[4], xv[4];
+            raw4_to_f32<T>(cp[k].q, qv);
+            raw4_to_f32<T>(cp[k].x, xv);
+            const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] +
+                                                            qv[3] * qv[3])), 1e-12f);
+            const v4f y2 = readout_mfma<T>(m2[k], cp[k].q, qv);
+            const v4f y3 = readout_mfma<T>(m3[k], cp[k].q, qv);
+            float c23[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                c23[j] = wt[2][j] * (y2[j] * inv + sk[2][j] * xv[j]) + wt[3][j] * (y3[j] * inv + sk[3][j] * xv[j]);
+            *reinterpret_cast<float4*>(col + ((4 * wv + k) * 16 + n) * REC + 4 * g) =
+                make_float4(c23[0], c23[1], c23[2], c23[3]);
+        }
     }
     __syncthreads();
 
-    // Directions 0 and 1: tile row hh, lane n holds pixel (h0 + hh, w0 + n).
-    const int64_t w = w0 + n;
-    const bool wvalid = w < W;
-#pragma unroll 2
-    for (int hh = 0; hh < 16; ++hh) {
-        const int64_t h = h0 + hh;
-        if (h >= H) break;
-        float qv[4] = {0.f, 0.f, 0.f, 0.f}, xv[4] = {0.f, 0.f, 0.f, 0.f};
-        uint2 qraw = make_uint2(0u, 0u);
-        if (wvalid) {
-            if constexpr (std::is_same<T, bf16_t>::value) {
-                qraw = *reinterpret_cast<const uint2*>(qb + (h * W + w) * C);
-                qv[0] = __uint_as_float(qraw.x << 16); qv[1] = __uint_as_float(qraw.x & 0xffff0000u);
-                qv[2] = __uint_as_float(qraw.y << 16); qv[3] = __uint_as_float(qraw.y & 0xffff0000u);
-            } else {
-                load4(qb + (h * W + w) * C, true, qv);
-            }
-            load4(xb + (h * W + w) * C, true, xv);
-        }
+    const int w = w0 + n;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int hh = 4 * wv + k, h = h0 + hh;
+        float qv[4], xv[4];
+        raw4_to_f32<T>(rp[k].q, qv);
+        raw4_to_f32<T>(rp[k].x, xv);
         const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] +
                                                         qv[3] * qv[3])), 1e-12f);
-        const float4 m0 = *reinterpret_cast<const float4*>(st[0] + h * (D * D));
-        const float4 m1 = *reinterpret_cast<const float4*>(st[1] + (H - 1 - h) * (D * D));
-        v4f y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (std::is_same<T, bf16_t>::value) {
-            const v4s qs = bf16x4_bits(qraw);
-            const float a0[4] = {m0.x, m0.y, m0.z, m0.w}, a1[4] = {m1.x, m1.y, m1.z, m1.w};
-            v4s h0, l0, h1, l1;
-            split_bf16(a0, h0, l0);
-            split_bf16(a1, h1, l1);
-            y0 = mfma_bf16(h0, qs, y0); y1 = mfma_bf16(h1, qs, y1);
-            y0 = mfma_bf16(l0, qs, y0); y1 = mfma_bf16(l1, qs, y1);
-        } else {
-            y0 = mfma4(m0.x, qv[0], y0); y1 = mfma4(m1.x, qv[0], y1);
-            y0 = mfma4(m0.y, qv[1], y0); y1 = mfma4(m1.y, qv[1], y1);
-            y0 = mfma4(m0.z, qv[2], y0); y1 = mfma4(m1.z, qv[2], y1);
-            y0 = mfma4(m0.w, qv[3], y0); y1 = mfma4(m1.w, qv[3], y1);
-        }
+        const v4f y0 = readout_mfma<T>(m0[k], rp[k].q, qv);
+        const v4f y1 = readout_mfma<T>(m1[k], rp[k].q, qv);
         const float4 c23 = *reinterpret_cast<const float4*>(col + (n * 16 + hh) * REC + 4 * g);
         const float c23v[4] = {c23.x, c23.y, c23.z, c23.w};
         float o[4];
@@ -1128,16 +1156,19 @@ __global__ __launch_bounds__(64) void srnl_readout16_kernel(const FuseParams p, 
         for (int j = 0; j < 4; ++j)
             o[j] = (wt[0][j] * (y0[j] * inv + sk[0][j] * xv[j]) + wt[1][j] * (y1[j] * inv + sk[1][j] * xv[j])) +
                    c23v[j];
-        if (wvalid) {
-            const int64_t at = (b * L + h * W + w) * C + cbase;
-            if (p.aux) {
-                float a[4];
-                load4(static_cast<const T*>(p.aux) + at, true, a);
+        if (p.aux) {
+            float a[4];
+            raw4_to_f32<T>(ra[k], a);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) o[j] += a[j];
-            }
+            for (int j = 0; j < 4; ++j) o[j] += a[j];
+        }
+        if (h < H && w < W) {
+            const int64_t at = (b * L + static_cast<int64_t>(h) * W + w) * C + cbase;
             if constexpr (sizeof(TO) == 4) {
                 *reinterpret_cast<float4*>(static_cast<float*>(p.out) + at) = make_float4(o[0], o[1], o[2], o[3]);
+            } else if constexpr (std::is_same<TO, bf16_t>::value) {
+                *reinterpret_cast<uint2*>(static_cast<TO*>(p.out) + at) =
+                    make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
             } else {
                 const uint32_t lo = static_cast<uint32_t>(from_f32<TO>(o[0]).bits) |
                                     (static_cast<uint32_t>(from_f32<TO>(o[1]).bits) << 16);
@@ -1371,10 +1402,10 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
             using T = decltype(tv);
             if (out_f32)
                 hipLaunchKernelGGL((srnl_readout16_kernel<T, float>), dim3(static_cast<unsigned>(n_tiles)),
-                                   dim3(64), 0, stream, fp, tiles_h, tiles_w);
+                                   dim3(256), 0, stream, fp, tiles_h, tiles_w);
             else
                 hipLaunchKernelGGL((srnl_readout16_kernel<T, T>), dim3(static_cast<unsigned>(n_tiles)),
-                                   dim3(64), 0, stream, fp, tiles_h, tiles_w);
+                                   dim3(256), 0, stream, fp, tiles_h, tiles_w);
         });
         if (rc) return rc;
         return check_launch("srnl_readout16_kernel");
