@@ -181,6 +181,17 @@ int vh_grn_forward(
     void* y, int32_t y_dtype, float* gx, float* inv_den, int64_t B, int64_t C, int64_t H, int64_t W,
     float eps, void* workspace, size_t workspace_bytes, void* stream);
 
+/* GRN statistics only, for consumers that apply GRN while loading its input
+ * (vh_pointwise_conv_nhwc_forward): gx [B, C], inv_den [B] as vh_grn_forward, and
+ * scale [B, C] = 1 + gamma * gx * inv_den, so that GRN(x) = x * scale + beta.
+ * Channels-last x [B, H, W, C] (C % 8 == 0, C <= 2048, 16-byte aligned); same
+ * workspace as vh_grn_forward.  Splits grn_forward_cuda
+ * (utils/csrc/grn_cuda.cu:290-320) at its statistics/apply boundary. */
+int vh_grn_scale_forward(
+    const void* x, int32_t io_dtype, const float* gamma, float* gx, float* inv_den, float* scale,
+    int64_t B, int64_t C, int64_t H, int64_t W, float eps, void* workspace,
+    size_t workspace_bytes, void* stream);
+
 /* LayerNorm over C for every pixel of x [B, C, H, W] (channels_last = 1: NHWC
  * storage, 0: NCHW storage), biased variance, y in the same storage order,
  * computed in fp32 and stored as y_dtype (VH_DTYPE_F32 is the reference's
@@ -229,6 +240,25 @@ int vh_dwconv2d_nhwc_forward(
     const void* x, int32_t io_dtype, const float* taps, const float* bias, int32_t ksize,
     int32_t epilogue, const void* aux, void* out, int64_t B, int64_t H, int64_t W, int64_t C,
     void* stream);
+
+/* 1x1 convolution on channels-last bf16 maps as a GEMM on the matrix cores:
+ * out [M, N] = epi(x' [M, K] . weight^T + bias) with weight [N, K] bf16 (the 1x1
+ * kernel as stored, cast to bf16 as autocast casts it), bias [N] fp32 (or NULL),
+ * M = B*H*W pixels, K % 32 == 0, N = 32, 64 or a multiple of 128,
+ * 16-byte aligned tensors.  The linear result is rounded to bf16 first, as the
+ * reference's autocast linear output is; then
+ *   epilogue 0: out = that value                              (proj_in, local_gate, W_q, proj_out)
+ *   epilogue 1: out = bf16(gelu(that value))                  (ffn.fc1 + ffn.act)
+ *   epilogue 2: out = bf16(residual + that value), residual [M, N] bf16  (ffn.fc2 + residual add)
+ * With grn_scale [M / pixels_per_image, K] and grn_beta [K] (both fp32, or both NULL)
+ * the operand is x' = bf16(x * grn_scale[image] + grn_beta), the GRN output the
+ * reference feeds to ffn.fc2 (vh_grn_scale_forward gives the scale).  No counterpart
+ * in the reference's native code: it runs nn.Conv2d / nn.Linear and the GELU, GRN and
+ * residual add as separate ops (models/block.py:70-107, models/layers.py:67-80). */
+int vh_pointwise_conv_nhwc_forward(
+    const void* x, int32_t io_dtype, const void* weight, const float* bias, int32_t epilogue,
+    const void* residual, const float* grn_scale, const float* grn_beta, int64_t pixels_per_image,
+    void* out, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Residual add on channels-last data: out[i] = residual[i] +
  * branch[i] * gamma[c] * drop_scale[b] (fp32 out; residual/branch io_dtype

@@ -136,6 +136,39 @@ def test_dwconv_rejects_bad_arguments(lib):
     assert b"aligned" in lib.vh_last_error()
 
 
+def test_pointwise_conv_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(0x1000)
+
+    def call(dtype=hip.VH_DTYPE_BF16, epilogue=0, residual=None, scale=None, beta=None, per_image=0,
+             m=64, n=64, k=64, x=p):
+        return lib.vh_pointwise_conv_nhwc_forward(x, dtype, p, p, epilogue, residual, scale, beta, per_image,
+                                                  p, m, n, k, None)
+
+    assert call(dtype=hip.VH_DTYPE_F32) == hip.VH_ERR_DTYPE
+    assert call(k=48) == hip.VH_ERR_SHAPE                # K % 32 != 0
+    assert call(n=96) == hip.VH_ERR_SHAPE                # not 32, 64 or a multiple of 128
+    assert call(n=48) == hip.VH_ERR_SHAPE
+    assert call(m=0) == hip.VH_ERR_SHAPE
+    assert call(epilogue=3) == hip.VH_ERR_ARG
+    assert call(epilogue=2) == hip.VH_ERR_ARG            # residual missing
+    assert call(scale=p) == hip.VH_ERR_ARG               # beta missing
+    assert call(scale=p, beta=p, per_image=48) == hip.VH_ERR_SHAPE   # M not a multiple of it
+    assert call(x=None) == hip.VH_ERR_ARG
+    assert call(x=ctypes.c_void_p(0x1008)) == hip.VH_ERR_ARG
+    assert b"aligned" in lib.vh_last_error()
+
+
+def test_grn_scale_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(0x1000)
+
+    def call(channels=64, ws=1 << 20, x=p):
+        return lib.vh_grn_scale_forward(x, hip.VH_DTYPE_BF16, p, p, p, p, 2, channels, 4, 4, 1e-6, p, ws, None)
+
+    assert call(x=None) == hip.VH_ERR_ARG
+    assert call(channels=12) == hip.VH_ERR_SHAPE
+    assert call(ws=16) == hip.VH_ERR_WORKSPACE
+
+
 def test_check_raises_with_message(lib):
     assert _spatial(lib, head_dim=12) == hip.VH_ERR_HEAD_DIM
     with pytest.raises(RuntimeError, match="head_dim"):

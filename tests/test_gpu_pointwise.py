@@ -1,0 +1,120 @@
+"""GPU parity of the matrix-core 1x1 convolution (``vh_pointwise_conv_nhwc_forward``) and
+of the GRN statistics entry (``vh_grn_scale_forward``).
+
+The GEMM is checked against the FP64 product of the same bf16 operands, with each fused
+step applied to the bf16-rounded value as the reference's autocast graph does; outputs
+are bf16, so the bar is a few bf16 roundings (normwise and elementwise 5e-3).  A second
+check runs the reference expression itself (``F.linear`` under bf16 autocast).
+"""
+
+import pytest
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from tests.helpers import assert_close, randn
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(t):
+    return t.to(torch.bfloat16)
+
+
+def _linear_ref(x, module):
+    """bf16(x W^T + b) in FP64 from the bf16 operands (CPU)."""
+    w = module.weight.detach().reshape(module.weight.shape[0], -1).cpu()
+    b = module.bias.detach().cpu()
+    y = x.double() @ _bf16(w).double().t() + _bf16(b).double()
+    return _bf16(y)
+
+
+@pytest.mark.parametrize("m", [1, 37, 256, 1000])
+@pytest.mark.parametrize("k,n", [(64, 32), (32, 32), (128, 64), (96, 128), (256, 128), (64, 256),
+                                 (1024, 256), (256, 1024), (512, 384), (2048, 512)])
+def test_pointwise_bias(device, m, k, n):
+    from visionhope_amd.utils import pointwise
+
+    conv = nn.Conv2d(k, n, 1)
+    with torch.no_grad():
+        conv.weight.copy_(randn(*conv.weight.shape, seed=1, scale=k ** -0.5))
+        conv.bias.copy_(randn(n, seed=2, scale=0.5))
+    x = _bf16(randn(m, k, seed=3))
+    got = pointwise.pointwise_conv(x.to(device), conv.to(device))
+    assert got.dtype == torch.bfloat16 and got.shape == (m, n)
+    assert_close(got.double().cpu().numpy(), _linear_ref(x, conv).double().numpy(), 5e-3, f"pw M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("k,n", [(64, 256), (256, 1024), (128, 64)])
+def test_pointwise_gelu(device, k, n):
+    from visionhope_amd.utils import pointwise
+
+    lin = nn.Linear(k, n)
+    x = _bf16(randn(3, 7, 11, k, seed=4))
+    got = pointwise.pointwise_conv(x.to(device), lin.to(device), pointwise.EPI_GELU)
+    expected = _bf16(F.gelu(_linear_ref(x, lin.cpu()).double()))
+    assert got.shape == (3, 7, 11, n)
+    assert_close(got.double().cpu().numpy(), expected.double().numpy(), 5e-3, "pw gelu")
+
+
+@pytest.mark.parametrize("k,n", [(256, 64), (1024, 256), (64, 32)])
+@pytest.mark.parametrize("with_grn", [False, True])
+def test_pointwise_residual_and_grn(device, k, n, with_grn):
+    """fc2 of the FFN: r + fc2(GRN(h)), the GRN applied to the operand as it is loaded."""
+    from visionhope_amd.utils import pointwise
+
+    images, h, w = 3, 5, 7          # 35 pixels per image: images split inside 16-row tiles
+    lin = nn.Linear(k, n)
+    x = _bf16(randn(images, h, w, k, seed=5))
+    r = _bf16(randn(images, h, w, n, seed=6))
+    grn = None
+    operand = x
+    if with_grn:
+        scale = 1 + randn(images, k, seed=7, scale=0.3)
+        beta = randn(k, seed=8, scale=0.2)
+        grn = (scale.to(device), beta.to(device))
+        # The kernel computes x * scale + beta in fp32 (one fused multiply-add); compare
+        # against that rounding, not the fp64 one, so the operands agree exactly.
+        operand = _bf16(torch.addcmul(beta.float(), x.float(), scale.float()[:, None, None, :]))
+    got = pointwise.pointwise_conv(x.to(device), lin.to(device), pointwise.EPI_ADD, residual=r.to(device), grn=grn)
+    expected = _bf16(r.double() + _linear_ref(operand, lin.cpu()).double())
+    assert_close(got.double().cpu().numpy(), expected.double().numpy(), 5e-3, f"pw add grn={with_grn}")
+
+
+def test_pointwise_matches_autocast_linear(device):
+    """The reference expression: F.linear under bf16 autocast (hipBLASLt), then GELU."""
+    from visionhope_amd.utils import pointwise
+
+    lin = nn.Linear(128, 512).to(device)
+    x = randn(4, 14, 14, 128, seed=9).to(device)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        ref = F.gelu(lin(x))
+    got = pointwise.pointwise_conv(_bf16(x), lin, pointwise.EPI_GELU)
+    assert ref.dtype == got.dtype == torch.bfloat16
+    assert_close(got.double().cpu().numpy(), ref.double().cpu().numpy(), 1e-2, "pw vs autocast linear")
+
+
+def test_pointwise_rejects_unsupported(device):
+    from visionhope_amd.utils import pointwise
+
+    with pytest.raises(ValueError):
+        pointwise.pointwise_conv(_bf16(randn(4, 48)).to(device), nn.Linear(48, 64).to(device))
+    with pytest.raises(ValueError):
+        pointwise.pointwise_conv(_bf16(randn(4, 64)).to(device), nn.Linear(64, 96).to(device))
+    with pytest.raises(ValueError):
+        pointwise.pointwise_conv(randn(4, 64).to(device), nn.Linear(64, 64).to(device))   # fp32 x
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_grn_scale_matches_grn(oracle, device, dtype):
+    """x * scale + beta reproduces the GRN output (oracle: utils/grn.py:26-38)."""
+    from visionhope_amd.utils.grn_cuda import grn_scale
+
+    x = randn(3, 64, 6, 5, seed=10).to(dtype).contiguous(memory_format=torch.channels_last)
+    gamma = randn(64, seed=11, scale=0.2)
+    beta = randn(64, seed=12, scale=0.2)
+    scale = grn_scale(x.to(device), gamma.to(device), 1e-6)
+    assert scale.shape == (3, 64) and scale.dtype == torch.float32
+    y = x.float() * scale.cpu()[:, :, None, None] + beta[None, :, None, None]
+    expected = oracle.grn(x.float().numpy(), gamma.numpy(), beta.numpy())
+    assert_close(y.numpy(), expected, 2e-5, "GRN scale")

@@ -149,8 +149,11 @@ __global__ __launch_bounds__(256) void grn_partial_kernel(const T* __restrict__ 
 __global__ __launch_bounds__(256) void grn_finalize_kernel(const float* __restrict__ partial,
                                                           float* __restrict__ gx,
                                                           float* __restrict__ inv_den, int64_t C,
-                                                          int64_t nslab, float eps) {
+                                                          int64_t nslab, float eps,
+                                                          const float* __restrict__ gamma = nullptr,
+                                                          float* __restrict__ scale = nullptr) {
     __shared__ float wsum[4];
+    __shared__ float inv_sh;
     const int64_t b = blockIdx.x;
     float local = 0.f;
     for (int64_t c = threadIdx.x; c < C; c += 256) {
@@ -176,7 +179,19 @@ __global__ __launch_bounds__(256) void grn_finalize_kernel(const float* __restri
     __syncthreads();
     if (threadIdx.x == 0) {
         const float total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-        inv_den[b] = 1.f / (total / static_cast<float>(C) + eps);
+        const float inv = 1.f / (total / static_cast<float>(C) + eps);
+        inv_den[b] = inv;
+        inv_sh = inv;
+    }
+    if (scale) {
+        // The per-(image, channel) factor 1 + gamma nx of the apply step, for consumers
+        // that apply GRN as they load its input (same fp32 operations as grn_apply8).
+        __syncthreads();
+        const float inv = inv_sh;
+        for (int64_t c = threadIdx.x; c < C; c += 256) {
+            const float nx = gx[b * C + c] * inv;
+            scale[b * C + c] = 1.f + gamma[c] * nx;
+        }
     }
 }
 
@@ -686,6 +701,38 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
     });
     if (rc) return rc;
     return check_launch("grn kernels");
+}
+
+int vh_grn_scale_forward(const void* x, int32_t io_dtype, const float* gamma, float* gx, float* inv_den,
+                         float* scale, int64_t B, int64_t C, int64_t H, int64_t W, float eps, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+    VH_REQUIRE(x && gamma && gx && inv_den && scale, VH_ERR_ARG, "GRN statistics pointers must not be null");
+    VH_REQUIRE(B > 0 && C > 0 && H > 0 && W > 0, VH_ERR_SHAPE, "GRN expects nonempty input");
+    VH_REQUIRE(B <= 65535, VH_ERR_SHAPE, "GRN batch must be <= 65535, got %lld", (long long)B);
+    VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "GRN supports FP32, FP16 and BF16 input");
+    const int64_t S = H * W;
+    VH_REQUIRE(grn_vectorised(C, x, x) && B * S * C < (int64_t(1) << 31), VH_ERR_SHAPE,
+               "GRN statistics need C %% 8 == 0, C <= 2048, 16-byte aligned x and B*H*W*C < 2^31");
+    const size_t need = vh_grn_workspace_bytes(B, C, H, W);
+    VH_REQUIRE(workspace && workspace_bytes >= need, VH_ERR_WORKSPACE,
+               "GRN workspace needs %zu bytes, got %zu", need, workspace ? workspace_bytes : (size_t)0);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    float* partial = static_cast<float*>(workspace);
+    const int G = static_cast<int>(C / 8);
+    const int R = std::max(1, 256 / G);
+    const int rows = static_cast<int>(grn_rows_per_slab(B, S));
+    const int vslab = static_cast<int>((S + rows - 1) / rows);
+    const size_t red = static_cast<size_t>(R) * static_cast<size_t>(C) * sizeof(float);
+    int rc = dispatch_t(io_dtype, [&](auto tv) {
+        using T = decltype(tv);
+        hipLaunchKernelGGL((grn_partial8_kernel<T>), dim3(static_cast<unsigned>(vslab), static_cast<unsigned>(B)),
+                           dim3(G * R), red, s, static_cast<const T*>(x), partial, static_cast<int>(C),
+                           static_cast<int>(S), rows, vslab);
+        hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, partial, gx,
+                           inv_den, C, static_cast<int64_t>(vslab), eps, gamma, scale);
+    });
+    if (rc) return rc;
+    return check_launch("grn statistics kernels");
 }
 
 int vh_add_layernorm2d_forward(const void* x, const void* r, int32_t io_dtype, const float* weight,

@@ -9,10 +9,10 @@ from .droppath import DropPath
 from .layers import FeedForwardNetwork, LayerNorm2d, build_norm
 from .operator import VisionHOPEOperator
 from .srnl_core.fused import srnl_spatial_readout, srnl_spatial_scan
-from ..utils import dwconv
-from ..utils.cached_params import linear_weights
+from ..utils import dwconv, pointwise
+from ..utils.cached_params import contiguous_fp32, linear_weights
 from ..utils.grn import GlobalResponseNorm
-from ..utils.grn_cuda import visionhope_grn
+from ..utils.grn_cuda import grn_scale, visionhope_grn
 from ..utils.layer_norm_cuda import (can_fuse_add_layernorm2d, can_fuse_layernorm2d, visionhope_add_layernorm2d,
                                      visionhope_layernorm2d)
 from ..utils.residual import can_fuse_residual_add, visionhope_residual_add
@@ -32,6 +32,18 @@ def _side_stream(device):
 def _is_pointwise(conv):
     return (isinstance(conv, nn.Conv2d) and conv.kernel_size == (1, 1) and conv.stride == (1, 1)
             and conv.padding == (0, 0) and conv.groups == 1)
+
+
+def _matrix_core_ok(t_nhwc, module):
+    """Whether the bf16 matrix-core 1x1 kernel covers ``module`` on the NHWC view ``t``."""
+    weight = module.weight
+    return (t_nhwc.is_contiguous() and t_nhwc.data_ptr() % 16 == 0 and module.bias is not None
+            and pointwise.supported(weight.shape[1], weight.shape[0]) and t_nhwc.shape[-1] == weight.shape[1])
+
+
+def _grn_beta(grn):
+    """GRN beta as a contiguous FP32 ``[C]`` vector (cached while unchanged)."""
+    return contiguous_fp32(grn.beta.detach().reshape(-1))
 
 
 def _is_exact_gelu(act):
@@ -133,9 +145,14 @@ class VisionHOPEBlock(nn.Module):
         autocast = torch.is_autocast_enabled("cuda")
         act = torch.get_autocast_dtype("cuda") if autocast else torch.float32
 
-        def pointwise(t_nhwc, module):
+        def project(t_nhwc, module, epilogue=pointwise.EPI_BIAS):
+            # bf16: the matrix-core kernel with the epilogue fused; otherwise the
+            # library GEMM on the autocast-cast operands and the epilogue after it.
+            if act == torch.bfloat16 and _matrix_core_ok(t_nhwc, module):
+                return pointwise.pointwise_conv(t_nhwc, module, epilogue)
             weight, bias = linear_weights(module, act)
-            return F.linear(t_nhwc.to(act), weight, bias)
+            y = F.linear(t_nhwc.to(act), weight, bias)
+            return F.gelu(y) if epilogue == pointwise.EPI_GELU else y
 
         def nchw(t_nhwc):
             return t_nhwc.permute(0, 3, 1, 2)
@@ -145,9 +162,9 @@ class VisionHOPEBlock(nn.Module):
         # Token-mixer branch.
         h = visionhope_layernorm2d(x, self.norm1.weight, self.norm1.bias, self.norm1.eps,
                                    force_channels_last=True, out_dtype=act)
-        inner = pointwise(h.permute(0, 2, 3, 1), self.proj_in)
+        inner = project(h.permute(0, 2, 3, 1), self.proj_in)
         if self.local_mode == "gated_dwconv7":
-            gate = pointwise(inner, self.local_gate)
+            gate = project(inner, self.local_gate)
             x_local = dwconv.depthwise_conv(nchw(inner), self.local_conv, dwconv.EPI_GATE, aux=nchw(gate))
         elif self.local_mode == "residual_dwconv":
             x_local = dwconv.depthwise_conv(nchw(inner), self.local_conv, dwconv.EPI_ADD_INPUT)
@@ -157,7 +174,7 @@ class VisionHOPEBlock(nn.Module):
         if path == "ordinary":
             branch = self._spatial_tail(x_local, True)
         elif path == "spatial" and x_local.dtype == act:
-            branch = nchw(pointwise(self._spatial_overlapped(x_local), self.proj_out))
+            branch = nchw(project(self._spatial_overlapped(x_local), self.proj_out))
         else:
             out = self.operator._forward_fast(x_local, path)
             if self.local_position is not None:
@@ -165,7 +182,7 @@ class VisionHOPEBlock(nn.Module):
                 # rounded once to the compute dtype, the input dtype of proj_out.
                 out = dwconv.depthwise_conv(x_local, self.local_position, dwconv.EPI_ADD_F32_AUX,
                                             aux=out).permute(0, 2, 3, 1)
-            branch = nchw(pointwise(out, self.proj_out))
+            branch = nchw(project(out, self.proj_out))
         # Feed-forward branch (the residual add fused into norm2 when LayerScale is folded).
         ffn = self.ffn
         if self.gamma1 is None and can_fuse_add_layernorm2d(x, branch, self.norm2.weight, self.norm2.bias):
@@ -175,13 +192,23 @@ class VisionHOPEBlock(nn.Module):
             x = self._residual_add(x, branch, self.gamma1)
             h = visionhope_layernorm2d(x, self.norm2.weight, self.norm2.bias, self.norm2.eps,
                                        force_channels_last=True, out_dtype=act)
-        f = F.gelu(pointwise(h.permute(0, 2, 3, 1), ffn.fc1))
+        f = project(h.permute(0, 2, 3, 1), ffn.fc1, pointwise.EPI_GELU)
         if ffn.use_dwconv:
             f = dwconv.depthwise_conv(nchw(f), ffn.dwconv, dwconv.EPI_ADD_GELU).permute(0, 2, 3, 1)
-        if isinstance(ffn.grn, GlobalResponseNorm):
+        use_grn = isinstance(ffn.grn, GlobalResponseNorm)
+        x_nhwc = x.permute(0, 2, 3, 1)
+        if (act == torch.bfloat16 and self.gamma2 is None and x.dtype == act and x_nhwc.is_contiguous()
+                and _matrix_core_ok(f, ffn.fc2)):
+            # GRN applied to fc2's operand as it is loaded, residual add in fc2's epilogue.
+            grn = None
+            if use_grn:
+                grn = (grn_scale(nchw(f), ffn.grn.gamma, ffn.grn.eps), _grn_beta(ffn.grn))
+            out = pointwise.pointwise_conv(f, ffn.fc2, pointwise.EPI_ADD, residual=x_nhwc, grn=grn)
+            return nchw(out)
+        if use_grn:
             f = visionhope_grn(nchw(f), ffn.grn.gamma, ffn.grn.beta, ffn.grn.eps,
                                out_dtype=act).permute(0, 2, 3, 1)
-        branch = nchw(pointwise(f, ffn.fc2))
+        branch = nchw(project(f, ffn.fc2))
         return self._residual_add(x, branch, self.gamma2)
 
     def _spatial_overlapped(self, x_local):
@@ -211,8 +238,11 @@ class VisionHOPEBlock(nn.Module):
         side.wait_stream(main)
         with torch.cuda.stream(side), torch.autocast("cuda", enabled=False):
             # Operands already in the compute dtype: the product autocast would run.
-            weight, bias = linear_weights(op.W_q, x_local.dtype)
-            torch.addmm(bias, x_nhwc.reshape(-1, channels), weight.t(), out=q.view(-1, channels))
+            if x_local.dtype == torch.bfloat16 and _matrix_core_ok(x_nhwc, op.W_q):
+                pointwise.pointwise_conv(x_nhwc, op.W_q, out=q)
+            else:
+                weight, bias = linear_weights(op.W_q, x_local.dtype)
+                torch.addmm(bias, x_nhwc.reshape(-1, channels), weight.t(), out=q.view(-1, channels))
             if lepe is not None:
                 dwconv.depthwise_conv(x_local, self.local_position, dwconv.EPI_PLAIN, out=lepe)
         ws = srnl_spatial_scan(memories, x_nhwc, chunks)

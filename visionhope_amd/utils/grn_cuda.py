@@ -62,3 +62,26 @@ def visionhope_grn(x, gamma, beta, eps, out_dtype=torch.float32):
     if x.shape[0] < 1 or x.shape[0] > 65535:
         raise ValueError("GRN expects nonempty input and batch <= 65535")
     return _VisionHOPEGRNFunction.apply(x, gamma, beta, eps, out_dtype)
+
+
+@on_tensor_device
+def grn_scale(x, gamma, eps):
+    """GRN statistics of the channels-last map ``x [B, C, H, W]``: the FP32 factor
+    ``scale [B, C] = 1 + gamma * nx`` with ``GRN(x) = x * scale + beta``
+    (``utils/grn.py:26-38``), for consumers that apply it while loading x."""
+    batch, channels, height, width = x.shape
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32) or not 1 <= batch <= 65535:
+        raise ValueError("GRN statistics expect FP32/FP16/BF16 input and 1 <= batch <= 65535")
+    if not x.is_contiguous(memory_format=torch.channels_last) or x.data_ptr() % 16:
+        raise ValueError("GRN statistics expect a 16-byte aligned channels-last map")
+    gamma = gamma.detach().reshape(-1).float().contiguous()
+    scale = torch.empty((batch, channels), device=x.device, dtype=torch.float32)
+    gx = torch.empty((batch, channels), device=x.device, dtype=torch.float32)
+    inv_den = torch.empty((batch,), device=x.device, dtype=torch.float32)
+    lib = hip.load_library()
+    ws = hip.workspace(lib.vh_grn_workspace_bytes(batch, channels, height, width), x.device)
+    hip.check(lib.vh_grn_scale_forward(
+        hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(gamma), hip.ptr(gx), hip.ptr(inv_den), hip.ptr(scale),
+        batch, channels, height, width, float(eps), hip.ptr(ws), ws.numel() * 4, hip.stream_of(x)),
+        "vh_grn_scale_forward")
+    return scale

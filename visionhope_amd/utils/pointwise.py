@@ -1,0 +1,98 @@
+"""1x1 convolutions of the VisionHOPE block as bf16 matrix-core GEMMs on channels-last maps.
+
+``pointwise_conv(x, module, epilogue)`` computes ``module`` (a 1x1 ``nn.Conv2d`` or an
+``nn.Linear``) on the NHWC view ``x [..., K]`` through ``vh_pointwise_conv_nhwc_forward``
+with the elementwise work around the projection fused:
+
+===============  ===========================================  ==============================
+epilogue         result (every step rounded to bf16)           reference expression
+===============  ===========================================  ==============================
+``EPI_BIAS``     x W^T + b                                     ``proj_in(x)``, ``fc1(x)`` ...
+``EPI_GELU``     gelu(x W^T + b)                               ``ffn.act(ffn.fc1(x))``
+``EPI_ADD``      r + (x W^T + b)                               ``x + ffn(...)`` (gamma folded)
+===============  ===========================================  ==============================
+
+With ``grn=(scale, beta)`` the operand is ``bf16(x * scale[image] + beta)``: the GRN output
+(``grn_scale`` gives the factor), applied as the operand is loaded
+(``models/block.py:70-107``, ``models/layers.py:67-80``).  Under bf16 autocast the
+reference rounds the same intermediates to bf16; only the fp32 summation order differs.
+"""
+
+import torch
+from torch import nn
+
+from . import hip
+from .cached_params import _key
+from .cuda import on_tensor_device
+
+EPI_BIAS, EPI_GELU, EPI_ADD = range(3)
+
+
+def is_pointwise(module):
+    """A Linear or an unpadded, ungrouped, stride-1 1x1 Conv2d."""
+    if isinstance(module, nn.Linear):
+        return True
+    return (isinstance(module, nn.Conv2d) and module.kernel_size == (1, 1) and module.stride == (1, 1)
+            and module.padding == (0, 0) and module.groups == 1 and module.dilation == (1, 1))
+
+
+def supported(in_features, out_features):
+    """Shapes the matrix-core kernel covers (K % 32 == 0; N = 32, 64 or a multiple of 128)."""
+    n, k = out_features, in_features
+    return k % 32 == 0 and (n in (32, 64) or n % 128 == 0)
+
+
+def pointwise_operands(module):
+    """``(weight [N, K] bf16, bias [N] fp32 holding bf16-rounded values or None)``: what
+    autocast casts the parameters to on every call, cached on the module while both are
+    unchanged."""
+    w, b = module.weight, module.bias
+    key = (_key(w), None if b is None else _key(b))
+    cached = getattr(module, "_vh_pointwise", None)
+    if cached is None or cached[0] != key:
+        weight = w.detach().reshape(w.shape[0], -1).to(torch.bfloat16).contiguous()
+        bias = None if b is None else b.detach().to(torch.bfloat16).float().contiguous()
+        object.__setattr__(module, "_vh_pointwise", (key, weight, bias))
+        cached = module._vh_pointwise
+    return cached[1], cached[2]
+
+
+@on_tensor_device
+def pointwise_conv(x, module, epilogue=EPI_BIAS, residual=None, grn=None, out=None):
+    """``x [..., K]`` contiguous bf16 (an NHWC map) -> ``[..., N]`` bf16 (module docstring).
+
+    ``residual`` (``EPI_ADD``) is shaped like the output; ``grn`` is ``(scale [B, K],
+    beta [K])`` FP32 for an ``x`` of ``B`` images of equal size; ``out`` receives the
+    result when given (contiguous, shaped like the output).
+    """
+    if not x.is_cuda or x.dtype != torch.bfloat16 or not x.is_contiguous() or x.data_ptr() % 16:
+        raise ValueError("pointwise_conv expects a contiguous 16-byte aligned CUDA bf16 tensor")
+    weight, bias = pointwise_operands(module)
+    n, k = weight.shape
+    if x.shape[-1] != k or not supported(k, n):
+        raise ValueError(f"pointwise_conv does not cover K={x.shape[-1]} -> N={n}")
+    m = x.numel() // k
+    shape = (*x.shape[:-1], n)
+    if out is None:
+        out = torch.empty(shape, device=x.device, dtype=torch.bfloat16)
+    elif out.shape != shape or out.dtype != torch.bfloat16 or not out.is_contiguous() or out.data_ptr() % 16:
+        raise ValueError("out must be a contiguous bf16 tensor shaped like the result")
+    if epilogue == EPI_ADD:
+        if (residual is None or residual.shape != shape or residual.dtype != torch.bfloat16
+                or not residual.is_contiguous() or residual.data_ptr() % 16):
+            raise ValueError("EPI_ADD needs a contiguous bf16 residual shaped like the result")
+    scale = beta = None
+    per_image = 0
+    if grn is not None:
+        scale, beta = grn
+        images = scale.shape[0]
+        if (scale.dtype != torch.float32 or beta.dtype != torch.float32 or scale.shape != (images, k)
+                or beta.numel() != k or m % images or not scale.is_contiguous() or not beta.is_contiguous()):
+            raise ValueError("grn needs FP32 scale [images, K] and beta [K]")
+        per_image = m // images
+    lib = hip.load_library()
+    hip.check(lib.vh_pointwise_conv_nhwc_forward(
+        hip.ptr(x), hip.VH_DTYPE_BF16, hip.ptr(weight), hip.ptr(bias), int(epilogue), hip.ptr(residual),
+        hip.ptr(scale), hip.ptr(beta), per_image, hip.ptr(out), m, n, k, hip.stream_of(x)),
+        "vh_pointwise_conv_nhwc_forward")
+    return out
