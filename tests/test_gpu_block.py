@@ -150,6 +150,34 @@ def test_fused_block_matches_oracle(oracle, device, local_mode, autocast):
                  f"fused block {local_mode} autocast={autocast}")
 
 
+@pytest.mark.parametrize("dim", [32, 64, 128])
+@pytest.mark.parametrize("native_gemm", [False, True])
+def test_fused_block_bf16_gemm_paths(oracle, device, monkeypatch, dim, native_gemm):
+    """bf16 autocast through either 1x1 path: the native matrix-core kernel for every
+    projection (fc1 + GELU, fc2 with the GRN apply and the residual add fused), or the
+    library GEMM for the wide ones, as small maps take by default."""
+    from visionhope_amd.inference.prepare import prepare_for_inference
+    from visionhope_amd.models import block as block_mod
+    from visionhope_amd.models.block import VisionHOPEBlock
+
+    if native_gemm:
+        monkeypatch.setattr(block_mod, "_MATRIX_CORE_MIN_PIXELS", 0)
+    torch.manual_seed(17)
+    block = VisionHOPEBlock(dim, head_dim=16)
+    perturb_block(block, seed=18)
+    reference = copy.deepcopy(block)
+    prepare_for_inference(reference)
+    gpu = block.to(device).to(memory_format=torch.channels_last)
+    prepare_for_inference(gpu)
+    x = randn(3, dim, 7, 12, seed=19)
+    expected = _cpu_block_reference(reference, x, oracle).numpy()
+    x_dev = x.to(device).contiguous(memory_format=torch.channels_last).bfloat16()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        out = gpu(x_dev)
+    assert out.dtype == torch.bfloat16
+    assert_close(out.double().cpu().numpy(), expected, 2e-2, f"fused block dim={dim} native={native_gemm}")
+
+
 def test_fused_block_falls_back_for_odd_layouts(device):
     from visionhope_amd.inference.prepare import prepare_for_inference
     from visionhope_amd.models.block import VisionHOPEBlock

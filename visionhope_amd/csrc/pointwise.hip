@@ -19,6 +19,8 @@
 // with 4 consecutive output channels of one pixel (one 8-byte store).  Any order of the
 // 32 k inside the instruction gives the same sum, as A and B use the same one.
 #include <algorithm>
+#include <cstdlib>
+#include <type_traits>
 
 #include "vh_common.h"
 
@@ -75,15 +77,52 @@ __device__ __forceinline__ float round_bf16(float v) {
 // Output channels are interleaved across pairs of 16-row MFMA tiles (tile 2p row r
 // is channel 32p + 8(r/4) + r%4, tile 2p+1 row r is channel 32p + 8(r/4) + 4 + r%4),
 // so each lane ends with 8 consecutive channels of one pixel: one 16-byte store.
-constexpr int PW_BK = 64, PW_LDS_ROW = PW_BK + 8;
+// Epilogue of one tile pair: lane holds channels n .. n+7 (from acc0 = tile 2q,
+// acc1 = tile 2q+1) of pixel m.
+template <int EPI>
+__device__ __forceinline__ void pw_store8(const PwParams& p, int64_t m, int n, const float (&bv)[8], const v4f_pw& acc0,
+                                          const v4f_pw& acc1) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = round_bf16(acc0[j] + bv[j]);
+        v[4 + j] = round_bf16(acc1[j] + bv[4 + j]);
+    }
+    if constexpr (EPI == PW_GELU) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = gelu_fast(v[j]);
+    } else if constexpr (EPI == PW_ADD) {
+        const uint4 r = *reinterpret_cast<const uint4*>(p.res + m * p.N + n);
+        v[0] += bf16_lo(r.x); v[1] += bf16_hi(r.x); v[2] += bf16_lo(r.y); v[3] += bf16_hi(r.y);
+        v[4] += bf16_lo(r.z); v[5] += bf16_hi(r.z); v[6] += bf16_lo(r.w); v[7] += bf16_hi(r.w);
+    }
+    *reinterpret_cast<uint4*>(p.out + m * p.N + n) =
+        make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+}
 
-template <int BM, int BN, int WGM, int EPI, bool PRO>
+__device__ __forceinline__ void pw_bias8(const PwParams& p, int n, float (&bv)[8]) {
+    if (p.bias) {
+        const float4 b0 = *reinterpret_cast<const float4*>(p.bias + n);
+        const float4 b1 = *reinterpret_cast<const float4*>(p.bias + n + 4);
+        bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w; bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bv[j] = 0.f;
+    }
+}
+
+// Row of w feeding MFMA row i16 of n tile tn, for the channel interleave above.
+__device__ __forceinline__ int pw_wrow(int tn, int i16) { return 32 * (tn / 2) + 8 * (i16 / 4) + 4 * (tn % 2) + (i16 % 4); }
+
+template <int BM, int BN, int WGM, int BK, int EPI, bool PRO>
 __global__ __launch_bounds__(256) void pointwise_gemm_kernel(const PwParams p) {
+    constexpr int PW_BK = BK, PW_LDS_ROW = BK + 8;
     static_assert(WGM == 1 || WGM == 2 || WGM == 4, "4 waves");
     constexpr int WGN = 4 / WGM, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
     static_assert(TN % 2 == 0 && TM >= 1, "n tiles come in pairs");
-    constexpr int A_CHUNKS = BM * PW_BK / 8 / 256, B_CHUNKS = BN * PW_BK / 8 / 256;   // 16-byte chunks per thread
-    static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small for 256 threads");
+    // 16-byte chunks of a k tile: CPR per row; per thread ceil(total / 256).
+    constexpr int CPR = PW_BK / 8, A_TOTAL = BM * CPR, B_TOTAL = BN * CPR;
+    constexpr int A_CHUNKS = (A_TOTAL + 255) / 256, B_CHUNKS = (B_TOTAL + 255) / 256;
     __shared__ __align__(16) bf16_t lds[2][(BM + BN) * PW_LDS_ROW];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
@@ -93,16 +132,16 @@ __global__ __launch_bounds__(256) void pointwise_gemm_kernel(const PwParams p) {
     const int K = p.K;
     const int ntiles = (K + PW_BK - 1) / PW_BK;
 
-    // Global chunk c of a tile: row c / 8, k offset 8 (c % 8).
+    // Global chunk c of a tile: row c / CPR, k offset 8 (c % CPR).
     uint4 ra[A_CHUNKS], rb[B_CHUNKS];
     auto gload = [&](int t) {
         const int kt = t * PW_BK;
 #pragma unroll
         for (int i = 0; i < A_CHUNKS; ++i) {
-            const int c = tid + 256 * i, row = c >> 3, kk = kt + 8 * (c & 7);
+            const int c = tid + 256 * i, row = c / CPR, kk = kt + 8 * (c % CPR);
             const int64_t m = std::min<int64_t>(m0 + row, p.M - 1);
             uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if (kk < K) {
+            if (kk < K && (A_TOTAL % 256 == 0 || c < A_TOTAL)) {
                 v = *reinterpret_cast<const uint4*>(p.x + m * K + kk);
                 if constexpr (PRO) {
                     const int64_t img = fast_div(static_cast<uint32_t>(m), p.rows_per_image);
@@ -113,9 +152,10 @@ __global__ __launch_bounds__(256) void pointwise_gemm_kernel(const PwParams p) {
         }
 #pragma unroll
         for (int i = 0; i < B_CHUNKS; ++i) {
-            const int c = tid + 256 * i, row = c >> 3, kk = kt + 8 * (c & 7);
-            rb[i] = kk < K ? *reinterpret_cast<const uint4*>(p.w + static_cast<int64_t>(n0 + row) * K + kk)
-                           : make_uint4(0u, 0u, 0u, 0u);
+            const int c = tid + 256 * i, row = c / CPR, kk = kt + 8 * (c % CPR);
+            rb[i] = (kk < K && (B_TOTAL % 256 == 0 || c < B_TOTAL))
+                        ? *reinterpret_cast<const uint4*>(p.w + static_cast<int64_t>(n0 + row) * K + kk)
+                        : make_uint4(0u, 0u, 0u, 0u);
         }
     };
     auto lstore = [&](int buf) {
@@ -123,19 +163,21 @@ __global__ __launch_bounds__(256) void pointwise_gemm_kernel(const PwParams p) {
 #pragma unroll
         for (int i = 0; i < A_CHUNKS; ++i) {
             const int c = tid + 256 * i;
-            *reinterpret_cast<uint4*>(base + (c >> 3) * PW_LDS_ROW + 8 * (c & 7)) = ra[i];
+            if (A_TOTAL % 256 == 0 || c < A_TOTAL)
+                *reinterpret_cast<uint4*>(base + (c / CPR) * PW_LDS_ROW + 8 * (c % CPR)) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < B_CHUNKS; ++i) {
             const int c = tid + 256 * i;
-            *reinterpret_cast<uint4*>(base + (BM + (c >> 3)) * PW_LDS_ROW + 8 * (c & 7)) = rb[i];
+            if (B_TOTAL % 256 == 0 || c < B_TOTAL)
+                *reinterpret_cast<uint4*>(base + (BM + c / CPR) * PW_LDS_ROW + 8 * (c % CPR)) = rb[i];
         }
     };
     // Row of w feeding MFMA row i16 of n tile tn (channel interleave above).
     int wrow[TN];
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
-        wrow[tn] = wn * WN + 32 * (tn / 2) + 8 * (i16 / 4) + 4 * (tn % 2) + (i16 % 4);
+        wrow[tn] = wn * WN + pw_wrow(tn, i16);
 
     v4f_pw acc[TN][TM];
 #pragma unroll
@@ -174,53 +216,116 @@ __global__ __launch_bounds__(256) void pointwise_gemm_kernel(const PwParams p) {
     for (int q = 0; q < TN / 2; ++q) {
         const int n = n0 + wn * WN + 32 * q + 8 * kg;
         float bv[8];
-        if (p.bias) {
-            const float4 b0 = *reinterpret_cast<const float4*>(p.bias + n);
-            const float4 b1 = *reinterpret_cast<const float4*>(p.bias + n + 4);
-            bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w; bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) bv[j] = 0.f;
-        }
+        pw_bias8(p, n, bv);
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
             const int64_t m = m0 + wm * WM + 16 * tm + i16;
-            if (m >= p.M) continue;
-            float v[8];
+            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm]);
+        }
+    }
+}
+
+// Narrow outputs (N = 32 or 64) with K <= 256: no LDS.  A wave owns 16 TM pixels and
+// every output channel; it issues all loads of its x rows at once (TM * KS 16-byte
+// fragments), reads the small weight fragments through L1 and writes each pixel's
+// channels once.
+template <int KS, int TN, int TM, int EPI, bool PRO>
+__global__ __launch_bounds__(256) void pointwise_narrow_kernel(const PwParams p) {
+    static_assert(TN % 2 == 0, "n tiles come in pairs");
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, i16 = lane & 15, kg = lane >> 4;
+    const int64_t m_wave = (static_cast<int64_t>(xcd_remap_any(blockIdx.x, gridDim.x)) * 4 + wv) * (16 * TM);
+    if (m_wave >= p.M) return;
+    constexpr int K = 32 * KS;
+    uint4 xf[TM][KS];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[j] = round_bf16(acc[2 * q][tm][j] + bv[j]);
-                v[4 + j] = round_bf16(acc[2 * q + 1][tm][j] + bv[4 + j]);
-            }
-            if constexpr (EPI == PW_GELU) {
+    for (int tm = 0; tm < TM; ++tm) {
+        const int64_t m = std::min<int64_t>(m_wave + 16 * tm + i16, p.M - 1);
+        const bf16_t* xr = p.x + m * K + 8 * kg;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = gelu_fast(v[j]);
-            } else if constexpr (EPI == PW_ADD) {
-                const uint4 r = *reinterpret_cast<const uint4*>(p.res + m * p.N + n);
-                v[0] += bf16_lo(r.x); v[1] += bf16_hi(r.x); v[2] += bf16_lo(r.y); v[3] += bf16_hi(r.y);
-                v[4] += bf16_lo(r.z); v[5] += bf16_hi(r.z); v[6] += bf16_lo(r.w); v[7] += bf16_hi(r.w);
-            }
-            *reinterpret_cast<uint4*>(p.out + m * p.N + n) =
-                make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                           pack_bf16x2(v[6], v[7]));
+        for (int ks = 0; ks < KS; ++ks) xf[tm][ks] = *reinterpret_cast<const uint4*>(xr + 32 * ks);
+        if constexpr (PRO) {
+            const int64_t img = fast_div(static_cast<uint32_t>(m), p.rows_per_image);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                xf[tm][ks] = grn_apply8(xf[tm][ks], p.pro_scale + img * K + 32 * ks + 8 * kg, p.pro_shift + 32 * ks + 8 * kg);
+        }
+    }
+    v4f_pw acc[TN][TM];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = v4f_pw{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        uint4 wf[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+            wf[tn] = *reinterpret_cast<const uint4*>(p.w + pw_wrow(tn, i16) * K + 32 * ks + 8 * kg);
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = mfma_16x16x32(wf[tn], xf[tm][ks], acc[tn][tm]);
+    }
+#pragma unroll
+    for (int q = 0; q < TN / 2; ++q) {
+        const int n = 32 * q + 8 * kg;
+        float bv[8];
+        pw_bias8(p, n, bv);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            const int64_t m = m_wave + 16 * tm + i16;
+            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm]);
         }
     }
 }
 
 namespace {
 
-// Tiles: N = 32 or 64 -> one block per 256 pixels x all N (x is read once);
-// N % 128 == 0 -> 128 x 128 blocks.
+// Narrow outputs (N = 32, 64) with K <= 64 take the LDS-free kernel with 64 pixels per
+// wave; the rest the LDS-tiled one (N = 32, 64: 256 pixels x all N per block, k step
+// 32; N % 128 == 0: 128 x 128, k step 64).  Measured on MI355X at the Tiny shapes.
+// VH_PW_CFG selects a variant for measurements: "n<TM>" (narrow, 16 TM pixels per
+// wave, K <= 256) or "w<BK>" (tiled, k step BK = 32 or 64).
 template <int EPI, bool PRO>
 int launch_pw(const PwParams& p, hipStream_t s) {
-    auto go = [&](auto kern, int bm, int bn) {
-        const dim3 grid(static_cast<unsigned>((p.M + bm - 1) / bm), static_cast<unsigned>(p.N / bn));
+    int narrow_tm = 4, bk = p.N <= 64 ? 32 : 64;
+    bool narrow = (p.N == 32 || p.N == 64) && (p.K == 32 || p.K == 64);
+    const bool narrow_ok = (p.N == 32 || p.N == 64) && (p.K == 32 || p.K == 64 || p.K == 128 || p.K == 256);
+    if (const char* env = std::getenv("VH_PW_CFG")) {
+        if (env[0] == 'n' && narrow_ok) { narrow = true; narrow_tm = std::atoi(env + 1); }
+        if (env[0] == 'w') { narrow = false; bk = std::atoi(env + 1); }
+    }
+    auto go = [&](auto kern, int64_t rows, int cols) {
+        const dim3 grid(static_cast<unsigned>((p.M + rows - 1) / rows), static_cast<unsigned>(p.N / cols));
         hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, p);
         return check_launch("pointwise_gemm_kernel");
     };
-    if (p.N == 32) return go(pointwise_gemm_kernel<256, 32, 4, EPI, PRO>, 256, 32);
-    if (p.N == 64) return go(pointwise_gemm_kernel<256, 64, 4, EPI, PRO>, 256, 64);
-    return go(pointwise_gemm_kernel<128, 128, 2, EPI, PRO>, 128, 128);
+    if (narrow) {
+        auto pick = [&](auto ks_c) {
+            constexpr int KS = decltype(ks_c)::value;
+            auto with_tn = [&](auto tn_c) {
+                constexpr int TN = decltype(tn_c)::value;
+                if (narrow_tm == 1) return go(pointwise_narrow_kernel<KS, TN, 1, EPI, PRO>, 64, p.N);
+                if (narrow_tm == 4) return go(pointwise_narrow_kernel<KS, TN, 4, EPI, PRO>, 256, p.N);
+                return go(pointwise_narrow_kernel<KS, TN, 2, EPI, PRO>, 128, p.N);
+            };
+            return p.N == 32 ? with_tn(std::integral_constant<int, 2>{}) : with_tn(std::integral_constant<int, 4>{});
+        };
+        switch (p.K) {
+            case 32: return pick(std::integral_constant<int, 1>{});
+            case 64: return pick(std::integral_constant<int, 2>{});
+            case 128: return pick(std::integral_constant<int, 4>{});
+            default: return pick(std::integral_constant<int, 8>{});
+        }
+    }
+    if (bk == 32) {
+        if (p.N == 32) return go(pointwise_gemm_kernel<256, 32, 4, 32, EPI, PRO>, 256, 32);
+        if (p.N == 64) return go(pointwise_gemm_kernel<256, 64, 4, 32, EPI, PRO>, 256, 64);
+        return go(pointwise_gemm_kernel<128, 128, 2, 32, EPI, PRO>, 128, 128);
+    }
+    if (p.N == 32) return go(pointwise_gemm_kernel<256, 32, 4, 64, EPI, PRO>, 256, 32);
+    if (p.N == 64) return go(pointwise_gemm_kernel<256, 64, 4, 64, EPI, PRO>, 256, 64);
+    return go(pointwise_gemm_kernel<128, 128, 2, 64, EPI, PRO>, 128, 128);
 }
 
 }  // namespace
