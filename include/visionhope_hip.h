@@ -260,6 +260,17 @@ int vh_pointwise_conv_nhwc_forward(
     const void* residual, const float* grn_scale, const float* grn_beta, int64_t pixels_per_image,
     void* out, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Per-channel bias and optional exact GELU on a channels-last map x [pixels, C]
+ * (io_dtype, C % 8 == 0, 16-byte aligned; out may alias x):
+ * out = act(round(x + bias)), act 0 = identity, 1 = GELU, rounded to io_dtype after
+ * each step.  With a BatchNorm folded into the preceding convolution's weights this
+ * is the BatchNorm output and its activation in the stem and downsample layers
+ * (models/layers.py:85-119).  No counterpart in the reference's native code (it runs
+ * nn.BatchNorm2d and nn.GELU). */
+int vh_bias_act_nhwc_forward(
+    const void* x, int32_t io_dtype, const float* bias, int32_t act, void* out,
+    int64_t total, int64_t channels, void* stream);
+
 /* Residual add on channels-last data: out[i] = residual[i] +
  * branch[i] * gamma[c] * drop_scale[b] (fp32 out; residual/branch io_dtype
  * each).  Replaces the Triton _residual_forward_kernel (utils/residual.py:31-52). */

@@ -169,6 +169,19 @@ def test_grn_scale_rejects_bad_arguments(lib):
     assert call(ws=16) == hip.VH_ERR_WORKSPACE
 
 
+def test_bias_act_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(0x1000)
+
+    def call(act=0, total=64, channels=16, x=p, dtype=hip.VH_DTYPE_BF16):
+        return lib.vh_bias_act_nhwc_forward(x, dtype, p, act, p, total, channels, None)
+
+    assert call(act=2) == hip.VH_ERR_ARG
+    assert call(channels=12) == hip.VH_ERR_SHAPE
+    assert call(total=40) == hip.VH_ERR_SHAPE           # not a whole number of pixels
+    assert call(dtype=9) == hip.VH_ERR_DTYPE
+    assert call(x=None) == hip.VH_ERR_ARG
+
+
 def test_check_raises_with_message(lib):
     assert _spatial(lib, head_dim=12) == hip.VH_ERR_HEAD_DIM
     with pytest.raises(RuntimeError, match="head_dim"):

@@ -164,3 +164,47 @@ def test_layernorm2d_bf16_store_is_round_to_nearest_even(device, channels):
     y16 = visionhope_layernorm2d(x, w, b, 1e-6, out_dtype=torch.bfloat16)
     assert y16.dtype == torch.bfloat16
     assert torch.equal(y16.view(torch.int16), y32.to(torch.bfloat16).view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("act", [0, 1])
+def test_bias_act(device, dtype, act):
+    """act(round(x + b)) per channel: the folded BatchNorm output and its GELU."""
+    from visionhope_amd.utils.conv_bn import bias_act
+
+    x = randn(2, 24, 5, 7, seed=41).to(dtype).contiguous(memory_format=torch.channels_last)
+    b = randn(24, seed=42)
+    got = bias_act(x.to(device), b.to(device), act)
+    y = (x.double() + b.double()[None, :, None, None]).to(dtype).double()
+    expected = torch.nn.functional.gelu(y).to(dtype) if act else y.to(dtype)
+    assert got.dtype == dtype
+    assert_close(got.double().cpu().numpy(), expected.double().numpy(), 1e-5 if dtype == torch.float32 else 4e-3,
+                 f"bias_act act={act}")
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_stem_and_downsample_fold_batchnorm(device, autocast):
+    """Prepared stem / downsample (BatchNorm folded into the convolution) against the
+    same modules unfolded, with BatchNorm statistics far from identity."""
+    from visionhope_amd.models.layers import Downsample, PatchEmbedding
+
+    torch.manual_seed(5)
+    for mod, x in ((PatchEmbedding(3, 64), randn(2, 3, 32, 32, seed=43)),
+                   (Downsample(64, 128), randn(2, 64, 14, 14, seed=44))):
+        for m in mod.modules():
+            if isinstance(m, torch.nn.BatchNorm2d):
+                with torch.no_grad():
+                    m.running_mean.copy_(randn(m.num_features, seed=45, scale=0.5))
+                    m.running_var.copy_(randn(m.num_features, seed=46).abs() + 0.5)
+                    m.weight.copy_(1 + randn(m.num_features, seed=47, scale=0.2))
+                    m.bias.copy_(randn(m.num_features, seed=48, scale=0.2))
+        mod = mod.to(device).to(memory_format=torch.channels_last).eval()
+        xd = x.to(device).contiguous(memory_format=torch.channels_last)
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+            expected = mod(xd)
+            mod._vh_fold_bn = True
+            got = mod(xd)
+            mod._vh_fold_bn = False
+        assert got.dtype == expected.dtype and got.shape == expected.shape
+        assert_close(got.double().cpu().numpy(), expected.double().cpu().numpy(), 2e-2 if autocast else 1e-5,
+                     f"{type(mod).__name__} folded autocast={autocast}")

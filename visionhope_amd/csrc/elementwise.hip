@@ -572,6 +572,30 @@ void launch_ln_nhwc(const void* x, const float* w, const float* b, void* yv, flo
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Per-channel bias + optional GELU on a channels-last map, 8 channels per thread:
+// out = act(round(x + b)), rounded to the io dtype after each step (the value a
+// BatchNorm folded into the preceding convolution produces, then its activation).
+// ---------------------------------------------------------------------------
+template <typename T, int ACT>
+__global__ __launch_bounds__(256) void bias_act8_kernel(const T* __restrict__ x, const float* __restrict__ bias,
+                                                       T* __restrict__ out, int64_t vectors, int channels) {
+    const int64_t v = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (v >= vectors) return;
+    const int64_t at = v * 8;
+    const int c = static_cast<int>(at % channels);
+    float a[8], b[8];
+    load8<T>(x + at, a);
+    load8<float>(bias + c, b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        a[j] = to_f32(from_f32<T>(a[j] + b[j]));
+        if constexpr (ACT == 1) a[j] = gelu_fast(a[j]);
+    }
+    store8<T>(out + at, a);
+}
+
 }  // namespace vh
 
 using namespace vh;
@@ -822,6 +846,32 @@ int vh_qnorm_forward(const void* q_raw, int32_t io_dtype, float* q, float* inv_n
     });
     if (rc) return rc;
     return check_launch("qnorm_kernel");
+}
+
+int vh_bias_act_nhwc_forward(const void* x, int32_t io_dtype, const float* bias, int32_t act, void* out,
+                             int64_t total, int64_t channels, void* stream) {
+    VH_REQUIRE(x && bias && out, VH_ERR_ARG, "bias + activation pointers must not be null");
+    VH_REQUIRE(total > 0 && channels > 0 && channels % 8 == 0 && total % channels == 0, VH_ERR_SHAPE,
+               "bias + activation needs C %% 8 == 0 and a whole number of pixels");
+    VH_REQUIRE(act == 0 || act == 1, VH_ERR_ARG, "unknown activation %d", act);
+    VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                            reinterpret_cast<uintptr_t>(bias);
+    VH_REQUIRE(align % 16 == 0, VH_ERR_ARG, "bias + activation tensors must be 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t vectors = total / 8;
+    const dim3 grid(static_cast<unsigned>((vectors + 255) / 256));
+    int rc = dispatch_t(io_dtype, [&](auto tv) {
+        using T = decltype(tv);
+        if (act == 1)
+            hipLaunchKernelGGL((bias_act8_kernel<T, 1>), grid, dim3(256), 0, s, static_cast<const T*>(x), bias,
+                               static_cast<T*>(out), vectors, static_cast<int>(channels));
+        else
+            hipLaunchKernelGGL((bias_act8_kernel<T, 0>), grid, dim3(256), 0, s, static_cast<const T*>(x), bias,
+                               static_cast<T*>(out), vectors, static_cast<int>(channels));
+    });
+    if (rc) return rc;
+    return check_launch("bias_act8_kernel");
 }
 
 int vh_residual_add_forward(const void* residual, int32_t residual_dtype, const void* branch,

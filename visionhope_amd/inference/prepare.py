@@ -4,7 +4,7 @@
 import torch
 
 from ..models.block import VisionHOPEBlock
-from ..models.layers import LayerNorm2d
+from ..models.layers import Downsample, LayerNorm2d, PatchEmbedding
 from ..models.operator import VisionHOPEOperator
 from ..models.srnl import SRNL
 from ..utils.grn import GlobalResponseNorm
@@ -33,6 +33,10 @@ def prepare_for_inference(model):
             counts["layernorm2d"] += 1
         elif isinstance(module, GlobalResponseNorm):
             counts["grn"] += 1
+        elif isinstance(module, (PatchEmbedding, Downsample)):
+            # Eval-mode BatchNorm folded into the convolution on the GPU path (no
+            # parameter changes: the folded copy is cached beside the module).
+            module._vh_fold_bn = True
     with torch.no_grad():
         for block in blocks:
             counts["line_mixer"] += 1

@@ -113,7 +113,38 @@ class PatchEmbedding(nn.Module):
         self.norm = nn.Identity()
 
     def forward(self, x):
+        if self._folded_path(x):
+            from ..utils.conv_bn import ACT_GELU, ACT_NONE, conv_bn_act
+            mods = list(self.proj)
+            i = 0
+            while i < len(mods):
+                gelu = i + 2 < len(mods) and isinstance(mods[i + 2], nn.GELU)
+                x = conv_bn_act(x, mods[i], mods[i + 1], ACT_GELU if gelu else ACT_NONE)
+                i += 3 if gelu else 2
+            return self.norm(x)
         return self.norm(self.proj(x))
+
+    def _folded_path(self, x):
+        """Prepared for inference, eval mode, channels-last CUDA input, and every stage a
+        foldable (Conv2d, BatchNorm2d[, exact GELU]) group."""
+        if not getattr(self, "_vh_fold_bn", False) or self.training or not x.is_cuda:
+            return False
+        if not x.is_contiguous(memory_format=torch.channels_last):
+            return False
+        from ..utils.conv_bn import foldable
+        mods = list(self.proj)
+        i = 0
+        while i < len(mods):
+            if i + 1 >= len(mods) or not foldable(mods[i], mods[i + 1]):
+                return False
+            nxt = mods[i + 2] if i + 2 < len(mods) else None
+            if isinstance(nxt, nn.GELU):
+                if nxt.approximate != "none":
+                    return False
+                i += 3
+            else:
+                i += 2
+        return True
 
 
 class Downsample(nn.Module):
@@ -125,4 +156,9 @@ class Downsample(nn.Module):
         self.norm = nn.BatchNorm2d(out_dim)
 
     def forward(self, x):
+        if (getattr(self, "_vh_fold_bn", False) and not self.training and x.is_cuda
+                and x.is_contiguous(memory_format=torch.channels_last)):
+            from ..utils.conv_bn import conv_bn_act, foldable
+            if foldable(self.proj, self.norm):
+                return conv_bn_act(x, self.proj, self.norm)
         return self.norm(self.proj(x))
