@@ -241,6 +241,23 @@ int vh_dwconv2d_nhwc_forward(
     int32_t epilogue, const void* aux, void* out, int64_t B, int64_t H, int64_t W, int64_t C,
     void* stream);
 
+/* Workspace of vh_dwconv2d_gelu_grn_forward: B * (blocks per image) * C fp32 partial
+ * sums, or 0 when the shape is not covered (C/8 must divide 256 and the kernel's
+ * 256-thread blocks must tile whole images). */
+size_t vh_dwconv2d_gelu_grn_workspace_bytes(int64_t B, int64_t H, int64_t W, int64_t C, int32_t ksize);
+
+/* The FFN middle on a channels-last x [B, H, W, C] (io_dtype): out = gelu_erf(x +
+ * conv(x) + b) as epilogue 3 of vh_dwconv2d_nhwc_forward, plus the GRN statistics of
+ * out (as stored) from partial sums taken in the same pass: gx [B, C], inv_den [B] and
+ * scale [B, C] = 1 + gamma * gx * inv_den as vh_grn_scale_forward gives them.  No
+ * counterpart in the reference's native code (models/layers.py:73-77 runs the
+ * depthwise conv, GELU and GRN as separate modules). */
+int vh_dwconv2d_gelu_grn_forward(
+    const void* x, int32_t io_dtype, const float* taps, const float* bias, int32_t ksize,
+    const float* gamma, float eps, void* out, float* gx, float* inv_den, float* scale,
+    int64_t B, int64_t H, int64_t W, int64_t C, void* workspace, size_t workspace_bytes,
+    void* stream);
+
 /* 1x1 convolution on channels-last bf16 maps as a GEMM on the matrix cores:
  * out [M, N] = epi(x' [M, K] . weight^T + bias) with weight [N, K] bf16 (the 1x1
  * kernel as stored, cast to bf16 as autocast casts it), bias [N] fp32 (or NULL),

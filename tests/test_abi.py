@@ -182,6 +182,18 @@ def test_bias_act_rejects_bad_arguments(lib):
     assert call(x=None) == hip.VH_ERR_ARG
 
 
+def test_dwconv_grn_workspace_query(lib):
+    # Covered: C/8 divides 256 and the 256-thread blocks tile whole images.
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(2, 56, 56, 256, 3) == 2 * 49 * 256 * 4
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(128, 14, 14, 1024, 3) == 128 * 14 * 1024 * 4
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 14, 14, 256, 3) == 0     # 896 threads per image
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 8, 8, 96, 3) == 0        # C/8 = 12 does not divide 256
+    p = ctypes.c_void_p(0x1000)
+    rc = lib.vh_dwconv2d_gelu_grn_forward(p, hip.VH_DTYPE_BF16, p, p, 3, p, ctypes.c_float(1e-6), p, p, p, p,
+                                          1, 14, 14, 256, p, 1 << 20, None)
+    assert rc == hip.VH_ERR_SHAPE
+
+
 def test_check_raises_with_message(lib):
     assert _spatial(lib, head_dim=12) == hip.VH_ERR_HEAD_DIM
     with pytest.raises(RuntimeError, match="head_dim"):

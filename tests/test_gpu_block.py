@@ -193,3 +193,36 @@ def test_fused_block_falls_back_for_odd_layouts(device):
         a = block(x)
         b = block(x.contiguous(memory_format=torch.channels_last))
     assert_close(a.cpu().numpy(), b.cpu().numpy(), 1e-4, "fused vs ordinary block")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(2, 64, 16, 16), (3, 256, 8, 24), (2, 1024, 14, 14)])
+def test_depthwise_gelu_grn_statistics(device, dtype, shape):
+    """The FFN middle with GRN statistics taken in the depthwise pass: the map equals the
+    plain fused depthwise + GELU (same arithmetic) and the scale matches the separate GRN
+    statistics pass on that map (FP32 sums in another order)."""
+    from visionhope_amd.utils import dwconv
+    from visionhope_amd.utils.grn_cuda import grn_scale
+
+    b, c, h, w = shape
+    conv = torch.nn.Conv2d(c, c, 3, padding=1, groups=c)
+    with torch.no_grad():
+        conv.weight.copy_(randn(*conv.weight.shape, seed=51, scale=0.3))
+        conv.bias.copy_(randn(c, seed=52, scale=0.1))
+    conv = conv.to(device)
+    gamma = randn(c, seed=53, scale=0.3).to(device)
+    x = randn(b, c, h, w, seed=54).to(dtype).to(device).contiguous(memory_format=torch.channels_last)
+    fused = dwconv.depthwise_conv_gelu_grn(x, conv, gamma, 1e-6)
+    assert fused is not None
+    out, scale = fused
+    plain = dwconv.depthwise_conv(x, conv, dwconv.EPI_ADD_GELU)
+    assert torch.equal(out, plain)
+    assert_close(scale.cpu().numpy(), grn_scale(plain, gamma, 1e-6).cpu().numpy(), 1e-5, "fused GRN scale")
+
+
+def test_depthwise_gelu_grn_declines_uncovered_shapes(device):
+    from visionhope_amd.utils import dwconv
+
+    conv = torch.nn.Conv2d(256, 256, 3, padding=1, groups=256).to(device)
+    x = torch.randn(1, 256, 14, 14, device=device).contiguous(memory_format=torch.channels_last)
+    assert dwconv.depthwise_conv_gelu_grn(x, conv, torch.ones(256, device=device), 1e-6) is None

@@ -17,7 +17,8 @@
 
 namespace vh {
 
-enum DwEpilogue { DW_PLAIN = 0, DW_ADD_INPUT = 1, DW_GATE = 2, DW_ADD_GELU = 3, DW_ACCUM_F32 = 4, DW_ADD_F32_AUX = 5 };
+enum DwEpilogue { DW_PLAIN = 0, DW_ADD_INPUT = 1, DW_GATE = 2, DW_ADD_GELU = 3, DW_ACCUM_F32 = 4, DW_ADD_F32_AUX = 5,
+                  DW_ADD_GELU_SUMSQ = 6 };   // 6: internal, DW_ADD_GELU + GRN partial sums (see below)
 
 struct DwParams {
     const void* x;
@@ -26,6 +27,7 @@ struct DwParams {
     const void* aux;     // gate for DW_GATE (io dtype); fp32 addend for DW_ADD_F32_AUX
     void* out;           // io dtype, or fp32 for DW_ACCUM_F32
     int64_t B, H, W, C;
+    float* partial;      // DW_ADD_GELU_SUMSQ: [B, blocks per image, C] sums of squares of out
 };
 
 // Launch geometry: thread index -> (image, row, segment, channel group), with the
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
         for (int i = 0; i < NI; ++i) {
             float v[8];
             decode8<T>(r[i], v);
-            if constexpr (EPI == DW_ADD_INPUT || EPI == DW_GATE || EPI == DW_ADD_GELU) {
+            if constexpr (EPI == DW_ADD_INPUT || EPI == DW_GATE || EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ) {
                 if (i >= R && i < R + P && dy == R) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) center[i - R][j] = v[j];
@@ -163,6 +165,7 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
         }
     }
     const int64_t pix0 = (static_cast<int64_t>(row0) + h) * W + w0;
+    [[maybe_unused]] float sumsq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int px = 0; px < P; ++px) {
         if (w0 + px >= W) break;
@@ -185,14 +188,42 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
                 load8<T>(static_cast<const T*>(p.aux) + at, gv);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) acc[px][j] = center[px][j] + sigmoid_fast(gv[j]) * acc[px][j];
-            } else if constexpr (EPI == DW_ADD_GELU) {
+            } else if constexpr (EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) acc[px][j] = gelu_fast(center[px][j] + acc[px][j]);
+                if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float r = to_f32(from_f32<T>(acc[px][j]));   // the stored value
+                        sumsq[j] += r * r;
+                    }
+                }
             } else if constexpr (EPI == DW_ADD_INPUT) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) acc[px][j] = center[px][j] + acc[px][j];
             }
             store8<T>(static_cast<T*>(p.out) + at, acc[px]);
+        }
+    }
+    if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
+        // GRN partial sums: this block's threads cover whole channel groups of one image
+        // (the host checks 256 % G == 0 and whole blocks per image), 256 / G threads per
+        // group; the first G threads add their group's rows in order (deterministic).
+        __shared__ float red[256 * 8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red[threadIdx.x * 8 + j] = sumsq[j];
+        __syncthreads();
+        const int G = static_cast<int>(g.G.d);
+        if (static_cast<int>(threadIdx.x) < G) {
+            float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int r = 0; r < 256 / G; ++r)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) tot[j] += red[(r * G + threadIdx.x) * 8 + j];
+            // Blocks of one image are consecutive logical blocks: partial [b][slab] is
+            // row idx / 256 of [B * blocks per image, C].
+            float* dst = p.partial + static_cast<int64_t>(idx / 256u) * C + 8 * threadIdx.x;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dst[j] = tot[j];
         }
     }
 }
@@ -228,6 +259,7 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
         q.x = static_cast<const char*>(dp.x) + skip * sizeof(T);
         q.out = static_cast<char*>(dp.out) + skip * out_size;
         if (dp.aux) q.aux = static_cast<const char*>(dp.aux) + skip * aux_size;
+        if (dp.partial) q.partial = dp.partial + b0 * (dp.H * segs * (dp.C / 8) / 256) * dp.C;
         DwGrid g;
         g.total = static_cast<uint32_t>(q.B * q.H * segs * (q.C / 8));
         g.G = make_fastdiv(static_cast<uint32_t>(q.C / 8));
@@ -240,20 +272,32 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
     case E: hipLaunchKernelGGL((dwconv_nhwc_kernel<K, E, T, P>), grid, dim3(256), 0, s, q, g, x_bytes); \
         break;
             VH_DW(DW_PLAIN) VH_DW(DW_ADD_INPUT) VH_DW(DW_GATE) VH_DW(DW_ADD_GELU) VH_DW(DW_ACCUM_F32)
-            VH_DW(DW_ADD_F32_AUX)
+            VH_DW(DW_ADD_F32_AUX) VH_DW(DW_ADD_GELU_SUMSQ)
 #undef VH_DW
         }
     }
 }
 
-template <int K, typename T>
-void launch_dw(int epi, const DwParams& dp, hipStream_t s) {
-    int px = dw_default_pixels(K, dp.W);
+inline int dw_pixels(int K, int64_t W) {
+    int px = dw_default_pixels(K, W);
     if (const char* env = std::getenv("VH_DW_PIXELS")) {
         const int v = std::atoi(env);
         if (v == 1 || v == 2 || v == 4 || v == 8) px = v;
     }
-    switch (px) {
+    return px;
+}
+
+// Blocks per image of the depthwise grid, or 0 when blocks do not tile whole images
+// and whole channel groups (the condition of the GRN partial-sum epilogue).
+inline int64_t dw_blocks_per_image(int K, int64_t H, int64_t W, int64_t C) {
+    const int64_t G = C / 8, segs = (W + dw_pixels(K, W) - 1) / dw_pixels(K, W);
+    if (C % 8 != 0 || G > 256 || 256 % G != 0 || (H * segs * G) % 256 != 0) return 0;
+    return H * segs * G / 256;
+}
+
+template <int K, typename T>
+void launch_dw(int epi, const DwParams& dp, hipStream_t s) {
+    switch (dw_pixels(K, dp.W)) {
         case 1: launch_dw_p<K, T, 1>(epi, dp, s); break;
         case 2: launch_dw_p<K, T, 2>(epi, dp, s); break;
         case 4: launch_dw_p<K, T, 4>(epi, dp, s); break;
@@ -284,7 +328,7 @@ extern "C" int vh_dwconv2d_nhwc_forward(const void* x, int32_t io_dtype, const f
     VH_REQUIRE(align % 16 == 0, VH_ERR_ARG, "depthwise conv tensors must be 16-byte aligned");
     VH_REQUIRE(H * W * C * dtype_bytes(io_dtype) < (int64_t(1) << 31), VH_ERR_SHAPE,
                "depthwise conv image too large (one image must be below 2 GiB)");
-    DwParams dp{x, taps, bias, aux, out, B, H, W, C};
+    DwParams dp{x, taps, bias, aux, out, B, H, W, C, nullptr};
     hipStream_t s = static_cast<hipStream_t>(stream);
     auto go = [&](auto tv) {
         using T = decltype(tv);
@@ -298,4 +342,49 @@ extern "C" int vh_dwconv2d_nhwc_forward(const void* x, int32_t io_dtype, const f
         default: go(f16_t{}); break;
     }
     return check_launch("dwconv_nhwc_kernel");
+}
+
+extern "C" size_t vh_dwconv2d_gelu_grn_workspace_bytes(int64_t B, int64_t H, int64_t W, int64_t C, int32_t ksize) {
+    if (B <= 0 || H <= 0 || W <= 0 || (ksize != 3 && ksize != 5 && ksize != 7)) return 0;
+    return static_cast<size_t>(B * dw_blocks_per_image(ksize, H, W, C) * C) * sizeof(float);
+}
+
+extern "C" int vh_dwconv2d_gelu_grn_forward(const void* x, int32_t io_dtype, const float* taps, const float* bias,
+                                            int32_t ksize, const float* gamma, float eps, void* out, float* gx,
+                                            float* inv_den, float* scale, int64_t B, int64_t H, int64_t W,
+                                            int64_t C, void* workspace, size_t workspace_bytes, void* stream) {
+    VH_REQUIRE(x && taps && out && gamma && gx && inv_den && scale, VH_ERR_ARG,
+               "depthwise conv + GRN statistics pointers must not be null");
+    VH_REQUIRE(B > 0 && H > 0 && W > 0 && C > 0 && B <= 65535, VH_ERR_SHAPE,
+               "depthwise conv + GRN statistics expects nonempty NHWC input and B <= 65535");
+    VH_REQUIRE(ksize == 3 || ksize == 5 || ksize == 7, VH_ERR_ARG, "kernel size must be 3, 5 or 7, got %d", ksize);
+    VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);
+    VH_REQUIRE(dw_blocks_per_image(ksize, H, W, C) > 0, VH_ERR_SHAPE,
+               "GRN partial sums need C/8 dividing 256 and whole 256-thread blocks per image");
+    VH_REQUIRE(H * W * C * dtype_bytes(io_dtype) < (int64_t(1) << 31), VH_ERR_SHAPE,
+               "depthwise conv image too large (one image must be below 2 GiB)");
+    const size_t need = vh_dwconv2d_gelu_grn_workspace_bytes(B, H, W, C, ksize);
+    VH_REQUIRE(workspace && workspace_bytes >= need, VH_ERR_WORKSPACE,
+               "depthwise conv + GRN statistics workspace needs %zu bytes, got %zu", need,
+               workspace ? workspace_bytes : (size_t)0);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                            reinterpret_cast<uintptr_t>(taps) | reinterpret_cast<uintptr_t>(bias);
+    VH_REQUIRE(align % 16 == 0, VH_ERR_ARG, "depthwise conv tensors must be 16-byte aligned");
+    DwParams dp{x, taps, bias, nullptr, out, B, H, W, C, static_cast<float*>(workspace)};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto go = [&](auto tv) {
+        using T = decltype(tv);
+        if (ksize == 3) launch_dw<3, T>(DW_ADD_GELU_SUMSQ, dp, s);
+        else if (ksize == 5) launch_dw<5, T>(DW_ADD_GELU_SUMSQ, dp, s);
+        else launch_dw<7, T>(DW_ADD_GELU_SUMSQ, dp, s);
+    };
+    switch (io_dtype) {
+        case VH_DTYPE_F32: go(float{}); break;
+        case VH_DTYPE_BF16: go(bf16_t{}); break;
+        default: go(f16_t{}); break;
+    }
+    int rc = check_launch("dwconv_nhwc_kernel (GRN partial sums)");
+    if (rc) return rc;
+    return launch_grn_finalize(static_cast<const float*>(workspace), gx, inv_den, B, C,
+                               dw_blocks_per_image(ksize, H, W, C), eps, gamma, scale, s);
 }

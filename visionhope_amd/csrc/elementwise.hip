@@ -596,6 +596,16 @@ __global__ __launch_bounds__(256) void bias_act8_kernel(const T* __restrict__ x,
     store8<T>(out + at, a);
 }
 
+// GRN statistics from per-slab partial sums of squares partial [B, nslab, C]: gx,
+// inv_den and (when scale is not null) scale = 1 + gamma * nx.  Shared with the
+// depthwise kernel that produces the partial sums in its epilogue.
+int launch_grn_finalize(const float* partial, float* gx, float* inv_den, int64_t B, int64_t C, int64_t nslab,
+                        float eps, const float* gamma, float* scale, hipStream_t s) {
+    hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, partial, gx, inv_den,
+                       C, nslab, eps, gamma, scale);
+    return check_launch("grn_finalize_kernel");
+}
+
 }  // namespace vh
 
 using namespace vh;

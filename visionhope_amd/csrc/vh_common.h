@@ -20,6 +20,10 @@ namespace vh {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// GRN statistics from per-slab partial sums of squares (elementwise.hip).
+int launch_grn_finalize(const float* partial, float* gx, float* inv_den, int64_t B, int64_t C, int64_t nslab,
+                        float eps, const float* gamma, float* scale, hipStream_t s);
+
 #define VH_REQUIRE(cond, code, ...)                        \
     do {                                                   \
         if (!(cond)) return ::vh::set_error((code), __VA_ARGS__); \

@@ -203,16 +203,27 @@ class VisionHOPEBlock(nn.Module):
             h = visionhope_layernorm2d(x, self.norm2.weight, self.norm2.bias, self.norm2.eps,
                                        force_channels_last=True, out_dtype=act)
         f = project(h.permute(0, 2, 3, 1), ffn.fc1, pointwise.EPI_GELU)
-        if ffn.use_dwconv:
-            f = dwconv.depthwise_conv(nchw(f), ffn.dwconv, dwconv.EPI_ADD_GELU).permute(0, 2, 3, 1)
         use_grn = isinstance(ffn.grn, GlobalResponseNorm)
         x_nhwc = x.permute(0, 2, 3, 1)
-        if (act == torch.bfloat16 and self.gamma2 is None and x.dtype == act and x_nhwc.is_contiguous()
-                and _matrix_core_ok(f, ffn.fc2)):
+        fc2_fused = (act == torch.bfloat16 and self.gamma2 is None and x.dtype == act and x_nhwc.is_contiguous()
+                     and _matrix_core_ok(f, ffn.fc2))
+        scale = None
+        if ffn.use_dwconv:
+            fused = None
+            if fc2_fused and use_grn:
+                # GRN statistics taken in the depthwise pass that produces GRN's input.
+                fused = dwconv.depthwise_conv_gelu_grn(nchw(f), ffn.dwconv, ffn.grn.gamma, ffn.grn.eps)
+            if fused is not None:
+                f, scale = fused[0].permute(0, 2, 3, 1), fused[1]
+            else:
+                f = dwconv.depthwise_conv(nchw(f), ffn.dwconv, dwconv.EPI_ADD_GELU).permute(0, 2, 3, 1)
+        if fc2_fused:
             # GRN applied to fc2's operand as it is loaded, residual add in fc2's epilogue.
             grn = None
             if use_grn:
-                grn = (grn_scale(nchw(f), ffn.grn.gamma, ffn.grn.eps), _grn_beta(ffn.grn))
+                if scale is None:
+                    scale = grn_scale(nchw(f), ffn.grn.gamma, ffn.grn.eps)
+                grn = (scale, _grn_beta(ffn.grn))
             out = pointwise.pointwise_conv(f, ffn.fc2, pointwise.EPI_ADD, residual=x_nhwc, grn=grn)
             return nchw(out)
         if use_grn:

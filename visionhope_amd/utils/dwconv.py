@@ -105,3 +105,31 @@ def depthwise_conv(x, conv, epilogue=EPI_PLAIN, aux=None, out=None):
         int(epilogue), hip.ptr(aux), hip.ptr(out), batch, height, width, channels, hip.stream_of(x)),
         "vh_dwconv2d_nhwc_forward")
     return out
+
+
+@on_tensor_device
+def depthwise_conv_gelu_grn(x, conv, gamma, eps):
+    """``gelu(x + conv(x))`` (``EPI_ADD_GELU``) and the GRN scale ``[B, C]`` of that output
+    (``1 + gamma * nx``, ``utils/grn.py:26-38``) from one pass over the map; ``None`` when
+    the shape is outside what the fused statistics cover (then use ``depthwise_conv`` and
+    ``grn_scale``)."""
+    if not x.is_cuda or x.dtype not in _DTYPES or not is_depthwise(conv):
+        raise ValueError("depthwise_conv_gelu_grn expects a CUDA map and a depthwise Conv2d")
+    batch, channels, height, width = x.shape
+    lib = hip.load_library()
+    nbytes = lib.vh_dwconv2d_gelu_grn_workspace_bytes(batch, height, width, channels, conv.kernel_size[0])
+    if nbytes == 0 or batch > 65535:
+        return None
+    taps, bias = depthwise_taps(conv)
+    x = _channels_last(x)
+    gamma = gamma.detach().reshape(-1).float().contiguous()
+    out = torch.empty_like(x, memory_format=torch.channels_last)
+    scale = torch.empty((batch, channels), device=x.device, dtype=torch.float32)
+    gx = torch.empty((batch, channels), device=x.device, dtype=torch.float32)
+    inv_den = torch.empty((batch,), device=x.device, dtype=torch.float32)
+    ws = hip.workspace(nbytes, x.device)
+    hip.check(lib.vh_dwconv2d_gelu_grn_forward(
+        hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(taps), hip.ptr(bias), conv.kernel_size[0], hip.ptr(gamma),
+        float(eps), hip.ptr(out), hip.ptr(gx), hip.ptr(inv_den), hip.ptr(scale), batch, height, width, channels,
+        hip.ptr(ws), ws.numel() * 4, hip.stream_of(x)), "vh_dwconv2d_gelu_grn_forward")
+    return out, scale
