@@ -19,6 +19,7 @@
 // with 4 consecutive output channels of one pixel (one 8-byte store).  Any order of the
 // 32 k inside the instruction gives the same sum, as A and B use the same one.
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <type_traits>
 
@@ -114,8 +115,8 @@ __device__ __forceinline__ void pw_bias8(const PwParams& p, int n, float (&bv)[8
 // Row of w feeding MFMA row i16 of n tile tn, for the channel interleave above.
 __device__ __forceinline__ int pw_wrow(int tn, int i16) { return 32 * (tn / 2) + 8 * (i16 / 4) + 4 * (tn % 2) + (i16 % 4); }
 
-template <int BM, int BN, int WGM, int BK, int EPI, bool PRO>
-__global__ __launch_bounds__(256) void pointwise_gemm_kernel(const PwParams p) {
+template <int BM, int BN, int WGM, int BK, int EPI, bool PRO, int OCC = 1>
+__global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams p) {
     constexpr int PW_BK = BK, PW_LDS_ROW = BK + 8;
     static_assert(WGM == 1 || WGM == 2 || WGM == 4, "4 waves");
     constexpr int WGN = 4 / WGM, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
@@ -282,13 +283,12 @@ __global__ __launch_bounds__(256) void pointwise_narrow_kernel(const PwParams p)
 namespace {
 
 // Narrow outputs (N = 32, 64) with K <= 64 take the LDS-free kernel with 64 pixels per
-// wave; the rest the LDS-tiled one (N = 32, 64: 256 pixels x all N per block, k step
-// 32; N % 128 == 0: 128 x 128, k step 64).  Measured on MI355X at the Tiny shapes.
-// VH_PW_CFG selects a variant for measurements: "n<TM>" (narrow, 16 TM pixels per
-// wave, K <= 256) or "w<BK>" (tiled, k step BK = 32 or 64).
+// wave; the rest the LDS-tiled one with the tile chosen below.  VH_PW_CFG selects a
+// variant for measurements: "n<TM>" (narrow, 16 TM pixels per wave, K <= 256),
+// "w<BK>" (the earlier fixed tiles, k step 32 or 64) or "t<BM>x<BN>k<BK>o<OCC>".
 template <int EPI, bool PRO>
 int launch_pw(const PwParams& p, hipStream_t s) {
-    int narrow_tm = 4, bk = p.N <= 64 ? 32 : 64;
+    int narrow_tm = 4, bk = 0;
     bool narrow = (p.N == 32 || p.N == 64) && (p.K == 32 || p.K == 64);
     const bool narrow_ok = (p.N == 32 || p.N == 64) && (p.K == 32 || p.K == 64 || p.K == 128 || p.K == 256);
     if (const char* env = std::getenv("VH_PW_CFG")) {
@@ -317,6 +317,29 @@ int launch_pw(const PwParams& p, hipStream_t s) {
             case 128: return pick(std::integral_constant<int, 4>{});
             default: return pick(std::integral_constant<int, 8>{});
         }
+    }
+    if (const char* env = std::getenv("VH_PW_CFG")) {
+        // t<BM>x<BN>k<BK>o<OCC> (tiled variants for measurements, N % BN == 0)
+        int bm = 0, bn = 0, kk = 0, occ = 0;
+        if (std::sscanf(env, "t%dx%dk%do%d", &bm, &bn, &kk, &occ) == 4 && p.N % bn == 0) {
+#define VH_PWT(BM_, BN_, WGM_, BK_, OCC_)                                                                 \
+    if (bm == BM_ && bn == BN_ && kk == BK_ && occ == OCC_)                                              \
+        return go(pointwise_gemm_kernel<BM_, BN_, WGM_, BK_, EPI, PRO, OCC_>, BM_, BN_);
+            VH_PWT(128, 128, 2, 32, 2) VH_PWT(128, 128, 2, 32, 3) VH_PWT(128, 128, 2, 64, 2)
+            VH_PWT(64, 128, 2, 32, 2) VH_PWT(64, 128, 2, 32, 4) VH_PWT(64, 128, 2, 64, 2) VH_PWT(64, 128, 2, 64, 3)
+            VH_PWT(128, 64, 2, 32, 4) VH_PWT(256, 128, 4, 32, 2) VH_PWT(128, 256, 2, 32, 1)
+#undef VH_PWT
+        }
+    }
+    if (bk == 0) {
+        // Defaults measured on MI355X at the Tiny shapes (B = 128).  Short products want
+        // small tiles and many resident blocks (more k tiles in flight per CU); deep
+        // ones, 128 x 128 tiles with a 64-deep k step.
+        if (p.N == 32) return go(pointwise_gemm_kernel<256, 32, 4, 32, EPI, PRO>, 256, 32);
+        if (p.N == 64) return go(pointwise_gemm_kernel<128, 64, 2, 32, EPI, PRO, 4>, 128, 64);
+        if (p.K <= 128 || (p.K == 256 && p.N >= 512)) return go(pointwise_gemm_kernel<64, 128, 2, 32, EPI, PRO, 4>, 64, 128);
+        if (p.K == 256) return go(pointwise_gemm_kernel<64, 128, 2, 64, EPI, PRO, 2>, 64, 128);
+        return go(pointwise_gemm_kernel<128, 128, 2, 64, EPI, PRO, 2>, 128, 128);
     }
     if (bk == 32) {
         if (p.N == 32) return go(pointwise_gemm_kernel<256, 32, 4, 32, EPI, PRO>, 256, 32);
