@@ -146,39 +146,74 @@ __global__ __launch_bounds__(256) void grn_partial_kernel(const T* __restrict__ 
     }
 }
 
-__global__ __launch_bounds__(256) void grn_finalize_kernel(const float* __restrict__ partial,
-                                                          float* __restrict__ gx,
-                                                          float* __restrict__ inv_den, int64_t C,
-                                                          int64_t nslab, float eps,
-                                                          const float* __restrict__ gamma = nullptr,
-                                                          float* __restrict__ scale = nullptr) {
-    __shared__ float wsum[4];
+// One block of 1024 threads per image.  With C < 1024 the threads split the slabs
+// into SG = 1024 / C groups (thread t: channel t % C, slabs t / C, t / C + SG, ...),
+// so many partial sums are in flight at once; the groups are then added in a fixed
+// order (deterministic).
+constexpr int kGrnFinalizeThreads = 1024;
+
+__global__ __launch_bounds__(kGrnFinalizeThreads) void grn_finalize_kernel(const float* __restrict__ partial,
+                                                                           float* __restrict__ gx,
+                                                                           float* __restrict__ inv_den, int64_t C,
+                                                                           int64_t nslab, float eps,
+                                                                           const float* __restrict__ gamma = nullptr,
+                                                                           float* __restrict__ scale = nullptr) {
+    constexpr int NT = kGrnFinalizeThreads;
+    __shared__ float wsum[NT / 64];
+    __shared__ float red[NT];
     __shared__ float inv_sh;
     const int64_t b = blockIdx.x;
+    const int t = threadIdx.x;
     float local = 0.f;
-    for (int64_t c = threadIdx.x; c < C; c += 256) {
-        // Four independent partial sums keep four loads in flight.
-        const float* pc = partial + b * nslab * C + c;
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-        int64_t s = 0;
-        for (; s + 4 <= nslab; s += 4) {
-            a0 += pc[s * C];
-            a1 += pc[(s + 1) * C];
-            a2 += pc[(s + 2) * C];
-            a3 += pc[(s + 3) * C];
+    if (C < NT) {
+        const int SG = static_cast<int>(NT / C);
+        const int sg = static_cast<int>(t / C);
+        const int64_t c = t % C;
+        float a0 = 0.f, a1 = 0.f;
+        if (sg < SG) {
+            const float* pc = partial + b * nslab * C + c;
+            int64_t s = sg;
+            for (; s + SG < nslab; s += 2 * SG) {
+                a0 += pc[s * C];
+                a1 += pc[(s + SG) * C];
+            }
+            if (s < nslab) a0 += pc[s * C];
         }
-        for (; s < nslab; ++s) a0 += pc[s * C];
-        const float acc = (a0 + a1) + (a2 + a3);
-        const float g = sqrtf(acc);
-        gx[b * C + c] = g;
-        local += g;
+        red[t] = a0 + a1;
+        __syncthreads();
+        if (sg == 0) {
+            float acc = 0.f;
+            for (int q = 0; q < SG; ++q) acc += red[q * C + c];
+            const float g = sqrtf(acc);
+            gx[b * C + c] = g;
+            local = g;
+        }
+    } else {
+        for (int64_t c = t; c < C; c += NT) {
+            // Four independent partial sums keep four loads in flight.
+            const float* pc = partial + b * nslab * C + c;
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+            int64_t s = 0;
+            for (; s + 4 <= nslab; s += 4) {
+                a0 += pc[s * C];
+                a1 += pc[(s + 1) * C];
+                a2 += pc[(s + 2) * C];
+                a3 += pc[(s + 3) * C];
+            }
+            for (; s < nslab; ++s) a0 += pc[s * C];
+            const float acc = (a0 + a1) + (a2 + a3);
+            const float g = sqrtf(acc);
+            gx[b * C + c] = g;
+            local += g;
+        }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off);
-    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = local;
+    if ((t & 63) == 0) wsum[t >> 6] = local;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const float total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    if (t == 0) {
+        float total = 0.f;
+        for (int w = 0; w < NT / 64; ++w) total += wsum[w];
         const float inv = 1.f / (total / static_cast<float>(C) + eps);
         inv_den[b] = inv;
         inv_sh = inv;
@@ -188,7 +223,7 @@ __global__ __launch_bounds__(256) void grn_finalize_kernel(const float* __restri
         // that apply GRN as they load its input (same fp32 operations as grn_apply8).
         __syncthreads();
         const float inv = inv_sh;
-        for (int64_t c = threadIdx.x; c < C; c += 256) {
+        for (int64_t c = t; c < C; c += NT) {
             const float nx = gx[b * C + c] * inv;
             scale[b * C + c] = 1.f + gamma[c] * nx;
         }
@@ -601,7 +636,7 @@ __global__ __launch_bounds__(256) void bias_act8_kernel(const T* __restrict__ x,
 // depthwise kernel that produces the partial sums in its epilogue.
 int launch_grn_finalize(const float* partial, float* gx, float* inv_den, int64_t B, int64_t C, int64_t nslab,
                         float eps, const float* gamma, float* scale, hipStream_t s) {
-    hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, partial, gx, inv_den,
+    hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s, partial, gx, inv_den,
                        C, nslab, eps, gamma, scale);
     return check_launch("grn_finalize_kernel");
 }
@@ -708,7 +743,7 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
             hipLaunchKernelGGL((grn_partial8_kernel<T>), dim3(static_cast<unsigned>(vslab), static_cast<unsigned>(B)),
                                dim3(G * R), red, s, static_cast<const T*>(x), partial, static_cast<int>(C),
                                static_cast<int>(S), rows, vslab);
-            hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, partial,
+            hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s, partial,
                                gx, inv_den, C, static_cast<int64_t>(vslab), eps);
             dispatch_t(y_dtype, [&](auto ov) {
                 using TO = decltype(ov);
@@ -724,7 +759,7 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
         using T = decltype(tv);
         hipLaunchKernelGGL((grn_partial_kernel<T>), dim3(static_cast<unsigned>(nslab), static_cast<unsigned>(B)),
                            dim3(256), lds, s, static_cast<const T*>(x), partial, C, S, nslab);
-        hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, partial,
+        hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s, partial,
                            gx, inv_den, C, nslab, eps);
         dispatch_t(y_dtype, [&](auto ov) {
             using TO = decltype(ov);
@@ -762,7 +797,7 @@ int vh_grn_scale_forward(const void* x, int32_t io_dtype, const float* gamma, fl
         hipLaunchKernelGGL((grn_partial8_kernel<T>), dim3(static_cast<unsigned>(vslab), static_cast<unsigned>(B)),
                            dim3(G * R), red, s, static_cast<const T*>(x), partial, static_cast<int>(C),
                            static_cast<int>(S), rows, vslab);
-        hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, partial, gx,
+        hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s, partial, gx,
                            inv_den, C, static_cast<int64_t>(vslab), eps, gamma, scale);
     });
     if (rc) return rc;
