@@ -57,13 +57,16 @@ def test_pointwise_gelu(device, k, n):
     assert_close(got.double().cpu().numpy(), expected.double().numpy(), 5e-3, "pw gelu")
 
 
-@pytest.mark.parametrize("k,n", [(256, 64), (1024, 256), (64, 32)])
+@pytest.mark.parametrize("k,n", [(256, 64), (1024, 256), (64, 32), (512, 128), (128, 512)])
 @pytest.mark.parametrize("with_grn", [False, True])
-def test_pointwise_residual_and_grn(device, k, n, with_grn):
-    """fc2 of the FFN: r + fc2(GRN(h)), the GRN applied to the operand as it is loaded."""
+@pytest.mark.parametrize("hw", [(5, 7), (16, 20)])
+def test_pointwise_residual_and_grn(device, k, n, with_grn, hw):
+    """fc2 of the FFN: r + fc2(GRN(h)), the GRN applied to the operand as it is loaded:
+    per chunk from global memory when images are smaller than a tile (35 pixels: images
+    split inside 16-row tiles), staged in LDS per k tile otherwise (320 pixels)."""
     from visionhope_amd.utils import pointwise
 
-    images, h, w = 3, 5, 7          # 35 pixels per image: images split inside 16-row tiles
+    images, (h, w) = 3, hw
     lin = nn.Linear(k, n)
     x = _bf16(randn(images, h, w, k, seed=5))
     r = _bf16(randn(images, h, w, n, seed=6))

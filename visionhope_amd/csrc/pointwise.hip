@@ -115,7 +115,11 @@ __device__ __forceinline__ void pw_bias8(const PwParams& p, int n, float (&bv)[8
 // Row of w feeding MFMA row i16 of n tile tn, for the channel interleave above.
 __device__ __forceinline__ int pw_wrow(int tn, int i16) { return 32 * (tn / 2) + 8 * (i16 / 4) + 4 * (tn % 2) + (i16 % 4); }
 
-template <int BM, int BN, int WGM, int BK, int EPI, bool PRO, int OCC = 1>
+// PRO: 0 no GRN prologue; 1 GRN applied to each x chunk as it is loaded (scale and
+// beta read from global memory per chunk); 2 the k tile's scale rows of the block's
+// (at most two) images and beta staged in LDS with the operand tiles and applied to the
+// x fragments as they are read (the host takes 2 when an image has at least BM pixels).
+template <int BM, int BN, int WGM, int BK, int EPI, int PRO, int OCC = 1>
 __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams p) {
     constexpr int PW_BK = BK, PW_LDS_ROW = BK + 8;
     static_assert(WGM == 1 || WGM == 2 || WGM == 4, "4 waves");
@@ -125,6 +129,7 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
     constexpr int CPR = PW_BK / 8, A_TOTAL = BM * CPR, B_TOTAL = BN * CPR;
     constexpr int A_CHUNKS = (A_TOTAL + 255) / 256, B_CHUNKS = (B_TOTAL + 255) / 256;
     __shared__ __align__(16) bf16_t lds[2][(BM + BN) * PW_LDS_ROW];
+    __shared__ __align__(16) float grn_s[2][PRO == 2 ? 3 * BK : 4];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const int wm = wv % WGM, wn = wv / WGM;
@@ -133,10 +138,24 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
     const int K = p.K;
     const int ntiles = (K + PW_BK - 1) / PW_BK;
 
+    [[maybe_unused]] int64_t img0 = 0, last_img = 0;
+    [[maybe_unused]] float4 rs = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (PRO == 2) {
+        img0 = fast_div(static_cast<uint32_t>(m0), p.rows_per_image);
+        last_img = fast_div(static_cast<uint32_t>(p.M - 1), p.rows_per_image);
+    }
     // Global chunk c of a tile: row c / CPR, k offset 8 (c % CPR).
     uint4 ra[A_CHUNKS], rb[B_CHUNKS];
     auto gload = [&](int t) {
         const int kt = t * PW_BK;
+        if constexpr (PRO == 2) {
+            if (tid < 3 * PW_BK / 4) {
+                const int which = tid / (PW_BK / 4), kk = kt + 4 * (tid % (PW_BK / 4));
+                const float* src = which < 2 ? p.pro_scale + std::min<int64_t>(img0 + which, last_img) * K + kk
+                                             : p.pro_shift + kk;
+                rs = kk < K ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < A_CHUNKS; ++i) {
             const int c = tid + 256 * i, row = c / CPR, kk = kt + 8 * (c % CPR);
@@ -144,7 +163,7 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
             uint4 v = make_uint4(0u, 0u, 0u, 0u);
             if (kk < K && (A_TOTAL % 256 == 0 || c < A_TOTAL)) {
                 v = *reinterpret_cast<const uint4*>(p.x + m * K + kk);
-                if constexpr (PRO) {
+                if constexpr (PRO == 1) {
                     const int64_t img = fast_div(static_cast<uint32_t>(m), p.rows_per_image);
                     v = grn_apply8(v, p.pro_scale + img * K + kk, p.pro_shift + kk);
                 }
@@ -161,6 +180,10 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
     };
     auto lstore = [&](int buf) {
         bf16_t* base = lds[buf];
+        if constexpr (PRO == 2) {
+            if (tid < 3 * PW_BK / 4)
+                *reinterpret_cast<float4*>(&grn_s[buf][(tid / (PW_BK / 4)) * PW_BK + 4 * (tid % (PW_BK / 4))]) = rs;
+        }
 #pragma unroll
         for (int i = 0; i < A_CHUNKS; ++i) {
             const int c = tid + 256 * i;
@@ -179,6 +202,16 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
         wrow[tn] = wn * WN + pw_wrow(tn, i16);
+
+    // Staged scale row (0: first image of the block, 1: the next) of each x fragment row.
+    [[maybe_unused]] int rel[TM];
+    if constexpr (PRO == 2) {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            const int64_t m = std::min<int64_t>(m0 + wm * WM + 16 * tm + i16, p.M - 1);
+            rel[tm] = static_cast<int>(fast_div(static_cast<uint32_t>(m), p.rows_per_image) - img0);
+        }
+    }
 
     v4f_pw acc[TN][TM];
 #pragma unroll
@@ -200,8 +233,12 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
             for (int tn = 0; tn < TN; ++tn)
                 af[tn] = *reinterpret_cast<const uint4*>(base + (BM + wrow[tn]) * PW_LDS_ROW + 32 * ks + 8 * kg);
 #pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
+            for (int tm = 0; tm < TM; ++tm) {
                 bfr[tm] = *reinterpret_cast<const uint4*>(base + (wm * WM + 16 * tm + i16) * PW_LDS_ROW + 32 * ks + 8 * kg);
+                if constexpr (PRO == 2)
+                    bfr[tm] = grn_apply8(bfr[tm], &grn_s[buf][rel[tm] * PW_BK + 32 * ks + 8 * kg],
+                                         &grn_s[buf][2 * PW_BK + 32 * ks + 8 * kg]);
+            }
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
@@ -286,8 +323,9 @@ namespace {
 // wave; the rest the LDS-tiled one with the tile chosen below.  VH_PW_CFG selects a
 // variant for measurements: "n<TM>" (narrow, 16 TM pixels per wave, K <= 256),
 // "w<BK>" (the earlier fixed tiles, k step 32 or 64) or "t<BM>x<BN>k<BK>o<OCC>".
-template <int EPI, bool PRO>
+template <int EPI, bool PRO_ON>
 int launch_pw(const PwParams& p, hipStream_t s) {
+    constexpr int PRO = PRO_ON ? 1 : 0;
     int narrow_tm = 4, bk = 0;
     bool narrow = (p.N == 32 || p.N == 64) && (p.K == 32 || p.K == 64);
     const bool narrow_ok = (p.N == 32 || p.N == 64) && (p.K == 32 || p.K == 64 || p.K == 128 || p.K == 256);
@@ -305,9 +343,9 @@ int launch_pw(const PwParams& p, hipStream_t s) {
             constexpr int KS = decltype(ks_c)::value;
             auto with_tn = [&](auto tn_c) {
                 constexpr int TN = decltype(tn_c)::value;
-                if (narrow_tm == 1) return go(pointwise_narrow_kernel<KS, TN, 1, EPI, PRO>, 64, p.N);
-                if (narrow_tm == 4) return go(pointwise_narrow_kernel<KS, TN, 4, EPI, PRO>, 256, p.N);
-                return go(pointwise_narrow_kernel<KS, TN, 2, EPI, PRO>, 128, p.N);
+                if (narrow_tm == 1) return go(pointwise_narrow_kernel<KS, TN, 1, EPI, PRO_ON>, 64, p.N);
+                if (narrow_tm == 4) return go(pointwise_narrow_kernel<KS, TN, 4, EPI, PRO_ON>, 256, p.N);
+                return go(pointwise_narrow_kernel<KS, TN, 2, EPI, PRO_ON>, 128, p.N);
             };
             return p.N == 32 ? with_tn(std::integral_constant<int, 2>{}) : with_tn(std::integral_constant<int, 4>{});
         };
@@ -331,15 +369,34 @@ int launch_pw(const PwParams& p, hipStream_t s) {
 #undef VH_PWT
         }
     }
+    // The GRN prologue is staged in LDS (PRO 2) when every block spans at most two
+    // images (at least BM pixels per image).
+    auto tiled = [&](auto bm_c, auto bn_c, auto wgm_c, auto bk_c, auto occ_c) {
+        constexpr int BM_ = decltype(bm_c)::value, BN_ = decltype(bn_c)::value, WGM_ = decltype(wgm_c)::value;
+        constexpr int BK_ = decltype(bk_c)::value, OCC_ = decltype(occ_c)::value;
+        if (PRO_ON && p.rows_per_image.d >= static_cast<uint32_t>(BM_))
+            return go(pointwise_gemm_kernel<BM_, BN_, WGM_, BK_, EPI, 2, OCC_>, BM_, BN_);
+        return go(pointwise_gemm_kernel<BM_, BN_, WGM_, BK_, EPI, PRO, OCC_>, BM_, BN_);
+    };
     if (bk == 0) {
         // Defaults measured on MI355X at the Tiny shapes (B = 128).  Short products want
         // small tiles and many resident blocks (more k tiles in flight per CU); deep
         // ones, 128 x 128 tiles with a 64-deep k step.
-        if (p.N == 32) return go(pointwise_gemm_kernel<256, 32, 4, 32, EPI, PRO>, 256, 32);
-        if (p.N == 64) return go(pointwise_gemm_kernel<128, 64, 2, 32, EPI, PRO, 4>, 128, 64);
-        if (p.K <= 128 || (p.K == 256 && p.N >= 512)) return go(pointwise_gemm_kernel<64, 128, 2, 32, EPI, PRO, 4>, 64, 128);
-        if (p.K == 256) return go(pointwise_gemm_kernel<64, 128, 2, 64, EPI, PRO, 2>, 64, 128);
-        return go(pointwise_gemm_kernel<128, 128, 2, 64, EPI, PRO, 2>, 128, 128);
+        using std::integral_constant;
+        if (p.N == 32)
+            return tiled(integral_constant<int, 256>{}, integral_constant<int, 32>{}, integral_constant<int, 4>{},
+                         integral_constant<int, 32>{}, integral_constant<int, 1>{});
+        if (p.N == 64)
+            return tiled(integral_constant<int, 128>{}, integral_constant<int, 64>{}, integral_constant<int, 2>{},
+                         integral_constant<int, 32>{}, integral_constant<int, 4>{});
+        if (p.K <= 128 || (p.K == 256 && p.N >= 512))
+            return tiled(integral_constant<int, 64>{}, integral_constant<int, 128>{}, integral_constant<int, 2>{},
+                         integral_constant<int, 32>{}, integral_constant<int, 4>{});
+        if (p.K == 256)
+            return tiled(integral_constant<int, 64>{}, integral_constant<int, 128>{}, integral_constant<int, 2>{},
+                         integral_constant<int, 64>{}, integral_constant<int, 2>{});
+        return tiled(integral_constant<int, 128>{}, integral_constant<int, 128>{}, integral_constant<int, 2>{},
+                     integral_constant<int, 64>{}, integral_constant<int, 2>{});
     }
     if (bk == 32) {
         if (p.N == 32) return go(pointwise_gemm_kernel<256, 32, 4, 32, EPI, PRO>, 256, 32);
