@@ -267,15 +267,34 @@ int vh_dwconv2d_gelu_grn_forward(
  *   epilogue 0: out = that value                              (proj_in, local_gate, W_q, proj_out)
  *   epilogue 1: out = bf16(gelu(that value))                  (ffn.fc1 + ffn.act)
  *   epilogue 2: out = bf16(residual + that value), residual [M, N] bf16  (ffn.fc2 + residual add)
+ *   epilogue 3: out = bf16(silu(that value))                  (head_pre_logits + folded head_norm + head_act)
  * With grn_scale [M / pixels_per_image, K] and grn_beta [K] (both fp32, or both NULL)
  * the operand is x' = bf16(x * grn_scale[image] + grn_beta), the GRN output the
  * reference feeds to ffn.fc2 (vh_grn_scale_forward gives the scale).  No counterpart
- * in the reference's native code: it runs nn.Conv2d / nn.Linear and the GELU, GRN and
- * residual add as separate ops (models/block.py:70-107, models/layers.py:67-80). */
+ * in the reference's native code: it runs nn.Conv2d / nn.Linear and the GELU, GRN,
+ * residual add and SiLU as separate ops (models/block.py:70-107, models/layers.py:67-80,
+ * models/hierarchical.py:62-84). */
 int vh_pointwise_conv_nhwc_forward(
     const void* x, int32_t io_dtype, const void* weight, const float* bias, int32_t epilogue,
     const void* residual, const float* grn_scale, const float* grn_beta, int64_t pixels_per_image,
     void* out, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* 3x3 convolution, padding 1, stride 1 or 2, on a channels-last map as an implicit GEMM
+ * on the matrix cores: out [B, Ho, Wo, N] bf16 = act(bf16(conv(x, weight) + bias)),
+ * rounded to bf16 after the sum and after the activation (act 0 = none, 1 = exact GELU).
+ * x [B, H, W, Cin] bf16 with Cin % 32 == 0, or Cin = 3 (the image: fp32, rounded to
+ * bf16 on load as autocast rounds it, or bf16).  weight bf16 [N, K]: for Cin % 32 == 0
+ * the convolution weight in channels-last order [N, 3, 3, Cin] (K = 9 Cin); for Cin = 3,
+ * K = 64 with weight[n][4 (3 kh + kw) + c] and zeros at c = 3 and taps 9..15.  bias [N]
+ * fp32.  N = 32, 64 or a multiple of 128; Ho = (H - 1) / stride + 1, likewise Wo;
+ * weight, bias, out (and x unless Cin = 3) 16-byte aligned.  With an eval-mode
+ * BatchNorm folded into weight and bias this is Conv2d + BatchNorm2d (+ GELU) of the
+ * stem and the downsample layers (models/layers.py:85-119).  No counterpart in the
+ * reference's native code (it runs nn.Conv2d, nn.BatchNorm2d and nn.GELU). */
+int vh_conv3x3_nhwc_forward(
+    const void* x, int32_t x_dtype, const void* weight, const float* bias, int32_t act, void* out,
+    int64_t batch, int64_t height, int64_t width, int64_t in_channels, int64_t out_channels,
+    int32_t stride, void* stream);
 
 /* Per-channel bias and optional exact GELU on a channels-last map x [pixels, C]
  * (io_dtype, C % 8 == 0, 16-byte aligned; out may alias x):

@@ -149,7 +149,7 @@ def test_pointwise_conv_rejects_bad_arguments(lib):
     assert call(n=96) == hip.VH_ERR_SHAPE                # not 32, 64 or a multiple of 128
     assert call(n=48) == hip.VH_ERR_SHAPE
     assert call(m=0) == hip.VH_ERR_SHAPE
-    assert call(epilogue=3) == hip.VH_ERR_ARG
+    assert call(epilogue=4) == hip.VH_ERR_ARG
     assert call(epilogue=2) == hip.VH_ERR_ARG            # residual missing
     assert call(scale=p) == hip.VH_ERR_ARG               # beta missing
     assert call(scale=p, beta=p, per_image=48) == hip.VH_ERR_SHAPE   # M not a multiple of it
@@ -180,6 +180,25 @@ def test_bias_act_rejects_bad_arguments(lib):
     assert call(total=40) == hip.VH_ERR_SHAPE           # not a whole number of pixels
     assert call(dtype=9) == hip.VH_ERR_DTYPE
     assert call(x=None) == hip.VH_ERR_ARG
+
+
+def test_conv3x3_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(0x1000)
+
+    def call(dtype=hip.VH_DTYPE_BF16, act=0, cin=32, cout=64, stride=1, b=2, x=p, h=8):
+        return lib.vh_conv3x3_nhwc_forward(x, dtype, p, p, act, p, b, h, 8, cin, cout, stride, None)
+
+    assert call(stride=3) == hip.VH_ERR_ARG
+    assert call(act=2) == hip.VH_ERR_ARG
+    assert call(cin=48) == hip.VH_ERR_SHAPE              # neither 3 nor a multiple of 32
+    assert call(cout=96) == hip.VH_ERR_SHAPE             # not 32, 64 or a multiple of 128
+    assert call(dtype=hip.VH_DTYPE_F32) == hip.VH_ERR_DTYPE   # fp32 only for the 3-channel image
+    assert call(cin=3, dtype=hip.VH_DTYPE_F16) == hip.VH_ERR_DTYPE
+    assert call(b=0) == hip.VH_ERR_SHAPE
+    assert call(h=1 << 20, b=1 << 12) == hip.VH_ERR_SHAPE    # more than 2^31 output pixels
+    assert call(x=None) == hip.VH_ERR_ARG
+    assert call(x=ctypes.c_void_p(0x1008)) == hip.VH_ERR_ARG  # misaligned bf16 map
+    assert b"aligned" in lib.vh_last_error()
 
 
 def test_dwconv_grn_workspace_query(lib):

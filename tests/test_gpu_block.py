@@ -155,13 +155,14 @@ def test_fused_block_matches_oracle(oracle, device, local_mode, autocast):
 def test_fused_block_bf16_gemm_paths(oracle, device, monkeypatch, dim, native_gemm):
     """bf16 autocast through either 1x1 path: the native matrix-core kernel for every
     projection (fc1 + GELU, fc2 with the GRN apply and the residual add fused), or the
-    library GEMM for the wide ones, as small maps take by default."""
+    library GEMM with separate elementwise passes (the path of shapes the kernel does not
+    cover)."""
     from visionhope_amd.inference.prepare import prepare_for_inference
     from visionhope_amd.models import block as block_mod
     from visionhope_amd.models.block import VisionHOPEBlock
 
-    if native_gemm:
-        monkeypatch.setattr(block_mod, "_MATRIX_CORE_MIN_PIXELS", 0)
+    if not native_gemm:
+        monkeypatch.setattr(block_mod, "_matrix_core_ok", lambda t, module: False)
     torch.manual_seed(17)
     block = VisionHOPEBlock(dim, head_dim=16)
     perturb_block(block, seed=18)

@@ -23,51 +23,9 @@
 #include <cstdlib>
 #include <type_traits>
 
-#include "vh_common.h"
+#include "pw_common.h"
 
 namespace vh {
-
-enum PwEpilogue { PW_BIAS = 0, PW_GELU = 1, PW_ADD = 2 };
-
-struct PwParams {
-    const bf16_t* x;        // [M, K]
-    const bf16_t* w;        // [N, K]
-    const float* bias;      // [N] fp32 (values added before the first rounding) or null
-    const bf16_t* res;      // [M, N] residual (PW_ADD)
-    bf16_t* out;            // [M, N]
-    const float* pro_scale; // [images, K] GRN scale 1 + gamma * nx, or null (no prologue)
-    const float* pro_shift; // [K] GRN beta
-    int64_t M;
-    int N, K;
-    FastDiv rows_per_image; // pixels per image (prologue)
-};
-
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef float v4f_pw __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v4f_pw mfma_16x16x32(const uint4& a, const uint4& b, v4f_pw c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c,
-                                                    0, 0, 0);
-}
-
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
-// GRN apply on 8 consecutive bf16 of row m: bf16(h * s + beta), s and beta fp32.
-__device__ __forceinline__ uint4 grn_apply8(uint4 v, const float* s, const float* beta) {
-    const float4 s0 = *reinterpret_cast<const float4*>(s), s1 = *reinterpret_cast<const float4*>(s + 4);
-    const float4 b0 = *reinterpret_cast<const float4*>(beta), b1 = *reinterpret_cast<const float4*>(beta + 4);
-    uint4 r;
-    r.x = pack_bf16x2(bf16_lo(v.x) * s0.x + b0.x, bf16_hi(v.x) * s0.y + b0.y);
-    r.y = pack_bf16x2(bf16_lo(v.y) * s0.z + b0.z, bf16_hi(v.y) * s0.w + b0.w);
-    r.z = pack_bf16x2(bf16_lo(v.z) * s1.x + b1.x, bf16_hi(v.z) * s1.y + b1.y);
-    r.w = pack_bf16x2(bf16_lo(v.w) * s1.z + b1.z, bf16_hi(v.w) * s1.w + b1.w);
-    return r;
-}
-
-__device__ __forceinline__ float round_bf16(float v) {
-    return __uint_as_float(static_cast<uint32_t>(from_f32<bf16_t>(v).bits) << 16);
-}
 
 // Block tile BM x BN of the output, k in steps of BK = 64 through LDS (two buffers):
 // each thread moves 16-byte chunks global -> registers -> LDS (rows of x and w are
@@ -78,43 +36,6 @@ __device__ __forceinline__ float round_bf16(float v) {
 // Output channels are interleaved across pairs of 16-row MFMA tiles (tile 2p row r
 // is channel 32p + 8(r/4) + r%4, tile 2p+1 row r is channel 32p + 8(r/4) + 4 + r%4),
 // so each lane ends with 8 consecutive channels of one pixel: one 16-byte store.
-// Epilogue of one tile pair: lane holds channels n .. n+7 (from acc0 = tile 2q,
-// acc1 = tile 2q+1) of pixel m.
-template <int EPI>
-__device__ __forceinline__ void pw_store8(const PwParams& p, int64_t m, int n, const float (&bv)[8], const v4f_pw& acc0,
-                                          const v4f_pw& acc1) {
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        v[j] = round_bf16(acc0[j] + bv[j]);
-        v[4 + j] = round_bf16(acc1[j] + bv[4 + j]);
-    }
-    if constexpr (EPI == PW_GELU) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = gelu_fast(v[j]);
-    } else if constexpr (EPI == PW_ADD) {
-        const uint4 r = *reinterpret_cast<const uint4*>(p.res + m * p.N + n);
-        v[0] += bf16_lo(r.x); v[1] += bf16_hi(r.x); v[2] += bf16_lo(r.y); v[3] += bf16_hi(r.y);
-        v[4] += bf16_lo(r.z); v[5] += bf16_hi(r.z); v[6] += bf16_lo(r.w); v[7] += bf16_hi(r.w);
-    }
-    *reinterpret_cast<uint4*>(p.out + m * p.N + n) =
-        make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
-}
-
-__device__ __forceinline__ void pw_bias8(const PwParams& p, int n, float (&bv)[8]) {
-    if (p.bias) {
-        const float4 b0 = *reinterpret_cast<const float4*>(p.bias + n);
-        const float4 b1 = *reinterpret_cast<const float4*>(p.bias + n + 4);
-        bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w; bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) bv[j] = 0.f;
-    }
-}
-
-// Row of w feeding MFMA row i16 of n tile tn, for the channel interleave above.
-__device__ __forceinline__ int pw_wrow(int tn, int i16) { return 32 * (tn / 2) + 8 * (i16 / 4) + 4 * (tn % 2) + (i16 % 4); }
-
 // PRO: 0 no GRN prologue; 1 GRN applied to each x chunk as it is loaded (scale and
 // beta read from global memory per chunk); 2 the k tile's scale rows of the block's
 // (at most two) images and beta staged in LDS with the operand tiles and applied to the
@@ -133,8 +54,9 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const int wm = wv % WGM, wn = wv / WGM;
-    const int64_t m0 = static_cast<int64_t>(xcd_remap_any(blockIdx.x, gridDim.x)) * BM;
-    const int n0 = static_cast<int>(blockIdx.y) * BN;
+    int64_t m0;
+    int n0;
+    pw_tile<BM, BN>(p, m0, n0);
     const int K = p.K;
     const int ntiles = (K + PW_BK - 1) / PW_BK;
 
@@ -263,6 +185,141 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
     }
 }
 
+// ---------------------------------------------------------------------------
+// Deep products (K % 64 == 0): the operand tiles go global -> LDS directly
+// (global_load_lds_dwordx4, no registers), three k tiles in a ring, so two tiles'
+// loads are in flight while the third feeds the matrix cores.  Each wave waits for its
+// own copies of the next tile (s_waitcnt vmcnt) and a barrier then publishes them to
+// the other waves; the copies are issued from inline assembly, so the compiler's own
+// wait insertion (which would drain every copy at each barrier) does not apply and the
+// counts below are the complete synchronisation.
+// LDS layout: 16-byte chunk c (0..7) of tile row r sits at slot 8r + (c ^ (r & 7)), so
+// one wave instruction fills 8 rows (8 lanes per 128-byte row, coalesced) and the 16
+// rows of a fragment read fall in distinct bank groups.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
+    // M0 holds the wave's LDS destination; lane i writes 16 bytes at M0 + 16 i.
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
+                 : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int BM, int BN, int WGM, int EPI, bool PRO, int OCC>
+__global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams p) {
+    constexpr int BK = 64, WGN = 4 / WGM, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
+    static_assert(TN % 2 == 0 && BM % 32 == 0 && BN % 32 == 0, "tile shape");
+    constexpr int A_INS = BM / 32, B_INS = BN / 32;             // wave instructions per operand and stage
+    constexpr int D = A_INS + B_INS + (PRO ? 1 : 0);            // copies per wave and stage
+    constexpr int GRN_BYTES = PRO ? 3 * BK * 4 : 0;
+    constexpr int STAGE = (BM + BN) * BK * 2 + GRN_BYTES;
+    __shared__ __align__(16) unsigned char lds[3 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
+    const int wm = wv % WGM, wn = wv / WGM;
+    int64_t m0;
+    int n0;
+    pw_tile<BM, BN>(p, m0, n0);
+    const int K = p.K, ntiles = K / BK;
+    typedef __attribute__((address_space(3))) unsigned char lds_byte;
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_byte*)lds));
+
+    // Source of this lane's chunk in each copy instruction (k offset added per tile).
+    const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+    const bf16_t* asrc[A_INS];
+    const bf16_t* bsrc[B_INS];
+#pragma unroll
+    for (int i = 0; i < A_INS; ++i) {
+        const int64_t m = std::min<int64_t>(m0 + (wv * A_INS + i) * 8 + lrow, p.M - 1);
+        asrc[i] = p.x + m * K + 8 * lchunk;
+    }
+#pragma unroll
+    for (int i = 0; i < B_INS; ++i) bsrc[i] = p.w + static_cast<int64_t>(n0 + (wv * B_INS + i) * 8 + lrow) * K + 8 * lchunk;
+    [[maybe_unused]] const float* gsrc = nullptr;
+    [[maybe_unused]] int64_t img0 = 0;
+    if constexpr (PRO) {
+        img0 = fast_div(static_cast<uint32_t>(m0), p.rows_per_image);
+        const int64_t last_img = fast_div(static_cast<uint32_t>(p.M - 1), p.rows_per_image);
+        const int j = 12 * wv + std::min(lane, 11), which = j / 16, off = 4 * (j % 16);
+        gsrc = which < 2 ? p.pro_scale + std::min<int64_t>(img0 + which, last_img) * K + off : p.pro_shift + off;
+    }
+    auto issue = [&](int t) {
+        const uint32_t sb = lds0 + (t % 3) * STAGE;
+        const int kt = t * BK;
+#pragma unroll
+        for (int i = 0; i < A_INS; ++i)
+            lds_dma16(asrc[i] + kt, __builtin_amdgcn_readfirstlane(sb + (wv * A_INS + i) * 1024));
+#pragma unroll
+        for (int i = 0; i < B_INS; ++i)
+            lds_dma16(bsrc[i] + kt, __builtin_amdgcn_readfirstlane(sb + BM * BK * 2 + (wv * B_INS + i) * 1024));
+        if constexpr (PRO) {
+            // 48 chunks of scale (two image rows) and beta: 12 per wave.
+            if (lane < 12) lds_dma16(gsrc + kt, __builtin_amdgcn_readfirstlane(sb + (BM + BN) * BK * 2 + wv * 12 * 16));
+        }
+    };
+    auto slot = [](int r, int c) { return (r * 8 + (c ^ (r & 7))) * 16; };
+    int brow[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) brow[tn] = wn * WN + pw_wrow(tn, i16);
+    [[maybe_unused]] int rel[TM];
+    if constexpr (PRO) {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            const int64_t m = std::min<int64_t>(m0 + wm * WM + 16 * tm + i16, p.M - 1);
+            rel[tm] = static_cast<int>(fast_div(static_cast<uint32_t>(m), p.rows_per_image) - img0);
+        }
+    }
+
+    v4f_pw acc[TN][TM];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = v4f_pw{0.f, 0.f, 0.f, 0.f};
+
+    issue(0);
+    if (ntiles > 1) issue(1);
+    for (int t = 0; t < ntiles; ++t) {
+        if (t + 1 < ntiles) wait_vmem<D>();
+        else wait_vmem<0>();
+        block_barrier();
+        if (t + 2 < ntiles) issue(t + 2);
+        const unsigned char* sa = lds + (t % 3) * STAGE;
+        const unsigned char* sbp = sa + BM * BK * 2;
+        [[maybe_unused]] const float* sg = reinterpret_cast<const float*>(sa + (BM + BN) * BK * 2);
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            const int c = 4 * ks + kg;
+            uint4 af[TN], bfr[TM];
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) af[tn] = *reinterpret_cast<const uint4*>(sbp + slot(brow[tn], c));
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                bfr[tm] = *reinterpret_cast<const uint4*>(sa + slot(wm * WM + 16 * tm + i16, c));
+                if constexpr (PRO) bfr[tm] = grn_apply8(bfr[tm], sg + rel[tm] * BK + 8 * c, sg + 2 * BK + 8 * c);
+            }
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = mfma_16x16x32(af[tn], bfr[tm], acc[tn][tm]);
+        }
+    }
+
+#pragma unroll
+    for (int q = 0; q < TN / 2; ++q) {
+        const int n = n0 + wn * WN + 32 * q + 8 * kg;
+        float bv[8];
+        pw_bias8(p, n, bv);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            const int64_t m = m0 + wm * WM + 16 * tm + i16;
+            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm]);
+        }
+    }
+}
+
 // Narrow outputs (N = 32 or 64) with K <= 256: no LDS.  A wave owns 16 TM pixels and
 // every output channel; it issues all loads of its x rows at once (TM * KS 16-byte
 // fragments), reads the small weight fragments through L1 and writes each pixel's
@@ -334,7 +391,7 @@ int launch_pw(const PwParams& p, hipStream_t s) {
         if (env[0] == 'w') { narrow = false; bk = std::atoi(env + 1); }
     }
     auto go = [&](auto kern, int64_t rows, int cols) {
-        const dim3 grid(static_cast<unsigned>((p.M + rows - 1) / rows), static_cast<unsigned>(p.N / cols));
+        const dim3 grid(static_cast<unsigned>((p.M + rows - 1) / rows * (p.N / cols)));
         hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, p);
         return check_launch("pointwise_gemm_kernel");
     };
@@ -357,6 +414,17 @@ int launch_pw(const PwParams& p, hipStream_t s) {
         }
     }
     if (const char* env = std::getenv("VH_PW_CFG")) {
+        // d<BM>x<BN>o<OCC>: LDS-copy ring kernel (K % 64 == 0, N % BN == 0)
+        int dm = 0, dn = 0, docc = 0;
+        if (std::sscanf(env, "d%dx%do%d", &dm, &dn, &docc) == 3 && p.N % dn == 0 && p.K % 64 == 0) {
+            const bool stage_grn = PRO_ON && p.rows_per_image.d >= static_cast<uint32_t>(dm);
+#define VH_PWD(BM_, BN_, WGM_, OCC_)                                                                     \
+    if (dm == BM_ && dn == BN_ && docc == OCC_ && (stage_grn || !PRO_ON))                                \
+        return go(pointwise_dma_kernel<BM_, BN_, WGM_, EPI, PRO_ON, OCC_>, BM_, BN_);
+            VH_PWD(128, 128, 2, 1) VH_PWD(128, 128, 2, 2) VH_PWD(64, 128, 2, 2) VH_PWD(64, 128, 2, 3)
+            VH_PWD(128, 64, 2, 2) VH_PWD(128, 64, 2, 3) VH_PWD(256, 128, 4, 1)
+#undef VH_PWD
+        }
         // t<BM>x<BN>k<BK>o<OCC> (tiled variants for measurements, N % BN == 0)
         int bm = 0, bn = 0, kk = 0, occ = 0;
         if (std::sscanf(env, "t%dx%dk%do%d", &bm, &bn, &kk, &occ) == 4 && p.N % bn == 0) {
@@ -378,10 +446,20 @@ int launch_pw(const PwParams& p, hipStream_t s) {
             return go(pointwise_gemm_kernel<BM_, BN_, WGM_, BK_, EPI, 2, OCC_>, BM_, BN_);
         return go(pointwise_gemm_kernel<BM_, BN_, WGM_, BK_, EPI, PRO, OCC_>, BM_, BN_);
     };
+    if (bk == 0 && p.K % 64 == 0 && p.K >= 128 && (p.N == 64 || (p.N % 128 == 0 && (p.K >= 256 || p.N <= 256)))) {
+        // Deep products: the LDS-copy ring (measured on MI355X at the Tiny shapes,
+        // B = 128: 5-40 % faster than the register-staged tiles from K = 128 up, except
+        // K = 128 with N = 512, where the wide output favours the 4-resident tiles).
+        const bool stage_grn = PRO_ON && p.rows_per_image.d >= (p.N == 64 ? 128u : 64u);
+        if (!PRO_ON || stage_grn) {
+            if (p.N == 64) return go(pointwise_dma_kernel<128, 64, 2, EPI, PRO_ON, 3>, 128, 64);
+            if (p.K >= 1024) return go(pointwise_dma_kernel<64, 128, 2, EPI, PRO_ON, 2>, 64, 128);
+            return go(pointwise_dma_kernel<64, 128, 2, EPI, PRO_ON, 3>, 64, 128);
+        }
+    }
     if (bk == 0) {
-        // Defaults measured on MI355X at the Tiny shapes (B = 128).  Short products want
-        // small tiles and many resident blocks (more k tiles in flight per CU); deep
-        // ones, 128 x 128 tiles with a 64-deep k step.
+        // Shorter products: register-staged tiles.  They want small tiles and many
+        // resident blocks (more k tiles in flight per CU).
         using std::integral_constant;
         if (p.N == 32)
             return tiled(integral_constant<int, 256>{}, integral_constant<int, 32>{}, integral_constant<int, 4>{},
@@ -426,7 +504,7 @@ extern "C" int vh_pointwise_conv_nhwc_forward(const void* x, int32_t io_dtype, c
     VH_REQUIRE(N == 32 || N == 64 || N % 128 == 0, VH_ERR_SHAPE,
                "pointwise conv needs N = 32, 64 or a multiple of 128, got %lld", (long long)N);
     VH_REQUIRE(M * std::max(N, K) < (int64_t(1) << 40), VH_ERR_SHAPE, "pointwise conv operands too large");
-    VH_REQUIRE(epilogue >= PW_BIAS && epilogue <= PW_ADD, VH_ERR_ARG, "unknown epilogue %d", epilogue);
+    VH_REQUIRE(epilogue >= PW_BIAS && epilogue <= PW_SILU, VH_ERR_ARG, "unknown epilogue %d", epilogue);
     VH_REQUIRE(epilogue != PW_ADD || residual != nullptr, VH_ERR_ARG, "epilogue 2 needs the residual");
     VH_REQUIRE((grn_scale == nullptr) == (grn_beta == nullptr), VH_ERR_ARG,
                "GRN scale and beta must be given together");
@@ -454,6 +532,7 @@ extern "C" int vh_pointwise_conv_nhwc_forward(const void* x, int32_t io_dtype, c
     switch (epilogue) {
         case PW_BIAS: return pro ? launch_pw<PW_BIAS, true>(p, s) : launch_pw<PW_BIAS, false>(p, s);
         case PW_GELU: return pro ? launch_pw<PW_GELU, true>(p, s) : launch_pw<PW_GELU, false>(p, s);
+        case PW_SILU: return pro ? launch_pw<PW_SILU, true>(p, s) : launch_pw<PW_SILU, false>(p, s);
         default: return pro ? launch_pw<PW_ADD, true>(p, s) : launch_pw<PW_ADD, false>(p, s);
     }
 }

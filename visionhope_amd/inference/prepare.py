@@ -37,6 +37,10 @@ def prepare_for_inference(model):
             # Eval-mode BatchNorm folded into the convolution on the GPU path (no
             # parameter changes: the folded copy is cached beside the module).
             module._vh_fold_bn = True
+        if hasattr(module, "head_pre_logits") and hasattr(module, "head_norm"):
+            # The classifier head's BatchNorm likewise, with the LayerNorm and SiLU fused
+            # around the 1x1 projection.
+            module._vh_fold_head = True
     with torch.no_grad():
         for block in blocks:
             counts["line_mixer"] += 1

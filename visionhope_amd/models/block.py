@@ -34,21 +34,23 @@ def _is_pointwise(conv):
             and conv.padding == (0, 0) and conv.groups == 1)
 
 
-# Below this many pixels the 1x1 projections go to the library GEMM: its tiles keep the
-# matrix cores busier on short, deep products (measured on MI355X at the Tiny stage-4
-# shapes, 6272 pixels with K up to 2048), while the native kernel wins on the long
-# narrow products of the early stages and by fusing the surrounding elementwise work.
-_MATRIX_CORE_MIN_PIXELS = 16384
+# Short (few-pixel) products with K x N at or above this go to the library GEMM: on the
+# Tiny stage-4 FFN (6272 pixels, 512 <-> 2048 channels) its tiles keep the matrix cores
+# busier than the native kernel's, more than the fused epilogue saves (measured on
+# MI355X, whole forward).  Every other projection takes the native kernel.
+_LIBRARY_MIN_KN = 1 << 20
+_LIBRARY_MAX_PIXELS = 16384
 
 
 def _matrix_core_ok(t_nhwc, module):
-    """Whether the bf16 matrix-core 1x1 kernel takes ``module`` on the NHWC view ``t``."""
+    """Whether the bf16 matrix-core 1x1 kernel takes ``module`` on the NHWC view ``t``
+    (otherwise the library GEMM runs on the autocast-cast operands)."""
     weight = module.weight
     n, k = weight.shape[0], weight.shape[1]
     pixels = t_nhwc.numel() // max(t_nhwc.shape[-1], 1)
     return (t_nhwc.is_contiguous() and t_nhwc.data_ptr() % 16 == 0 and module.bias is not None
             and pointwise.supported(k, n) and t_nhwc.shape[-1] == k
-            and (pixels >= _MATRIX_CORE_MIN_PIXELS or n <= 64))
+            and (pixels >= _LIBRARY_MAX_PIXELS or k * n < _LIBRARY_MIN_KN))
 
 
 def _grn_beta(grn):

@@ -5,7 +5,7 @@ from torch import nn
 
 from .block import VisionHOPEBlock
 from .common import ClassificationModel, initialize_weights
-from .layers import Downsample, PatchEmbedding, build_norm
+from .layers import Downsample, LayerNorm2d, PatchEmbedding, build_norm
 
 
 class HierarchicalVisionHOPE(ClassificationModel):
@@ -78,8 +78,48 @@ class HierarchicalVisionHOPE(ClassificationModel):
     def forward_features(self, x):
         for downsample, stage in zip(self.downsample_layers, self.stages):
             x = self._run_blocks(stage, downsample(x))
+        if self._fused_head_ok(x):
+            return self._fused_head(x)
         x = self.norm(x)
         x = self.head_pre_logits(x)
         x = self.head_norm(x)
         x = self.head_act(x)
         return x.mean(dim=[2, 3])
+
+    def _fused_head_ok(self, x):
+        """Prepared for inference, eval mode, bf16 autocast on a channels-last CUDA map,
+        LayerNorm2d norm, a foldable head BatchNorm, and SiLU."""
+        if (not getattr(self, "_vh_fold_head", False) or self.training or not x.is_cuda
+                or not torch.is_autocast_enabled("cuda") or torch.get_autocast_dtype("cuda") != torch.bfloat16
+                or not isinstance(self.norm, LayerNorm2d) or type(self.head_act) is not nn.SiLU):
+            return False
+        from ..utils import pointwise
+        from ..utils.conv_bn import foldable
+        from ..utils.layer_norm_cuda import can_fuse_layernorm2d
+        conv = self.head_pre_logits
+        return (x.is_contiguous(memory_format=torch.channels_last)
+                and can_fuse_layernorm2d(x, self.norm.weight, self.norm.bias)
+                and pointwise.is_pointwise(conv) and foldable(conv, self.head_norm)
+                and pointwise.supported(conv.in_channels, conv.out_channels))
+
+    def _fused_head(self, x):
+        """``mean(silu(head_norm(head_pre_logits(norm(x)))))`` in two native passes: the
+        LayerNorm stored as bf16 (the value autocast feeds the 1x1 conv), then the 1x1 conv
+        with the eval BatchNorm folded into it and the SiLU in the GEMM epilogue, each
+        rounded to bf16 as the autocast reference rounds them (reference
+        ``models/hierarchical.py:78-85``)."""
+        from ..utils import pointwise
+        from ..utils.conv_bn import folded_weights
+        from ..utils.layer_norm_cuda import visionhope_layernorm2d
+
+        h = visionhope_layernorm2d(x, self.norm.weight, self.norm.bias, self.norm.eps,
+                                   force_channels_last=True, out_dtype=torch.bfloat16)
+        conv = self.head_pre_logits
+        weight, bias = folded_weights(conv, self.head_norm)
+        cached = getattr(conv, "_vh_head_gemm", None)
+        if cached is None or cached[0] is not weight:
+            object.__setattr__(conv, "_vh_head_gemm", (weight, weight.reshape(weight.shape[0], -1)
+                                                       .to(torch.bfloat16).contiguous()))
+            cached = conv._vh_head_gemm
+        y = pointwise.pointwise_gemm(h.permute(0, 2, 3, 1), cached[1], bias, pointwise.EPI_SILU)
+        return y.permute(0, 3, 1, 2).mean(dim=[2, 3])

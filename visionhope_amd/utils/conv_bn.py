@@ -3,10 +3,13 @@ folded into the convolution (inference only).
 
 In eval mode ``bn(conv(x)) = conv(x; W s) + ((b - mean) s + beta)`` with
 ``s = gamma / sqrt(var + eps)`` per output channel (``models/layers.py:85-119``). The
-folded weight goes to the library convolution (cast by autocast as the original would be);
-the folded bias and the activation run in one native channels-last pass
-(``vh_bias_act_nhwc_forward``), which rounds the BatchNorm output and the activation output
-to the activation dtype, as the unfolded modules do.
+3x3 convolutions of the Tiny stem and downsample layers run as one native implicit GEMM
+with the folded bias and the GELU in its epilogue (``vh_conv3x3_nhwc_forward``: the
+folded weight rounded to bf16 as autocast rounds it, the sum and the activation each
+rounded to bf16). Other shapes go to the library convolution with the folded weight,
+followed by one native channels-last pass for the bias and activation
+(``vh_bias_act_nhwc_forward``), which rounds the BatchNorm output and the activation
+output to the activation dtype, as the unfolded modules do.
 """
 
 import torch
@@ -58,9 +61,66 @@ def bias_act(x, bias, act=ACT_NONE):
     return x
 
 
+def _bf16_compute(x, conv):
+    """The convolution computes in bf16: a bf16 map, or the fp32 image under bf16 autocast
+    (which the reference's autocast conv would round to bf16)."""
+    if x.dtype == torch.bfloat16:
+        return True
+    return (x.dtype == torch.float32 and conv.in_channels == 3 and torch.is_autocast_enabled("cuda")
+            and torch.get_autocast_dtype("cuda") == torch.bfloat16)
+
+
+def native_conv3x3_ok(x, conv):
+    """Whether ``vh_conv3x3_nhwc_forward`` takes ``conv`` on the channels-last map ``x``."""
+    n, c = conv.out_channels, conv.in_channels
+    return (x.is_cuda and x.dim() == 4 and x.shape[1] == c and conv.kernel_size == (3, 3)
+            and conv.padding == (1, 1) and conv.dilation == (1, 1) and conv.groups == 1
+            and conv.stride in ((1, 1), (2, 2)) and conv.padding_mode == "zeros"
+            and x.is_contiguous(memory_format=torch.channels_last) and (c == 3 or c % 32 == 0)
+            and (n in (32, 64) or n % 128 == 0) and _bf16_compute(x, conv))
+
+
+def gemm_weight(conv, weight):
+    """The folded weight as the implicit-GEMM operand ``[N, K]`` bf16 (layout in
+    ``include/visionhope_hip.h``: channels-last taps, and for 3 input channels the taps
+    padded to 4 channels and 16 taps), cached next to the folded weight it comes from."""
+    cached = getattr(conv, "_vh_conv_gemm", None)
+    if cached is None or cached[0] is not weight:
+        with torch.no_grad():
+            n, c = weight.shape[0], weight.shape[1]
+            taps = weight.permute(0, 2, 3, 1).reshape(n, 9, c)
+            if c == 3:
+                padded = torch.zeros(n, 16, 4, device=weight.device, dtype=weight.dtype)
+                padded[:, :9, :3] = taps
+                taps = padded
+            gemm = taps.reshape(n, -1).to(torch.bfloat16).contiguous()
+        object.__setattr__(conv, "_vh_conv_gemm", (weight, gemm))
+        cached = conv._vh_conv_gemm
+    return cached[1]
+
+
+@on_tensor_device
+def conv3x3_bias_act(x, conv, weight, bias, act=ACT_NONE):
+    """``act(conv(x; weight) + bias)`` for a 3x3, padding-1 ``conv`` on the channels-last
+    map ``x`` through the native implicit GEMM; bf16 channels-last output."""
+    gemm = gemm_weight(conv, weight)
+    b, c, h, w = x.shape
+    s = conv.stride[0]
+    n = conv.out_channels
+    out = torch.empty((b, n, (h - 1) // s + 1, (w - 1) // s + 1), device=x.device, dtype=torch.bfloat16,
+                      memory_format=torch.channels_last)
+    lib = hip.load_library()
+    hip.check(lib.vh_conv3x3_nhwc_forward(
+        hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(gemm), hip.ptr(bias), int(act), hip.ptr(out),
+        b, h, w, c, n, s, hip.stream_of(x)), "vh_conv3x3_nhwc_forward")
+    return out
+
+
 def conv_bn_act(x, conv, bn, act=ACT_NONE):
     """``act(bn(conv(x)))`` for an eval-mode BatchNorm, folded (module docstring)."""
     weight, bias = folded_weights(conv, bn)
+    if native_conv3x3_ok(x, conv):
+        return conv3x3_bias_act(x, conv, weight, bias, act)
     y = F.conv2d(x, weight, None, conv.stride, conv.padding, conv.dilation, conv.groups)
     if not y.is_contiguous(memory_format=torch.channels_last) or y.data_ptr() % 16:
         y = y.contiguous(memory_format=torch.channels_last)

@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "vh_layernorm2d_forward", "vh_add_layernorm2d_forward", "vh_qnorm_forward", "vh_residual_add_forward",
     "vh_dwconv2d_nhwc_forward", "vh_grn_scale_forward", "vh_pointwise_conv_nhwc_forward",
     "vh_bias_act_nhwc_forward", "vh_dwconv2d_gelu_grn_workspace_bytes", "vh_dwconv2d_gelu_grn_forward",
+    "vh_conv3x3_nhwc_forward",
 )
 
 
@@ -91,6 +92,8 @@ _SIGNATURES = {
     "vh_pointwise_conv_nhwc_forward": (ctypes.c_int, [
         _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "vh_bias_act_nhwc_forward": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _i64, _i64, _vp]),
+    "vh_conv3x3_nhwc_forward": (ctypes.c_int, [
+        _vp, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _vp]),
     "vh_dwconv2d_gelu_grn_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i32]),
     "vh_dwconv2d_gelu_grn_forward": (ctypes.c_int, [
         _vp, _i32, _vp, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),

@@ -10,6 +10,8 @@ epilogue         result (every step rounded to bf16)           reference express
 ``EPI_BIAS``     x W^T + b                                     ``proj_in(x)``, ``fc1(x)`` ...
 ``EPI_GELU``     gelu(x W^T + b)                               ``ffn.act(ffn.fc1(x))``
 ``EPI_ADD``      r + (x W^T + b)                               ``x + ffn(...)`` (gamma folded)
+``EPI_SILU``     silu(x W^T + b)                               ``head_act(head_norm(...))``
+                                                               (BatchNorm folded)
 ===============  ===========================================  ==============================
 
 With ``grn=(scale, beta)`` the operand is ``bf16(x * scale[image] + beta)``: the GRN output
@@ -25,7 +27,7 @@ from . import hip
 from .cached_params import _key
 from .cuda import on_tensor_device
 
-EPI_BIAS, EPI_GELU, EPI_ADD = range(3)
+EPI_BIAS, EPI_GELU, EPI_ADD, EPI_SILU = range(4)
 
 
 def is_pointwise(module):
@@ -57,7 +59,6 @@ def pointwise_operands(module):
     return cached[1], cached[2]
 
 
-@on_tensor_device
 def pointwise_conv(x, module, epilogue=EPI_BIAS, residual=None, grn=None, out=None):
     """``x [..., K]`` contiguous bf16 (an NHWC map) -> ``[..., N]`` bf16 (module docstring).
 
@@ -65,9 +66,19 @@ def pointwise_conv(x, module, epilogue=EPI_BIAS, residual=None, grn=None, out=No
     beta [K])`` FP32 for an ``x`` of ``B`` images of equal size; ``out`` receives the
     result when given (contiguous, shaped like the output).
     """
+    weight, bias = pointwise_operands(module)
+    return pointwise_gemm(x, weight, bias, epilogue, residual, grn, out)
+
+
+@on_tensor_device
+def pointwise_gemm(x, weight, bias, epilogue=EPI_BIAS, residual=None, grn=None, out=None):
+    """``pointwise_conv`` on explicit operands: ``weight [N, K]`` contiguous bf16 and
+    ``bias [N]`` fp32 (or None)."""
     if not x.is_cuda or x.dtype != torch.bfloat16 or not x.is_contiguous() or x.data_ptr() % 16:
         raise ValueError("pointwise_conv expects a contiguous 16-byte aligned CUDA bf16 tensor")
-    weight, bias = pointwise_operands(module)
+    if (weight.dtype != torch.bfloat16 or weight.dim() != 2 or not weight.is_contiguous()
+            or (bias is not None and (bias.dtype != torch.float32 or bias.numel() != weight.shape[0]))):
+        raise ValueError("pointwise_conv needs a contiguous bf16 weight [N, K] and an fp32 bias [N]")
     n, k = weight.shape
     if x.shape[-1] != k or not supported(k, n):
         raise ValueError(f"pointwise_conv does not cover K={x.shape[-1]} -> N={n}")
