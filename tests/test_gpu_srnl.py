@@ -39,13 +39,17 @@ def test_sequence_forward_fp32_head_dims(oracle, device, head_dim, kind):
     assert_close(y.cpu().numpy(), expected, FP32_TOL, f"d={head_dim} {kind}")
 
 
-@pytest.mark.parametrize("lines_per_wave", [1, 2, 4])
+SCAN16_PACKINGS = ["1x4", "2x4", "4x4", "1x2", "2x2"]   # <lines per wave>x<16-slot tiles per wave>
+
+
+@pytest.mark.parametrize("packing", SCAN16_PACKINGS)
 @pytest.mark.parametrize("height,width", [(7, 7), (14, 14), (6, 9), (19, 37)])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL)])
-def test_spatial_scan16_lines_per_wave(oracle, device, monkeypatch, lines_per_wave, height, width, dtype, tol):
-    """head_dim 16 scan with 1, 2 or 4 lines packed per wave (forced; the library packs by
-    itself only at full-GPU line counts): short and long chunks, rectangular images."""
-    monkeypatch.setenv("VH_SCAN_LINES_PER_WAVE", str(lines_per_wave))
+def test_spatial_scan16_packing(oracle, device, monkeypatch, packing, height, width, dtype, tol):
+    """head_dim 16 scan with 1, 2 or 4 lines and 2 or 4 token tiles per wave (forced; the
+    library picks a packing by itself from the line count): short and long chunks (more
+    than one tile per chunk), rectangular images."""
+    monkeypatch.setenv("VH_SCAN_PACK", packing)
     heads = 4
     channels = heads * 16
     mems = memories(4, heads, 16, kind="strong", seed=height * 31 + width)
@@ -55,23 +59,24 @@ def test_spatial_scan16_lines_per_wave(oracle, device, monkeypatch, lines_per_wa
     wts = 1 + randn(4, channels, seed=74, scale=0.1)
     got = _spatial(device, x, q, mems, skip, wts, (width, width, height, height))
     expected = oracle.operator_forward(x.float().numpy(), q.float().numpy(), mems, skip.numpy(), wts.numpy(), 16)
-    assert_close(got, expected, tol, f"scan16 NL={lines_per_wave} {height}x{width} {dtype}")
+    assert_close(got, expected, tol, f"scan16 packing {packing} {height}x{width} {dtype}")
 
 
-@pytest.mark.parametrize("lines_per_wave", [2, 4])
+@pytest.mark.parametrize("packing", ["2x4", "4x4", "1x2", "2x2"])
 @pytest.mark.parametrize("chunks", [(5, 16), (17, 33)])
-def test_sequence_scan16_lines_per_wave(oracle, device, monkeypatch, lines_per_wave, chunks):
-    """Packed sequences with head_dim 16 and 4 heads, lines packed per wave, padded chunks."""
+def test_sequence_scan16_packing(oracle, device, monkeypatch, packing, chunks):
+    """Packed sequences with head_dim 16 and 4 heads, lines and tiles packed per wave,
+    padded chunks."""
     from visionhope_amd.models.srnl_core.chunk import srnl_packed_forward
 
-    monkeypatch.setenv("VH_SCAN_LINES_PER_WAVE", str(lines_per_wave))
+    monkeypatch.setenv("VH_SCAN_PACK", packing)
     batch, directions, heads, length = 2, 2, 4, 83
-    mems = memories(directions, heads, 16, kind="perturbed", seed=lines_per_wave)
+    mems = memories(directions, heads, 16, kind="perturbed", seed=int(packing[0]))
     x, q = _packed_case(batch, directions, heads, length, 16, torch.float32, seed=81)
     y = srnl_packed_forward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device),
                             q.to(device), list(chunks), q_raw=True)
     expected = oracle.sequence_forward(x.numpy(), q.numpy(), mems, list(chunks))
-    assert_close(y.cpu().numpy(), expected, FP32_TOL, f"sequence NL={lines_per_wave} chunks={chunks}")
+    assert_close(y.cpu().numpy(), expected, FP32_TOL, f"sequence packing {packing} chunks={chunks}")
 
 
 def test_config1_standalone_srnl(oracle, device):

@@ -26,6 +26,7 @@
 //     chunks uses 16x16-pixel MFMA tiles (srnl_readout16_kernel); every other
 //     case one thread per output in the reference's summation order.
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <type_traits>
 
@@ -75,6 +76,7 @@ struct ScanParams {
     int per_line_state;  // 1: memories hold one state per line (chunk.cu:287, StateCount == N)
     int x_vec;           // input rows are aligned for vector loads
     int lines_per_wave;  // head_dim 16: lines packed into one wave (1, 2 or 4)
+    int tiles_per_wave;  // head_dim 16: 16-slot column tiles per wave (2 or 4, >= lines_per_wave)
     int aligned;         // spatial input with chunks (W, W, H, H): chunk c of scan r is a row/column
     Consts k;
 };
@@ -497,16 +499,22 @@ __device__ __forceinline__ int64_t token_offset(const LineInput& in, int r, int6
     else return tok * in.st;
 }
 
-// NL lines per wave (NL in {1, 2, 4}): the NL lines share (b, r) and take consecutive
-// heads.  Each tile gives every line S = 64/NL token slots; lane l owns slot l % S of
-// line l / S for the per-token work, and MFMA column tile tc (16 slots) belongs to line
-// tc / (4/NL).  G of every line is spread over 64/NL lanes, RL = 4/NL lanes per row,
-// E = 4 NL entries per lane, so a row dot needs log2(RL) DPP steps.  Packing lines lets
-// short chunks (row length 14 or 7) fill the 64 lanes of the token phase.
-template <typename T, int NL, bool SPATIAL>
+// NL lines per wave (NL in {1, 2, 4}) and TCW column tiles of 16 token slots per wave
+// (TCW in {2, 4}, NL <= TCW): the NL lines share (b, r) and take consecutive heads.
+// Each tile gives every line S = 16 TCW / NL token slots; lane l < 16 TCW owns slot
+// l % S of line l / S for the per-token work (the other lanes idle there), and MFMA
+// column tile tc belongs to line tc / (TCW / NL).  G of every line is spread over 64/NL
+// lanes, RL = 4/NL lanes per row, E = 4 NL entries per lane, so a row dot needs
+// log2(RL) DPP steps.  Packing lines lets short chunks (row length 14 or 7) fill the
+// token slots; two tiles per wave instead of four halve the wave's token work and
+// double the number of waves, so two waves share each SIMD and hide each other's
+// latency when the lines would otherwise give one wave per SIMD.
+template <typename T, int NL, int TCW, bool SPATIAL>
 __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
-    constexpr int D = 16, TT = 64, ROWS = 3 * D + 2, GS = D + 1, DKS = TT + 4;
-    constexpr int S = TT / NL, TPL = 4 / NL, RL = 4 / NL, E = D / RL, SR = 64 * D;
+    static_assert((TCW == 2 || TCW == 4) && NL <= TCW, "tile packing");
+    constexpr int D = 16, TT = 16 * TCW, ROWS = 3 * D + 2, GS = D + 1, DKS = TT + 4;
+    constexpr int S = TT / NL, TPL = TCW / NL, RL = 4 / NL, E = D / RL, SR = 64 * D;
+    constexpr int NU = NL == 1 ? 1 : TCW;   // state sets the column tiles read
     __shared__ __align__(16) float St[NL * SR];       // per line: 50 state rows + zero rows
     __shared__ __align__(16) float Gs[NL * D * GS];
     __shared__ __align__(16) float kk[TT * D];        // normalised keys [slot][16]
@@ -542,16 +550,17 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
     const int lam_g = lane / (16 * RL);                 // recurrence layout
     const int grow = (lane % (16 * RL)) / RL, c0 = (lane % RL) * E;
     const int my_slot = lane % S;
-    const T* xcol[4];
+    const bool slot_lane = lane < TT;
+    const T* xcol[TCW];
 #pragma unroll
-    for (int tc = 0; tc < 4; ++tc)
+    for (int tc = 0; tc < TCW; ++tc)
         xcol[tc] = static_cast<const T*>(p.x.ptr) + b * p.x.sb + r * p.x.sr + (head0 + tc / TPL) * p.x.sh + 4 * q;
 
     // x operands of a tile move as raw bits: the loads are issued without a branch
     // (invalid slots read their line's first token) and decoded only where used, so a
     // prefetch never waits for memory before the work it overlaps.
     using Raw = typename std::conditional<sizeof(T) == 4, uint4, uint2>::type;
-    Raw xr_next[4];
+    Raw xr_next[TCW];
     unsigned valid_next = 0;
     bool have_next = false;
     // Row/column chunks (the spatial operator): token i of chunk cc of scan r is pixel
@@ -565,12 +574,12 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
         pc = (r & 1) ? L - 1 : 0;
         pst = static_cast<int>(p.x.st);
     }
-    auto issue_tile = [&](int64_t cc, int base, int cnt, Raw (&raw)[4], unsigned& valid) {
+    auto issue_tile = [&](int64_t cc, int base, int cnt, Raw (&raw)[TCW], unsigned& valid) {
         valid = 0;
-        int64_t offs[4];
+        int64_t offs[TCW];
         if (SPATIAL && p.aligned) {
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
+            for (int tc = 0; tc < TCW; ++tc) {
                 const int slot = (tc % TPL) * 16 + i16;
                 const bool ok = slot < cnt && cc * C + base + slot < p.L;
                 valid |= ok ? (1u << tc) : 0u;
@@ -578,7 +587,7 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
             }
         } else {
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
+            for (int tc = 0; tc < TCW; ++tc) {
                 const int slot = (tc % TPL) * 16 + i16;
                 const int64_t tok = cc * C + base + slot;
                 const bool ok = slot < cnt && tok < p.L;
@@ -588,10 +597,10 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
         }
         if (p.x_vec) {
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) raw[tc] = *reinterpret_cast<const Raw*>(xcol[tc] + offs[tc]);
+            for (int tc = 0; tc < TCW; ++tc) raw[tc] = *reinterpret_cast<const Raw*>(xcol[tc] + offs[tc]);
         } else {
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
+            for (int tc = 0; tc < TCW; ++tc) {
                 const T* src = xcol[tc] + offs[tc];
                 if constexpr (sizeof(T) == 4) {
                     raw[tc] = make_uint4(__float_as_uint(src[0]), __float_as_uint(src[1]), __float_as_uint(src[2]),
@@ -603,9 +612,9 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
             }
         }
     };
-    auto decode_tile = [&](const Raw (&raw)[4], unsigned valid, float (&xo)[4][4]) {
+    auto decode_tile = [&](const Raw (&raw)[TCW], unsigned valid, float (&xo)[TCW][4]) {
 #pragma unroll
-        for (int tc = 0; tc < 4; ++tc) {
+        for (int tc = 0; tc < TCW; ++tc) {
             float v[4];
             if constexpr (sizeof(T) == 4) {
                 v[0] = __uint_as_float(raw[tc].x); v[1] = __uint_as_float(raw[tc].y);
@@ -636,7 +645,7 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
 
         for (int base = 0; base < C; base += S) {
             const int cnt = min(S, C - base);
-            float xo[4][4];
+            float xo[TCW][4];
             if (!have_next) issue_tile(c, base, cnt, xr_next, valid_next);
             decode_tile(xr_next, valid_next, xo);
             // ---- projections on MFMA, norms per token; then each lane computes the
@@ -644,9 +653,9 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
             // All four column tiles at once (no control flow between them), so their
             // MFMA chains and reductions overlap instead of running back to back.  A
             // column tile without tokens sees x = 0 and yields zero keys and differences.
-            float ak[TPL == 4 ? 1 : 4][4], av[TPL == 4 ? 1 : 4][4], ev[TPL == 4 ? 1 : 4][4], aa[TPL == 4 ? 1 : 4][4];
+            float ak[NU][4], av[NU][4], ev[NU][4], aa[NU][4];
 #pragma unroll
-            for (int u = 0; u < (TPL == 4 ? 1 : 4); ++u) {
+            for (int u = 0; u < NU; ++u) {
                 const float* Sl = St + (u / TPL) * SR;
                 const float4 k4 = *reinterpret_cast<const float4*>(Sl + (2 * D + i16) * D + 4 * q);
                 const float4 v4 = *reinterpret_cast<const float4*>(Sl + (D + i16) * D + 4 * q);
@@ -657,9 +666,8 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 ev[u][0] = e4.x; ev[u][1] = e4.y; ev[u][2] = e4.z; ev[u][3] = e4.w;
                 aa[u][0] = a4.x; aa[u][1] = a4.y; aa[u][2] = a4.z; aa[u][3] = a4.w;
             }
-            v4f kacc[4], vacc[4];
-            float pe[4], pa[4];
-            constexpr int NU = TPL == 4 ? 1 : 4;
+            v4f kacc[TCW], vacc[TCW];
+            float pe[TCW], pa[TCW];
             [[maybe_unused]] v4s akh[NU], akl[NU], avh[NU], avl[NU];
             if constexpr (std::is_same<T, bf16_t>::value) {
 #pragma unroll
@@ -669,8 +677,8 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 }
             }
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
-                const int u = TPL == 4 ? 0 : tc;
+            for (int tc = 0; tc < TCW; ++tc) {
+                const int u = NU == 1 ? 0 : tc;
                 kacc[tc] = v4f{0.f, 0.f, 0.f, 0.f};
                 vacc[tc] = v4f{0.f, 0.f, 0.f, 0.f};
                 if constexpr (std::is_same<T, bf16_t>::value) {
@@ -690,18 +698,18 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 pe[tc] = ev[u][0] * xo[tc][0] + ev[u][1] * xo[tc][1] + ev[u][2] * xo[tc][2] + ev[u][3] * xo[tc][3];
                 pa[tc] = aa[u][0] * xo[tc][0] + aa[u][1] * xo[tc][1] + aa[u][2] * xo[tc][2] + aa[u][3] * xo[tc][3];
             }
-            float kn[4];
+            float kn[TCW];
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
+            for (int tc = 0; tc < TCW; ++tc) {
                 kn[tc] = kacc[tc][0] * kacc[tc][0] + kacc[tc][1] * kacc[tc][1] + kacc[tc][2] * kacc[tc][2] +
                          kacc[tc][3] * kacc[tc][3];
                 kn[tc] = xor16_32_sum(kn[tc]);
                 pe[tc] = xor16_32_sum(pe[tc]);
                 pa[tc] = xor16_32_sum(pa[tc]);
             }
-            float dsq[4], ksq[4];
+            float dsq[TCW], ksq[TCW];
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
+            for (int tc = 0; tc < TCW; ++tc) {
                 const float inv = rsqrtf(kn[tc] + 1e-6f);
                 float kv[4], df[4];
                 dsq[tc] = 0.f;
@@ -719,15 +727,16 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 for (int j = 0; j < 4; ++j) dkT[(4 * q + j) * DKS + t] = df[j];
             }
 #pragma unroll
-            for (int tc = 0; tc < 4; ++tc) {
+            for (int tc = 0; tc < TCW; ++tc) {
                 dsq[tc] = xor16_32_sum(dsq[tc]);
                 ksq[tc] = xor16_32_sum(ksq[tc]);
             }
-            // Lane 16 tc + i16 owns the token of column i16 of tile tc.
-            const float tok_ksq = q == 0 ? ksq[0] : q == 1 ? ksq[1] : q == 2 ? ksq[2] : ksq[3];
-            const float tok_dsq = q == 0 ? dsq[0] : q == 1 ? dsq[1] : q == 2 ? dsq[2] : dsq[3];
-            const float tok_ep = q == 0 ? pe[0] : q == 1 ? pe[1] : q == 2 ? pe[2] : pe[3];
-            const float tok_ap = q == 0 ? pa[0] : q == 1 ? pa[1] : q == 2 ? pa[2] : pa[3];
+            // Lane 16 tc + i16 owns the token of column i16 of tile tc (lanes past the
+            // tiles take tile 0's values and are masked below).
+#define VH_OWN(v) (TCW == 4 ? (q == 0 ? v[0] : q == 1 ? v[1] : q == 2 ? v[2 % TCW] : v[3 % TCW]) \
+                             : (q == 1 ? v[1] : v[0]))
+            const float tok_ksq = VH_OWN(ksq), tok_dsq = VH_OWN(dsq), tok_ep = VH_OWN(pe), tok_ap = VH_OWN(pa);
+#undef VH_OWN
             float my_alpha, my_eff;
             {
                 const float ep = fminf(10.f, fmaxf(-10.f, tok_ep));
@@ -758,7 +767,7 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
             //      beta_sj = (A_{j-1}/A_s) eta_s (k_s.k_j), w_s = (A_3/A_s) eta_s.
             //      Slots past the chunk act as the identity (alpha 1, eta 0). ----
             {
-                const bool valid = my_slot < cnt;
+                const bool valid = slot_lane && my_slot < cnt;
                 const float al_t = valid ? my_alpha : 1.f;
                 const float et_t = valid ? my_eff : 0.f;
                 const int j = lane & 3;
@@ -767,10 +776,11 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 const float na1 = quad_perm<0xF9>(al_t), na2 = quad_perm<0xFE>(al_t), na3 = quad_perm<0xFF>(al_t);
                 float kd1 = 0.f, kd2 = 0.f, kd3 = 0.f;
                 {
-                    const int t1 = max(lane - 1, 0), t2 = max(lane - 2, 0), t3 = max(lane - 3, 0);
+                    const int t0 = min(lane, TT - 1);
+                    const int t1 = max(t0 - 1, 0), t2 = max(t0 - 2, 0), t3 = max(t0 - 3, 0);
 #pragma unroll
                     for (int e = 0; e < D; e += 4) {
-                        const float4 k0 = *reinterpret_cast<const float4*>(kk + lane * D + e);
+                        const float4 k0 = *reinterpret_cast<const float4*>(kk + t0 * D + e);
                         const float4 k1 = *reinterpret_cast<const float4*>(kk + t1 * D + e);
                         const float4 k2 = *reinterpret_cast<const float4*>(kk + t2 * D + e);
                         const float4 k3 = *reinterpret_cast<const float4*>(kk + t3 * D + e);
@@ -792,8 +802,10 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 if (j == 0) cf_w *= na3;
                 const float cf_A3 = quad_perm<0x00>(al_t) * quad_perm<0x55>(al_t) * quad_perm<0xAA>(al_t) *
                                     quad_perm<0xFF>(al_t);
-                *reinterpret_cast<float4*>(cf + lane * 8) = make_float4(cf_a, cf_b1, cf_b2, cf_b3);
-                *reinterpret_cast<float4*>(cf + lane * 8 + 4) = make_float4(cf_w, cf_A3, 0.f, 0.f);
+                if (slot_lane) {
+                    *reinterpret_cast<float4*>(cf + lane * 8) = make_float4(cf_a, cf_b1, cf_b2, cf_b3);
+                    *reinterpret_cast<float4*>(cf + lane * 8 + 4) = make_float4(cf_w, cf_A3, 0.f, 0.f);
+                }
             }
             __syncthreads();
             // ---- serial recurrence, 4 tokens per step; the operands of the next step
@@ -1251,24 +1263,28 @@ template <int D, typename T>
 void launch_scan(const ScanParams& sp, hipStream_t stream) {
     const int64_t lines = sp.B * sp.R * sp.heads;
     if constexpr (D == 16) {
-        const int nl = sp.lines_per_wave;
+        const int nl = sp.lines_per_wave, tcw = sp.tiles_per_wave;
         const unsigned grid = static_cast<unsigned>(lines / nl);
-        auto go = [&](auto nlc, auto spc) {
-            hipLaunchKernelGGL((srnl_scan16_kernel<T, decltype(nlc)::value, decltype(spc)::value>), dim3(grid),
-                               dim3(64), 0, stream, sp);
+        auto go = [&](auto nlc, auto tcc, auto spc) {
+            hipLaunchKernelGGL((srnl_scan16_kernel<T, decltype(nlc)::value, decltype(tcc)::value,
+                                                   decltype(spc)::value>),
+                               dim3(grid), dim3(64), 0, stream, sp);
         };
         using S1 = std::integral_constant<int, 1>;
         using S2 = std::integral_constant<int, 2>;
         using S4 = std::integral_constant<int, 4>;
-        if (sp.x.spatial) {
-            if (nl == 4) go(S4{}, std::true_type{});
-            else if (nl == 2) go(S2{}, std::true_type{});
-            else go(S1{}, std::true_type{});
-        } else {
-            if (nl == 4) go(S4{}, std::false_type{});
-            else if (nl == 2) go(S2{}, std::false_type{});
-            else go(S1{}, std::false_type{});
-        }
+        auto pack = [&](auto spc) {
+            if (tcw == 2) {
+                if (nl == 2) go(S2{}, S2{}, spc);
+                else go(S1{}, S2{}, spc);
+            } else {
+                if (nl == 4) go(S4{}, S4{}, spc);
+                else if (nl == 2) go(S2{}, S4{}, spc);
+                else go(S1{}, S4{}, spc);
+            }
+        };
+        if (sp.x.spatial) pack(std::true_type{});
+        else pack(std::false_type{});
     } else
         hipLaunchKernelGGL((srnl_scan_kernel<D, T>), dim3(static_cast<unsigned>(lines)),
                            dim3(ScanCfg<D>::NT), 0, stream, sp);
@@ -1303,19 +1319,31 @@ int64_t max_chunk_count(int64_t length, const int64_t* chunks, int64_t R) {
 }
 
 // Shared validation + scan launch for every SRNL entry point.
-// Lines per wave of the head_dim-16 scan.  Packing NL lines multiplies the useful
-// work of the token phase for chunks of at most 64/NL tokens and shortens every row
-// dot, but divides the number of waves: pack only while at least one wave per SIMD
-// (1024 on MI355X) remains.  The lines of a wave share (b, r), so NL divides heads.
-// VH_SCAN_LINES_PER_WAVE = 1, 2 or 4 forces a packing (when heads allows it).
-int scan16_lines_per_wave(int64_t lines, int64_t heads) {
-    if (const char* env = std::getenv("VH_SCAN_LINES_PER_WAVE")) {
-        const int forced = std::atoi(env);
-        if ((forced == 1 || forced == 2 || forced == 4) && heads % forced == 0) return forced;
+// Packing of the head_dim-16 scan: NL lines and TCW 16-slot column tiles per wave.
+// Packing lines multiplies the useful work of the token phase for chunks of at most
+// 16 TCW / NL tokens and shortens every row dot, but divides the number of waves.  The
+// scan is latency-bound, so two waves per SIMD (2048 on MI355X) beat fuller tiles with
+// one: measured on MI355X at the Tiny stages (B = 128), 2 lines x 2 tiles for 4096 and
+// 8192 lines (chunks 14 and 7) is 12-15 % faster than 4 x 4, and 1 line x 4 tiles for
+// 2048 lines (chunk 28) 13 % faster than 2 x 4.  The lines of a wave share (b, r), so NL
+// divides heads.  VH_SCAN_PACK = "<NL>x<TCW>" forces a packing (when heads allows it).
+void scan16_packing(int64_t lines, int64_t heads, int* nl, int* tcw) {
+    if (const char* env = std::getenv("VH_SCAN_PACK")) {
+        int fl = 0, ft = 0;
+        if (std::sscanf(env, "%dx%d", &fl, &ft) == 2 && (fl == 1 || fl == 2 || fl == 4) && (ft == 2 || ft == 4) &&
+            fl <= ft && heads % fl == 0) {
+            *nl = fl;
+            *tcw = ft;
+            return;
+        }
     }
-    if (heads % 4 == 0 && lines >= 4 * 1024) return 4;
-    if (heads % 2 == 0 && lines >= 2 * 1024) return 2;
-    return 1;
+    if (heads % 2 == 0 && lines >= 4 * 1024) {
+        *nl = 2;
+        *tcw = 2;
+    } else {
+        *nl = 1;
+        *tcw = 4;
+    }
 }
 
 int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv, const float* Mk,
@@ -1364,7 +1392,7 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
         sp.x_vec = ok ? 1 : 0;
     }
     sp.k = make_consts(consts);
-    sp.lines_per_wave = scan16_lines_per_wave(lines, heads);
+    scan16_packing(lines, heads, &sp.lines_per_wave, &sp.tiles_per_wave);
     sp.aligned = x.spatial && R == 4 && chunks[0] == x.W && chunks[1] == x.W && chunks[2] == x.H &&
                  chunks[3] == x.H && x.H * x.W * x.st < (int64_t(1) << 31);
     rc = dispatch_d(d, [&](auto dc) {
