@@ -237,3 +237,45 @@ def test_invariant_divisor_multiplication_is_exact():
             assert 0 <= n <= top
             assert (n * m) >> shift == n // d, (n, d)
             assert n * m < (1 << 64)
+
+
+def test_gelu_fit_accuracy():
+    """The device GELU's erfc fit, evaluated step by step in float32 with the constants
+    read from the kernel header, against x * Phi(x) in float64 (scipy's ndtr)."""
+    import re
+    from scipy.special import ndtr
+
+    src = (Path(__file__).resolve().parents[1] / "visionhope_amd" / "csrc" / "vh_common.h").read_text()
+    body = src[src.index("float gelu_fast(float x)"):]
+    body = body[:body.index("\n}\n")]
+    # p = c5; p = p * t -/+ c_k ...: the literals after the first `p = ` in order, with their signs
+    lines = [ln.strip() for ln in body.splitlines() if ln.strip().startswith(("float p =", "p = p * t"))]
+    coeffs = []
+    for ln in lines:
+        lit = float(re.search(r"([0-9]+\.[0-9]+)f", ln).group(1))
+        coeffs.append(-lit if ("- " in ln.split("=")[1] and "p * t" in ln) else lit)
+    assert len(coeffs) == 6
+    f32 = np.float32
+    x = np.concatenate([np.linspace(-12, 12, 200001), np.linspace(-1e-3, 1e-3, 2001)]).astype(f32)
+    z = np.abs(x) * f32(0.70710678118654752)
+    t = (f32(1) / (f32(1) + f32(0.5) * z)).astype(f32)
+    p = f32(coeffs[0])
+    for c in coeffs[1:]:
+        p = (p * t + f32(c)).astype(f32)
+    half_erfc = (t * np.exp2((p - (f32(0.72134752044448170) * x) * x).astype(f32))).astype(f32)
+    g = (x * np.where(x < 0, half_erfc, f32(1) - half_erfc)).astype(f32).astype(np.float64)
+    exact = x.astype(np.float64) * ndtr(x.astype(np.float64))
+    err = np.abs(g - exact)
+    assert err.max() < 2e-6
+    big = np.abs(exact) > 1e-6
+    assert (err[big] / np.abs(exact[big])).max() < 1.2e-5
+    # a dropped or mis-signed coefficient fails the same bound
+    for k in range(6):
+        bad = list(coeffs)
+        bad[k] = -bad[k]
+        p = f32(bad[0])
+        for c in bad[1:]:
+            p = (p * t + f32(c)).astype(f32)
+        h = (t * np.exp2((p - (f32(0.72134752044448170) * x) * x).astype(f32))).astype(f32)
+        gb = (x * np.where(x < 0, h, f32(1) - h)).astype(f32).astype(np.float64)
+        assert np.abs(gb - exact).max() > 1e-3
