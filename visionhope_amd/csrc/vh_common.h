@@ -205,8 +205,8 @@ __device__ __forceinline__ float sigmoid_fast(float v) {
 // relatively accurate; in fp32 the result is within 1e-5 (relative) of x * Phi(x) over
 // the whole real line.
 __device__ __forceinline__ float gelu_fast(float x) {
-    const float z = fabsf(x) * 0.70710678118654752f;
-    const float t = __builtin_amdgcn_rcpf(1.f + 0.5f * z);
+    // t = 1 / (1 + z/2) with z = |x| / sqrt(2)
+    const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(x), 0.35355339059327376f, 1.f));
     float p = 0.3292495f;
     p = p * t - 1.0203389f;
     p = p * t + 0.68085486f;
@@ -215,7 +215,8 @@ __device__ __forceinline__ float gelu_fast(float x) {
     p = p * t - 2.8271523f;
     // exponent log2(e) * (P(t) - z^2) - 1, with z^2 = x^2 / 2
     const float half_erfc = t * __builtin_amdgcn_exp2f(p - (0.72134752044448170f * x) * x);
-    return x * (x < 0.f ? half_erfc : 1.f - half_erfc);
+    // x Phi(x) = max(x, 0) - |x| erfc(|x| / sqrt(2)) / 2 on both sides of 0
+    return fmaf(-fabsf(x), half_erfc, fmaxf(x, 0.f));
 }
 
 }  // namespace vh
