@@ -499,6 +499,36 @@ __device__ __forceinline__ int64_t token_offset(const LineInput& in, int r, int6
     else return tok * in.st;
 }
 
+// Gates of one token from its pre-activations pe = x.e and pa = x.a, ||k - v||^2 and
+// ||k||^2 (reference chunk.cu:382-393, memory.cuh:219-233):
+//   eta = ETA_SCALE softplus(clamp(pe)), alpha = ALPHA_MIN + (1 - ALPHA_MIN) sigmoid(clamp(pa + bias)),
+//   cap = STAB_MU (1 - alpha) / (sqrt(||k - v||^2 + 1e-12) + 1e-6), eff = cap (1 - exp(-eta / cap)),
+//   eff = min(eff, nextafter(FACTOR alpha / max(||k||^2, 1e-20), 0)) with the spectral clamp.
+// On the hardware exp2, log2, reciprocal and square root (about one ulp each), as the
+// reference's --use_fast_math build evaluates them with approximate intrinsics of its
+// own.  pe <= 10 after the clamp, so the reference's softplus branch for inputs above 20
+// never applies.  1 - exp(-r) is its Taylor series below r = 1/4 (relative error under
+// 2e-8 there, where 1 - exp2 would cancel) and 1 - exp2(-r log2 e) above.  The bound is
+// positive (alpha > 0), so nextafter toward 0 is one less in its bit pattern.
+__device__ __forceinline__ void token_gates_fast(const Consts& k, float pe, float pa, float dsq, float ksq,
+                                                 float& alpha, float& eff) {
+    constexpr float kLog2e = 1.44269504088896341f, kLn2 = 0.69314718055994531f;
+    const float ep = fminf(10.f, fmaxf(-10.f, pe));
+    const float ap = fminf(10.f, fmaxf(-10.f, pa + k.alpha_bias));
+    const float eta = k.eta_scale * (kLn2 * __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(kLog2e * ep)));
+    alpha = k.alpha_min + (1.f - k.alpha_min) * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-kLog2e * ap));
+    const float dn = __builtin_amdgcn_sqrtf(dsq + 1e-12f);
+    const float cap = k.stab_mu * (1.f - alpha) * __builtin_amdgcn_rcpf(dn + 1e-6f);
+    const float r = eta * __builtin_amdgcn_rcpf(cap);
+    const float series =
+        r * (1.f - r * (0.5f - r * (1.f / 6.f - r * (1.f / 24.f - r * (1.f / 120.f - r * (1.f / 720.f))))));
+    eff = cap * (r < 0.25f ? series : 1.f - __builtin_amdgcn_exp2f(-kLog2e * r));
+    if (k.clamp) {
+        const float bound = k.factor * alpha * __builtin_amdgcn_rcpf(fmaxf(ksq, 1e-20f));
+        eff = fminf(eff, __uint_as_float(__float_as_uint(bound) - 1u));
+    }
+}
+
 // NL lines per wave (NL in {1, 2, 4}) and TCW column tiles of 16 token slots per wave
 // (TCW in {2, 4}, NL <= TCW): the NL lines share (b, r) and take consecutive heads.
 // Each tile gives every line S = 16 TCW / NL token slots; lane l < 16 TCW owns slot
@@ -739,15 +769,8 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
 #undef VH_OWN
             float my_alpha, my_eff;
             {
-                const float ep = fminf(10.f, fmaxf(-10.f, tok_ep));
-                const float ap = fminf(10.f, fmaxf(-10.f, tok_ap + p.k.alpha_bias));
-                const float sp = ep > 20.f ? ep : logf(1.f + expf(ep));
-                const float eta = p.k.eta_scale * sp;
-                const float alpha = p.k.alpha_min + (1.f - p.k.alpha_min) * (1.f / (1.f + expf(-ap)));
-                const float dn = sqrtf(tok_dsq + 1e-12f);
-                const float cap = p.k.stab_mu * (1.f - alpha) / (dn + 1e-6f);
-                float eff = cap * (-expm1f(-(eta / cap)));
-                if (p.k.clamp) eff = fminf(eff, nextafterf(p.k.factor * alpha / fmaxf(tok_ksq, 1e-20f), 0.f));
+                float alpha, eff;
+                token_gates_fast(p.k, tok_ep, tok_ap, tok_dsq, tok_ksq, alpha, eff);
                 my_alpha = alpha;
                 my_eff = eff;
             }
