@@ -698,12 +698,21 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
             }
             v4f kacc[TCW], vacc[TCW];
             float pe[TCW], pa[TCW];
-            [[maybe_unused]] v4s akh[NU], akl[NU], avh[NU], avl[NU];
-            if constexpr (std::is_same<T, bf16_t>::value) {
+            // bf16: the gate pre-activations x.e and x.a come from a third product whose
+            // operand rows 4q and 4q+1 are e and a (the rest zero), so every lane of token
+            // column i16 receives them in accumulator entries 0 and 1, with no reduction.
+            constexpr bool kMfmaBf16 = std::is_same<T, bf16_t>::value;
+            [[maybe_unused]] v4s akh[NU], akl[NU], avh[NU], avl[NU], gh[NU], gl[NU];
+            if constexpr (kMfmaBf16) {
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
                     split_bf16(ak[u], akh[u], akl[u]);
                     split_bf16(av[u], avh[u], avl[u]);
+                    // state rows 48 (e), 49 (a) and 50 (zero) by the lane's operand row i16
+                    const float4 g4 = *reinterpret_cast<const float4*>(
+                        St + (u / TPL) * SR + (3 * D + min(i16 & 3, 2)) * D + 4 * q);
+                    const float ga[4] = {g4.x, g4.y, g4.z, g4.w};
+                    split_bf16(ga, gh[u], gl[u]);
                 }
             }
 #pragma unroll
@@ -718,15 +727,19 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                     vacc[tc] = mfma_bf16(avh[u], xs, vacc[tc]);
                     kacc[tc] = mfma_bf16(akl[u], xs, kacc[tc]);
                     vacc[tc] = mfma_bf16(avl[u], xs, vacc[tc]);
+                    v4f gacc = mfma_bf16(gh[u], xs, v4f{0.f, 0.f, 0.f, 0.f});
+                    gacc = mfma_bf16(gl[u], xs, gacc);
+                    pe[tc] = gacc[0];
+                    pa[tc] = gacc[1];
                 } else {
 #pragma unroll
                     for (int st = 0; st < 4; ++st) {
                         kacc[tc] = mfma4(ak[u][st], xo[tc][st], kacc[tc]);
                         vacc[tc] = mfma4(av[u][st], xo[tc][st], vacc[tc]);
                     }
+                    pe[tc] = ev[u][0] * xo[tc][0] + ev[u][1] * xo[tc][1] + ev[u][2] * xo[tc][2] + ev[u][3] * xo[tc][3];
+                    pa[tc] = aa[u][0] * xo[tc][0] + aa[u][1] * xo[tc][1] + aa[u][2] * xo[tc][2] + aa[u][3] * xo[tc][3];
                 }
-                pe[tc] = ev[u][0] * xo[tc][0] + ev[u][1] * xo[tc][1] + ev[u][2] * xo[tc][2] + ev[u][3] * xo[tc][3];
-                pa[tc] = aa[u][0] * xo[tc][0] + aa[u][1] * xo[tc][1] + aa[u][2] * xo[tc][2] + aa[u][3] * xo[tc][3];
             }
             float kn[TCW];
 #pragma unroll
@@ -734,22 +747,25 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 kn[tc] = kacc[tc][0] * kacc[tc][0] + kacc[tc][1] * kacc[tc][1] + kacc[tc][2] * kacc[tc][2] +
                          kacc[tc][3] * kacc[tc][3];
                 kn[tc] = xor16_32_sum(kn[tc]);
-                pe[tc] = xor16_32_sum(pe[tc]);
-                pa[tc] = xor16_32_sum(pa[tc]);
+                if constexpr (!kMfmaBf16) {
+                    pe[tc] = xor16_32_sum(pe[tc]);
+                    pa[tc] = xor16_32_sum(pa[tc]);
+                }
             }
+            // ||k||^2 of the normalised key is ||k~||^2 / (||k~||^2 + 1e-6), taken from the
+            // reduced norm instead of a second reduction.
             float dsq[TCW], ksq[TCW];
 #pragma unroll
             for (int tc = 0; tc < TCW; ++tc) {
                 const float inv = rsqrtf(kn[tc] + 1e-6f);
                 float kv[4], df[4];
                 dsq[tc] = 0.f;
-                ksq[tc] = 0.f;
+                ksq[tc] = kn[tc] * inv * inv;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     kv[j] = kacc[tc][j] * inv;
                     df[j] = kv[j] - vacc[tc][j];
                     dsq[tc] += df[j] * df[j];
-                    ksq[tc] += kv[j] * kv[j];
                 }
                 const int t = 16 * tc + i16;
                 *reinterpret_cast<float4*>(kk + t * D + 4 * q) = make_float4(kv[0], kv[1], kv[2], kv[3]);
@@ -757,10 +773,7 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
                 for (int j = 0; j < 4; ++j) dkT[(4 * q + j) * DKS + t] = df[j];
             }
 #pragma unroll
-            for (int tc = 0; tc < TCW; ++tc) {
-                dsq[tc] = xor16_32_sum(dsq[tc]);
-                ksq[tc] = xor16_32_sum(ksq[tc]);
-            }
+            for (int tc = 0; tc < TCW; ++tc) dsq[tc] = xor16_32_sum(dsq[tc]);
             // Lane 16 tc + i16 owns the token of column i16 of tile tc (lanes past the
             // tiles take tile 0's values and are masked below).
 #define VH_OWN(v) (TCW == 4 ? (q == 0 ? v[0] : q == 1 ? v[1] : q == 2 ? v[2 % TCW] : v[3 % TCW]) \
