@@ -110,6 +110,24 @@ int vh_srnl_spatial_readout(
     int64_t W, int64_t C, int32_t head_dim, const int64_t chunks[4], const void* workspace,
     size_t workspace_bytes, void* stream);
 
+/* Backward of the packed SRNL forward: vh_srnl_sequence_forward (q_raw = 1, q [B, R, N,
+ * heads*d] in io_dtype) or vh_srnl_forward (q_raw = 0, pre-normalised fp32 q [B, R, heads,
+ * N, d]), with the same x, memories, memories_per_line and chunks.  dy [B, R, heads, N, d]
+ * fp32 is the gradient of y; outputs fp32: dx like x, dq like q, and the gradients of the
+ * five initial memories (summed over the batch when shared).  Chunks in [1, 64], head_dim
+ * 4, 8, 16 or 32; workspace from vh_srnl_backward_workspace_bytes.  Replaces
+ * srnl_backward / srnl_backward_qraw (models/srnl_core/csrc/chunk.cu:511-1057, bound at
+ * chunk.py:289-359 and 510-588); the forward is recomputed from the inputs instead of
+ * read from tensors saved by a training forward. */
+size_t vh_srnl_backward_workspace_bytes(int64_t B, int64_t R, int64_t heads, int64_t N, int32_t head_dim,
+                                        const int64_t* chunks);
+int vh_srnl_backward(
+    const void* x, const void* q, int32_t io_dtype, int32_t q_raw, const float* dy,
+    const float* M_m, const float* M_v, const float* M_k, const float* M_eta, const float* M_alpha,
+    int32_t memories_per_line, float* dx, float* dq, float* dM_m, float* dM_v, float* dM_k, float* dM_eta,
+    float* dM_alpha, int64_t B, int64_t R, int64_t heads, int64_t N, int32_t head_dim, const int64_t* chunks,
+    const vh_srnl_consts* consts, void* workspace, size_t workspace_bytes, void* stream);
+
 /* The reference's fused spatial entry with its own argument layout: X and
  * Q_raw are the serialized stacks [B, 4, H*W, C]; Out is [B, H, W, C] fp32;
  * chunks are (W, W, H, H).  Replaces srnl_line_forward_seq_noatomic

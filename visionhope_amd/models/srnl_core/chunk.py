@@ -12,7 +12,6 @@ import os
 import torch
 
 from ...utils import hip
-from ...utils.autograd import backward_unavailable
 from ...utils.cuda import on_tensor_device
 
 MAX_CHUNK = 64
@@ -104,6 +103,39 @@ def srnl_packed_forward(memories, x, q, chunk_sizes, *, q_raw):
     return out
 
 
+@on_tensor_device
+def srnl_packed_backward(memories, x, q, chunk_sizes, dy, *, q_raw):
+    """Gradients of ``srnl_packed_forward`` (same arguments) for the output gradient
+    ``dy [B, R, heads, N, d]``: ``(dM_m, dM_v, dM_k, dM_eta, dM_alpha, dx, dq)`` shaped and
+    typed like the corresponding inputs (``vh_srnl_backward``; reference
+    ``chunk.cu:511-1057``).  The forward is recomputed from the inputs."""
+    batch, directions, heads, length, head_dim = x.shape
+    chunks = [int(c) for c in chunk_sizes]
+    if len(chunks) != directions or min(chunks) <= 0 or max(chunks) > MAX_CHUNK:
+        raise ValueError(f"SRNL backward needs one chunk length in [1, {MAX_CHUNK}] per direction")
+    n_flat = batch * directions * heads
+    states, per_line = _float_memories(memories, directions, heads, head_dim, n_flat)
+    x_c = x.contiguous()
+    q_c = q.contiguous() if q_raw else q.float().contiguous()
+    dy_c = dy.float().contiguous()
+    dx = torch.empty(x_c.shape, device=x.device, dtype=torch.float32)
+    dq = torch.empty(q_c.shape, device=x.device, dtype=torch.float32)
+    dmem = [torch.empty_like(m) for m in states]
+    lib = hip.load_library()
+    chunk_ptr, _keep = hip.int64_array(chunks)
+    nbytes = lib.vh_srnl_backward_workspace_bytes(batch, directions, heads, length, head_dim, chunk_ptr)
+    if nbytes == 0:
+        raise ValueError(f"SRNL backward does not cover head_dim={head_dim} with chunks {chunks}")
+    ws = hip.workspace(nbytes, x.device)
+    hip.check(lib.vh_srnl_backward(
+        hip.ptr(x_c), hip.ptr(q_c), hip.dtype_code(x_c.dtype), int(bool(q_raw)), hip.ptr(dy_c),
+        *[hip.ptr(m) for m in states], per_line, hip.ptr(dx), hip.ptr(dq), *[hip.ptr(m) for m in dmem],
+        batch, directions, heads, length, head_dim, chunk_ptr, srnl_consts(), hip.ptr(ws), ws.numel() * 4,
+        hip.stream_of(x_c)), "vh_srnl_backward")
+    grads = [g.view(m.shape).to(m.dtype) for g, m in zip(dmem, memories)]
+    return (*grads, dx.to(x.dtype), dq.to(q.dtype))
+
+
 class SRNLNormalizedQueryFunction(torch.autograd.Function):
     """Forward of ``chunk.py:168-284``: normalised FP32 queries, chunks of at most 64."""
 
@@ -124,11 +156,17 @@ class SRNLNormalizedQueryFunction(torch.autograd.Function):
         if chunk_size > MAX_CHUNK:
             raise ValueError(f"chunk_size={chunk_size} exceeds MAX_CHUNK={MAX_CHUNK} in CUDA kernel")
         memories = (M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0)
-        return srnl_packed_forward(memories, x, q, [int(chunk_size)] * x.shape[1], q_raw=False)
+        chunks = [int(chunk_size)] * x.shape[1]
+        ctx.save_for_backward(*memories, x, q)
+        ctx.chunks = chunks
+        return srnl_packed_forward(memories, x, q, chunks, q_raw=False)
 
     @staticmethod
     def backward(ctx, dY):
-        backward_unavailable("SRNL")
+        """Reference ``chunk.py:289-359``: gradients of the memories, x and q."""
+        *memories, x, q = ctx.saved_tensors
+        grads = srnl_packed_backward(memories, x, q, ctx.chunks, dY, q_raw=False)
+        return (*grads, None)
 
 
 class SRNLRawQueryFunction(torch.autograd.Function):
@@ -159,11 +197,16 @@ class SRNLRawQueryFunction(torch.autograd.Function):
         if chunk_size > MAX_CHUNK:
             raise ValueError(f"chunk_size={chunk_size} exceeds MAX_CHUNK={MAX_CHUNK} in CUDA kernel")
         memories = (M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0)
-        return srnl_packed_forward(memories, x, q_raw, [int(chunk_size)] * 4, q_raw=True)
+        ctx.save_for_backward(*memories, x, q_raw)
+        ctx.chunks = [int(chunk_size)] * 4
+        return srnl_packed_forward(memories, x, q_raw, ctx.chunks, q_raw=True)
 
     @staticmethod
     def backward(ctx, dY):
-        backward_unavailable("SRNL")
+        """Reference ``chunk.py:510-588``: gradients of the memories, x and the raw queries."""
+        *memories, x, q_raw = ctx.saved_tensors
+        grads = srnl_packed_backward(memories, x, q_raw, ctx.chunks, dY, q_raw=True)
+        return (*grads, None, None, None)
 
 
 def can_fuse_raw_query(x, q_raw, num_heads, head_dim):

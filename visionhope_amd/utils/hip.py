@@ -31,7 +31,7 @@ EXPORTED_SYMBOLS = (
     "vh_layernorm2d_forward", "vh_add_layernorm2d_forward", "vh_qnorm_forward", "vh_residual_add_forward",
     "vh_dwconv2d_nhwc_forward", "vh_grn_scale_forward", "vh_pointwise_conv_nhwc_forward",
     "vh_bias_act_nhwc_forward", "vh_dwconv2d_gelu_grn_workspace_bytes", "vh_dwconv2d_gelu_grn_forward",
-    "vh_conv3x3_nhwc_forward",
+    "vh_conv3x3_nhwc_forward", "vh_srnl_backward_workspace_bytes", "vh_srnl_backward",
 )
 
 
@@ -67,6 +67,10 @@ _SIGNATURES = {
         _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _I64P, _CP, _vp, _sz, _vp]),
     "vh_srnl_spatial_readout": (ctypes.c_int, [
         _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _I64P, _vp, _sz, _vp]),
+    "vh_srnl_backward_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i32, _I64P]),
+    "vh_srnl_backward": (ctypes.c_int, [
+        _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+        _i64, _i64, _i64, _i64, _i32, _I64P, _CP, _vp, _sz, _vp]),
     "vh_srnl_line_forward_seq_noatomic": (ctypes.c_int, [
         _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
         _i64, _i64, _i64, _i64, _i32, _CP, _vp, _sz, _vp]),
