@@ -143,6 +143,35 @@ def measure_tail(device):
     return out
 
 
+def measure_srnl_backward(device):
+    """vh_srnl_backward on config 1 (standalone SRNL, fp32, d = 32) and on the lines of one
+    Tiny stage-3 operator (B = 128, bf16, d = 16): event-timed ms, and TFLOP/s of three
+    times the reference's forward FLOP count (the backward recomputes the forward and
+    runs the reverse recurrence, about twice its MACs) against the FP32 peak."""
+    import torch
+    from visionhope_amd.models.srnl_core.chunk import srnl_packed_backward
+
+    stream = torch.cuda.current_stream(device)
+    gen = torch.Generator(device=device).manual_seed(SEED)
+    out = {}
+    for tag, batch, dirs, heads, grid, d, dtype in (("config1_2x196x64_d32_fp32", 2, 1, 2, 14, 32, torch.float32),
+                                                    ("tiny_stage3_128x14x14x128_d16_bf16", 128, 4, 8, 14, 16,
+                                                     torch.bfloat16)):
+        n = grid * grid
+        mems = _perturbed_memories(heads, d, device, gen)
+        mems = tuple(m[:dirs].contiguous() for m in mems)
+        x = torch.randn(batch, dirs, heads, n, d, device=device, generator=gen).to(dtype)
+        q = torch.randn(batch, dirs, n, heads * d, device=device, generator=gen).to(dtype)
+        dy = torch.randn(batch, dirs, heads, n, d, device=device, generator=gen)
+        chunks = [grid] * dirs
+        ms = event_time_ms(lambda: srnl_packed_backward(mems, x, q, chunks, dy, q_raw=True), stream, 3, warmup=1)
+        flops = 3 * srnl_flops(batch, grid, grid, heads * d, d, chunks)
+        out[f"srnl_backward_{tag}"] = {"ms": round(ms, 3), "forward_equiv_gflop": round(flops / 1e9, 3),
+                                       "tflops": round(flops / ms / 1e9, 3),
+                                       "frac_fp32_peak": round(flops / ms / 1e9 / FP32_PEAK_TFLOPS, 4)}
+    return out
+
+
 def build_tiny(device, channels_last=True):
     import torch
     from visionhope_amd.inference.prepare import prepare_for_inference
@@ -310,6 +339,7 @@ def main(argv=None):
 
         stage_rows, srnl_flops_total, srnl_ms_total, srnl_bytes = measure_srnl_stages(device, args.batch)
         tail = measure_tail(device)
+        tail.update(measure_srnl_backward(device))
 
     images_per_s = args.batch * 1000.0 / ms
     achieved = srnl_flops_total / srnl_ms_total / 1e9  # TFLOP/s
