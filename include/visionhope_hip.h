@@ -333,6 +333,56 @@ int vh_residual_add_forward(
     const float* gamma, const float* drop_scale, float* out,
     int64_t total, int64_t channels, int64_t spatial, void* stream);
 
+/* Direction fusion backward (replaces visionhope_postprocess_scale_backward,
+ * utils/csrc/direction_fusion.cpp:2, direction_fusion.cu:123-691, bound at
+ * utils/direction_fusion.py:108-120).  dout: FP32 [B, C, H, W] (channels-last storage if
+ * dout_channels_last, else NCHW); y, x: [B, 4, heads, H*W, head_dim] in io_dtype; dy, dx:
+ * same layout and dtype; d_dskip: FP32 [C] or [4, C] (skip_per_dir); d_scale: FP32 [4, C].
+ * Parameter gradients are summed in a fixed order (deterministic). */
+size_t vh_postprocess_scale_backward_workspace_bytes(int64_t B, int64_t heads, int64_t H, int64_t W,
+                                                     int32_t head_dim, int32_t skip_per_dir);
+int vh_postprocess_scale_backward(const float* dout, int32_t dout_channels_last, const void* y, const void* x,
+                                  int32_t io_dtype, const float* d_skip, int32_t skip_per_dir, const float* scale,
+                                  void* dy, void* dx, float* d_dskip, float* d_scale, int64_t B, int64_t heads,
+                                  int64_t H, int64_t W, int32_t head_dim, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/* GRN backward (replaces grn_backward_cuda, utils/csrc/grn.cpp:4-11, grn_cuda.cu:126-359,
+ * bound at utils/grn_cuda.py:51-82).  dout: FP32 channels-last [B, C, H, W]; x: the forward
+ * input (channels-last, io_dtype); gx [B, C] and inv_den [B] as written by vh_grn_forward;
+ * dx: channels-last in io_dtype; dgamma, dbeta: FP32 [C]. */
+size_t vh_grn_backward_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W);
+int vh_grn_backward(const float* dout, const void* x, int32_t io_dtype, const float* gamma, const float* gx,
+                    const float* inv_den, void* dx, float* dgamma, float* dbeta, int64_t B, int64_t C, int64_t H,
+                    int64_t W, void* workspace, size_t workspace_bytes, void* stream);
+
+/* LayerNorm2d backward (replaces the Triton _layernorm2d_backward_kernel and
+ * _layernorm2d_reduce_kernel, utils/layer_norm_cuda.py:59-121,148-192).  dy: FP32
+ * channels-last; x: the forward input (channels-last, io_dtype); mean, rstd: [B*H*W] as
+ * written by vh_layernorm2d_forward; dx: channels-last in io_dtype; dweight, dbias: FP32
+ * [C].  C <= 1024. */
+size_t vh_layernorm2d_backward_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W);
+int vh_layernorm2d_backward(const float* dy, const void* x, int32_t io_dtype, const float* weight, const float* mean,
+                            const float* rstd, void* dx, float* dweight, float* dbias, int64_t B, int64_t C,
+                            int64_t H, int64_t W, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Query normalisation backward (replaces visionhope_qnorm_backward,
+ * utils/csrc/query_normalization.cpp:3, query_normalization.cu:78-134).  dq_out, q_out:
+ * FP32 [B, R, heads, N, d]; inv_norm: [B, R, heads, N] as written by vh_qnorm_forward;
+ * dq_raw: [B, R, N, heads*d] in io_dtype. */
+int vh_qnorm_backward(const float* dq_out, const float* q_out, const float* inv_norm, void* dq_raw, int32_t io_dtype,
+                      int64_t B, int64_t R, int64_t N, int64_t heads, int32_t head_dim, void* stream);
+
+/* Residual add backward (replaces the Triton _residual_backward_kernel and
+ * _residual_reduce_kernel, utils/residual.py:55-101,132-170).  dout: FP32 channels-last
+ * [B, C, H, W] (total = B*C*H*W values, spatial = H*W); branch: the forward's branch in
+ * branch_dtype; gamma [C], mask [B] FP32; dbranch in branch_dtype; dgamma FP32 [C].
+ * The residual's gradient is dout itself. */
+size_t vh_residual_add_backward_workspace_bytes(int64_t total, int64_t channels);
+int vh_residual_add_backward(const float* dout, const void* branch, int32_t branch_dtype, const float* gamma,
+                             const float* mask, void* dbranch, float* dgamma, int64_t total, int64_t channels,
+                             int64_t spatial, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

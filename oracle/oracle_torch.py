@@ -16,17 +16,22 @@ subgradient conventions of its backward (``chunk.cu:511-1057``, ``memory.cuh:253
 * the query normalisation ``q / max(||q||, 1e-12)`` drops the projection term below the
   epsilon (``chunk.cu:1042-1043``).
 
-Pinning (``tests/test_oracle_backward.py``): the forward equals the C oracle and the
-independent NumPy formulation of ``oracle.py`` on the same inputs, and
-``torch.autograd.gradcheck`` checks every gradient against central finite differences in
-float64.
+The operator tail (``direction_fusion_torch``, ``grn_torch``, ``layernorm2d_torch``,
+``qnorm_torch``, ``residual_add_torch``) restates the forwards of
+``utils/csrc/direction_fusion.cu:11-65``, ``utils/grn.py:26-38``, ``models/layers.py:25-35``,
+``utils/csrc/query_normalization.cu:10-40`` and ``utils/residual.py:31-52``; their
+gradients are the checker of the tail backward kernels.
+
+Pinning (``tests/test_oracle_backward.py``): every forward equals the C oracle and/or the
+NumPy formulation of ``oracle.py`` on the same inputs, and ``torch.autograd.gradcheck``
+checks every gradient against central finite differences in float64.
 """
 
 from __future__ import annotations
 
 import torch
 
-from .oracle import Consts
+from .oracle import Consts, restore_index
 
 
 def _line(x, q, mm, mv, mk, ev, av, c_len, q_raw, k):
@@ -100,3 +105,52 @@ def sequence_forward_torch(x_packed, q, memories, chunks, *, q_raw=True, consts=
                          [n % (r * heads) for n in range(n_lines)], [chunks[lr] for lr in line_r],
                          q_raw=q_raw, consts=consts)
     return y.reshape(b, r, heads, length, d)
+
+
+def direction_fusion_torch(y, x, d_skip, scale, height, width):
+    """``out[b, c, pixel] = sum_r scale[r, c] (y_r + skip_r[c] x_r)[t_r(pixel)]``, NCHW.
+
+    y, x ``[B, 4, heads, L, d]``; d_skip ``[heads, d]`` or ``[4, heads, d]``; scale ``[4, C]``.
+    """
+    b, _, heads, length, d = y.shape
+    c = heads * d
+    skip = d_skip.reshape(-1, c)
+    out = 0
+    for r in range(4):
+        k = skip[r if skip.shape[0] == 4 else 0].reshape(heads, 1, d)
+        seq = (y[:, r] + k * x[:, r]).permute(0, 2, 1, 3).reshape(b, length, c)
+        idx = torch.as_tensor(restore_index(r, height, width), dtype=torch.long)
+        # restored[:, idx[t]] = seq[:, t]  <=>  restored = seq[:, inverse(idx)]
+        inv = torch.empty_like(idx)
+        inv[idx] = torch.arange(length)
+        out = out + scale[r] * seq[:, inv]
+    return out.reshape(b, height, width, c).permute(0, 3, 1, 2)
+
+
+def grn_torch(x, gamma, beta, eps=1e-6):
+    """``x (1 + gamma nx) + beta``, nx = ||x_c|| / (mean_c ||x_c|| + eps), NCHW."""
+    c = x.shape[1]
+    gx = torch.linalg.vector_norm(x, dim=(2, 3), keepdim=True)   # subgradient 0 at a zero channel
+    nx = gx / (gx.mean(dim=1, keepdim=True) + eps)
+    return x * (1 + gamma.reshape(1, c, 1, 1) * nx) + beta.reshape(1, c, 1, 1)
+
+
+def layernorm2d_torch(x, weight, bias, eps=1e-6):
+    """LayerNorm over channels per pixel, biased variance, NCHW."""
+    c = x.shape[1]
+    mean = x.mean(dim=1, keepdim=True)
+    var = ((x - mean) ** 2).mean(dim=1, keepdim=True)
+    return (x - mean) / torch.sqrt(var + eps) * weight.reshape(1, c, 1, 1) + bias.reshape(1, c, 1, 1)
+
+
+def qnorm_torch(q_raw, heads, head_dim):
+    """``[B, R, N, heads d]`` -> ``q / max(|q|, 1e-12)`` as ``[B, R, heads, N, d]``."""
+    b, r, length, _ = q_raw.shape
+    q = q_raw.reshape(b, r, length, heads, head_dim).permute(0, 1, 3, 2, 4)
+    return q / torch.clamp_min(q.norm(dim=-1, keepdim=True), 1e-12)
+
+
+def residual_add_torch(residual, branch, gamma, drop_scale):
+    """``residual + branch gamma_c drop_scale_b`` on NCHW tensors."""
+    c = branch.shape[1]
+    return residual + branch * gamma.reshape(1, c, 1, 1) * drop_scale.reshape(-1, 1, 1, 1)

@@ -69,3 +69,75 @@ def test_torch_oracle_catches_a_dropped_state_term():
     assert torch.equal(y, y2)   # same inputs, same output (determinism)
     tm_bad = [tm[0], tm[1] * 0, tm[2], tm[3], tm[4]]
     assert (srnl_lines_torch(tx, tq, tm_bad, [0], [4]) - y).abs().max() > 1e-3
+
+
+def _np(t):
+    return t.detach().numpy()
+
+
+def test_torch_tail_forwards_match_numpy_oracle(oracle):
+    """Each tail forward of the differentiable oracle against the NumPy restatement."""
+    from oracle import oracle_torch as ot
+
+    b, heads, d, h, w = 2, 3, 4, 5, 7
+    c, length = heads * d, h * w
+    y = randn(b, 4, heads, length, d, seed=61).double()
+    x = randn(b, 4, heads, length, d, seed=62).double()
+    for skip_shape in ((heads, d), (4, heads, d)):
+        skip = randn(*skip_shape, seed=63).double()
+        scale = randn(4, c, seed=64).double()
+        want = oracle.direction_fusion(_np(y), _np(x), _np(skip), _np(scale), h, w)
+        got = _np(ot.direction_fusion_torch(y, x, skip, scale, h, w))
+        assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    xm = randn(b, c, h, w, seed=65).double()
+    gamma, beta = randn(c, seed=66).double(), randn(c, seed=67).double()
+    want = oracle.grn(_np(xm), _np(gamma), _np(beta))
+    assert np.abs(_np(ot.grn_torch(xm, gamma, beta)) - want).max() <= 1e-5 * np.abs(want).max()
+    want = oracle.layernorm2d(_np(xm), _np(gamma), _np(beta))
+    assert np.abs(_np(ot.layernorm2d_torch(xm, gamma, beta)) - want).max() <= 1e-5 * np.abs(want).max()
+    q = randn(b, 4, length, c, seed=68).double()
+    q[0, 1, 2, :d] = 0.0
+    want, _ = oracle.qnorm(_np(q), heads, d)
+    assert np.abs(_np(ot.qnorm_torch(q, heads, d)) - want).max() <= 1e-6
+    res = randn(b, c, h, w, seed=69).double()
+    drop = torch.tensor([0.0, 2.0], dtype=torch.float64)
+    want = oracle.residual_add(_np(res).transpose(0, 2, 3, 1), _np(xm).transpose(0, 2, 3, 1), _np(gamma), _np(drop))
+    got = _np(ot.residual_add_torch(res, xm, gamma, drop)).transpose(0, 2, 3, 1)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+
+
+def test_torch_tail_gradients_match_finite_differences():
+    from oracle import oracle_torch as ot
+
+    b, heads, d, h, w = 2, 2, 2, 3, 4
+    c, length = heads * d, h * w
+    f64 = dict(dtype=torch.float64, requires_grad=True)
+    y = torch.randn(b, 4, heads, length, d, **f64)
+    x = torch.randn(b, 4, heads, length, d, **f64)
+    for skip_shape in ((heads, d), (4, heads, d)):
+        skip = torch.randn(*skip_shape, **f64)
+        scale = torch.randn(4, c, **f64)
+        assert torch.autograd.gradcheck(lambda *a: ot.direction_fusion_torch(*a, h, w), (y, x, skip, scale))
+    xm = torch.randn(b, c, h, w, **f64)
+    gamma, beta = torch.randn(c, **f64), torch.randn(c, **f64)
+    assert torch.autograd.gradcheck(ot.grn_torch, (xm, gamma, beta))
+    assert torch.autograd.gradcheck(ot.layernorm2d_torch, (xm, gamma, beta))
+    q = torch.randn(b, 4, length, c, **f64)
+    assert torch.autograd.gradcheck(lambda t: ot.qnorm_torch(t, heads, d), (q,))
+    res = torch.randn(b, c, h, w, **f64)
+    drop = torch.tensor([0.0, 2.0], dtype=torch.float64)
+    assert torch.autograd.gradcheck(lambda r_, b_, g_: ot.residual_add_torch(r_, b_, g_, drop), (res, xm, gamma))
+
+
+def test_torch_fusion_catches_a_swapped_direction():
+    """A planted mistake: exchanging the two column scans changes the fused output, so the
+    forward pin above checks the restore maps the gradients are routed through."""
+    from oracle import oracle_torch as ot
+
+    b, heads, d, h, w = 1, 1, 2, 3, 4
+    y = randn(b, 4, heads, h * w, d, seed=71).double()
+    x = randn(b, 4, heads, h * w, d, seed=72).double()
+    skip, scale = randn(heads, d, seed=73).double(), torch.ones(4, heads * d, dtype=torch.float64)
+    good = ot.direction_fusion_torch(y, x, skip, scale, h, w)
+    bad = ot.direction_fusion_torch(y[:, [0, 1, 3, 2]], x[:, [0, 1, 3, 2]], skip, scale, h, w)
+    assert (good - bad).abs().max() > 1e-3

@@ -7,7 +7,7 @@ run the same native forward with per-direction chunk lengths.
 
 import torch
 
-from .chunk import MAX_CHUNK, SUPPORTED_HEAD_DIMS, srnl_packed_forward
+from .chunk import MAX_CHUNK, SUPPORTED_HEAD_DIMS, srnl_packed_backward, srnl_packed_forward
 from ...utils.autograd import backward_unavailable
 
 
@@ -63,11 +63,19 @@ class SRNLVariableLineFunction(torch.autograd.Function):
         if row <= 0 or col <= 0 or seq_len % row or seq_len % col:
             raise ValueError("varline chunk sizes must divide the serialized length")
         memories = (M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0)
-        return srnl_packed_forward(memories, x, q_raw, [row, row, col, col], q_raw=True)
+        ctx.save_for_backward(*memories, x, q_raw)
+        ctx.chunks = [row, row, col, col]
+        return srnl_packed_forward(memories, x, q_raw, ctx.chunks, q_raw=True)
 
     @staticmethod
     def backward(ctx, dY):
-        backward_unavailable("SRNL variable lines")
+        """Reference ``lines.py:645-671`` (``lines.cu:252-760``): gradients of the memories,
+        x and the raw queries.  Native while both chunk lengths are at most 64."""
+        *memories, x, q_raw = ctx.saved_tensors
+        if max(ctx.chunks) > MAX_CHUNK:
+            backward_unavailable("SRNL variable lines with a chunk above 64")
+        grads = srnl_packed_backward(memories, x, q_raw, ctx.chunks, dY, q_raw=True)
+        return (*grads, None, None, None, None, None)
 
 
 def srnl_long_chunk(M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0, x, q_raw, chunk_size, num_heads, head_dim):

@@ -9,7 +9,6 @@ native kernel restores each scan to image order and writes FP32
 import torch
 
 from . import hip
-from .autograd import backward_unavailable
 from .cuda import on_tensor_device
 
 
@@ -41,11 +40,35 @@ class VisionHOPEPostprocessScaleFunction(torch.autograd.Function):
             int(skip.numel() == 4 * channels), hip.ptr(scale), hip.ptr(out), batch, heads,
             int(height), int(width), head_dim, int(bool(channels_last)), hip.stream_of(y_c)),
             "vh_postprocess_scale_forward")
+        ctx.save_for_backward(y_c, x_c, skip, scale)
+        ctx.dims = (batch, heads, int(height), int(width), head_dim)
+        ctx.shapes = (d_skip.shape, direction_scale.shape)
         return out
 
     @staticmethod
+    @on_tensor_device
     def backward(ctx, d_out):
-        backward_unavailable("direction fusion")
+        """Reference ``utils/direction_fusion.py:108-120``: dy, dx in the dtype of y, x;
+        FP32 gradients of d_skip and direction_scale in their shapes."""
+        y, x, skip, scale = ctx.saved_tensors
+        batch, heads, height, width, head_dim = ctx.dims
+        g = d_out.float()
+        channels_last = g.is_contiguous(memory_format=torch.channels_last) and not g.is_contiguous()
+        g = g.contiguous(memory_format=torch.channels_last) if channels_last else g.contiguous()
+        per_dir = int(skip.numel() == 4 * heads * head_dim)
+        dy = torch.empty_like(y)
+        dx = torch.empty_like(x)
+        d_skip = torch.empty(skip.shape, device=y.device, dtype=torch.float32)
+        d_scale = torch.empty(scale.shape, device=y.device, dtype=torch.float32)
+        lib = hip.load_library()
+        ws = hip.workspace(lib.vh_postprocess_scale_backward_workspace_bytes(batch, heads, height, width, head_dim,
+                                                                             per_dir), y.device)
+        hip.check(lib.vh_postprocess_scale_backward(
+            hip.ptr(g), int(channels_last), hip.ptr(y), hip.ptr(x), hip.dtype_code(y.dtype), hip.ptr(skip), per_dir,
+            hip.ptr(scale), hip.ptr(dy), hip.ptr(dx), hip.ptr(d_skip), hip.ptr(d_scale), batch, heads, height, width,
+            head_dim, hip.ptr(ws), ws.numel() * 4, hip.stream_of(y)), "vh_postprocess_scale_backward")
+        skip_shape, scale_shape = ctx.shapes
+        return dy, dx, d_skip.view(skip_shape), d_scale.view(scale_shape), None, None, None
 
 
 def can_fuse_scale_postprocess(y, x, d_skip, direction_scale, height, width):

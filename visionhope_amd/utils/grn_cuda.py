@@ -7,7 +7,6 @@ import torch
 from torch.autograd import Function
 
 from . import hip
-from .autograd import backward_unavailable
 from .cuda import on_tensor_device
 
 
@@ -18,6 +17,7 @@ class _VisionHOPEGRNFunction(Function):
         batch, channels, height, width = x.shape
         if not x.is_contiguous(memory_format=torch.channels_last):
             x = x.contiguous(memory_format=torch.channels_last)
+        gamma_shape, beta_shape = gamma.shape, beta.shape
         gamma = gamma.detach().reshape(-1).float().contiguous()
         beta = beta.detach().reshape(-1).float().contiguous()
         y = torch.empty_like(x, dtype=out_dtype, memory_format=torch.channels_last)
@@ -31,11 +31,29 @@ class _VisionHOPEGRNFunction(Function):
             hip.dtype_code(out_dtype), hip.ptr(gx), hip.ptr(inv_den), batch, channels, height, width,
             float(eps),
             hip.ptr(ws), ws.numel() * 4, hip.stream_of(x)), "vh_grn_forward")
+        ctx.save_for_backward(x, gamma, gx, inv_den)
+        ctx.param_shapes = (gamma_shape, beta_shape)
         return y
 
     @staticmethod
+    @on_tensor_device
     def backward(ctx, dout):
-        backward_unavailable("GRN")
+        """Reference ``utils/grn_cuda.py:51-82``: dx in x's dtype (channels-last), FP32
+        dgamma and dbeta in the parameters' shapes."""
+        x, gamma, gx, inv_den = ctx.saved_tensors
+        batch, channels, height, width = x.shape
+        g = dout.to(dtype=torch.float32, memory_format=torch.channels_last)
+        dx = torch.empty_like(x, memory_format=torch.channels_last)
+        dgamma = torch.empty(channels, device=x.device, dtype=torch.float32)
+        dbeta = torch.empty(channels, device=x.device, dtype=torch.float32)
+        lib = hip.load_library()
+        ws = hip.workspace(lib.vh_grn_backward_workspace_bytes(batch, channels, height, width), x.device)
+        hip.check(lib.vh_grn_backward(
+            hip.ptr(g), hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(gamma), hip.ptr(gx), hip.ptr(inv_den),
+            hip.ptr(dx), hip.ptr(dgamma), hip.ptr(dbeta), batch, channels, height, width, hip.ptr(ws),
+            ws.numel() * 4, hip.stream_of(x)), "vh_grn_backward")
+        gamma_shape, beta_shape = ctx.param_shapes
+        return dx, dgamma.view(gamma_shape), dbeta.view(beta_shape), None, None
 
 
 def can_fuse_grn(x, gamma, beta):

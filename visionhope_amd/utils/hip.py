@@ -32,6 +32,10 @@ EXPORTED_SYMBOLS = (
     "vh_dwconv2d_nhwc_forward", "vh_grn_scale_forward", "vh_pointwise_conv_nhwc_forward",
     "vh_bias_act_nhwc_forward", "vh_dwconv2d_gelu_grn_workspace_bytes", "vh_dwconv2d_gelu_grn_forward",
     "vh_conv3x3_nhwc_forward", "vh_srnl_backward_workspace_bytes", "vh_srnl_backward",
+    "vh_postprocess_scale_backward_workspace_bytes", "vh_postprocess_scale_backward",
+    "vh_grn_backward_workspace_bytes", "vh_grn_backward", "vh_layernorm2d_backward_workspace_bytes",
+    "vh_layernorm2d_backward", "vh_qnorm_backward", "vh_residual_add_backward_workspace_bytes",
+    "vh_residual_add_backward",
 )
 
 
@@ -71,6 +75,19 @@ _SIGNATURES = {
     "vh_srnl_backward": (ctypes.c_int, [
         _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
         _i64, _i64, _i64, _i64, _i32, _I64P, _CP, _vp, _sz, _vp]),
+    "vh_postprocess_scale_backward_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i32, _i32]),
+    "vh_postprocess_scale_backward": (ctypes.c_int, [
+        _vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp, _sz, _vp]),
+    "vh_grn_backward_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "vh_grn_backward": (ctypes.c_int, [
+        _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "vh_layernorm2d_backward_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "vh_layernorm2d_backward": (ctypes.c_int, [
+        _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "vh_residual_add_backward_workspace_bytes": (_sz, [_i64, _i64]),
+    "vh_residual_add_backward": (ctypes.c_int, [
+        _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "vh_qnorm_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _vp]),
     "vh_srnl_line_forward_seq_noatomic": (ctypes.c_int, [
         _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
         _i64, _i64, _i64, _i64, _i32, _CP, _vp, _sz, _vp]),

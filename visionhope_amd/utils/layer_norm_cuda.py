@@ -8,7 +8,6 @@ import torch
 from torch.autograd import Function
 
 from . import hip
-from .autograd import backward_unavailable
 from .cuda import on_tensor_device
 
 
@@ -24,20 +23,48 @@ class _VisionHOPELayerNorm2dFunction(Function):
         elif not channels_last and not x.is_contiguous():
             x = x.contiguous()
         fmt = torch.channels_last if channels_last else torch.contiguous_format
+        weight_shape, bias_shape = weight.shape, bias.shape
         weight = weight.detach().reshape(-1).float().contiguous()
         bias = bias.detach().reshape(-1).float().contiguous()
         y = torch.empty_like(x, dtype=out_dtype, memory_format=fmt)
+        keep = ctx.needs_input_grad[0] or ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
+        rows = batch * height * width
+        mean = torch.empty(rows, device=x.device, dtype=torch.float32) if keep else None
+        rstd = torch.empty(rows, device=x.device, dtype=torch.float32) if keep else None
         lib = hip.load_library()
         hip.check(lib.vh_layernorm2d_forward(
             hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(weight), hip.ptr(bias), hip.ptr(y),
-            hip.dtype_code(out_dtype), None, None, batch, channels, height, width, float(eps),
+            hip.dtype_code(out_dtype), hip.ptr(mean), hip.ptr(rstd), batch, channels, height, width, float(eps),
             int(channels_last),
             hip.stream_of(x)), "vh_layernorm2d_forward")
+        if keep:
+            ctx.save_for_backward(x, weight, mean, rstd)
+            ctx.param_shapes = (weight_shape, bias_shape)
         return y
 
     @staticmethod
+    @on_tensor_device
     def backward(ctx, dy):
-        backward_unavailable("LayerNorm2d")
+        """Reference ``utils/layer_norm_cuda.py:148-192``: dx in x's dtype (channels-last),
+        FP32 dweight and dbias.  The statistics (mean and rstd per pixel, pixel order) are
+        those the forward wrote; an NCHW input is re-laid out once here."""
+        x, weight, mean, rstd = ctx.saved_tensors
+        batch, channels, height, width = x.shape
+        if not x.is_contiguous(memory_format=torch.channels_last):
+            # NCHW forward: its statistics are in (b, h, w) order as well
+            x = x.contiguous(memory_format=torch.channels_last)
+        g = dy.to(dtype=torch.float32, memory_format=torch.channels_last)
+        dx = torch.empty_like(x, memory_format=torch.channels_last)
+        dweight = torch.empty(channels, device=x.device, dtype=torch.float32)
+        dbias = torch.empty(channels, device=x.device, dtype=torch.float32)
+        lib = hip.load_library()
+        ws = hip.workspace(lib.vh_layernorm2d_backward_workspace_bytes(batch, channels, height, width), x.device)
+        hip.check(lib.vh_layernorm2d_backward(
+            hip.ptr(g), hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(weight), hip.ptr(mean), hip.ptr(rstd),
+            hip.ptr(dx), hip.ptr(dweight), hip.ptr(dbias), batch, channels, height, width, hip.ptr(ws),
+            ws.numel() * 4, hip.stream_of(x)), "vh_layernorm2d_backward")
+        weight_shape, bias_shape = ctx.param_shapes
+        return dx, dweight.view(weight_shape), dbias.view(bias_shape), None, None, None
 
 
 def can_fuse_layernorm2d(x, weight, bias):

@@ -5,7 +5,6 @@
 import torch
 
 from . import hip
-from .autograd import backward_unavailable
 from .cuda import on_tensor_device
 
 
@@ -24,11 +23,25 @@ class VisionHOPEQNormFunction(torch.autograd.Function):
             hip.ptr(q_raw_c), hip.dtype_code(q_raw_c.dtype), hip.ptr(out), hip.ptr(inv), batch,
             directions, length, int(num_heads), int(head_dim), hip.stream_of(q_raw_c)),
             "vh_qnorm_forward")
+        ctx.save_for_backward(out, inv)
+        ctx.raw = (q_raw_c.dtype, int(num_heads), int(head_dim))
         return out
 
     @staticmethod
+    @on_tensor_device
     def backward(ctx, d_q_out):
-        backward_unavailable("query normalisation")
+        """Reference ``utils/query_normalization.py:67-76``: the raw query's gradient
+        ``[B, 4, N, heads*d]`` in its dtype."""
+        out, inv = ctx.saved_tensors
+        dtype, heads, head_dim = ctx.raw
+        batch, directions, _, length, _ = out.shape
+        g = d_q_out.float().contiguous()
+        dq = torch.empty((batch, directions, length, heads * head_dim), device=out.device, dtype=dtype)
+        lib = hip.load_library()
+        hip.check(lib.vh_qnorm_backward(
+            hip.ptr(g), hip.ptr(out), hip.ptr(inv), hip.ptr(dq), hip.dtype_code(dtype), batch, directions, length,
+            heads, head_dim, hip.stream_of(out)), "vh_qnorm_backward")
+        return dq, None, None
 
 
 def can_fuse_qnorm(q_raw, num_heads, head_dim):

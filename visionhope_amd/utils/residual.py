@@ -6,7 +6,6 @@ import torch
 from torch.autograd import Function
 
 from . import hip
-from .autograd import backward_unavailable
 from .cuda import on_tensor_device
 
 
@@ -19,6 +18,7 @@ class _VisionHOPEResidualFunction(Function):
         total = batch * spatial * channels
         residual = residual.contiguous(memory_format=torch.channels_last)
         branch = branch.contiguous(memory_format=torch.channels_last)
+        gamma_shape = gamma.shape
         gamma = gamma.detach().reshape(-1).float().contiguous()
         mask = mask.float().contiguous()
         out = torch.empty_like(branch, dtype=torch.float32, memory_format=torch.channels_last)
@@ -27,11 +27,28 @@ class _VisionHOPEResidualFunction(Function):
             hip.ptr(residual), hip.dtype_code(residual.dtype), hip.ptr(branch),
             hip.dtype_code(branch.dtype), hip.ptr(gamma), hip.ptr(mask), hip.ptr(out), total,
             channels, spatial, hip.stream_of(branch)), "vh_residual_add_forward")
+        ctx.save_for_backward(branch, gamma, mask)
+        ctx.gamma_shape = gamma_shape
         return out
 
     @staticmethod
+    @on_tensor_device
     def backward(ctx, dout):
-        backward_unavailable("residual add")
+        """Reference ``utils/residual.py:130-170``: dresidual = dout, dbranch in the branch's
+        dtype (channels-last), FP32 dgamma."""
+        branch, gamma, mask = ctx.saved_tensors
+        batch, channels, height, width = branch.shape
+        g = dout.to(dtype=torch.float32, memory_format=torch.channels_last)
+        total = g.numel()
+        dbranch = torch.empty_like(branch, memory_format=torch.channels_last)
+        dgamma = torch.empty(channels, device=branch.device, dtype=torch.float32)
+        lib = hip.load_library()
+        ws = hip.workspace(lib.vh_residual_add_backward_workspace_bytes(total, channels), branch.device)
+        hip.check(lib.vh_residual_add_backward(
+            hip.ptr(g), hip.ptr(branch), hip.dtype_code(branch.dtype), hip.ptr(gamma), hip.ptr(mask),
+            hip.ptr(dbranch), hip.ptr(dgamma), total, channels, height * width, hip.ptr(ws), ws.numel() * 4,
+            hip.stream_of(branch)), "vh_residual_add_backward")
+        return g, dbranch, dgamma.view(ctx.gamma_shape), None
 
 
 def can_fuse_residual_add(residual, branch, gamma):
