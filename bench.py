@@ -67,6 +67,21 @@ def event_time_ms(fn, stream, iters, warmup=2):
     return start.elapsed_time(end) / iters
 
 
+def graph_time_ms(fn, iters, warmup=2):
+    """Like ``event_time_ms`` for ``fn`` captured once in a HIP graph and replayed: the
+    GPU time of its launches without the Python wrapper's host time between them (how a
+    serving loop runs these ops)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    ms = event_time_ms(graph.replay, torch.cuda.current_stream(), iters, warmup)
+    del graph
+    return ms
+
+
 def _perturbed_memories(heads, head_dim, device, gen):
     """Repo default init for the matrix memories, N(0, 0.1^2) gate vectors so gates vary."""
     import torch
@@ -110,7 +125,8 @@ def measure_srnl_stages(device, batch):
 
 
 def measure_tail(device):
-    """Fusion, GRN and LN at B=128, 56x56x96 and 28x28x192, bf16: GB/s of compulsory traffic."""
+    """Fusion, GRN and LN at B=128, 56x56x96 and 28x28x192, bf16: GB/s of compulsory traffic,
+    each op timed as graph replays (GPU time of its launches)."""
     import torch
     from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
     from visionhope_amd.utils.grn_cuda import visionhope_grn
@@ -135,11 +151,50 @@ def measure_tail(device):
                 ("fusion", lambda: visionhope_postprocess_scale(ys, xs, skip, scale, grid, grid, True), 20),
                 ("grn", lambda: visionhope_grn(xc, gamma, beta, 1e-6), 6),
                 ("layernorm", lambda: visionhope_layernorm2d(xc, gamma, beta, 1e-6), 6)):
-            ms = event_time_ms(fn, stream, 10)
+            ms = graph_time_ms(fn, 10)
             gbs = bytes_per * n / ms / 1e6
             out[f"{name}_{tag}"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
                                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
         del x, ys, xs
+    return out
+
+
+def measure_tail_backward(device):
+    """Backward of fusion, GRN and LN (autograd, the native backward entries) at B=128,
+    56x56x96, bf16 activations: GB/s of compulsory traffic per element (fusion: fp32
+    dout + four y and x reads + four dy and dx writes = 36 B; GRN and LN: fp32 dout, the
+    bf16 input and the bf16 input gradient = 8 B) against the HBM peak."""
+    import torch
+    from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
+    from visionhope_amd.utils.grn_cuda import visionhope_grn
+    from visionhope_amd.utils.layer_norm_cuda import visionhope_layernorm2d
+
+    stream = torch.cuda.current_stream(device)
+    gen = torch.Generator(device=device).manual_seed(SEED)
+    batch, grid, channels = 128, 56, 96
+    heads, head_dim = channels // 16, 16
+    n = batch * grid * grid * channels
+    x = torch.randn(batch, grid, grid, channels, device=device, generator=gen).bfloat16()
+    xc = x.permute(0, 3, 1, 2).requires_grad_()
+    gamma = (torch.randn(channels, device=device, generator=gen) * 0.1).requires_grad_()
+    beta = (torch.randn(channels, device=device, generator=gen) * 0.1).requires_grad_()
+    ys = torch.randn(batch, 4, heads, grid * grid, head_dim, device=device, generator=gen).bfloat16().requires_grad_()
+    xs = torch.randn(batch, 4, heads, grid * grid, head_dim, device=device, generator=gen).bfloat16().requires_grad_()
+    skip = (torch.randn(heads, head_dim, device=device, generator=gen) * 0.1).requires_grad_()
+    scale = (1 + torch.randn(4, channels, device=device, generator=gen) * 0.1).requires_grad_()
+    dout = torch.randn(batch, grid, grid, channels, device=device, generator=gen).permute(0, 3, 1, 2)
+    out = {}
+    for name, fwd, inputs, bytes_per in (
+            ("fusion", lambda: visionhope_postprocess_scale(ys, xs, skip, scale, grid, grid, True),
+             (ys, xs, skip, scale), 36),
+            ("grn", lambda: visionhope_grn(xc, gamma, beta, 1e-6), (xc, gamma, beta), 8),
+            ("layernorm", lambda: visionhope_layernorm2d(xc, gamma, beta, 1e-6), (xc, gamma, beta), 8)):
+        y = fwd()
+        ms = event_time_ms(lambda: torch.autograd.grad(y, inputs, dout, retain_graph=True), stream, 5)
+        gbs = bytes_per * n / ms / 1e6
+        out[f"{name}_backward_{grid}x{grid}x{channels}"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+        del y
     return out
 
 
@@ -273,6 +328,9 @@ def main(argv=None):
                         help="profiling workload for rocprofv3 --pmc: the per-stage SRNL launches and "
                              "one FP32 copy of COPY_CALIBRATION_BYTES (HBM counter calibration); "
                              "no model forward, no JSON line")
+    parser.add_argument("--tail-only", action="store_true",
+                        help="profiling workload for rocprofv3: the config-2 fusion, GRN and LayerNorm "
+                             "launches of the `kernels` entry and the calibration copy; no JSON line")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -283,6 +341,15 @@ def main(argv=None):
 
     if args.stages_only:
         return profile_stages(torch.device("cuda:0"), args.batch)
+    if args.tail_only:
+        with torch.inference_mode():
+            for name, row in measure_tail(torch.device("cuda:0")).items():
+                print(name, row, flush=True)
+            src = torch.ones(COPY_CALIBRATION_BYTES // 4, device="cuda:0")
+            torch.mul(src, 1.0, out=torch.empty_like(src))
+            torch.cuda.synchronize()
+        print(f"calibration copy: {COPY_CALIBRATION_BYTES} bytes read and written", flush=True)
+        return 0
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
@@ -340,6 +407,8 @@ def main(argv=None):
         stage_rows, srnl_flops_total, srnl_ms_total, srnl_bytes = measure_srnl_stages(device, args.batch)
         tail = measure_tail(device)
         tail.update(measure_srnl_backward(device))
+        with torch.inference_mode(False), torch.enable_grad():   # autograd tensors, outside inference mode
+            tail.update(measure_tail_backward(device))
 
     images_per_s = args.batch * 1000.0 / ms
     achieved = srnl_flops_total / srnl_ms_total / 1e9  # TFLOP/s

@@ -15,10 +15,14 @@ FP32_TOL = 1e-5
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("channels_last", [False, True])
 @pytest.mark.parametrize("per_direction", [False, True])
-def test_direction_fusion(oracle, device, dtype, channels_last, per_direction):
+@pytest.mark.parametrize("heads,head_dim,height,width", [(3, 16, 6, 9), (5, 8, 13, 17), (2, 64, 16, 8),
+                                                         (1, 4, 5, 3)])
+def test_direction_fusion(oracle, device, dtype, channels_last, per_direction, heads, head_dim, height, width):
+    """Every fusion kernel (tiled 8x8 channels-last with partial edge tiles, scalar NCHW,
+    head_dim 4 below the 8-channel vectors) against the oracle."""
     from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
 
-    batch, heads, head_dim, height, width = 2, 3, 16, 6, 9
+    batch = 2
     y = randn(batch, 4, heads, height * width, head_dim, seed=1).to(dtype)
     x = randn(batch, 4, heads, height * width, head_dim, seed=2).to(dtype)
     skip = randn(*((4, heads, head_dim) if per_direction else (heads, head_dim)), seed=3, scale=0.1)

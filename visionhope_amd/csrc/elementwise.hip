@@ -107,6 +107,79 @@ __global__ __launch_bounds__(256) void direction_fusion8_kernel(const FusionPara
     store8<float>(p.out + (b * L + pix) * static_cast<int64_t>(C) + c0, z);
 }
 
+// Channels-last output, D >= 8, tiled: one workgroup per (image, TH x TW pixel tile,
+// group of at most 96 channels); the launch uses 4 x 4 tiles (measured best against 8 x 8,
+// 4 x 8, 2 x 8 and 16 x 16 at 56x56x96 and 28x28x192).  The row scans (directions 0, 1) are read with the tile's
+// pixels in row-major order and the column scans (2, 3) in column-major order, so
+// consecutive lanes read consecutive tokens of one head (runs of TW or TH tokens) in both
+// cases.  The per-pixel sums meet in LDS (at most 64 x 96 floats, so several workgroups
+// share a CU), then the tile is written as channels-last pixel rows.  Summation order
+// ((c0 + c1) + c2) + c3 as above.
+template <int D, typename T>
+__global__ __launch_bounds__(256) void direction_fusion_tile_kernel(const FusionParams p, const uint32_t tiles_w,
+                                                                    const int th_log2, const int tw_log2,
+                                                                    const int heads_per_block, const float inv_g) {
+    constexpr int GD = D / 8;
+    extern __shared__ float acc[];   // [TH * TW pixels, row-major][heads_per_block * D]
+    const int C = static_cast<int>(p.heads) * D;
+    const int head0 = static_cast<int>(blockIdx.z) * heads_per_block;
+    const int nh = min(heads_per_block, static_cast<int>(p.heads) - head0);
+    const int CB = nh * D, G = nh * GD;
+    const int TH = 1 << th_log2, TW = 1 << tw_log2, npx = TH * TW;
+    const int64_t L = p.H * p.W;
+    const int64_t b = blockIdx.y;
+    const int th0 = static_cast<int>(blockIdx.x / tiles_w) * TH, tw0 = static_cast<int>(blockIdx.x % tiles_w) * TW;
+    const T* y = static_cast<const T*>(p.y);
+    const T* x = static_cast<const T*>(p.x);
+    const int64_t stride_dir = p.heads * L * D;
+    const int items = npx * G;
+#pragma unroll
+    for (int phase = 0; phase < 2; ++phase) {
+        // item k = (head, pixel, group): group fastest, then the pixel in scan order
+        for (int k = threadIdx.x; k < items; k += 256) {
+            const int gi = k % GD, kk = k / GD, q = kk & (npx - 1), hl = kk >> (th_log2 + tw_log2);
+            const int ph = phase == 0 ? q >> tw_log2 : q & (TH - 1);
+            const int pw = phase == 0 ? q & (TW - 1) : q >> th_log2;
+            const int64_t h = th0 + ph, w = tw0 + pw;
+            if (h >= p.H || w >= p.W) continue;
+            const int head = head0 + hl;
+            const int c0 = head * D + gi * 8;
+            const int64_t base = (b * 4 * p.heads + head) * L * D + gi * 8;
+            float* a = acc + (ph * TW + pw) * CB + hl * D + gi * 8;
+            float out[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) out[j] = a[j];
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr) {
+                const int r = 2 * phase + rr;
+                const int64_t at = base + r * stride_dir + pixel_to_scan(r, h, w, p.H, p.W) * D;
+                float yv[8], xv[8];
+                load8<T>(y + at, yv);
+                load8<T>(x + at, xv);
+                const float* sk = p.skip + (p.skip_per_dir ? r * C : 0) + c0;
+                const float* sc = p.scale + r * C + c0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float v = yv[j] + sk[j] * xv[j];
+                    out[j] = r == 0 ? sc[j] * v : out[j] + sc[j] * v;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[j] = out[j];
+        }
+        __syncthreads();
+    }
+    for (uint32_t k = threadIdx.x; k < static_cast<uint32_t>(items); k += 256u) {
+        uint32_t q, cg;
+        divmod24(k, static_cast<uint32_t>(G), inv_g, q, cg);
+        const int64_t h = th0 + (q >> tw_log2), w = tw0 + (q & static_cast<uint32_t>(TW - 1));
+        if (h >= p.H || w >= p.W) continue;
+        const float* a = acc + q * CB + cg * 8;
+        const float z[8] = {a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7]};
+        store8<float>(p.out + (b * L + h * p.W + w) * static_cast<int64_t>(C) + head0 * D + cg * 8, z);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // GRN (utils/grn.py:26-38, utils/csrc/grn_cuda.cu:46-124) on channels-last x.
 //   pass 1  partial[b, slab, c] = sum over the slab's pixels of x^2
@@ -663,6 +736,27 @@ int vh_postprocess_scale_forward(const void* Y, const void* X, int32_t io_dtype,
                             reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(d_skip) |
                             reinterpret_cast<uintptr_t>(scale);
     const int64_t groups = H * W * heads * (head_dim / 8);
+    if (channels_last && head_dim >= 8 && align % 16 == 0) {
+        const int th_log2 = 2, tw_log2 = 2;
+        const int64_t tiles_w = (W + (1 << tw_log2) - 1) >> tw_log2, tiles_h = (H + (1 << th_log2) - 1) >> th_log2;
+        const int hpb = static_cast<int>(std::min<int64_t>(heads, std::max(1, 96 / head_dim)));
+        const int64_t chunks = (heads + hpb - 1) / hpb;
+        const size_t lds = static_cast<size_t>((1 << (th_log2 + tw_log2)) * hpb * head_dim) * sizeof(float);
+        const dim3 grid(static_cast<unsigned>(tiles_w * tiles_h), static_cast<unsigned>(B),
+                        static_cast<unsigned>(chunks));
+        const float inv_g = 1.0f / static_cast<float>(hpb * (head_dim / 8));
+        int rc = dispatch_d(head_dim, [&](auto dc) {
+            constexpr int D = decltype(dc)::value;
+            if constexpr (D >= 8) {
+                dispatch_t(io_dtype, [&](auto tv) {
+                    hipLaunchKernelGGL((direction_fusion_tile_kernel<D, decltype(tv)>), grid, dim3(256), lds, s, fp,
+                                       static_cast<uint32_t>(tiles_w), th_log2, tw_log2, hpb, inv_g);
+                });
+            }
+        });
+        if (rc) return rc;
+        return check_launch("direction_fusion_tile_kernel");
+    }
     if (channels_last && head_dim >= 8 && align % 16 == 0 && groups < (int64_t(1) << 24)) {
         const dim3 grid(static_cast<unsigned>((groups + 255) / 256), static_cast<unsigned>(B));
         const float inv_w = 1.0f / static_cast<float>(W);
