@@ -67,19 +67,20 @@ def event_time_ms(fn, stream, iters, warmup=2):
     return start.elapsed_time(end) / iters
 
 
-def graph_time_ms(fn, iters, warmup=2):
-    """Like ``event_time_ms`` for ``fn`` captured once in a HIP graph and replayed: the
-    GPU time of its launches without the Python wrapper's host time between them (how a
-    serving loop runs these ops)."""
+def graph_time_ms(fn, iters, reps=3):
+    """Milliseconds per call of ``fn`` with ``iters`` back-to-back calls captured in one HIP
+    graph, replayed ``reps`` times: the GPU time of its launches without the Python
+    wrapper's host time between them (how a serving loop runs these ops)."""
     import torch
     fn()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        fn()
-    ms = event_time_ms(graph.replay, torch.cuda.current_stream(), iters, warmup)
+        for _ in range(iters):
+            fn()
+    ms = event_time_ms(graph.replay, torch.cuda.current_stream(), reps, warmup=1)
     del graph
-    return ms
+    return ms / iters
 
 
 def _perturbed_memories(heads, head_dim, device, gen):
@@ -151,7 +152,7 @@ def measure_tail(device):
                 ("fusion", lambda: visionhope_postprocess_scale(ys, xs, skip, scale, grid, grid, True), 20),
                 ("grn", lambda: visionhope_grn(xc, gamma, beta, 1e-6), 6),
                 ("layernorm", lambda: visionhope_layernorm2d(xc, gamma, beta, 1e-6), 6)):
-            ms = graph_time_ms(fn, 10)
+            ms = graph_time_ms(fn, 20)
             gbs = bytes_per * n / ms / 1e6
             out[f"{name}_{tag}"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
                                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}

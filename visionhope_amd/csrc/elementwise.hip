@@ -351,25 +351,58 @@ __global__ __launch_bounds__(256) void grn_partial8_kernel(const T* __restrict__
     }
 }
 
+// GRN apply (y = x scale_c + beta_c, 8 channels per thread, 16-byte loads) with the
+// statistics pass folded in: every workgroup of image b first
+// reduces the per-slab partial sums of all C channels (fixed order, so every workgroup of
+// the image gets bit-identical gx and inv_den) and workgroup 0 of the image stores them.
+// This saves the separate statistics launch between the two streaming passes.
+// 256 threads; thread t streams channel group t % G of rows t / G (t / G < 256 / G).
 template <typename T, typename TO>
-__global__ __launch_bounds__(256) void grn_apply8_kernel(const T* __restrict__ x, const float* __restrict__ gamma,
-                                                        const float* __restrict__ beta,
-                                                        const float* __restrict__ gx,
-                                                        const float* __restrict__ inv_den, TO* __restrict__ y,
-                                                        int C, int S, int rows_per_block) {
-    const int G = C / 8, R = static_cast<int>(blockDim.x) / G;
-    const int g = static_cast<int>(threadIdx.x) % G, rr = static_cast<int>(threadIdx.x) / G;
+__global__ __launch_bounds__(256) void grn_stats_apply8_kernel(const T* __restrict__ x, const float* __restrict__ partial,
+                                                               const float* __restrict__ gamma,
+                                                               const float* __restrict__ beta, float* __restrict__ gx,
+                                                               float* __restrict__ inv_den, TO* __restrict__ y, int C,
+                                                               int S, int nslab, int rows_per_block, float eps) {
+    extern __shared__ float gsh[];   // [C]
+    __shared__ float wsum[4];
+    const int t = static_cast<int>(threadIdx.x);
     const int b = blockIdx.y;
-    const int s0 = blockIdx.x * rows_per_block, s1 = min(S, s0 + rows_per_block);
-    const float inv = inv_den[b];
+    float local = 0.f;
+    for (int c = t; c < C; c += 256) {
+        const float* pc = partial + static_cast<int64_t>(b) * nslab * C + c;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        int s = 0;
+        for (; s + 4 <= nslab; s += 4) {
+            a0 += pc[s * C];
+            a1 += pc[(s + 1) * C];
+            a2 += pc[(s + 2) * C];
+            a3 += pc[(s + 3) * C];
+        }
+        for (; s < nslab; ++s) a0 += pc[s * C];
+        const float g = sqrtf((a0 + a1) + (a2 + a3));
+        gsh[c] = g;
+        local += g;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off);
+    if ((t & 63) == 0) wsum[t >> 6] = local;
+    __syncthreads();
+    const float inv = 1.f / ((((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) / static_cast<float>(C) + eps);
+    if (blockIdx.x == 0) {
+        for (int c = t; c < C; c += 256) gx[static_cast<int64_t>(b) * C + c] = gsh[c];
+        if (t == 0) inv_den[b] = inv;
+    }
+    const int G = C / 8, R = 256 / G;
+    const int g = t % G, rr = t / G;
+    if (rr >= R) return;
     float sc[8], bt[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int c = g * 8 + j;
-        const float nx = gx[static_cast<int64_t>(b) * C + c] * inv;
-        sc[j] = 1.f + gamma[c] * nx;
+        sc[j] = 1.f + gamma[c] * (gsh[c] * inv);
         bt[j] = beta[c];
     }
+    const int s0 = blockIdx.x * rows_per_block, s1 = min(S, s0 + rows_per_block);
     const int64_t base = static_cast<int64_t>(b) * S * C + g * 8;
     for (int s = s0 + rr; s < s1; s += R) {
         float v[8];
@@ -837,13 +870,12 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
             hipLaunchKernelGGL((grn_partial8_kernel<T>), dim3(static_cast<unsigned>(vslab), static_cast<unsigned>(B)),
                                dim3(G * R), red, s, static_cast<const T*>(x), partial, static_cast<int>(C),
                                static_cast<int>(S), rows, vslab);
-            hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s, partial,
-                               gx, inv_den, C, static_cast<int64_t>(vslab), eps);
             dispatch_t(y_dtype, [&](auto ov) {
                 using TO = decltype(ov);
-                hipLaunchKernelGGL((grn_apply8_kernel<T, TO>), dim3(apply_blocks, static_cast<unsigned>(B)),
-                                   dim3(G * R), 0, s, static_cast<const T*>(x), gamma, beta, gx, inv_den,
-                                   static_cast<TO*>(y), static_cast<int>(C), static_cast<int>(S), apply_rows);
+                hipLaunchKernelGGL((grn_stats_apply8_kernel<T, TO>), dim3(apply_blocks, static_cast<unsigned>(B)),
+                                   dim3(256), static_cast<size_t>(C) * sizeof(float), s, static_cast<const T*>(x),
+                                   partial, gamma, beta, gx, inv_den, static_cast<TO*>(y), static_cast<int>(C),
+                                   static_cast<int>(S), vslab, apply_rows, eps);
             });
         });
         if (rc) return rc;
