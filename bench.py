@@ -241,6 +241,38 @@ def build_tiny(device, channels_last=True):
     return model
 
 
+def measure_base512(device, batch=8, reps=5):
+    """Config 4: VisionHOPE-Base at 512x512, B=8, bf16 autocast, prepared, the four stage
+    feature maps (no task head; 128^2 / 64^2 / 32^2 / 16^2 token grids, chunks of 128 at
+    stage 1), one forward captured in a HIP graph: ms per forward and images/s."""
+    import torch
+    from visionhope_amd.inference.prepare import prepare_for_inference
+    from visionhope_amd.models import create_model
+
+    torch.manual_seed(SEED)
+    model = create_model("visionhope_base", drop_path_rate=0.0).to(device).to(memory_format=torch.channels_last)
+    model.eval()
+    prepare_for_inference(model)
+    gen = torch.Generator().manual_seed(SEED + 4)
+    images = torch.randn(batch, 3, 512, 512, generator=gen).to(device).contiguous(memory_format=torch.channels_last)
+
+    def forward():
+        with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return model.forward_intermediates(images)
+
+    feats = forward()
+    torch.cuda.synchronize()
+    if not all(torch.isfinite(f).all() for f in feats):
+        raise FloatingPointError("Base 512 forward produced NaN/Inf")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        forward()
+    ms = event_time_ms(graph.replay, torch.cuda.current_stream(device), reps, warmup=2)
+    del graph, model
+    return {"base512_b8_features": {"ms_per_forward": round(ms, 3), "images_per_s": round(batch * 1000.0 / ms, 1),
+                                    "feature_shapes": [list(f.shape) for f in feats]}}
+
+
 def cpu_baseline(sample_batch=8, reps=3):
     """Tiny forward on the host: PyTorch CPU for convs/linears/norms and the CPU oracle
     (oracle/liboracle_srnl.so, OpenMP) for the four-direction SRNL operator."""
@@ -407,6 +439,7 @@ def main(argv=None):
 
         stage_rows, srnl_flops_total, srnl_ms_total, srnl_bytes = measure_srnl_stages(device, args.batch)
         tail = measure_tail(device)
+        tail.update(measure_base512(device))
         tail.update(measure_srnl_backward(device))
         with torch.inference_mode(False), torch.enable_grad():   # autograd tensors, outside inference mode
             tail.update(measure_tail_backward(device))

@@ -304,7 +304,7 @@ int vh_pointwise_conv_nhwc_forward(
  * bf16 on load as autocast rounds it, or bf16).  weight bf16 [N, K]: for Cin % 32 == 0
  * the convolution weight in channels-last order [N, 3, 3, Cin] (K = 9 Cin); for Cin = 3,
  * K = 64 with weight[n][4 (3 kh + kw) + c] and zeros at c = 3 and taps 9..15.  bias [N]
- * fp32.  N = 32, 64 or a multiple of 128; Ho = (H - 1) / stride + 1, likewise Wo;
+ * fp32.  N a multiple of 32; Ho = (H - 1) / stride + 1, likewise Wo;
  * weight, bias, out (and x unless Cin = 3) 16-byte aligned.  With an eval-mode
  * BatchNorm folded into weight and bias this is Conv2d + BatchNorm2d (+ GELU) of the
  * stem and the downsample layers (models/layers.py:85-119).  No counterpart in the

@@ -191,7 +191,7 @@ def test_conv3x3_rejects_bad_arguments(lib):
     assert call(stride=3) == hip.VH_ERR_ARG
     assert call(act=2) == hip.VH_ERR_ARG
     assert call(cin=48) == hip.VH_ERR_SHAPE              # neither 3 nor a multiple of 32
-    assert call(cout=96) == hip.VH_ERR_SHAPE             # not 32, 64 or a multiple of 128
+    assert call(cout=80) == hip.VH_ERR_SHAPE             # not a multiple of 32
     assert call(dtype=hip.VH_DTYPE_F32) == hip.VH_ERR_DTYPE   # fp32 only for the 3-channel image
     assert call(cin=3, dtype=hip.VH_DTYPE_F16) == hip.VH_ERR_DTYPE
     assert call(b=0) == hip.VH_ERR_SHAPE

@@ -36,6 +36,11 @@ def _reference(x, weight, bias, stride, act):
     (96, 128, 1, (7, 9), 1, torch.bfloat16),    # Cin % 64 != 0 with k tiles of 32
     (128, 256, 2, (10, 10), 0, torch.bfloat16),
     (256, 512, 2, (7, 7), 0, torch.bfloat16),   # downsample 3 at 14 -> 7 shape class
+    (3, 96, 2, (20, 18), 1, torch.float32),     # N = 96: BN = 32 tiles
+    (96, 96, 1, (11, 10), 0, torch.bfloat16),   # Base stem, last conv
+    (96, 192, 2, (12, 12), 0, torch.bfloat16),  # Base downsamples: N % 64 == 0 (BN = 64)
+    (192, 448, 2, (8, 9), 0, torch.bfloat16),
+    (448, 640, 2, (6, 6), 0, torch.bfloat16),
 ])
 def test_conv3x3(device, cin, cout, stride, hw, act, in_dtype):
     from visionhope_amd.utils.conv_bn import conv3x3_bias_act
@@ -84,9 +89,9 @@ def test_conv3x3_rejects(device):
     # stride 3
     assert lib.vh_conv3x3_nhwc_forward(hip.ptr(x), bf16, hip.ptr(w), hip.ptr(b), 0, hip.ptr(out),
                                        1, 8, 8, 32, 64, 3, s) != 0
-    # out_channels 96
+    # out_channels 48 (not a multiple of 32)
     assert lib.vh_conv3x3_nhwc_forward(hip.ptr(x), bf16, hip.ptr(w), hip.ptr(b), 0, hip.ptr(out),
-                                       1, 8, 8, 32, 96, 1, s) != 0
+                                       1, 8, 8, 32, 48, 1, s) != 0
     # fp32 map with 32 channels
     assert lib.vh_conv3x3_nhwc_forward(hip.ptr(x), hip.VH_DTYPE_F32, hip.ptr(w), hip.ptr(b), 0, hip.ptr(out),
                                        1, 8, 8, 32, 64, 1, s) != 0

@@ -171,18 +171,18 @@ int launch_conv(const ConvParams& cp, hipStream_t s) {
     };
     if constexpr (MODE != CONV_TAPS) {
         // K = 64 in two k tiles; N = 32 (the Tiny stem) or a multiple of 64.
-        if (p.N == 32) return go(conv3x3_kernel<256, 32, 4, 32, EPI, MODE, 2>, 256, 32);
-        if (p.N == 64) return go(conv3x3_kernel<128, 64, 2, 32, EPI, MODE, 3>, 128, 64);
-        return go(conv3x3_kernel<64, 128, 2, 32, EPI, MODE, 3>, 64, 128);
+        if (p.N % 128 == 0) return go(conv3x3_kernel<64, 128, 2, 32, EPI, MODE, 3>, 64, 128);
+        if (p.N % 64 == 0) return go(conv3x3_kernel<128, 64, 2, 32, EPI, MODE, 3>, 128, 64);
+        return go(conv3x3_kernel<256, 32, 4, 32, EPI, MODE, 2>, 256, 32);
     } else {
         if (cp.Cin % 64 != 0) {   // Cin = 32, 96, ...: k tiles of 32
-            if (p.N == 32) return go(conv3x3_kernel<256, 32, 4, 32, EPI, MODE, 2>, 256, 32);
-            if (p.N == 64) return go(conv3x3_kernel<128, 64, 2, 32, EPI, MODE, 3>, 128, 64);
-            return go(conv3x3_kernel<64, 128, 2, 32, EPI, MODE, 3>, 64, 128);
+            if (p.N % 128 == 0) return go(conv3x3_kernel<64, 128, 2, 32, EPI, MODE, 3>, 64, 128);
+            if (p.N % 64 == 0) return go(conv3x3_kernel<128, 64, 2, 32, EPI, MODE, 3>, 128, 64);
+            return go(conv3x3_kernel<256, 32, 4, 32, EPI, MODE, 2>, 256, 32);
         }
-        if (p.N == 32) return go(conv3x3_kernel<256, 32, 4, 64, EPI, MODE, 1>, 256, 32);
-        if (p.N == 64) return go(conv3x3_kernel<128, 64, 2, 64, EPI, MODE, 2>, 128, 64);
-        return go(conv3x3_kernel<64, 128, 2, 64, EPI, MODE, 2>, 64, 128);
+        if (p.N % 128 == 0) return go(conv3x3_kernel<64, 128, 2, 64, EPI, MODE, 2>, 64, 128);
+        if (p.N % 64 == 0) return go(conv3x3_kernel<128, 64, 2, 64, EPI, MODE, 2>, 128, 64);
+        return go(conv3x3_kernel<256, 32, 4, 64, EPI, MODE, 1>, 256, 32);
     }
 }
 
@@ -208,8 +208,8 @@ extern "C" int vh_conv3x3_nhwc_forward(const void* x, int32_t x_dtype, const voi
                "conv3x3 needs in_channels = 3 or a multiple of 32, got %lld", (long long)in_channels);
     VH_REQUIRE(x_dtype == VH_DTYPE_BF16 || (rgb && x_dtype == VH_DTYPE_F32), VH_ERR_DTYPE,
                "conv3x3 reads a bf16 map (or an fp32 3-channel image), got code %d", x_dtype);
-    VH_REQUIRE(out_channels == 32 || out_channels == 64 || out_channels % 128 == 0, VH_ERR_SHAPE,
-               "conv3x3 needs out_channels = 32, 64 or a multiple of 128, got %lld", (long long)out_channels);
+    VH_REQUIRE(out_channels % 32 == 0, VH_ERR_SHAPE, "conv3x3 needs out_channels a multiple of 32, got %lld",
+               (long long)out_channels);
     const int64_t ho = (height - 1) / stride + 1, wo = (width - 1) / stride + 1;
     const int64_t m = batch * ho * wo;
     VH_REQUIRE(m < (int64_t(1) << 31) && batch * height * width * std::max<int64_t>(in_channels, 4) < (int64_t(1) << 40),

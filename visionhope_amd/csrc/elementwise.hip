@@ -355,9 +355,11 @@ __global__ __launch_bounds__(256) void grn_partial8_kernel(const T* __restrict__
 // statistics pass folded in: every workgroup of image b first
 // reduces the per-slab partial sums of all C channels (fixed order, so every workgroup of
 // the image gets bit-identical gx and inv_den) and workgroup 0 of the image stores them.
-// This saves the separate statistics launch between the two streaming passes.
+// This saves the separate statistics launch between the two streaming passes; it is used
+// while the partial sums of one image are small (FOLD).  Without FOLD the workgroup reads
+// gx and inv_den that grn_finalize_kernel wrote.
 // 256 threads; thread t streams channel group t % G of rows t / G (t / G < 256 / G).
-template <typename T, typename TO>
+template <typename T, typename TO, bool FOLD>
 __global__ __launch_bounds__(256) void grn_stats_apply8_kernel(const T* __restrict__ x, const float* __restrict__ partial,
                                                                const float* __restrict__ gamma,
                                                                const float* __restrict__ beta, float* __restrict__ gx,
@@ -368,7 +370,11 @@ __global__ __launch_bounds__(256) void grn_stats_apply8_kernel(const T* __restri
     const int t = static_cast<int>(threadIdx.x);
     const int b = blockIdx.y;
     float local = 0.f;
-    for (int c = t; c < C; c += 256) {
+    if constexpr (!FOLD) {
+        for (int c = t; c < C; c += 256) gsh[c] = gx[static_cast<int64_t>(b) * C + c];
+        __syncthreads();
+    }
+    for (int c = t; FOLD && c < C; c += 256) {
         const float* pc = partial + static_cast<int64_t>(b) * nslab * C + c;
         float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
         int s = 0;
@@ -387,8 +393,9 @@ __global__ __launch_bounds__(256) void grn_stats_apply8_kernel(const T* __restri
     for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off);
     if ((t & 63) == 0) wsum[t >> 6] = local;
     __syncthreads();
-    const float inv = 1.f / ((((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) / static_cast<float>(C) + eps);
-    if (blockIdx.x == 0) {
+    const float inv = FOLD ? 1.f / ((((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) / static_cast<float>(C) + eps)
+                           : inv_den[b];
+    if (FOLD && blockIdx.x == 0) {
         for (int c = t; c < C; c += 256) gx[static_cast<int64_t>(b) * C + c] = gsh[c];
         if (t == 0) inv_den[b] = inv;
     }
@@ -863,19 +870,31 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
         const int rows = static_cast<int>(grn_rows_per_slab(B, S));
         const int vslab = static_cast<int>((S + rows - 1) / rows);
         const size_t red = static_cast<size_t>(R) * static_cast<size_t>(C) * sizeof(float);
-        const int apply_rows = std::max(R, static_cast<int>(std::min<int64_t>(S, 4 * R)));
+        const int apply_rows = std::max(R, static_cast<int>(std::min<int64_t>(S, std::max(4 * R, 16))));
         const unsigned apply_blocks = static_cast<unsigned>((S + apply_rows - 1) / apply_rows);
         int rc = dispatch_t(io_dtype, [&](auto tv) {
             using T = decltype(tv);
             hipLaunchKernelGGL((grn_partial8_kernel<T>), dim3(static_cast<unsigned>(vslab), static_cast<unsigned>(B)),
                                dim3(G * R), red, s, static_cast<const T*>(x), partial, static_cast<int>(C),
                                static_cast<int>(S), rows, vslab);
+            // fold the statistics into the apply pass while each workgroup's extra read of the
+            // partial sums (vslab x C floats) stays small next to its share of x
+            const bool fold = static_cast<int64_t>(vslab) * C <= 8192;
+            if (!fold)
+                hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s,
+                                   partial, gx, inv_den, C, static_cast<int64_t>(vslab), eps);
             dispatch_t(y_dtype, [&](auto ov) {
                 using TO = decltype(ov);
-                hipLaunchKernelGGL((grn_stats_apply8_kernel<T, TO>), dim3(apply_blocks, static_cast<unsigned>(B)),
-                                   dim3(256), static_cast<size_t>(C) * sizeof(float), s, static_cast<const T*>(x),
-                                   partial, gamma, beta, gx, inv_den, static_cast<TO*>(y), static_cast<int>(C),
-                                   static_cast<int>(S), vslab, apply_rows, eps);
+                const dim3 grid(apply_blocks, static_cast<unsigned>(B));
+                const size_t lds = static_cast<size_t>(C) * sizeof(float);
+                if (fold)
+                    hipLaunchKernelGGL((grn_stats_apply8_kernel<T, TO, true>), grid, dim3(256), lds, s,
+                                       static_cast<const T*>(x), partial, gamma, beta, gx, inv_den, static_cast<TO*>(y),
+                                       static_cast<int>(C), static_cast<int>(S), vslab, apply_rows, eps);
+                else
+                    hipLaunchKernelGGL((grn_stats_apply8_kernel<T, TO, false>), grid, dim3(256), lds, s,
+                                       static_cast<const T*>(x), partial, gamma, beta, gx, inv_den, static_cast<TO*>(y),
+                                       static_cast<int>(C), static_cast<int>(S), vslab, apply_rows, eps);
             });
         });
         if (rc) return rc;

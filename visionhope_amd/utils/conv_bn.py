@@ -3,7 +3,8 @@ folded into the convolution (inference only).
 
 In eval mode ``bn(conv(x)) = conv(x; W s) + ((b - mean) s + beta)`` with
 ``s = gamma / sqrt(var + eps)`` per output channel (``models/layers.py:85-119``). The
-3x3 convolutions of the Tiny stem and downsample layers run as one native implicit GEMM
+3x3 convolutions of the stem and downsample layers (every width that is a multiple of 32:
+Tiny, Small and Base) run as one native implicit GEMM
 with the folded bias and the GELU in its epilogue (``vh_conv3x3_nhwc_forward``: the
 folded weight rounded to bf16 as autocast rounds it, the sum and the activation each
 rounded to bf16). Other shapes go to the library convolution with the folded weight,
@@ -77,7 +78,7 @@ def native_conv3x3_ok(x, conv):
             and conv.padding == (1, 1) and conv.dilation == (1, 1) and conv.groups == 1
             and conv.stride in ((1, 1), (2, 2)) and conv.padding_mode == "zeros"
             and x.is_contiguous(memory_format=torch.channels_last) and (c == 3 or c % 32 == 0)
-            and (n in (32, 64) or n % 128 == 0) and _bf16_compute(x, conv))
+            and n % 32 == 0 and _bf16_compute(x, conv))
 
 
 def gemm_weight(conv, weight):
