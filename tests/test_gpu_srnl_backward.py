@@ -121,7 +121,41 @@ def test_srnl_backward_rejects(device):
     from visionhope_amd.models.srnl_core.chunk import srnl_packed_backward
 
     mems = tuple(torch.from_numpy(m).to(device) for m in memories(4, 1, 16, seed=51))
-    x = torch.zeros(1, 4, 1, 70, 16, device=device)
-    q = torch.zeros(1, 4, 70, 16, device=device)
+    x = torch.zeros(1, 4, 1, 270, 16, device=device)
+    q = torch.zeros(1, 4, 270, 16, device=device)
     with pytest.raises(ValueError):
-        srnl_packed_backward(mems, x, q, [65, 8, 8, 8], torch.zeros_like(x), q_raw=True)   # chunk > 64
+        srnl_packed_backward(mems, x, q, [257, 8, 8, 8], torch.zeros_like(x), q_raw=True)   # chunk > 256
+
+
+@pytest.mark.parametrize("head_dim,chunks,length", [(16, [100, 100, 65, 65], 230), (32, [128, 128, 128, 128], 300),
+                                                    (8, [256, 3, 256, 3], 260)])
+def test_srnl_backward_long_chunks(device, head_dim, chunks, length):
+    """Chunks of 65 to 256 tokens (the long-line range; 256-token LDS buffers), mixed with
+    short chunks in other directions, ragged last chunks."""
+    from visionhope_amd.models.srnl_core.chunk import srnl_packed_backward
+
+    batch, directions, heads = 1, 4, 2
+    mems = memories(directions, heads, head_dim, kind="perturbed", seed=head_dim + 61)
+    x = randn(batch, directions, heads, length, head_dim, seed=62, scale=0.5)
+    q = randn(batch, directions, length, heads * head_dim, seed=63)
+    dy = randn(batch, directions, heads, length, head_dim, seed=64)
+    want = _oracle_grads(x, q, mems, chunks, dy, True)
+    got = srnl_packed_backward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device), q.to(device),
+                               chunks, dy.to(device), q_raw=True)
+    _check(got, want, f"d={head_dim} chunks={chunks}")
+
+
+def test_srnl_long_chunk_function_backward(device):
+    """Through the long-chunk autograd Function (chunk 96 > 64)."""
+    from visionhope_amd.models.srnl_core.lines import srnl_long_chunk
+
+    batch, heads, length, d = 1, 2, 200, 16
+    mems = [torch.from_numpy(m).to(device).requires_grad_() for m in memories(4, heads, d, kind="perturbed", seed=71)]
+    x = randn(batch, 4, heads, length, d, seed=72, scale=0.5).to(device).requires_grad_()
+    q = randn(batch, 4, length, heads * d, seed=73).to(device).requires_grad_()
+    y = srnl_long_chunk(*mems, x, q, 96, heads, d)
+    dy = randn(*y.shape, seed=74).to(device)
+    (y * dy).sum().backward()
+    want = _oracle_grads(x.detach().cpu(), q.detach().cpu(), [m.detach().cpu().numpy() for m in mems], [96] * 4,
+                         dy.cpu(), True)
+    _check([m.grad for m in mems] + [x.grad, q.grad], want, "long-chunk Function")

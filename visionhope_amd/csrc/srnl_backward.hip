@@ -34,7 +34,12 @@
 
 namespace vh {
 
-constexpr int kBwdMaxChunk = 64;
+constexpr int kBwdMaxChunk = 64;     // chunks up to this length use the small-LDS variant
+constexpr int kBwdLongChunk = 256;   // longest chunk of the backward (lines.cu:252-760 range)
+
+// The chunk buffers of a workgroup hold CMAX tokens: 64, or 256 when a direction's chunk
+// is longer (the long-line backward; about 42 KB of LDS more at d = 16).
+inline int bwd_cmax(int64_t max_chunk) { return max_chunk <= kBwdMaxChunk ? kBwdMaxChunk : kBwdLongChunk; }
 
 struct BwdParams {
     const void* x;      // [B, R, heads, N, D] io dtype
@@ -46,7 +51,7 @@ struct BwdParams {
     float* dq;          // layout of q, fp32
     float* dline;       // [lines, 3 D^2 + 2 D] per-line gradient of the initial state
     float* states;      // [lines, nc, 3 D^2 + 2 D] chunk-start states
-    float* gtraj;       // [lines, kBwdMaxChunk, D, D] gain trajectory of the current chunk
+    float* gtraj;       // [lines, CMAX, D, D] gain trajectory of the current chunk
     int64_t B, R, heads, N, nc;
     int chunk[4];
     vh_srnl_consts k;
@@ -75,7 +80,7 @@ __device__ __forceinline__ float softcap_dcap(float u, float e_neg) {
     return -expm1f(-u) - u * e_neg;
 }
 
-template <int D, typename T, bool QRAW>
+template <int D, typename T, bool QRAW, int CMAX>
 __global__ __launch_bounds__(D) void srnl_backward_kernel(const BwdParams p) {
     constexpr int SD = 3 * D * D + 2 * D, P = D + 1;
     __shared__ float Ms[3][D][P];       // chunk-start M_m, M_v, M_k
@@ -84,8 +89,8 @@ __global__ __launch_bounds__(D) void srnl_backward_kernel(const BwdParams p) {
     __shared__ float BG[D][P];          // dG rows
     __shared__ float Up[3][D][P];       // upstream state gradient dM'
     __shared__ float UpV[2][D];         // upstream de', da'
-    __shared__ float Kc[kBwdMaxChunk][D], Vc[kBwdMaxChunk][D];
-    __shared__ float Sc[kBwdMaxChunk][5];   // eta, alpha, d eta/d pre, d alpha/d pre, 1/|k~|
+    __shared__ float Kc[CMAX][D], Vc[CMAX][D];
+    __shared__ float Sc[CMAX][5];   // eta, alpha, d eta/d pre, d alpha/d pre, 1/|k~|
     __shared__ float Vec[6][D];         // x, dy, q^, r, r_bar / dk~, dv
 
     const int i = threadIdx.x;
@@ -130,7 +135,7 @@ __global__ __launch_bounds__(D) void srnl_backward_kernel(const BwdParams p) {
         dst[3 * D * D + D + i] = Ev[1][i];
     };
     float* my_states = p.states + ln * nc_alloc * SD;
-    float* my_traj = p.gtraj + ln * kBwdMaxChunk * D * D;
+    float* my_traj = p.gtraj + ln * CMAX * D * D;
 
     // Keys, values and gates of the tokens of chunk c from the state in Ms / Ev.
     auto token_data = [&](int64_t c) {
@@ -451,7 +456,7 @@ __global__ __launch_bounds__(256) void srnl_backward_reduce_kernel(const float* 
 namespace {
 
 struct BwdLayout {
-    int64_t lines, nc, sd;
+    int64_t lines, nc, sd, cmax;
     size_t states, traj, dline, total;
 };
 
@@ -463,7 +468,10 @@ BwdLayout bwd_layout(int64_t B, int64_t R, int64_t heads, int64_t N, int d, cons
     l.sd = 3 * int64_t(d) * d + 2 * d;
     auto round = [](size_t v) { return (v + 63) / 64 * 64; };
     l.states = round(static_cast<size_t>(l.lines * l.nc * l.sd));
-    l.traj = round(static_cast<size_t>(l.lines * kBwdMaxChunk * d * d));
+    int64_t cmax = 0;
+    for (int64_t r = 0; r < R; ++r) cmax = std::max<int64_t>(cmax, chunks[r]);
+    l.cmax = bwd_cmax(cmax);
+    l.traj = round(static_cast<size_t>(l.lines * l.cmax * d * d));
     l.dline = round(static_cast<size_t>(l.lines * l.sd));
     l.total = (l.states + l.traj + l.dline) * sizeof(float);
     return l;
@@ -481,7 +489,7 @@ size_t vh_srnl_backward_workspace_bytes(int64_t B, int64_t R, int64_t heads, int
     if (B <= 0 || R <= 0 || R > 4 || heads <= 0 || N <= 0 || chunks == nullptr) return 0;
     if (head_dim != 4 && head_dim != 8 && head_dim != 16 && head_dim != 32) return 0;
     for (int64_t r = 0; r < R; ++r)
-        if (chunks[r] <= 0 || chunks[r] > kBwdMaxChunk) return 0;
+        if (chunks[r] <= 0 || chunks[r] > kBwdLongChunk) return 0;
     return bwd_layout(B, R, heads, N, head_dim, chunks).total;
 }
 
@@ -499,8 +507,8 @@ int vh_srnl_backward(const void* x, const void* q, int32_t io_dtype, int32_t q_r
                "SRNL backward supports head_dim 4, 8, 16 and 32; got %d", head_dim);
     VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);
     for (int64_t r = 0; r < R; ++r)
-        VH_REQUIRE(chunks[r] > 0 && chunks[r] <= kBwdMaxChunk, VH_ERR_ARG,
-                   "SRNL backward chunk lengths must be in [1, %d], got %lld", kBwdMaxChunk, (long long)chunks[r]);
+        VH_REQUIRE(chunks[r] > 0 && chunks[r] <= kBwdLongChunk, VH_ERR_ARG,
+                   "SRNL backward chunk lengths must be in [1, %d], got %lld", kBwdLongChunk, (long long)chunks[r]);
     const BwdLayout lay = bwd_layout(B, R, heads, N, head_dim, chunks);
     VH_REQUIRE(workspace && workspace_bytes >= lay.total, VH_ERR_WORKSPACE,
                "SRNL backward workspace needs %zu bytes, got %zu", lay.total, workspace ? workspace_bytes : (size_t)0);
@@ -522,8 +530,13 @@ int vh_srnl_backward(const void* x, const void* q, int32_t io_dtype, int32_t q_r
     auto go = [&](auto dc, auto tv) {
         constexpr int D = decltype(dc)::value;
         using T = decltype(tv);
-        if (q_raw) hipLaunchKernelGGL((srnl_backward_kernel<D, T, true>), grid, dim3(D), 0, s, bp);
-        else hipLaunchKernelGGL((srnl_backward_kernel<D, T, false>), grid, dim3(D), 0, s, bp);
+        if (lay.cmax == kBwdMaxChunk) {
+            if (q_raw) hipLaunchKernelGGL((srnl_backward_kernel<D, T, true, kBwdMaxChunk>), grid, dim3(D), 0, s, bp);
+            else hipLaunchKernelGGL((srnl_backward_kernel<D, T, false, kBwdMaxChunk>), grid, dim3(D), 0, s, bp);
+        } else {
+            if (q_raw) hipLaunchKernelGGL((srnl_backward_kernel<D, T, true, kBwdLongChunk>), grid, dim3(D), 0, s, bp);
+            else hipLaunchKernelGGL((srnl_backward_kernel<D, T, false, kBwdLongChunk>), grid, dim3(D), 0, s, bp);
+        }
     };
     auto by_type = [&](auto dc) {
         switch (io_dtype) {

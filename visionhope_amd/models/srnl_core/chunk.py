@@ -15,6 +15,7 @@ from ...utils import hip
 from ...utils.cuda import on_tensor_device
 
 MAX_CHUNK = 64
+BACKWARD_MAX_CHUNK = 256   # the backward kernel's longest chunk (the long-line range)
 SUPPORTED_HEAD_DIMS = (4, 8, 16, 32, 64)
 
 
@@ -108,11 +109,12 @@ def srnl_packed_backward(memories, x, q, chunk_sizes, dy, *, q_raw):
     """Gradients of ``srnl_packed_forward`` (same arguments) for the output gradient
     ``dy [B, R, heads, N, d]``: ``(dM_m, dM_v, dM_k, dM_eta, dM_alpha, dx, dq)`` shaped and
     typed like the corresponding inputs (``vh_srnl_backward``; reference
-    ``chunk.cu:511-1057``).  The forward is recomputed from the inputs."""
+    ``chunk.cu:511-1057``, and ``lines.cu:252-760`` for chunks of 65 to 256 tokens).  The
+    forward is recomputed from the inputs."""
     batch, directions, heads, length, head_dim = x.shape
     chunks = [int(c) for c in chunk_sizes]
-    if len(chunks) != directions or min(chunks) <= 0 or max(chunks) > MAX_CHUNK:
-        raise ValueError(f"SRNL backward needs one chunk length in [1, {MAX_CHUNK}] per direction")
+    if len(chunks) != directions or min(chunks) <= 0 or max(chunks) > BACKWARD_MAX_CHUNK:
+        raise ValueError(f"SRNL backward needs one chunk length in [1, {BACKWARD_MAX_CHUNK}] per direction")
     n_flat = batch * directions * heads
     states, per_line = _float_memories(memories, directions, heads, head_dim, n_flat)
     x_c = x.contiguous()

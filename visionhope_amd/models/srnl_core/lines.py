@@ -1,4 +1,5 @@
-"""Long chunks and rectangular row/column scans (replaces ``models/srnl_core/lines.py``).
+"""Long chunks and rectangular row/column scans (replaces ``models/srnl_core/lines.py``),
+forward and (chunks of up to 256 tokens) backward.
 
 The reference needs separate tiled kernels once a chunk exceeds 64 tokens
 (``lines.py:183-671``); the MI355X scan tiles tokens internally, so both cases
@@ -7,7 +8,7 @@ run the same native forward with per-direction chunk lengths.
 
 import torch
 
-from .chunk import MAX_CHUNK, SUPPORTED_HEAD_DIMS, srnl_packed_backward, srnl_packed_forward
+from .chunk import BACKWARD_MAX_CHUNK, MAX_CHUNK, SUPPORTED_HEAD_DIMS, srnl_packed_backward, srnl_packed_forward
 from ...utils.autograd import backward_unavailable
 
 
@@ -43,11 +44,19 @@ class SRNLLongChunkFunction(torch.autograd.Function):
         if chunk_size <= MAX_CHUNK:
             raise ValueError("large-line CUDA kernel is only intended for chunk_size > base MAX_CHUNK.")
         memories = (M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0)
-        return srnl_packed_forward(memories, x, q_raw, [chunk_size] * x.shape[1], q_raw=True)
+        ctx.save_for_backward(*memories, x, q_raw)
+        ctx.chunks = [chunk_size] * x.shape[1]
+        return srnl_packed_forward(memories, x, q_raw, ctx.chunks, q_raw=True)
 
     @staticmethod
     def backward(ctx, dY):
-        backward_unavailable("SRNL long chunk")
+        """Reference ``lines.py:183-399`` (``lines.cu:252-760``): gradients of the memories, x
+        and the raw queries, for chunks of up to 256 tokens."""
+        *memories, x, q_raw = ctx.saved_tensors
+        if max(ctx.chunks) > BACKWARD_MAX_CHUNK:
+            backward_unavailable(f"SRNL long chunk above {BACKWARD_MAX_CHUNK}")
+        grads = srnl_packed_backward(memories, x, q_raw, ctx.chunks, dY, q_raw=True)
+        return (*grads, None, None, None, None)
 
 
 class SRNLVariableLineFunction(torch.autograd.Function):
@@ -70,10 +79,10 @@ class SRNLVariableLineFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dY):
         """Reference ``lines.py:645-671`` (``lines.cu:252-760``): gradients of the memories,
-        x and the raw queries.  Native while both chunk lengths are at most 64."""
+        x and the raw queries.  Native while both chunk lengths are at most 256."""
         *memories, x, q_raw = ctx.saved_tensors
-        if max(ctx.chunks) > MAX_CHUNK:
-            backward_unavailable("SRNL variable lines with a chunk above 64")
+        if max(ctx.chunks) > BACKWARD_MAX_CHUNK:
+            backward_unavailable(f"SRNL variable lines with a chunk above {BACKWARD_MAX_CHUNK}")
         grads = srnl_packed_backward(memories, x, q_raw, ctx.chunks, dY, q_raw=True)
         return (*grads, None, None, None, None, None)
 
