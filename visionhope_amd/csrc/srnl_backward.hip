@@ -57,10 +57,25 @@ struct BwdParams {
     vh_srnl_consts k;
 };
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the D-lane group of this lane, on the VALU (DPP and the gfx950 row swap; no LDS
+// round trip).  Every step adds lane pairs that exchange values (row mirror, half-row
+// mirror, quad xor 1 and 2, row xor), so all lanes of a group end with the same bits.
 template <int D>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = D / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, D);
+    static_assert(D == 4 || D == 8 || D == 16 || D == 32, "group of 4, 8, 16 or 32 lanes");
+    if constexpr (D >= 16) v += dpp_f<0x140>(v);   // row_mirror: lane l <-> 15 - l
+    if constexpr (D >= 8) v += dpp_f<0x141>(v);    // row_half_mirror: l <-> 7 - l in each 8
+    v += dpp_f<0xB1>(v);                           // quad_perm [1, 0, 3, 2]
+    v += dpp_f<0x4E>(v);                           // quad_perm [2, 3, 0, 1]
+    if constexpr (D == 32) {
+        const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+    }
     return v;
 }
 
@@ -80,21 +95,34 @@ __device__ __forceinline__ float softcap_dcap(float u, float e_neg) {
     return -expm1f(-u) - u * e_neg;
 }
 
-template <int D, typename T, bool QRAW, int CMAX>
-__global__ __launch_bounds__(D) void srnl_backward_kernel(const BwdParams p) {
+// LPW lines per workgroup, D lanes each (lines ln = LPW blockIdx.x + sub share (b, r), so
+// they run the same chunk schedule and meet every barrier together).
+template <int D, typename T, bool QRAW, int CMAX, int LPW>
+__global__ __launch_bounds__(D * LPW) void srnl_backward_kernel(const BwdParams p) {
     constexpr int SD = 3 * D * D + 2 * D, P = D + 1;
-    __shared__ float Ms[3][D][P];       // chunk-start M_m, M_v, M_k
-    __shared__ float Ev[2][D];          // chunk-start e, a
-    __shared__ float Gs[D][P];          // a gain matrix (rows by lane)
-    __shared__ float BG[D][P];          // dG rows
-    __shared__ float Up[3][D][P];       // upstream state gradient dM'
-    __shared__ float UpV[2][D];         // upstream de', da'
-    __shared__ float Kc[CMAX][D], Vc[CMAX][D];
-    __shared__ float Sc[CMAX][5];   // eta, alpha, d eta/d pre, d alpha/d pre, 1/|k~|
-    __shared__ float Vec[6][D];         // x, dy, q^, r, r_bar / dk~, dv
+    __shared__ float Ms_[LPW][3][D][P];     // chunk-start M_m, M_v, M_k
+    __shared__ float Ev_[LPW][2][D];        // chunk-start e, a
+    __shared__ float Gs_[LPW][D][P];        // a gain matrix (rows by lane)
+    __shared__ float BG_[LPW][D][P];        // dG rows
+    __shared__ float Up_[LPW][3][D][P];     // upstream state gradient dM'
+    __shared__ float UpV_[LPW][2][D];       // upstream de', da'
+    __shared__ float Kc_[LPW][CMAX][D], Vc_[LPW][CMAX][D];
+    __shared__ float Sc_[LPW][CMAX][5];     // eta, alpha, d eta/d pre, d alpha/d pre, 1/|k~|
+    __shared__ float Vec_[LPW][6][D];       // x, dy, q^, r, r_bar / dk~, dv
+    const int sub = static_cast<int>(threadIdx.x) / D;
+    float(&Ms)[3][D][P] = Ms_[sub];
+    float(&Ev)[2][D] = Ev_[sub];
+    float(&Gs)[D][P] = Gs_[sub];
+    float(&BG)[D][P] = BG_[sub];
+    float(&Up)[3][D][P] = Up_[sub];
+    float(&UpV)[2][D] = UpV_[sub];
+    float(&Kc)[CMAX][D] = Kc_[sub];
+    float(&Vc)[CMAX][D] = Vc_[sub];
+    float(&Sc)[CMAX][5] = Sc_[sub];
+    float(&Vec)[6][D] = Vec_[sub];
 
-    const int i = threadIdx.x;
-    const int64_t ln = blockIdx.x;
+    const int i = static_cast<int>(threadIdx.x) % D;
+    const int64_t ln = static_cast<int64_t>(blockIdx.x) * LPW + sub;
     const int64_t RH = p.R * p.heads;
     const int64_t s = p.per_line ? ln : ln % RH;
     const int r_dir = static_cast<int>((ln / p.heads) % p.R);
@@ -526,16 +554,35 @@ int vh_srnl_backward(const void* x, const void* q, int32_t io_dtype, int32_t q_r
     bp.k = *consts;
     hipStream_t s = static_cast<hipStream_t>(stream);
     VH_REQUIRE(lay.lines < (int64_t(1) << 31), VH_ERR_SHAPE, "SRNL backward: too many lines");
-    const dim3 grid(static_cast<unsigned>(lay.lines));
+    // Lines per workgroup: consecutive heads of one (b, r), as many as LDS allows (one line
+    // of d = 16 with 64-token buffers needs about 19 KB; 256-token buffers 43 KB; d = 32
+    // about 52 and 105 KB).
+    auto launch = [&](auto kern, int lpw, int d) {
+        hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(lay.lines / lpw)), dim3(d * lpw), 0, s, bp);
+    };
     auto go = [&](auto dc, auto tv) {
         constexpr int D = decltype(dc)::value;
         using T = decltype(tv);
+        constexpr int LS = D <= 16 ? 4 : 2;   // 64-token buffers
+        constexpr int LL = D <= 16 ? 2 : 1;   // 256-token buffers
         if (lay.cmax == kBwdMaxChunk) {
-            if (q_raw) hipLaunchKernelGGL((srnl_backward_kernel<D, T, true, kBwdMaxChunk>), grid, dim3(D), 0, s, bp);
-            else hipLaunchKernelGGL((srnl_backward_kernel<D, T, false, kBwdMaxChunk>), grid, dim3(D), 0, s, bp);
+            const bool packed = heads % LS == 0;
+            if (q_raw) {
+                if (packed) launch(srnl_backward_kernel<D, T, true, kBwdMaxChunk, LS>, LS, D);
+                else launch(srnl_backward_kernel<D, T, true, kBwdMaxChunk, 1>, 1, D);
+            } else {
+                if (packed) launch(srnl_backward_kernel<D, T, false, kBwdMaxChunk, LS>, LS, D);
+                else launch(srnl_backward_kernel<D, T, false, kBwdMaxChunk, 1>, 1, D);
+            }
         } else {
-            if (q_raw) hipLaunchKernelGGL((srnl_backward_kernel<D, T, true, kBwdLongChunk>), grid, dim3(D), 0, s, bp);
-            else hipLaunchKernelGGL((srnl_backward_kernel<D, T, false, kBwdLongChunk>), grid, dim3(D), 0, s, bp);
+            const bool packed = heads % LL == 0;
+            if (q_raw) {
+                if (packed) launch(srnl_backward_kernel<D, T, true, kBwdLongChunk, LL>, LL, D);
+                else launch(srnl_backward_kernel<D, T, true, kBwdLongChunk, 1>, 1, D);
+            } else {
+                if (packed) launch(srnl_backward_kernel<D, T, false, kBwdLongChunk, LL>, LL, D);
+                else launch(srnl_backward_kernel<D, T, false, kBwdLongChunk, 1>, 1, D);
+            }
         }
     };
     auto by_type = [&](auto dc) {
