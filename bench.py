@@ -249,10 +249,11 @@ def measure_base512(device, batch=8, reps=5):
     from visionhope_amd.inference.prepare import prepare_for_inference
     from visionhope_amd.models import create_model
 
-    torch.manual_seed(SEED)
-    model = create_model("visionhope_base", drop_path_rate=0.0).to(device).to(memory_format=torch.channels_last)
-    model.eval()
-    prepare_for_inference(model)
+    with torch.inference_mode(False):   # parameters are ordinary tensors even inside the bench's inference mode
+        torch.manual_seed(SEED)
+        model = create_model("visionhope_base", drop_path_rate=0.0).to(device).to(memory_format=torch.channels_last)
+        model.eval()
+        prepare_for_inference(model)
     gen = torch.Generator().manual_seed(SEED + 4)
     images = torch.randn(batch, 3, 512, 512, generator=gen).to(device).contiguous(memory_format=torch.channels_last)
 
@@ -265,7 +266,7 @@ def measure_base512(device, batch=8, reps=5):
     if not all(torch.isfinite(f).all() for f in feats):
         raise FloatingPointError("Base 512 forward produced NaN/Inf")
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.inference_mode(), torch.cuda.graph(graph):
         forward()
     ms = event_time_ms(graph.replay, torch.cuda.current_stream(device), reps, warmup=2)
     del graph, model
