@@ -30,7 +30,7 @@ def _check(got, want, tol, what):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("per_dir", [False, True])
 @pytest.mark.parametrize("channels_last", [False, True])
-@pytest.mark.parametrize("shape", [(2, 3, 8, 5, 7), (2, 5, 64, 4, 6), (8, 6, 16, 28, 28)])
+@pytest.mark.parametrize("shape", [(2, 3, 8, 5, 7), (2, 5, 64, 4, 6), (8, 6, 16, 28, 28), (2, 4, 4, 6, 5), (2, 12, 16, 9, 10)])
 def test_direction_fusion_backward(device, dtype, per_dir, channels_last, shape):
     from oracle.oracle_torch import direction_fusion_torch
     from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale

@@ -27,21 +27,33 @@ int dispatch_io(int t, F&& f) {
 
 size_t round256(size_t v) { return (v + 255) / 256 * 256; }
 
-// out_a[j] = sum_p part[p][j] for j < na, out_b[j - na] for na <= j < width; the parts are
-// summed in the order p = q, q + 4, ... by four thread rows, then the four rows in order.
+// out_a[j] = sum_p part[p][j] for j < na, out_b[j - na] for na <= j < width.  A workgroup
+// covers 16 columns with 16 thread rows; row q sums the parts p = q, q + 16, ... into four
+// interleaved accumulators (four loads in flight), then the 16 rows are added in order, so
+// the result does not depend on scheduling.
 __global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict__ part, int64_t parts,
                                                          int64_t width, int64_t na, float* __restrict__ out_a,
                                                          float* __restrict__ out_b) {
-    __shared__ float red[4][64];
-    const int64_t col = static_cast<int64_t>(blockIdx.x) * 64 + (threadIdx.x & 63);
-    const int row = threadIdx.x >> 6;
-    float acc = 0.f;
-    if (col < width)
-        for (int64_t p = row; p < parts; p += 4) acc += part[p * width + col];
-    red[row][threadIdx.x & 63] = acc;
+    __shared__ float red[16][17];
+    const int lc = threadIdx.x & 15, row = threadIdx.x >> 4;
+    const int64_t col = static_cast<int64_t>(blockIdx.x) * 16 + lc;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    if (col < width) {
+        int64_t p = row;
+        for (; p + 48 < parts; p += 64) {
+            a0 += part[p * width + col];
+            a1 += part[(p + 16) * width + col];
+            a2 += part[(p + 32) * width + col];
+            a3 += part[(p + 48) * width + col];
+        }
+        for (; p < parts; p += 16) a0 += part[p * width + col];
+    }
+    red[row][lc] = (a0 + a1) + (a2 + a3);
     __syncthreads();
     if (row == 0 && col < width) {
-        const float v = ((red[0][threadIdx.x] + red[1][threadIdx.x]) + red[2][threadIdx.x]) + red[3][threadIdx.x];
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v += red[q][lc];
         if (col < na) out_a[col] = v;
         else out_b[col - na] = v;
     }
@@ -49,7 +61,7 @@ __global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict
 
 void launch_column_sum(const float* part, int64_t parts, int64_t width, int64_t na, float* out_a, float* out_b,
                        hipStream_t s) {
-    hipLaunchKernelGGL(column_sum_kernel, dim3(static_cast<unsigned>((width + 63) / 64)), dim3(256), 0, s, part,
+    hipLaunchKernelGGL(column_sum_kernel, dim3(static_cast<unsigned>((width + 15) / 16)), dim3(256), 0, s, part,
                        parts, width, na, out_a, out_b);
 }
 
@@ -171,6 +183,117 @@ __global__ __launch_bounds__(256) void fusion_backward_kernel(const FusionBwdPar
             for (int r = 0; r < 4; ++r) prow[(nk + r) * C + c] = ss[r];
         }
         __syncthreads();
+    }
+}
+
+// Tiled variant for D >= 8 (16-byte accesses): one workgroup per (image, band of 4 pixel
+// rows, group of at most 96 channels) walks the band's 4x4 tiles.  Each tile's dout block
+// is staged in LDS; the row scans (directions 0, 1) are visited with the tile's pixels in
+// row-major order and the column scans (2, 3) in column-major order, so consecutive lanes
+// touch consecutive tokens of one head in both (the access pattern of the tiled forward).
+// Thread t keeps channel group t % G for the whole band and sums in registers; the pixel
+// rows of the workgroup are added in LDS in a fixed order.  Partial rows [B * bands][width].
+template <int D, typename T>
+__global__ __launch_bounds__(256) void fusion_backward_tile_kernel(const FusionBwdParams p, const int heads_per_block) {
+    constexpr int GD = D / 8;
+    const int64_t b = blockIdx.y, band = blockIdx.x;
+    const int C = static_cast<int>(p.heads) * D;
+    const int head0 = static_cast<int>(blockIdx.z) * heads_per_block;
+    const int nh = min(heads_per_block, static_cast<int>(p.heads) - head0);
+    const int CB = nh * D, G = nh * GD, PPB = 256 / G;
+    const int64_t L = p.H * p.W, stride_dir = p.heads * L * D;
+    const int nk = p.skip_per_dir ? 4 : 1, width = (nk + 4) * C;
+    const int t = static_cast<int>(threadIdx.x);
+    const int cg = t % G, pr = t / G;
+    const bool active = pr < PPB;
+    const int hl = cg / GD, gi = cg % GD, head = head0 + hl;
+    const int c0 = head * D + gi * 8;
+    const T* y = static_cast<const T*>(p.y);
+    const T* x = static_cast<const T*>(p.x);
+    T* dy = static_cast<T*>(p.dy);
+    T* dx = static_cast<T*>(p.dx);
+    extern __shared__ float lds[];
+    float* gt = lds;              // [16 pixels][CB] dout of the current tile
+    float* red = lds + 16 * CB;   // [PPB][CB] reduction rows
+    float s[4][8], k[4][8], acc_k[4][8], acc_s[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            s[r][j] = active ? p.scale[r * C + c0 + j] : 0.f;
+            k[r][j] = active ? p.skip[(p.skip_per_dir ? r * C : 0) + c0 + j] : 0.f;
+            acc_k[r][j] = 0.f;
+            acc_s[r][j] = 0.f;
+        }
+    const int64_t base = (b * 4 * p.heads + head) * L * D + gi * 8;
+    const int64_t h0 = band * 4;
+    const int64_t tiles_w = (p.W + 3) / 4;
+    for (int64_t tw = 0; tw < tiles_w; ++tw) {
+        const int64_t w0 = tw * 4;
+        for (int e = t; e < 16 * CB; e += 256) {
+            const int q = e / CB, c = e % CB;
+            const int64_t h = h0 + (q >> 2), w = w0 + (q & 3);
+            float g = 0.f;
+            if (h < p.H && w < p.W) {
+                const int64_t l = h * p.W + w, ch = head0 * D + c;
+                g = p.channels_last ? p.dout[(b * L + l) * C + ch] : p.dout[(b * C + ch) * L + l];
+            }
+            gt[q * CB + c] = g;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int phase = 0; phase < 2; ++phase) {
+            for (int q = pr; active && q < 16; q += PPB) {
+                const int ph = phase == 0 ? q >> 2 : q & 3, pw = phase == 0 ? q & 3 : q >> 2;
+                const int64_t h = h0 + ph, w = w0 + pw;
+                if (h >= p.H || w >= p.W) continue;
+                const float* g8 = gt + (ph * 4 + pw) * CB + hl * D + gi * 8;
+#pragma unroll
+                for (int rr = 0; rr < 2; ++rr) {
+                    const int r = 2 * phase + rr;
+                    const int64_t at = base + r * stride_dir + pixel_to_scan(r, h, w, p.H, p.W) * D;
+                    float yv[8], xv[8], oy[8], ox[8];
+                    load8<T>(y + at, yv);
+                    load8<T>(x + at, xv);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float gs = g8[j] * s[r][j];
+                        oy[j] = gs;
+                        ox[j] = gs * k[r][j];
+                        acc_k[r][j] += gs * xv[j];
+                        acc_s[r][j] += g8[j] * (yv[j] + k[r][j] * xv[j]);
+                    }
+                    store8<T>(dy + at, oy);
+                    store8<T>(dx + at, ox);
+                }
+            }
+        }
+        __syncthreads();
+    }
+    float* prow = p.part + (b * gridDim.x + band) * width;
+    for (int r = 0; r < 4; ++r) {
+        for (int kind = 0; kind < 2; ++kind) {
+            if (active) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) red[pr * CB + hl * D + gi * 8 + j] = kind == 0 ? acc_k[r][j] : acc_s[r][j];
+            }
+            __syncthreads();
+            if (active && pr == 0) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float v = 0.f;
+                    for (int q = 0; q < PPB; ++q) v += red[q * CB + hl * D + gi * 8 + j];
+                    if (kind == 1) prow[(nk + r) * C + c0 + j] = v;
+                    else if (nk == 4) prow[r * C + c0 + j] = v;
+                    else acc_k[r][j] = v;   // shared skip: the four directions are added below
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (nk == 1 && active && pr == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) prow[c0 + j] = ((acc_k[0][j] + acc_k[1][j]) + acc_k[2][j]) + acc_k[3][j];
     }
 }
 
@@ -475,7 +598,10 @@ extern "C" {
 size_t vh_postprocess_scale_backward_workspace_bytes(int64_t B, int64_t heads, int64_t H, int64_t W,
                                                      int32_t head_dim, int32_t skip_per_dir) {
     if (B <= 0 || heads <= 0 || H <= 0 || W <= 0 || head_dim <= 0) return 0;
-    return fusion_layout(B, heads * head_dim, H * W, skip_per_dir).bytes;
+    // either kernel's partial rows (the tiled one writes one row per image and band of 4 rows)
+    const size_t tiled = round256(static_cast<size_t>(B * ((H + 3) / 4) * ((skip_per_dir ? 4 : 1) + 4) * heads *
+                                                      head_dim) * sizeof(float));
+    return std::max(tiled, fusion_layout(B, heads * head_dim, H * W, skip_per_dir).bytes);
 }
 
 int vh_postprocess_scale_backward(const float* dout, int32_t dout_channels_last, const void* y, const void* x,
@@ -491,12 +617,39 @@ int vh_postprocess_scale_backward(const float* dout, int32_t dout_channels_last,
     const int64_t C = heads * head_dim;
     VH_REQUIRE(C <= (int64_t(1) << 20), VH_ERR_SHAPE, "too many channels (%lld)", (long long)C);
     const FusionLayout f = fusion_layout(B, C, H * W, skip_per_dir);
-    VH_REQUIRE(workspace && workspace_bytes >= f.bytes, VH_ERR_WORKSPACE,
-               "direction fusion backward workspace needs %zu bytes, got %zu", f.bytes,
+    const size_t need = vh_postprocess_scale_backward_workspace_bytes(B, heads, H, W, head_dim, skip_per_dir);
+    VH_REQUIRE(workspace && workspace_bytes >= need, VH_ERR_WORKSPACE,
+               "direction fusion backward workspace needs %zu bytes, got %zu", need,
                workspace ? workspace_bytes : (size_t)0);
     hipStream_t s = static_cast<hipStream_t>(stream);
     FusionBwdParams p{dout, y, x, d_skip, scale, dy, dx, static_cast<float*>(workspace), heads, H, W, head_dim,
                       f.seg_len, skip_per_dir ? 1 : 0, dout_channels_last ? 1 : 0};
+    const uintptr_t align = reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(x) |
+                            reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(dx);
+    if (head_dim >= 8 && head_dim % 8 == 0 && head_dim <= 64 && align % 16 == 0) {
+        // at most 96 channels (12 groups of 8) per workgroup: the kernel's one-pixel-per-thread-row layout
+        const int hpb = static_cast<int>(std::min<int64_t>(heads, std::max(1, 96 / head_dim)));
+        const int64_t bands = (H + 3) / 4, chunks = (heads + hpb - 1) / hpb;
+        const size_t lds = static_cast<size_t>(16 * hpb * head_dim + 256 * 8) * sizeof(float);
+        const dim3 grid(static_cast<unsigned>(bands), static_cast<unsigned>(B), static_cast<unsigned>(chunks));
+        int ok = 1;
+        const int rc = dispatch_io(io_dtype, [&](auto tv) {
+            using T = decltype(tv);
+            switch (head_dim) {
+                case 8: hipLaunchKernelGGL((fusion_backward_tile_kernel<8, T>), grid, dim3(256), lds, s, p, hpb); break;
+                case 16: hipLaunchKernelGGL((fusion_backward_tile_kernel<16, T>), grid, dim3(256), lds, s, p, hpb); break;
+                case 32: hipLaunchKernelGGL((fusion_backward_tile_kernel<32, T>), grid, dim3(256), lds, s, p, hpb); break;
+                case 64: hipLaunchKernelGGL((fusion_backward_tile_kernel<64, T>), grid, dim3(256), lds, s, p, hpb); break;
+                default: ok = 0;
+            }
+        });
+        if (rc) return rc;
+        if (ok) {
+            launch_column_sum(p.part, B * bands, (skip_per_dir ? 4 : 1) * C + 4 * C, (skip_per_dir ? 4 : 1) * C,
+                              d_dskip, d_scale, s);
+            return check_launch("direction fusion backward (tiled)");
+        }
+    }
     const int rc = dispatch_io(io_dtype, [&](auto tv) {
         hipLaunchKernelGGL((fusion_backward_kernel<decltype(tv)>), dim3(static_cast<unsigned>(f.segments),
                            static_cast<unsigned>(B)), dim3(256), 0, s, p);
