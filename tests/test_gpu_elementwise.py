@@ -74,7 +74,7 @@ def test_config2_full_size(oracle, device, shape):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("channels,height,width", [(96, 7, 5), (256, 14, 14), (7, 3, 3), (2048, 7, 7), (1792, 16, 16)])
+@pytest.mark.parametrize("channels,height,width", [(96, 7, 5), (256, 14, 14), (7, 3, 3), (2048, 7, 7), (1792, 16, 16), (2560, 9, 7)])
 @pytest.mark.parametrize("channels_last", [True, False])
 def test_grn(oracle, device, dtype, channels, height, width, channels_last):
     from visionhope_amd.utils.grn import global_response_norm

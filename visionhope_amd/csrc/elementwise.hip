@@ -351,13 +351,91 @@ __global__ __launch_bounds__(256) void grn_partial8_kernel(const T* __restrict__
     }
 }
 
+// Wide maps (C / 8 > 256 channel groups, e.g. 2560 FFN channels): thread t takes channel
+// groups t, t + 256, ... of every row of the slab (partial sums) or of the workgroup's rows
+// (apply, from the gx and inv_den that grn_finalize_kernel wrote).
+template <typename T>
+__global__ __launch_bounds__(256) void grn_partial8_wide_kernel(const T* __restrict__ x, float* __restrict__ partial,
+                                                               int C, int S, int rows_per_slab, int nslab) {
+    const int G = C / 8, b = blockIdx.y, slab = blockIdx.x;
+    const int s0 = slab * rows_per_slab, s1 = min(S, s0 + rows_per_slab);
+    for (int g = threadIdx.x; g < G; g += 256) {
+        const T* xb = x + static_cast<int64_t>(b) * S * C + g * 8;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int s = s0; s < s1; ++s) {
+            float v[8];
+            load8<T>(xb + static_cast<int64_t>(s) * C, v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] += v[j] * v[j];
+        }
+        store8<float>(partial + (static_cast<int64_t>(b) * nslab + slab) * C + g * 8, acc);
+    }
+}
+
+// gx[b, c] = sqrt(sum over the slabs), one thread per channel (grid: channel blocks x images,
+// so small batches still spread over the GPU).
+__global__ __launch_bounds__(256) void grn_gx_kernel(const float* __restrict__ partial, float* __restrict__ gx, int C,
+                                                    int nslab) {
+    const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (c >= C) return;
+    const float* pc = partial + static_cast<int64_t>(b) * nslab * C + c;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int s = 0;
+    for (; s + 4 <= nslab; s += 4) {
+        a0 += pc[s * C];
+        a1 += pc[(s + 1) * C];
+        a2 += pc[(s + 2) * C];
+        a3 += pc[(s + 3) * C];
+    }
+    for (; s < nslab; ++s) a0 += pc[s * C];
+    gx[static_cast<int64_t>(b) * C + c] = sqrtf((a0 + a1) + (a2 + a3));
+}
+
+// Apply for wide maps: every workgroup of image b forms inv_den from gx (fixed order, so all
+// workgroups agree bit for bit) and workgroup 0 stores it.
+template <typename T, typename TO>
+__global__ __launch_bounds__(256) void grn_apply8_wide_kernel(const T* __restrict__ x, const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta,
+                                                             const float* __restrict__ gx,
+                                                             float* __restrict__ inv_den, TO* __restrict__ y,
+                                                             int C, int S, int rows_per_block, float eps) {
+    const int G = C / 8, b = blockIdx.y;
+    const int s0 = blockIdx.x * rows_per_block, s1 = min(S, s0 + rows_per_block);
+    __shared__ float wsum[4];
+    float local = 0.f;
+    for (int c = threadIdx.x; c < C; c += 256) local += gx[static_cast<int64_t>(b) * C + c];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = local;
+    __syncthreads();
+    const float inv = 1.f / ((((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) / static_cast<float>(C) + eps);
+    if (blockIdx.x == 0 && threadIdx.x == 0) inv_den[b] = inv;
+    for (int g = threadIdx.x; g < G; g += 256) {
+        float sc[8], bt[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = g * 8 + j;
+            sc[j] = 1.f + gamma[c] * (gx[static_cast<int64_t>(b) * C + c] * inv);
+            bt[j] = beta[c];
+        }
+        const int64_t base = static_cast<int64_t>(b) * S * C + g * 8;
+        for (int s = s0; s < s1; ++s) {
+            float v[8];
+            load8<T>(x + base + static_cast<int64_t>(s) * C, v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = v[j] * sc[j] + bt[j];
+            store8<TO>(y + base + static_cast<int64_t>(s) * C, v);
+        }
+    }
+}
+
 // GRN apply (y = x scale_c + beta_c, 8 channels per thread, 16-byte loads) with the
 // statistics pass folded in: every workgroup of image b first
 // reduces the per-slab partial sums of all C channels (fixed order, so every workgroup of
 // the image gets bit-identical gx and inv_den) and workgroup 0 of the image stores them.
 // This saves the separate statistics launch between the two streaming passes; it is used
 // while the partial sums of one image are small (FOLD).  Without FOLD the workgroup reads
-// gx and inv_den that grn_finalize_kernel wrote.
+// gx that grn_gx_kernel wrote and forms inv_den from it the same way.
 // 256 threads; thread t streams channel group t % G of rows t / G (t / G < 256 / G).
 template <typename T, typename TO, bool FOLD>
 __global__ __launch_bounds__(256) void grn_stats_apply8_kernel(const T* __restrict__ x, const float* __restrict__ partial,
@@ -371,8 +449,11 @@ __global__ __launch_bounds__(256) void grn_stats_apply8_kernel(const T* __restri
     const int b = blockIdx.y;
     float local = 0.f;
     if constexpr (!FOLD) {
-        for (int c = t; c < C; c += 256) gsh[c] = gx[static_cast<int64_t>(b) * C + c];
-        __syncthreads();
+        for (int c = t; c < C; c += 256) {
+            const float g = gx[static_cast<int64_t>(b) * C + c];
+            gsh[c] = g;
+            local += g;
+        }
     }
     for (int c = t; FOLD && c < C; c += 256) {
         const float* pc = partial + static_cast<int64_t>(b) * nslab * C + c;
@@ -393,10 +474,10 @@ __global__ __launch_bounds__(256) void grn_stats_apply8_kernel(const T* __restri
     for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off);
     if ((t & 63) == 0) wsum[t >> 6] = local;
     __syncthreads();
-    const float inv = FOLD ? 1.f / ((((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) / static_cast<float>(C) + eps)
-                           : inv_den[b];
-    if (FOLD && blockIdx.x == 0) {
-        for (int c = t; c < C; c += 256) gx[static_cast<int64_t>(b) * C + c] = gsh[c];
+    const float inv = 1.f / ((((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) / static_cast<float>(C) + eps);
+    if (blockIdx.x == 0) {
+        if (FOLD)
+            for (int c = t; c < C; c += 256) gx[static_cast<int64_t>(b) * C + c] = gsh[c];
         if (t == 0) inv_den[b] = inv;
     }
     const int G = C / 8, R = 256 / G;
@@ -881,8 +962,8 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
             // partial sums (vslab x C floats) stays small next to its share of x
             const bool fold = static_cast<int64_t>(vslab) * C <= 8192;
             if (!fold)
-                hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s,
-                                   partial, gx, inv_den, C, static_cast<int64_t>(vslab), eps);
+                hipLaunchKernelGGL(grn_gx_kernel, dim3(static_cast<unsigned>((C + 255) / 256), static_cast<unsigned>(B)),
+                                   dim3(256), 0, s, partial, gx, static_cast<int>(C), vslab);
             dispatch_t(y_dtype, [&](auto ov) {
                 using TO = decltype(ov);
                 const dim3 grid(apply_blocks, static_cast<unsigned>(B));
@@ -899,6 +980,29 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
         });
         if (rc) return rc;
         return check_launch("grn vectorised kernels");
+    }
+    const bool aligned = (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16 == 0;
+    if (C % 8 == 0 && C / 8 > 256 && aligned && B * S * C < (int64_t(1) << 31)) {
+        const int rows = static_cast<int>(grn_rows_per_slab(B, S));
+        const int vslab = static_cast<int>((S + rows - 1) / rows);
+        const int apply_rows = static_cast<int>(std::min<int64_t>(S, 8));
+        const unsigned apply_blocks = static_cast<unsigned>((S + apply_rows - 1) / apply_rows);
+        int rc = dispatch_t(io_dtype, [&](auto tv) {
+            using T = decltype(tv);
+            hipLaunchKernelGGL((grn_partial8_wide_kernel<T>), dim3(static_cast<unsigned>(vslab), static_cast<unsigned>(B)),
+                               dim3(256), 0, s, static_cast<const T*>(x), partial, static_cast<int>(C),
+                               static_cast<int>(S), rows, vslab);
+            hipLaunchKernelGGL(grn_gx_kernel, dim3(static_cast<unsigned>((C + 255) / 256), static_cast<unsigned>(B)),
+                               dim3(256), 0, s, partial, gx, static_cast<int>(C), vslab);
+            dispatch_t(y_dtype, [&](auto ov) {
+                using TO = decltype(ov);
+                hipLaunchKernelGGL((grn_apply8_wide_kernel<T, TO>), dim3(apply_blocks, static_cast<unsigned>(B)),
+                                   dim3(256), 0, s, static_cast<const T*>(x), gamma, beta, gx, inv_den,
+                                   static_cast<TO*>(y), static_cast<int>(C), static_cast<int>(S), apply_rows, eps);
+            });
+        });
+        if (rc) return rc;
+        return check_launch("grn wide vectorised kernels");
     }
     int rc = dispatch_t(io_dtype, [&](auto tv) {
         using T = decltype(tv);
