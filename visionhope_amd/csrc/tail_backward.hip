@@ -477,6 +477,110 @@ __global__ __launch_bounds__(256) void layernorm_backward_kernel(const float* __
     }
 }
 
+// Vectorised variant for C % 8 == 0 and 16-byte aligned rows: lane l of a row's TPR lanes
+// owns channel groups l + k TPR (k < GP) of 8 channels (16-byte x loads, two 16-byte dy
+// loads); TPR = the power of two at or above C / 8 / GP.
+template <typename T, int TPR, int GP>
+__global__ __launch_bounds__(256) void layernorm_backward8_kernel(const float* __restrict__ dy, const T* __restrict__ x,
+                                                                  const float* __restrict__ w,
+                                                                  const float* __restrict__ mean,
+                                                                  const float* __restrict__ rstd, T* __restrict__ dx,
+                                                                  float* __restrict__ part, int64_t rows, int C) {
+    constexpr int RPB = 256 / TPR;
+    const int lane = threadIdx.x % TPR, G = C / 8;
+    float dw[GP][8], db[GP][8], wv[GP][8];
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+        const int g = lane + k * TPR;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            dw[k][j] = db[k][j] = 0.f;
+            wv[k][j] = g < G ? w[g * 8 + j] : 0.f;
+        }
+    }
+    const float inv_c = 1.f / static_cast<float>(C);
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR; row < rows;
+         row += static_cast<int64_t>(gridDim.x) * RPB) {
+        const float mu = mean[row], rs = rstd[row];
+        float g8[GP][8], xh[GP][8];
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < GP; ++k) {
+            const int g = lane + k * TPR;
+            if (g < G) {
+                float d[8], xv[8];
+                load8<float>(dy + row * C + g * 8, d);
+                load8<T>(x + row * C + g * 8, xv);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    xh[k][j] = (xv[j] - mu) * rs;
+                    g8[k][j] = d[j] * wv[k][j];
+                    dw[k][j] += d[j] * xh[k][j];
+                    db[k][j] += d[j];
+                    s1 += g8[k][j];
+                    s2 += g8[k][j] * xh[k][j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xh[k][j] = g8[k][j] = 0.f;
+            }
+        }
+#pragma unroll
+        for (int off = TPR / 2; off > 0; off >>= 1) {
+            s1 += __shfl_xor(s1, off);
+            s2 += __shfl_xor(s2, off);
+        }
+        s1 *= inv_c;
+        s2 *= inv_c;
+#pragma unroll
+        for (int k = 0; k < GP; ++k) {
+            const int g = lane + k * TPR;
+            if (g < G) {
+                float o[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = (g8[k][j] - s1 - xh[k][j] * s2) * rs;
+                store8<T>(dx + row * C + g * 8, o);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < GP; ++k)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int off = TPR; off < 64; off <<= 1) {
+                dw[k][j] += __shfl_xor(dw[k][j], off);
+                db[k][j] += __shfl_xor(db[k][j], off);
+            }
+    __shared__ float red[4][2][TPR * GP * 8];
+    const int wave = threadIdx.x / 64;
+    if ((threadIdx.x & 63) < TPR) {
+#pragma unroll
+        for (int k = 0; k < GP; ++k)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                red[wave][0][(lane + k * TPR) * 8 + j] = dw[k][j];
+                red[wave][1][(lane + k * TPR) * 8 + j] = db[k][j];
+            }
+    }
+    __syncthreads();
+    float* prow = part + static_cast<int64_t>(blockIdx.x) * 2 * C;
+    for (int c = threadIdx.x; c < C; c += 256) {
+        prow[c] = ((red[0][0][c] + red[1][0][c]) + red[2][0][c]) + red[3][0][c];
+        prow[C + c] = ((red[0][1][c] + red[1][1][c]) + red[2][1][c]) + red[3][1][c];
+    }
+}
+
+// (TPR, GP) of the vectorised LayerNorm backward for C % 8 == 0, C <= 1024.
+void ln8_shape(int64_t C, int* tpr, int* gp) {
+    const int64_t G = C / 8;
+    *gp = G > 64 ? 2 : 1;
+    const int64_t per = (G + *gp - 1) / *gp;
+    int t = 2;
+    while (t < per) t <<= 1;
+    *tpr = t;
+}
+
 int64_t ln_backward_blocks(int64_t rows, int tpr) {
     const int64_t rpb = 256 / tpr;
     return std::max<int64_t>(1, std::min<int64_t>((rows + rpb - 1) / rpb, 1024));
@@ -714,7 +818,12 @@ int vh_layernorm2d_backward(const float* dy, const void* x, int32_t io_dtype, co
     VH_REQUIRE(C <= 1024, VH_ERR_SHAPE, "LayerNorm2d backward supports at most 1024 channels, got %lld",
                (long long)C);
     const int64_t rows = B * H * W;
-    const int tpr = ln_tpr(C);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dx) |
+                            reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(weight);
+    int tpr8 = 0, gp8 = 0;
+    ln8_shape(C, &tpr8, &gp8);
+    const bool vec = C % 8 == 0 && align % 16 == 0;
+    const int tpr = vec ? tpr8 : ln_tpr(C);
     const int64_t blocks = ln_backward_blocks(rows, tpr);
     const size_t need = vh_layernorm2d_backward_workspace_bytes(B, C, H, W);
     VH_REQUIRE(workspace && workspace_bytes >= need, VH_ERR_WORKSPACE,
@@ -727,6 +836,20 @@ int vh_layernorm2d_backward(const float* dy, const void* x, int32_t io_dtype, co
         using T = decltype(tv);
         const T* xp = static_cast<const T*>(x);
         T* dxp = static_cast<T*>(dx);
+#define VH_LN_BWD8(TPR, GP) \
+    hipLaunchKernelGGL((layernorm_backward8_kernel<T, TPR, GP>), grid, dim3(256), 0, s, dy, xp, weight, mean, rstd, \
+                       dxp, part, rows, c)
+        if (vec) {
+            if (gp8 == 2) VH_LN_BWD8(64, 2);
+            else if (tpr8 == 2) VH_LN_BWD8(2, 1);
+            else if (tpr8 == 4) VH_LN_BWD8(4, 1);
+            else if (tpr8 == 8) VH_LN_BWD8(8, 1);
+            else if (tpr8 == 16) VH_LN_BWD8(16, 1);
+            else if (tpr8 == 32) VH_LN_BWD8(32, 1);
+            else VH_LN_BWD8(64, 1);
+            return;
+        }
+#undef VH_LN_BWD8
 #define VH_LN_BWD(TPR, MAXV) \
     hipLaunchKernelGGL((layernorm_backward_kernel<T, TPR, MAXV>), grid, dim3(256), 0, s, dy, xp, weight, mean, rstd, \
                        dxp, part, rows, c)
