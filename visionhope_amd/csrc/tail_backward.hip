@@ -341,6 +341,73 @@ __global__ __launch_bounds__(256) void grn_backward_partial_kernel(const float* 
     }
 }
 
+// 16-byte variants (C % 8 == 0, C / 8 <= 256, aligned): thread t owns channel group t % G of
+// pixel rows t / G, t / G + 256 / G, ... of the slab (partial sums), or one 8-channel group
+// of one pixel (dx).
+template <typename T>
+__global__ __launch_bounds__(256) void grn_backward_partial8_kernel(const float* __restrict__ dout,
+                                                                    const T* __restrict__ x, float* __restrict__ part,
+                                                                    int64_t S, int C, int64_t slab) {
+    const int64_t b = blockIdx.y, sl = blockIdx.x;
+    const int64_t s_begin = sl * slab, s_end = std::min<int64_t>(S, s_begin + slab);
+    const int G = C / 8, R = 256 / G;
+    const int t = static_cast<int>(threadIdx.x), g = t % G, rr = t / G;
+    float sdx[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, sd[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (rr < R) {
+        for (int64_t s = s_begin + rr; s < s_end; s += R) {
+            const int64_t i = (b * S + s) * C + g * 8;
+            float d[8], xv[8];
+            load8<float>(dout + i, d);
+            load8<T>(x + i, xv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                sdx[j] += d[j] * xv[j];
+                sd[j] += d[j];
+            }
+        }
+    }
+    __shared__ float red[2][256 * 8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        red[0][t * 8 + j] = sdx[j];
+        red[1][t * 8 + j] = sd[j];
+    }
+    __syncthreads();
+    if (t < G) {
+        float* prow = part + (b * gridDim.x + sl) * 2 * C;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float a = 0.f, d = 0.f;
+            for (int q = 0; q < R; ++q) {
+                a += red[0][(q * G + t) * 8 + j];
+                d += red[1][(q * G + t) * 8 + j];
+            }
+            prow[t * 8 + j] = a;
+            prow[C + t * 8 + j] = d;
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void grn_backward_dx8_kernel(const float* __restrict__ dout, const T* __restrict__ x,
+                                                               const float* __restrict__ coef, T* __restrict__ dx,
+                                                               int64_t groups, int64_t S, int C) {
+    const int G = C / 8;
+    for (int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; q < groups;
+         q += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t g = q % G, b = q / (S * G);
+        const float* cf = coef + b * 2 * C + g * 8;
+        float d[8], xv[8], a[8], c2[8], o[8];
+        load8<float>(dout + q * 8, d);
+        load8<T>(x + q * 8, xv);
+        load8<float>(cf, a);
+        load8<float>(cf + C, c2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = d[j] * a[j] + c2[j] * xv[j];
+        store8<T>(dx + q * 8, o);
+    }
+}
+
 // One workgroup per image: per-channel sums over the slabs, then the coefficients of dx
 // (coef[b][0][c] = 1 + gamma nx, coef[b][1][c] = the x factor) and the per-image parameter
 // partials pp[b] = (P_c nx_c, sum dout).
@@ -789,8 +856,23 @@ int vh_grn_backward(const float* dout, const void* x, int32_t io_dtype, const fl
     const int c = static_cast<int>(C);
     const int64_t total = B * S * C;
     const unsigned dx_blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 8192));
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dx) |
+                            reinterpret_cast<uintptr_t>(dout) | reinterpret_cast<uintptr_t>(workspace) | g.part;
+    const bool vec = C % 8 == 0 && C / 8 <= 256 && align % 16 == 0;
     const int rc = dispatch_io(io_dtype, [&](auto tv) {
         using T = decltype(tv);
+        if (vec) {
+            hipLaunchKernelGGL((grn_backward_partial8_kernel<T>), dim3(static_cast<unsigned>(g.nslab),
+                               static_cast<unsigned>(B)), dim3(256), 0, s, dout, static_cast<const T*>(x), part, S, c,
+                               g.slab);
+            hipLaunchKernelGGL(grn_backward_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, part,
+                               gamma, gx, inv_den, coef, pp, g.nslab, c);
+            const int64_t groups = total / 8;
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((groups + 255) / 256, 8192));
+            hipLaunchKernelGGL((grn_backward_dx8_kernel<T>), dim3(blocks), dim3(256), 0, s, dout,
+                               static_cast<const T*>(x), coef, static_cast<T*>(dx), groups, S, c);
+            return;
+        }
         hipLaunchKernelGGL((grn_backward_partial_kernel<T>), dim3(static_cast<unsigned>(g.nslab),
                            static_cast<unsigned>(B)), dim3(256), 0, s, dout, static_cast<const T*>(x), part, S, c,
                            g.slab);
