@@ -143,3 +143,39 @@ def test_fused_classifier_head(device):
         got = model._fused_head(x)
     assert got.dtype == expected.dtype and got.shape == expected.shape
     assert_close(got.double().cpu().numpy(), expected.double().cpu().numpy(), 2e-2, "fused head")
+
+
+@pytest.mark.parametrize("embed_dim", [96, 80])
+def test_prepared_base_stem_pads_narrow_widths(device, monkeypatch, embed_dim):
+    """A stem whose inner widths are not multiples of 32 (Base: 48, here also 40) runs every
+    convolution natively on zero-padded channels when its output width allows (96), or
+    falls back to the library for the convolutions it cannot pad (80); either way it matches
+    the unfolded stem under bf16 autocast."""
+    import copy
+
+    from visionhope_amd.models.layers import PatchEmbedding
+
+    torch.manual_seed(3)
+    ref = PatchEmbedding(3, embed_dim).to(device).to(memory_format=torch.channels_last).eval()
+    with torch.no_grad():
+        for m in ref.modules():
+            if isinstance(m, nn.BatchNorm2d):
+                m.running_mean.normal_(0, 0.1)
+                m.running_var.uniform_(0.5, 1.5)
+                m.weight.normal_(1, 0.1)
+                m.bias.normal_(0, 0.1)
+    folded = copy.deepcopy(ref)
+    folded._vh_fold_bn = True
+    x = randn(2, 3, 40, 36, seed=71).to(device).contiguous(memory_format=torch.channels_last)
+    calls = []
+    real_conv2d = F.conv2d
+    monkeypatch.setattr(F, "conv2d", lambda *a, **k: calls.append(1) or real_conv2d(*a, **k))
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        got = folded(x)
+    monkeypatch.setattr(F, "conv2d", real_conv2d)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        want = ref(x)
+    assert got.shape == want.shape == (2, embed_dim, 10, 9)
+    if embed_dim == 96:
+        assert not calls, "the padded Base stem should not call the library convolution"
+    assert_close(got.float().cpu().numpy(), want.float().cpu().numpy(), 2e-2, f"stem {embed_dim}")

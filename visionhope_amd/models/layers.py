@@ -114,12 +114,23 @@ class PatchEmbedding(nn.Module):
 
     def forward(self, x):
         if self._folded_path(x):
-            from ..utils.conv_bn import ACT_GELU, ACT_NONE, conv_bn_act
+            from ..utils.conv_bn import ACT_GELU, ACT_NONE, conv_bn_act, conv_bn_act_padded, padded_native_ok
             mods = list(self.proj)
             i = 0
             while i < len(mods):
                 gelu = i + 2 < len(mods) and isinstance(mods[i + 2], nn.GELU)
-                x = conv_bn_act(x, mods[i], mods[i + 1], ACT_GELU if gelu else ACT_NONE)
+                act = ACT_GELU if gelu else ACT_NONE
+                conv = mods[i]
+                last = i + (3 if gelu else 2) >= len(mods)
+                # Widths off the implicit GEMM's multiples of 32 (Base: 48): zero-padded
+                # channels inside the stem; the stem's output keeps its real width.
+                narrow = conv.out_channels % 32 != 0 or x.shape[1] != conv.in_channels
+                if narrow and padded_native_ok(x, conv) and (not last or conv.out_channels % 32 == 0):
+                    x = conv_bn_act_padded(x, conv, mods[i + 1], act, pad_out=not last)
+                else:
+                    if x.shape[1] != conv.in_channels:   # drop the zero padding for the library path
+                        x = x[:, :conv.in_channels].contiguous(memory_format=torch.channels_last)
+                    x = conv_bn_act(x, conv, mods[i + 1], act)
                 i += 3 if gelu else 2
             return self.norm(x)
         return self.norm(self.proj(x))

@@ -107,7 +107,7 @@ def conv3x3_bias_act(x, conv, weight, bias, act=ACT_NONE):
     gemm = gemm_weight(conv, weight)
     b, c, h, w = x.shape
     s = conv.stride[0]
-    n = conv.out_channels
+    n = weight.shape[0]
     out = torch.empty((b, n, (h - 1) // s + 1, (w - 1) // s + 1), device=x.device, dtype=torch.bfloat16,
                       memory_format=torch.channels_last)
     lib = hip.load_library()
@@ -115,6 +115,47 @@ def conv3x3_bias_act(x, conv, weight, bias, act=ACT_NONE):
         hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(gemm), hip.ptr(bias), int(act), hip.ptr(out),
         b, h, w, c, n, s, hip.stream_of(x)), "vh_conv3x3_nhwc_forward")
     return out
+
+
+def _round32(n):
+    return (n + 31) // 32 * 32
+
+
+def padded_native_ok(x, conv):
+    """Whether ``conv_bn_act_padded`` can run ``conv`` natively on ``x`` (whose channels may
+    already carry zero padding beyond ``conv.in_channels``)."""
+    c = x.shape[1]
+    return (x.is_cuda and x.dim() == 4 and c >= conv.in_channels and (c == 3 or c % 32 == 0)
+            and conv.kernel_size == (3, 3) and conv.padding == (1, 1) and conv.dilation == (1, 1)
+            and conv.groups == 1 and conv.stride in ((1, 1), (2, 2)) and conv.padding_mode == "zeros"
+            and x.is_contiguous(memory_format=torch.channels_last) and _bf16_compute(x, conv)
+            and (c == conv.in_channels or c % 32 == 0))
+
+
+def conv_bn_act_padded(x, conv, bn, act=ACT_NONE, pad_out=False):
+    """``conv_bn_act`` for widths the implicit GEMM does not take (not a multiple of 32): the
+    folded weight gets zero rows up to the next multiple of 32 outputs (``pad_out``) and zero
+    columns for the zero channels ``x`` already carries; the padded bias is 0.  A padded
+    output channel is then exactly act(0) = 0 (GELU or none), so the next convolution's zero
+    weight columns see zeros and the real channels are unchanged.  Returns the map with
+    ``round32(out_channels)`` channels when ``pad_out``, else with ``out_channels``."""
+    weight, bias = folded_weights(conv, bn)
+    n, cin = weight.shape[0], weight.shape[1]
+    c = x.shape[1]
+    n_pad = _round32(n) if pad_out else n
+    key = (id(weight), c, n_pad)
+    cached = getattr(conv, "_vh_padded", None)
+    if cached is None or cached[0] != key or cached[1] is not weight:
+        with torch.no_grad():
+            w = torch.zeros(n_pad, c, 3, 3, device=weight.device, dtype=weight.dtype)
+            w[:n, :cin] = weight
+            w = w.contiguous(memory_format=torch.channels_last)
+            b = torch.zeros(n_pad, device=bias.device, dtype=bias.dtype)
+            b[:n] = bias
+        object.__setattr__(conv, "_vh_padded", (key, weight, w, b))
+        cached = conv._vh_padded
+    w, b = cached[2], cached[3]
+    return conv3x3_bias_act(x, conv, w, b, act)
 
 
 def conv_bn_act(x, conv, bn, act=ACT_NONE):
