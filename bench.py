@@ -191,10 +191,13 @@ def measure_tail_backward(device):
             ("grn", lambda: visionhope_grn(xc, gamma, beta, 1e-6), (xc, gamma, beta), 8),
             ("layernorm", lambda: visionhope_layernorm2d(xc, gamma, beta, 1e-6), (xc, gamma, beta), 8)):
         y = fwd()
+        # eager autograd (the backward is not captured in a graph: autograd runs it on its
+        # own device thread), so short kernels include the host time between launches
         ms = event_time_ms(lambda: torch.autograd.grad(y, inputs, dout, retain_graph=True), stream, 5)
         gbs = bytes_per * n / ms / 1e6
         out[f"{name}_backward_{grid}x{grid}x{channels}"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
-                                                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+                                                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
+                                                            "timing": "eager autograd"}
         del y
     return out
 
@@ -365,6 +368,9 @@ def main(argv=None):
     parser.add_argument("--tail-only", action="store_true",
                         help="profiling workload for rocprofv3: the config-2 fusion, GRN and LayerNorm "
                              "launches of the `kernels` entry and the calibration copy; no JSON line")
+    parser.add_argument("--backward-only", action="store_true",
+                        help="profiling workload for rocprofv3: the SRNL backward and the fusion, GRN and "
+                             "LayerNorm backward launches of the `kernels` entry; no JSON line")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -375,6 +381,13 @@ def main(argv=None):
 
     if args.stages_only:
         return profile_stages(torch.device("cuda:0"), args.batch)
+    if args.backward_only:
+        device = torch.device("cuda:0")
+        rows = measure_srnl_backward(device)
+        rows.update(measure_tail_backward(device))
+        for name, row in rows.items():
+            print(name, row, flush=True)
+        return 0
     if args.tail_only:
         with torch.inference_mode():
             for name, row in measure_tail(torch.device("cuda:0")).items():
