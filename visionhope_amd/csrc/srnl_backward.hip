@@ -259,17 +259,19 @@ __global__ __launch_bounds__(D * LPW) void srnl_backward_kernel(const BwdParams 
         // S <- S G (row i of each matrix, through Up as scratch), e <- G^T e, a <- G^T a
 #pragma unroll 1
         for (int m = 0; m < 3; ++m) {
-            float row[D];
+            // out = row_i(M_m) G, accumulated over the rows l of G: row l is one broadcast
+            // read of D consecutive floats for every lane, so its loads issue back to back
+            float out[D];
 #pragma unroll
-            for (int l = 0; l < D; ++l) row[l] = Ms[m][i][l];
-#pragma unroll 1
-            for (int j = 0; j < D; ++j) {
-                lds_fence();
-                float acc = 0.f;
+            for (int j = 0; j < D; ++j) out[j] = 0.f;
 #pragma unroll
-                for (int l = 0; l < D; ++l) acc += row[l] * Gs[l][j];
-                Up[m][i][j] = acc;
+            for (int l = 0; l < D; ++l) {
+                const float r = Ms[m][i][l];
+#pragma unroll
+                for (int j = 0; j < D; ++j) out[j] += r * Gs[l][j];
             }
+#pragma unroll
+            for (int j = 0; j < D; ++j) Up[m][i][j] = out[j];
         }
         float ne = 0.f, na = 0.f;
 #pragma unroll
@@ -324,16 +326,12 @@ __global__ __launch_bounds__(D * LPW) void srnl_backward_kernel(const BwdParams 
         for (int j = 0; j < D; ++j) bg[j] = Ev[0][i] * UpV[0][j] + Ev[1][i] * UpV[1][j];
 #pragma unroll 1
         for (int m = 0; m < 3; ++m) {
-            float col[D];
+            // bg += column_i(M_m)^T dM'_m, over the rows l of dM'_m (broadcast row reads)
 #pragma unroll
-            for (int l = 0; l < D; ++l) col[l] = Ms[m][l][i];
+            for (int l = 0; l < D; ++l) {
+                const float cl = Ms[m][l][i];
 #pragma unroll
-            for (int j = 0; j < D; ++j) {
-                lds_fence();
-                float a = 0.f;
-#pragma unroll
-                for (int l = 0; l < D; ++l) a += col[l] * Up[m][l][j];
-                bg[j] += a;
+                for (int j = 0; j < D; ++j) bg[j] += cl * Up[m][l][j];
             }
         }
         float acc_e = 0.f, acc_a = 0.f;
