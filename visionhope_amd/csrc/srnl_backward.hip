@@ -345,17 +345,17 @@ __global__ __launch_bounds__(D * LPW) void srnl_backward_kernel(const BwdParams 
         // of dM', in place; the tokens below add to it), de = G de'.
 #pragma unroll 1
         for (int m = 0; m < 3; ++m) {
-            float row[D];
+            float out[D];
 #pragma unroll
-            for (int l = 0; l < D; ++l) row[l] = Up[m][i][l];
-#pragma unroll 1
-            for (int j = 0; j < D; ++j) {
-                lds_fence();
-                float a = 0.f;
+            for (int j = 0; j < D; ++j) out[j] = 0.f;
 #pragma unroll
-                for (int l = 0; l < D; ++l) a += row[l] * Gs[j][l];
-                Up[m][i][j] = a;
+            for (int l = 0; l < D; ++l) {   // column l of G: a broadcast read for every lane
+                const float r = Up[m][i][l];
+#pragma unroll
+                for (int j = 0; j < D; ++j) out[j] += r * Gs[j][l];
             }
+#pragma unroll
+            for (int j = 0; j < D; ++j) Up[m][i][j] = out[j];
         }
         __syncthreads();
 
