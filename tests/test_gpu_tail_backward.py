@@ -27,10 +27,11 @@ def _check(got, want, tol, what):
         assert_close(g.detach().double().cpu().numpy(), w.numpy(), tol, f"{what} gradient {i}")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("per_dir", [False, True])
 @pytest.mark.parametrize("channels_last", [False, True])
-@pytest.mark.parametrize("shape", [(2, 3, 8, 5, 7), (2, 5, 64, 4, 6), (8, 6, 16, 28, 28), (2, 4, 4, 6, 5), (2, 12, 16, 9, 10)])
+@pytest.mark.parametrize("shape", [(2, 3, 8, 5, 7), (2, 5, 64, 4, 6), (8, 6, 16, 28, 28), (2, 4, 4, 6, 5),
+                                   (2, 12, 16, 9, 10), (1, 1, 16, 1, 1)])
 def test_direction_fusion_backward(device, dtype, per_dir, channels_last, shape):
     from oracle.oracle_torch import direction_fusion_torch
     from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
@@ -53,7 +54,7 @@ def test_direction_fusion_backward(device, dtype, per_dir, channels_last, shape)
     _check([t.grad for t in leaves], want, TOL[dtype], f"fusion {shape} {dtype} per_dir={per_dir}")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(2, 24, 5, 7), (3, 300, 4, 4), (4, 96, 28, 28), (1, 8, 1, 1)])
 def test_grn_backward(device, dtype, shape):
     from oracle.oracle_torch import grn_torch
@@ -72,8 +73,8 @@ def test_grn_backward(device, dtype, shape):
     _check([t.grad for t in leaves], want, TOL[dtype], f"GRN {shape} {dtype}")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("channels", [8, 24, 96, 192, 384, 768, 1000])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("channels", [8, 24, 96, 192, 384, 768, 1000, 3])
 @pytest.mark.parametrize("channels_last", [True, False])
 def test_layernorm2d_backward(device, dtype, channels, channels_last):
     from oracle.oracle_torch import layernorm2d_torch
