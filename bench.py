@@ -277,6 +277,107 @@ def measure_base512(device, batch=8, reps=5):
                                     "feature_shapes": [list(f.shape) for f in feats]}}
 
 
+CONFIG3 = dict(batch=32, grid=56, channels=96, head_dim=32)
+
+
+def _config3_operator(device):
+    """Config 3: the four-direction operator (96 channels, 3 heads of 32, chunks 56), repo
+    default init plus N(0, 0.1^2) gate vectors and skip, 1 + N(0, 0.1^2) direction scales,
+    fast inference; its bf16 channels-last input [32, 96, 56, 56] (what proj_in feeds it
+    under autocast)."""
+    import torch
+    from visionhope_amd.models import VisionHOPEOperator
+
+    c = CONFIG3
+    with torch.inference_mode(False):
+        torch.manual_seed(SEED)
+        op = VisionHOPEOperator(c["channels"], head_dim=c["head_dim"], direction_merge="scale").to(device).eval()
+        gen = torch.Generator(device=device).manual_seed(SEED + 3)
+        with torch.no_grad():
+            for p in (op.srnl.M_eta_0, op.srnl.M_alpha_0, op.d_skip):
+                p.copy_(torch.randn(p.shape, device=device, generator=gen) * 0.1)
+            op.direction_scale.add_(torch.randn(op.direction_scale.shape, device=device, generator=gen) * 0.1)
+        op.fast_inference = True
+    gen = torch.Generator().manual_seed(SEED + 33)
+    x = torch.randn(c["batch"], c["grid"], c["grid"], c["channels"], generator=gen).bfloat16().to(device)
+    return op, x.permute(0, 3, 1, 2)
+
+
+def measure_operator_config3(device, reps=10):
+    """Config 3 timed two ways: the whole operator forward (W_q projection, scans, readout
+    and fusion; one forward per HIP graph replay) and its SRNL launch pair alone (scan +
+    readout, event-timed on its stream).  The bound is max(FLOP / FP32 matrix peak, bytes /
+    HBM peak): the recurrence computes in FP32, and the compulsory bytes are x and q in bf16
+    and the FP32 output."""
+    import torch
+    from visionhope_amd.models.srnl_core.fused import srnl_spatial_inference
+
+    c = CONFIG3
+    op, x = _config3_operator(device)
+
+    def forward():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            return op(x)
+
+    forward()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        forward()
+    ms_op = event_time_ms(graph.replay, torch.cuda.current_stream(device), reps, warmup=2)
+    del graph
+    x_nhwc = x.permute(0, 2, 3, 1)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        q_nhwc = op.W_q(x_nhwc)
+    mems = tuple(m.detach() for m in op.srnl.initial_memories)
+    wts = op.direction_weights().detach().float()
+    chunks = (c["grid"],) * 4
+    ms = event_time_ms(lambda: srnl_spatial_inference(mems, x_nhwc, q_nhwc, op.d_skip, wts, chunks),
+                       torch.cuda.current_stream(device), reps)
+    flops = srnl_flops(c["batch"], c["grid"], c["grid"], c["channels"], c["head_dim"], chunks)
+    nbytes = c["batch"] * c["grid"] * c["grid"] * c["channels"] * (2 + 2 + 4)
+    bound_ms = max(flops / FP32_PEAK_TFLOPS / 1e9, nbytes / HBM_PEAK_GBS / 1e6)
+    return {"operator_config3_b32_56x56x96_d32_bf16": {
+        "ms_operator_forward": round(ms_op, 4), "ms_srnl_scan_readout": round(ms, 4),
+        "algorithmic_gflop": round(flops / 1e9, 3), "algorithmic_mb": round(nbytes / 1e6, 1),
+        "tflops": round(flops / ms / 1e9, 3), "frac_fp32_peak": round(flops / ms / 1e9 / FP32_PEAK_TFLOPS, 4),
+        "roofline_bound_ms": round(bound_ms, 4), "frac_of_roofline": round(bound_ms / ms, 4),
+        "bound": "fp32 matrix (FLOP) vs HBM (bytes), the larger"}}
+
+
+def profile_config3(device):
+    """Three config-3 operator forwards (eager, bf16 autocast) for kernel traces."""
+    import torch
+
+    op, x = _config3_operator(device)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        for i in range(3):
+            op(x)
+            torch.cuda.synchronize()
+            print(f"config 3 operator forward {i}", flush=True)
+    return 0
+
+
+def profile_base512(device, batch=8):
+    """Three Base 512 B=8 feature forwards (prepared, bf16 autocast, eager) for kernel traces."""
+    import torch
+    from visionhope_amd.inference.prepare import prepare_for_inference
+    from visionhope_amd.models import create_model
+
+    torch.manual_seed(SEED)
+    model = create_model("visionhope_base", drop_path_rate=0.0).to(device).to(memory_format=torch.channels_last)
+    model.eval()
+    prepare_for_inference(model)
+    gen = torch.Generator().manual_seed(SEED + 4)
+    images = torch.randn(batch, 3, 512, 512, generator=gen).to(device).contiguous(memory_format=torch.channels_last)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        for i in range(3):
+            model.forward_intermediates(images)
+            torch.cuda.synchronize()
+            print(f"Base 512 B={batch} forward {i}", flush=True)
+    return 0
+
+
 def cpu_baseline(sample_batch=8, reps=3):
     """Tiny forward on the host: PyTorch CPU for convs/linears/norms and the CPU oracle
     (oracle/liboracle_srnl.so, OpenMP) for the four-direction SRNL operator."""
@@ -368,6 +469,10 @@ def main(argv=None):
     parser.add_argument("--tail-only", action="store_true",
                         help="profiling workload for rocprofv3: the config-2 fusion, GRN and LayerNorm "
                              "launches of the `kernels` entry and the calibration copy; no JSON line")
+    parser.add_argument("--config3-only", action="store_true",
+                        help="profiling workload for rocprofv3: three config-3 operator forwards; no JSON line")
+    parser.add_argument("--base512-only", action="store_true",
+                        help="profiling workload for rocprofv3: three Base 512 B=8 feature forwards; no JSON line")
     parser.add_argument("--backward-only", action="store_true",
                         help="profiling workload for rocprofv3: the SRNL backward and the fusion, GRN and "
                              "LayerNorm backward launches of the `kernels` entry; no JSON line")
@@ -381,6 +486,10 @@ def main(argv=None):
 
     if args.stages_only:
         return profile_stages(torch.device("cuda:0"), args.batch)
+    if args.config3_only:
+        return profile_config3(torch.device("cuda:0"))
+    if args.base512_only:
+        return profile_base512(torch.device("cuda:0"))
     if args.backward_only:
         device = torch.device("cuda:0")
         rows = measure_srnl_backward(device)
@@ -453,6 +562,7 @@ def main(argv=None):
 
         stage_rows, srnl_flops_total, srnl_ms_total, srnl_bytes = measure_srnl_stages(device, args.batch)
         tail = measure_tail(device)
+        tail.update(measure_operator_config3(device))
         tail.update(measure_base512(device))
         tail.update(measure_srnl_backward(device))
         with torch.inference_mode(False), torch.enable_grad():   # autograd tensors, outside inference mode

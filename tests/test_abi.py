@@ -224,3 +224,26 @@ def test_check_raises_with_message(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(hip.NativeLibraryMissing):
         hip.load_library(tmp_path / "absent.so")
+
+
+def _backward(lib, directions=4, consts=None):
+    p = ctypes.c_void_p(0x1000)
+    arr, keep = hip.int64_array([4] * 4)
+    return lib.vh_srnl_backward(p, p, hip.VH_DTYPE_F32, 1, p, p, p, p, p, p, 0, p, p, p, p, p, p, p,
+                                2, directions, 2, 8, 16, arr, consts if consts is not None else _consts(),
+                                p, 1 << 30, None)
+
+
+def test_srnl_backward_validates_directions_and_constants(lib):
+    """The backward checks what the forward checks: 1, 2 or 4 directions and the ranges of
+    the stability constants (a zero injection margin would give NaN gradients)."""
+    assert _backward(lib, directions=3) == hip.VH_ERR_SHAPE
+    assert b"directions" in lib.vh_last_error()
+    for bad, name in ((hip.make_consts(0.025, 1.5, 2.197224577, 0.999, True, 0.999999), b"MIN_RETENTION"),
+                      (hip.make_consts(0.025, 0.0, 2.197224577, 0.0, True, 0.999999), b"INJECTION_MARGIN"),
+                      (hip.make_consts(-1.0, 0.0, 2.197224577, 0.999, True, 0.999999), b"STEP_SCALE"),
+                      (hip.make_consts(0.025, 0.0, 2.197224577, 0.999, True, 1.5), b"SPECTRAL_MARGIN")):
+        assert _backward(lib, consts=bad) == hip.VH_ERR_ARG
+        assert name in lib.vh_last_error()
+    bad_margin = hip.make_consts(0.025, 0.0, 2.197224577, 0.999, True, 0.0)
+    assert _spatial(lib, consts=bad_margin) == hip.VH_ERR_ARG

@@ -159,3 +159,44 @@ def test_srnl_long_chunk_function_backward(device):
     want = _oracle_grads(x.detach().cpu(), q.detach().cpu(), [m.detach().cpu().numpy() for m in mems], [96] * 4,
                          dy.cpu(), True)
     _check([m.grad for m in mems] + [x.grad, q.grad], want, "long-chunk Function")
+
+
+@pytest.mark.parametrize("head_dim", [4, 8, 16])
+@pytest.mark.parametrize("heads", [2, 4, 8])
+@pytest.mark.parametrize("q_raw", [True, False])
+def test_srnl_backward_lines_per_workgroup(device, head_dim, heads, q_raw):
+    """Both launch shapes of the backward: heads % 4 == 0 packs 4 lines (consecutive heads of
+    one image and direction) into a workgroup at d <= 16, otherwise 1 line per workgroup.
+    Ragged last chunks, one length per direction."""
+    from visionhope_amd.models.srnl_core.chunk import srnl_packed_backward
+
+    batch, directions, length = 2, 4, 19
+    chunks = [6, 4, 7, 5]
+    mems = memories(directions, heads, head_dim, kind="perturbed", seed=100 + heads * head_dim)
+    x = randn(batch, directions, heads, length, head_dim, seed=101)
+    if q_raw:
+        q = randn(batch, directions, length, heads * head_dim, seed=102)
+    else:
+        q = randn(batch, directions, heads, length, head_dim, seed=102)
+        q = q / q.norm(dim=-1, keepdim=True)
+    dy = randn(batch, directions, heads, length, head_dim, seed=103)
+    want = _oracle_grads(x, q, mems, chunks, dy, q_raw)
+    got = srnl_packed_backward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device), q.to(device),
+                               chunks, dy.to(device), q_raw=q_raw)
+    _check(got, want, f"d={head_dim} heads={heads} q_raw={q_raw}")
+
+
+def test_srnl_backward_tiny_stage3_shape(device):
+    """The Tiny stage-3 operator's lines (8 heads of 16, 14x14 map, chunks of 14: the shape
+    the packed variant trains on), at batch 2, bf16 inputs as under autocast."""
+    from visionhope_amd.models.srnl_core.chunk import srnl_packed_backward
+
+    batch, directions, heads, d, length = 2, 4, 8, 16, 196
+    mems = memories(directions, heads, d, kind="perturbed", seed=111)
+    x = randn(batch, directions, heads, length, d, seed=112).bfloat16()
+    q = randn(batch, directions, length, heads * d, seed=113).bfloat16()
+    dy = randn(batch, directions, heads, length, d, seed=114)
+    want = _oracle_grads(x.float(), q.float(), mems, [14] * 4, dy, True)
+    got = srnl_packed_backward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device), q.to(device),
+                               [14] * 4, dy.to(device), q_raw=True)
+    _check([g.float() for g in got], want, "Tiny stage 3", tol=1e-2)

@@ -1279,17 +1279,6 @@ Consts make_consts(const vh_srnl_consts* k) {
                   k->spectral_clamp, k->spectral_factor};
 }
 
-int check_consts(const vh_srnl_consts* k) {
-    VH_REQUIRE(k != nullptr, VH_ERR_ARG, "SRNL constants must not be null");
-    VH_REQUIRE(k->min_retention >= 0.f && k->min_retention < 1.f, VH_ERR_ARG,
-               "MIN_RETENTION must be in [0, 1), got %g", (double)k->min_retention);
-    VH_REQUIRE(k->injection_margin > 0.f && k->injection_margin < 1.f, VH_ERR_ARG,
-               "INJECTION_MARGIN must be in (0, 1), got %g", (double)k->injection_margin);
-    VH_REQUIRE(k->step_scale > 0.f, VH_ERR_ARG, "STEP_SCALE must be positive, got %g",
-               (double)k->step_scale);
-    return VH_OK;
-}
-
 int check_memories(const float* a, const float* b, const float* c, const float* d, const float* e) {
     VH_REQUIRE(a && b && c && d && e, VH_ERR_ARG, "SRNL memories must not be null");
     return VH_OK;
@@ -1399,7 +1388,7 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
     for (int64_t r = 0; r < R; ++r)
         VH_REQUIRE(chunks[r] > 0 && chunks[r] <= (int64_t)1 << 30, VH_ERR_ARG,
                    "invalid chunk length %lld for direction %lld", (long long)chunks[r], (long long)r);
-    int rc = check_consts(consts);
+    int rc = check_srnl_consts(consts);
     if (rc) return rc;
     rc = check_memories(Mm, Mv, Mk, Me, Ma);
     if (rc) return rc;
@@ -1516,6 +1505,35 @@ int run_packed(const ScanParams& sp, const LineInput& q, int q_raw, int io_dtype
 }
 
 }  // namespace
+
+int check_spatial_shape(int64_t B, int64_t H, int64_t W, int64_t C, int32_t head_dim) {
+    VH_REQUIRE(H > 0 && W > 0 && C > 0 && B > 0, VH_ERR_SHAPE, "spatial SRNL needs nonempty [B,H,W,C]");
+    VH_REQUIRE(valid_head_dim(head_dim), VH_ERR_HEAD_DIM,
+               "head_dim must be one of 4, 8, 16, 32, 64; got %d", head_dim);
+    VH_REQUIRE(C % head_dim == 0, VH_ERR_SHAPE, "C=%lld is not a multiple of head_dim=%d",
+               (long long)C, head_dim);
+    VH_REQUIRE(H * W < (int64_t(1) << 24), VH_ERR_SHAPE, "spatial SRNL supports H*W < 2^24 pixels, got %lld",
+               (long long)(H * W));
+    return VH_OK;
+}
+
+int srnl_spatial_forward_ws(const void* x, const void* q, int32_t io_dtype, const float* M_m, const float* M_v,
+                            const float* M_k, const float* M_eta, const float* M_alpha, const float* d_skip,
+                            int32_t skip_per_direction, const float* dir_weight, float* out, int64_t B, int64_t H,
+                            int64_t W, int64_t C, int32_t head_dim, const int64_t chunks[4],
+                            const vh_srnl_consts* consts, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream) {
+    int rc = check_spatial_shape(B, H, W, C, head_dim);
+    if (rc) return rc;
+    const int64_t heads = C / head_dim;
+    LineInput xin{x, H * W * C, 0, head_dim, C, 1, H, W, 1.0f / static_cast<float>(H)};
+    ScanParams sp{};
+    rc = run_scan(xin, io_dtype, M_m, M_v, M_k, M_eta, M_alpha, B, 4, heads, H * W, head_dim, chunks, consts,
+                  workspace, workspace_bytes, stream, &sp);
+    if (rc) return rc;
+    return run_fuse(sp, x, q, 0, io_dtype, d_skip, skip_per_direction, dir_weight, out, H, W, C, head_dim, stream);
+}
+
 }  // namespace vh
 
 using namespace vh;
@@ -1535,22 +1553,9 @@ int vh_srnl_spatial_forward(const void* x, const void* q, int32_t io_dtype, cons
                             int64_t C, int32_t head_dim, const int64_t chunks[4],
                             const vh_srnl_consts* consts, void* workspace, size_t workspace_bytes,
                             void* stream) {
-    VH_REQUIRE(H > 0 && W > 0 && C > 0 && B > 0, VH_ERR_SHAPE, "spatial SRNL needs nonempty [B,H,W,C]");
-    VH_REQUIRE(valid_head_dim(head_dim), VH_ERR_HEAD_DIM,
-               "head_dim must be one of 4, 8, 16, 32, 64; got %d", head_dim);
-    VH_REQUIRE(C % head_dim == 0, VH_ERR_SHAPE, "C=%lld is not a multiple of head_dim=%d",
-               (long long)C, head_dim);
-    VH_REQUIRE(H * W < (int64_t(1) << 24), VH_ERR_SHAPE, "spatial SRNL supports H*W < 2^24 pixels, got %lld",
-               (long long)(H * W));
-    const int64_t heads = C / head_dim;
-    LineInput xin{x, H * W * C, 0, head_dim, C, 1, H, W, 1.0f / static_cast<float>(H)};
-    ScanParams sp{};
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    int rc = run_scan(xin, io_dtype, M_m, M_v, M_k, M_eta, M_alpha, B, 4, heads, H * W, head_dim,
-                      chunks, consts, workspace, workspace_bytes, s, &sp);
-    if (rc) return rc;
-    return run_fuse(sp, x, q, 0, io_dtype, d_skip, skip_per_direction, dir_weight, out, H, W, C,
-                    head_dim, s);
+    return srnl_spatial_forward_ws(x, q, io_dtype, M_m, M_v, M_k, M_eta, M_alpha, d_skip, skip_per_direction,
+                                   dir_weight, out, B, H, W, C, head_dim, chunks, consts, workspace, workspace_bytes,
+                                   static_cast<hipStream_t>(stream));
 }
 
 int vh_srnl_spatial_scan(const void* x, int32_t io_dtype, const float* M_m, const float* M_v, const float* M_k,

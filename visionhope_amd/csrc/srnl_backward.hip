@@ -527,8 +527,12 @@ int vh_srnl_backward(const void* x, const void* q, int32_t io_dtype, int32_t q_r
     VH_REQUIRE(x && q && dy && M_m && M_v && M_k && M_eta && M_alpha && dx && dq && dM_m && dM_v && dM_k &&
                    dM_eta && dM_alpha && chunks && consts,
                VH_ERR_ARG, "SRNL backward pointers must not be null");
-    VH_REQUIRE(B > 0 && R > 0 && R <= 4 && heads > 0 && N > 0, VH_ERR_SHAPE,
-               "SRNL backward needs nonempty [B, R <= 4, heads, N] lines");
+    VH_REQUIRE(B > 0 && heads > 0 && N > 0, VH_ERR_SHAPE, "SRNL backward needs nonempty [B, R, heads, N] lines");
+    VH_REQUIRE(R == 1 || R == 2 || R == 4, VH_ERR_SHAPE, "directions must be 1, 2 or 4, got %lld", (long long)R);
+    {
+        const int rc = check_srnl_consts(consts);
+        if (rc) return rc;
+    }
     VH_REQUIRE(head_dim == 4 || head_dim == 8 || head_dim == 16 || head_dim == 32, VH_ERR_HEAD_DIM,
                "SRNL backward supports head_dim 4, 8, 16 and 32; got %d", head_dim);
     VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);

@@ -20,6 +20,21 @@ namespace vh {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// Range checks of the recurrence's stability constants, shared by the forward and the
+// backward entry points (the reference validates the same ranges when it reads them from
+// the environment, models/srnl_core/chunk.py:50-58).
+int check_srnl_consts(const vh_srnl_consts* k);
+
+// The fused four-direction operator of vh_srnl_spatial_forward on a given workspace
+// (srnl.hip), and its shape checks.
+int check_spatial_shape(int64_t B, int64_t H, int64_t W, int64_t C, int32_t head_dim);
+int srnl_spatial_forward_ws(const void* x, const void* q, int32_t io_dtype, const float* M_m, const float* M_v,
+                            const float* M_k, const float* M_eta, const float* M_alpha, const float* d_skip,
+                            int32_t skip_per_direction, const float* dir_weight, float* out, int64_t B, int64_t H,
+                            int64_t W, int64_t C, int32_t head_dim, const int64_t chunks[4],
+                            const vh_srnl_consts* consts, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+
 // GRN statistics from per-slab partial sums of squares (elementwise.hip).
 int launch_grn_finalize(const float* partial, float* gx, float* inv_den, int64_t B, int64_t C, int64_t nslab,
                         float eps, const float* gamma, float* scale, hipStream_t s);

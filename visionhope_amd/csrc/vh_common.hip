@@ -22,6 +22,20 @@ int check_launch(const char* what) {
     return VH_OK;
 }
 
+int check_srnl_consts(const vh_srnl_consts* k) {
+    if (k == nullptr) return set_error(VH_ERR_ARG, "SRNL constants must not be null");
+    if (!(k->min_retention >= 0.f && k->min_retention < 1.f))
+        return set_error(VH_ERR_ARG, "MIN_RETENTION must be in [0, 1), got %g", (double)k->min_retention);
+    if (!(k->injection_margin > 0.f && k->injection_margin < 1.f))
+        return set_error(VH_ERR_ARG, "INJECTION_MARGIN must be in (0, 1), got %g", (double)k->injection_margin);
+    if (!(k->step_scale > 0.f))
+        return set_error(VH_ERR_ARG, "STEP_SCALE must be positive, got %g", (double)k->step_scale);
+    // spectral_factor = 2 * SPECTRAL_MARGIN with SPECTRAL_MARGIN in (0, 1]
+    if (k->spectral_clamp && !(k->spectral_factor > 0.f && k->spectral_factor <= 2.f))
+        return set_error(VH_ERR_ARG, "SPECTRAL_MARGIN must be in (0, 1], got %g", 0.5 * (double)k->spectral_factor);
+    return VH_OK;
+}
+
 }  // namespace vh
 
 extern "C" {

@@ -1,5 +1,8 @@
-"""Enable the MI355X inference path for SRNL components and VisionHOPE models
-(mirrors ``inference/prepare.py``)."""
+"""One-time switch of a VisionHOPE model (or a bare SRNL / operator) to its inference path.
+
+Public surface of the reference's ``inference/prepare.py:12-54``: ``prepare_for_inference``
+returns the same counts and folds LayerScale into the projections it scales, in place.
+"""
 
 import torch
 
@@ -9,53 +12,67 @@ from ..models.operator import VisionHOPEOperator
 from ..models.srnl import SRNL
 from ..utils.grn import GlobalResponseNorm
 
+_COUNT_KEYS = ("line_mixer", "srnl", "operator", "layernorm2d", "grn", "layerscale")
+
+
+def _enable(module):
+    """Switch one module to its inference path; the count key it belongs to, if any."""
+    if isinstance(module, SRNL):
+        module.fast_inference = True
+        return "srnl"
+    if isinstance(module, VisionHOPEOperator):
+        return "operator"
+    if isinstance(module, LayerNorm2d):
+        module.inference_layout = True
+        return "layernorm2d"
+    if isinstance(module, GlobalResponseNorm):
+        return "grn"
+    if isinstance(module, (PatchEmbedding, Downsample)):
+        # Eval BatchNorm folded into the convolution on the GPU path (a cached copy beside
+        # the module; the parameters are unchanged).
+        module._vh_fold_bn = True
+    if hasattr(module, "head_pre_logits") and hasattr(module, "head_norm"):
+        # The classifier head: its BatchNorm likewise, LayerNorm and SiLU fused around the
+        # 1x1 projection.
+        module._vh_fold_head = True
+    return None
+
+
+def _fold_layer_scale(block):
+    """Multiply each LayerScale into the output channels of the projection it scales
+    (``proj_out`` for ``gamma1``, ``ffn.fc2`` for ``gamma2``) and drop it.  Returns the
+    number folded."""
+    folded = 0
+    for name, projection in (("gamma1", block.proj_out), ("gamma2", block.ffn.fc2)):
+        gamma = getattr(block, name)
+        if gamma is None:
+            continue
+        scale = gamma.detach().reshape(-1).to(device=projection.weight.device, dtype=projection.weight.dtype)
+        projection.weight.mul_(scale.reshape((-1,) + (1,) * (projection.weight.dim() - 1)))
+        if projection.bias is not None:
+            projection.bias.mul_(scale)
+        setattr(block, name, None)
+        folded += 1
+    return folded
+
 
 def prepare_for_inference(model):
-    """Set evaluation mode and enable fast inference (``inference/prepare.py:12-54``).
-
-    Blocks fold LayerScale into projection weights in place; use an eval-only copy.
-    Returns preparation counts by component; ``line_mixer`` counts prepared blocks.
-    """
-    blocks = [module for module in model.modules() if isinstance(module, VisionHOPEBlock)]
-    for block in blocks:
-        if type(block.operator) is not VisionHOPEOperator or type(block.operator.srnl) is not SRNL:
-            raise ValueError("Production fusion requires the unmodified VisionHOPE operator and SRNL")
+    """Evaluation mode, fast inference everywhere, LayerScale folded into the blocks'
+    projection weights in place (prepare an eval-only copy).  Returns counts per
+    component; ``line_mixer`` counts the prepared blocks."""
+    blocks = [m for m in model.modules() if isinstance(m, VisionHOPEBlock)]
+    if any(type(b.operator) is not VisionHOPEOperator or type(b.operator.srnl) is not SRNL for b in blocks):
+        raise ValueError("Production fusion requires the unmodified VisionHOPE operator and SRNL")
     model.eval()
-    counts = dict(line_mixer=0, srnl=0, operator=0, layernorm2d=0, grn=0, layerscale=0)
+    counts = dict.fromkeys(_COUNT_KEYS, 0)
     for module in model.modules():
-        if isinstance(module, SRNL):
-            module.fast_inference = True
-            counts["srnl"] += 1
-        elif isinstance(module, VisionHOPEOperator):
-            counts["operator"] += 1
-        elif isinstance(module, LayerNorm2d):
-            module.inference_layout = True
-            counts["layernorm2d"] += 1
-        elif isinstance(module, GlobalResponseNorm):
-            counts["grn"] += 1
-        elif isinstance(module, (PatchEmbedding, Downsample)):
-            # Eval-mode BatchNorm folded into the convolution on the GPU path (no
-            # parameter changes: the folded copy is cached beside the module).
-            module._vh_fold_bn = True
-        if hasattr(module, "head_pre_logits") and hasattr(module, "head_norm"):
-            # The classifier head's BatchNorm likewise, with the LayerNorm and SiLU fused
-            # around the 1x1 projection.
-            module._vh_fold_head = True
+        key = _enable(module)
+        if key is not None:
+            counts[key] += 1
     with torch.no_grad():
         for block in blocks:
+            counts["layerscale"] += _fold_layer_scale(block)
             counts["line_mixer"] += 1
-            for gamma_name, projection in (("gamma1", block.proj_out), ("gamma2", block.ffn.fc2)):
-                gamma = getattr(block, gamma_name)
-                if gamma is None:
-                    continue
-                scale = gamma.detach().view(-1).to(dtype=projection.weight.dtype,
-                                                   device=projection.weight.device)
-                shape = (-1,) + (1,) * (projection.weight.ndim - 1)
-                projection.weight.mul_(scale.view(shape))
-                if projection.bias is not None:
-                    projection.bias.mul_(scale)
-                setattr(block, gamma_name, None)
-                counts["layerscale"] += 1
             block._inference_prepared = True
     if blocks:
         model._inference_prepared = True

@@ -1,4 +1,6 @@
-"""A reusable VisionHOPE block with its two residual branches (mirrors ``models/block.py``)."""
+"""The VisionHOPE block: its module tree (the checkpoint key format of the reference's
+``models/block.py``), its reference-order forward, and the fused inference forward that
+prepared models run on the GPU."""
 
 import torch
 from torch import nn
@@ -62,10 +64,24 @@ def _is_exact_gelu(act):
     return type(act) is nn.GELU and act.approximate == "none"
 
 
-class VisionHOPEBlock(nn.Module):
-    """VisionHOPE block accepting and returning NCHW features (``models/block.py:13-107``).
+# Depthwise kernel of the local mixing for each local_mode.
+_LOCAL_KERNELS = {"gated_dwconv7": 7, "residual_dwconv": 3, "silu_dwconv": 3}
 
-    ``mixer_dim`` sets the operator width and defaults to ``dim``.
+
+def _depthwise(channels, kernel):
+    return nn.Conv2d(channels, channels, kernel, padding=kernel // 2, groups=channels)
+
+
+class VisionHOPEBlock(nn.Module):
+    """Pre-norm VisionHOPE block on NCHW maps (reference ``models/block.py:13-107``):
+
+        x = x + cpe(x)                                   (optional 3x3 depthwise)
+        x = x + drop_path(gamma1 * spatial(norm1(x)))
+        x = x + drop_path(gamma2 * ffn(norm2(x)))
+
+    where ``spatial(h) = proj_out(operator(l) + lepe(l))`` with ``l`` the local mixing of
+    ``proj_in(h)`` (``local_mode``) and ``lepe`` an optional 5x5 depthwise position
+    encoding.  The operator runs on ``mixer_dim`` channels (default ``dim``).
     """
 
     def __init__(self, dim, head_dim=16, chunk_size=None, mlp_ratio=4.0,
@@ -75,43 +91,36 @@ class VisionHOPEBlock(nn.Module):
                  direction_merge="sum", use_block_cpe=True, use_output_lepe=True,
                  share_direction_skip=True):
         super().__init__()
-        mixer_dim = int(mixer_dim) if mixer_dim is not None else dim
-        if local_mode not in {"gated_dwconv7", "residual_dwconv", "silu_dwconv"}:
+        if local_mode not in _LOCAL_KERNELS:
             raise ValueError("Unsupported local_mode")
-        self.dim = dim
-        self.mixer_dim = mixer_dim
-        self.local_mode = local_mode
+        mixer_dim = dim if mixer_dim is None else int(mixer_dim)
+        self.dim, self.mixer_dim, self.local_mode = dim, mixer_dim, local_mode
         self._inference_prepared = False
-        self.cpe = nn.Conv2d(dim, dim, 3, padding=1, groups=dim) if use_block_cpe else None
+        self.cpe = _depthwise(dim, 3) if use_block_cpe else None
         self.norm1 = build_norm(dim, norm_layer)
 
+        # spatial branch; a learned per-direction scale replaces the plain sum
         self.proj_in = nn.Conv2d(dim, mixer_dim, 1)
-        if use_direction_scale and direction_merge == "sum":
-            direction_merge = "scale"
-        self.operator = VisionHOPEOperator(mixer_dim, head_dim, chunk_size, direction_merge,
-                                           share_direction_skip, _initialize=False)
-        local_kernel = 7 if local_mode == "gated_dwconv7" else 3
-        self.local_conv = nn.Conv2d(mixer_dim, mixer_dim, local_kernel,
-                                    padding=local_kernel // 2, groups=mixer_dim)
+        merge = "scale" if use_direction_scale and direction_merge == "sum" else direction_merge
+        self.operator = VisionHOPEOperator(mixer_dim, head_dim, chunk_size, merge, share_direction_skip,
+                                           _initialize=False)
+        self.local_conv = _depthwise(mixer_dim, _LOCAL_KERNELS[local_mode])
         self.local_gate = nn.Conv2d(mixer_dim, mixer_dim, 1) if local_mode == "gated_dwconv7" else None
         self.local_act = nn.SiLU() if local_mode == "silu_dwconv" else nn.Identity()
-        self.local_position = (nn.Conv2d(mixer_dim, mixer_dim, 5, padding=2, groups=mixer_dim)
-                               if use_output_lepe else None)
+        self.local_position = _depthwise(mixer_dim, 5) if use_output_lepe else None
         self.proj_out = nn.Linear(mixer_dim, dim)
         self.operator.reset_parameters()
         trunc_normal_(self.proj_out.weight, std=0.02)
         nn.init.zeros_(self.proj_out.bias)
 
+        # feed-forward branch
         self.drop_path = DropPath(drop_path) if drop_path > 0.0 else nn.Identity()
         self.norm2 = build_norm(dim, norm_layer)
-        self.ffn = FeedForwardNetwork(dim, int(dim * mlp_ratio), use_grn=use_grn,
-                                      use_dwconv=use_mlp_dwconv)
-        if layer_scale_init_value is not None and layer_scale_init_value > 0.0:
-            self.gamma1 = nn.Parameter(layer_scale_init_value * torch.ones(dim, 1, 1))
-            self.gamma2 = nn.Parameter(layer_scale_init_value * torch.ones(dim, 1, 1))
-        else:
-            self.gamma1 = None
-            self.gamma2 = None
+        self.ffn = FeedForwardNetwork(dim, int(dim * mlp_ratio), use_grn=use_grn, use_dwconv=use_mlp_dwconv)
+        scaled = layer_scale_init_value is not None and layer_scale_init_value > 0.0
+        for name in ("gamma1", "gamma2"):
+            value = nn.Parameter(torch.full((dim, 1, 1), float(layer_scale_init_value))) if scaled else None
+            setattr(self, name, value)
 
     def _fused_eligible(self, x):
         """Whether ``forward`` may take the fused inference path for ``x``.
@@ -247,10 +256,7 @@ class VisionHOPEBlock(nn.Module):
         skip_shape = (op.num_heads, op.head_dim) if op.share_direction_skip else (4, op.num_heads, op.head_dim)
         if op.d_skip.shape != skip_shape or op.d_skip.device != dev:
             raise ValueError("Directional skip has an invalid shape or device")
-        if op.direction_merge == "softmax":
-            weights = 4.0 * torch.softmax(op.direction_logits.detach().float(), dim=0)
-        else:
-            weights = op.direction_weights().detach().float()
+        weights = op._merge_weights()
         batch, channels, height, width = x_local.shape
         chunks = (width, width, height, height)
         x_nhwc = x_local.permute(0, 2, 3, 1)
@@ -275,11 +281,13 @@ class VisionHOPEBlock(nn.Module):
                                     out_dtype=x_local.dtype)
 
     def _local_features(self, x):
-        x_inner = self.proj_in(x)
+        """``proj_in`` followed by the local mixing of ``local_mode``."""
+        inner = self.proj_in(x)
+        conv = self.local_conv(inner)
         if self.local_mode == "gated_dwconv7":
-            return x_inner + torch.sigmoid(self.local_gate(x_inner)) * self.local_conv(x_inner)
-        x_conv = self.local_act(self.local_conv(x_inner))
-        return x_conv if self.local_mode == "silu_dwconv" else x_inner + x_conv
+            return inner + torch.sigmoid(self.local_gate(inner)) * conv
+        conv = self.local_act(conv)
+        return conv if self.local_mode == "silu_dwconv" else inner + conv
 
     def spatial_branch(self, x):
         channels_last = x.is_contiguous(memory_format=torch.channels_last)
@@ -321,7 +329,5 @@ class VisionHOPEBlock(nn.Module):
             return self._fused_forward(x)
         if self.cpe is not None:
             x = x + self.cpe(x)
-        branch = self.spatial_branch(self.norm1(x))
-        x = self._residual_add(x, branch, self.gamma1)
-        branch = self.ffn(self.norm2(x))
-        return self._residual_add(x, branch, self.gamma2)
+        x = self._residual_add(x, self.spatial_branch(self.norm1(x)), self.gamma1)
+        return self._residual_add(x, self.ffn(self.norm2(x)), self.gamma2)

@@ -1,7 +1,8 @@
-"""VisionHOPE Tiny, Small and Base configurations (mirrors ``models/factory.py``).
+"""The named VisionHOPE classifiers and their constructor (reference ``models/factory.py``).
 
-timm is not a dependency: ``register_model`` becomes a local registry and the
-ImageNet normalisation constants are spelled out.
+``MODEL_CONFIGS`` holds the reference's published widths and depths.  timm is not a
+dependency here: the model registry is a local dict and the ImageNet normalisation
+constants are written out.
 """
 
 from copy import deepcopy
@@ -28,27 +29,33 @@ def register_model(fn):
     return fn
 
 
+# Arguments of timm's model factory that VisionHOPE accepts only at their neutral value.
+_NEUTRAL_TIMM_ARGS = {"drop_rate": 0.0, "drop_connect_rate": None, "drop_block_rate": None,
+                      "global_pool": "avg", "bn_momentum": None, "bn_eps": None, "scriptable": False,
+                      "pretrained_cfg": None, "pretrained_cfg_overlay": None}
+
+
+def _default_cfg():
+    """The timm-style data configuration a classifier built here advertises."""
+    return {"url": "", "num_classes": 1000, "input_size": (3, 224, 224), "pool_size": None,
+            "crop_pct": 1.0, "interpolation": "bicubic", "mean": IMAGENET_DEFAULT_MEAN,
+            "std": IMAGENET_DEFAULT_STD, "classifier": "head"}
+
+
 def create_model(name, pretrained=False, checkpoint_path=None, **kwargs):
-    """Create a VisionHOPE model and optionally load a checkpoint (``factory.py:19-43``)."""
+    """Build a registered VisionHOPE model; with ``checkpoint_path``, load its native-name
+    weights (reference ``factory.py:19-43``).  ``pretrained`` needs a checkpoint path (no
+    download exists)."""
     if name not in MODEL_CONFIGS:
         raise ValueError(f"Unknown model {name!r}; choose from {tuple(MODEL_CONFIGS)}")
     if pretrained and not checkpoint_path:
         raise ValueError("Provide checkpoint_path for pretrained weights")
-    defaults = {"drop_rate": 0.0, "drop_connect_rate": None, "drop_block_rate": None,
-                "global_pool": "avg", "bn_momentum": None, "bn_eps": None,
-                "scriptable": False, "pretrained_cfg": None, "pretrained_cfg_overlay": None}
-    for key, default in defaults.items():
-        if key in kwargs:
-            value = kwargs.pop(key)
-            if value is not None and value != default:
-                raise ValueError(f"Unsupported {key}={value!r}")
-    config = deepcopy(MODEL_CONFIGS[name])
-    config.update(kwargs)
-    model = HierarchicalVisionHOPE(**config)
-    model.default_cfg = dict(url="", num_classes=1000, input_size=(3, 224, 224),
-                             pool_size=None, crop_pct=1.0, interpolation="bicubic",
-                             mean=IMAGENET_DEFAULT_MEAN, std=IMAGENET_DEFAULT_STD,
-                             classifier="head")
+    for key in [k for k in kwargs if k in _NEUTRAL_TIMM_ARGS]:
+        value = kwargs.pop(key)
+        if value is not None and value != _NEUTRAL_TIMM_ARGS[key]:
+            raise ValueError(f"Unsupported {key}={value!r}")
+    model = HierarchicalVisionHOPE(**{**deepcopy(MODEL_CONFIGS[name]), **kwargs})
+    model.default_cfg = _default_cfg()
     if checkpoint_path:
         from ..tools.checkpoint import load_checkpoint
         load_checkpoint(model, checkpoint_path)

@@ -1,4 +1,10 @@
-"""The four-stage hierarchical VisionHOPE family (mirrors ``models/hierarchical.py``)."""
+"""The four-stage hierarchical VisionHOPE backbone and classifier.
+
+Architecture and module names of the reference's ``models/hierarchical.py:11-85`` (the
+module tree is the checkpoint key format): a patch-embedding stem, three 2x downsamples,
+four stages of ``VisionHOPEBlock``, and a projection head (norm, 1x1 conv, BatchNorm,
+SiLU, average pool, linear).  ``_fused_head`` is this build's prepared-inference head.
+"""
 
 import torch
 from torch import nn
@@ -8,11 +14,21 @@ from .common import ClassificationModel, initialize_weights
 from .layers import Downsample, LayerNorm2d, PatchEmbedding, build_norm
 
 
-class HierarchicalVisionHOPE(ClassificationModel):
-    """Hierarchical VisionHOPE with a projection classifier head.
+def _four(values):
+    values = list(values)
+    if len(values) != 4:
+        raise ValueError("Hierarchical VisionHOPE requires four stage configurations")
+    return values
 
-    ``chunk_sizes=None`` uses row/column lengths at runtime, including rectangular
-    inputs.  Explicit four-element ``chunk_sizes`` select fixed chunks per stage.
+
+class HierarchicalVisionHOPE(ClassificationModel):
+    """VisionHOPE backbone with a projection classifier head.
+
+    Stage i runs ``depths[i]`` blocks of width ``embed_dims[i]`` whose operator mixes
+    ``mixer_dims[i]`` channels in heads of ``head_dim``.  ``chunk_sizes=None`` scans in
+    chunks of the row and column lengths of whatever map arrives (rectangular maps
+    included); four explicit values fix each stage's chunk length.  Stochastic depth
+    rises linearly from 0 to ``drop_path_rate`` over all blocks.
     """
 
     def __init__(self, in_chans=3, num_classes=1000, embed_dims=(64, 128, 256, 512),
@@ -23,43 +39,40 @@ class HierarchicalVisionHOPE(ClassificationModel):
                  use_direction_scale=True, direction_merge="sum", use_block_cpe=True,
                  use_output_lepe=True, projection_dim=1024, share_direction_skip=True):
         super().__init__()
+        if isinstance(mlp_ratios, (int, float)):
+            mlp_ratios = (float(mlp_ratios),) * 4
         self.num_classes = num_classes
-        self.embed_dims = list(embed_dims)
-        self.mixer_dims = list(mixer_dims) if mixer_dims is not None else list(embed_dims)
-        self.depths = list(depths)
-        self.chunk_sizes = [None] * 4 if chunk_sizes is None else list(chunk_sizes)
+        self.embed_dims = _four(embed_dims)
+        self.mixer_dims = _four(embed_dims if mixer_dims is None else mixer_dims)
+        self.depths = _four(depths)
+        self.chunk_sizes = _four((None,) * 4 if chunk_sizes is None else chunk_sizes)
+        mlp_ratios = _four(mlp_ratios)
+        if min(self.depths) < 1 or min(self.embed_dims) < 1:
+            raise ValueError("Stage depths and widths must be positive")
         self.head_dim = int(head_dim)
         self.img_size = img_size
         self.share_direction_skip = share_direction_skip
-        if isinstance(mlp_ratios, (int, float)):
-            mlp_ratios = [float(mlp_ratios)] * 4
-        if any(len(items) != 4 for items in (self.embed_dims, self.mixer_dims, self.depths,
-                                            self.chunk_sizes, mlp_ratios)):
-            raise ValueError("Hierarchical VisionHOPE requires four stage configurations")
-        if min(self.depths) < 1 or min(self.embed_dims) < 1:
-            raise ValueError("Stage depths and widths must be positive")
 
-        self.downsample_layers = nn.ModuleList([PatchEmbedding(in_chans, embed_dims[0])])
-        for i in range(3):
-            self.downsample_layers.append(Downsample(embed_dims[i], embed_dims[i + 1]))
-        rates = [value.item() for value in torch.linspace(0, drop_path_rate, sum(depths))]
+        widths = self.embed_dims
+        self.downsample_layers = nn.ModuleList(
+            [PatchEmbedding(in_chans, widths[0])] + [Downsample(widths[i - 1], widths[i]) for i in range(1, 4)])
+        drop_rates = torch.linspace(0, drop_path_rate, sum(self.depths)).tolist()
+        block_options = dict(head_dim=head_dim, local_mode=local_mode, norm_layer=norm_layer,
+                             layer_scale_init_value=layer_scale_init_value, use_grn=use_grn,
+                             use_mlp_dwconv=use_mlp_dwconv, use_direction_scale=use_direction_scale,
+                             direction_merge=direction_merge, use_block_cpe=use_block_cpe,
+                             use_output_lepe=use_output_lepe, share_direction_skip=share_direction_skip)
         self.stages = nn.ModuleList()
-        offset = 0
-        for i in range(4):
-            self.stages.append(nn.Sequential(*[
-                VisionHOPEBlock(
-                    dim=embed_dims[i], head_dim=head_dim, chunk_size=self.chunk_sizes[i],
-                    mlp_ratio=mlp_ratios[i], drop_path=rates[offset + j],
-                    mixer_dim=self.mixer_dims[i], local_mode=local_mode, norm_layer=norm_layer,
-                    layer_scale_init_value=layer_scale_init_value, use_grn=use_grn,
-                    use_mlp_dwconv=use_mlp_dwconv, use_direction_scale=use_direction_scale,
-                    direction_merge=direction_merge, use_block_cpe=use_block_cpe,
-                    use_output_lepe=use_output_lepe, share_direction_skip=share_direction_skip,
-                ) for j in range(depths[i])
-            ]))
-            offset += depths[i]
-        self.norm = build_norm(embed_dims[-1], norm_layer)
-        self.head_pre_logits = nn.Conv2d(embed_dims[-1], projection_dim, 1)
+        first = 0
+        for width, mixer, depth, chunk, ratio in zip(widths, self.mixer_dims, self.depths, self.chunk_sizes,
+                                                     mlp_ratios):
+            self.stages.append(nn.Sequential(*(
+                VisionHOPEBlock(dim=width, chunk_size=chunk, mlp_ratio=ratio, drop_path=drop_rates[first + j],
+                                mixer_dim=mixer, **block_options)
+                for j in range(depth))))
+            first += depth
+        self.norm = build_norm(widths[-1], norm_layer)
+        self.head_pre_logits = nn.Conv2d(widths[-1], projection_dim, 1)
         self.head_norm = nn.BatchNorm2d(projection_dim)
         self.head_act = nn.SiLU()
         self.num_features = int(projection_dim)
@@ -67,24 +80,23 @@ class HierarchicalVisionHOPE(ClassificationModel):
         self.grad_checkpointing = False
         self.apply(initialize_weights)
 
-    def forward_intermediates(self, x):
-        """Return the four stage features for detection and segmentation heads."""
-        outputs = []
+    def _stage_outputs(self, x):
         for downsample, stage in zip(self.downsample_layers, self.stages):
             x = self._run_blocks(stage, downsample(x))
-            outputs.append(x)
-        return tuple(outputs)
+            yield x
+
+    def forward_intermediates(self, x):
+        """The four stage feature maps (inputs of detection and segmentation heads)."""
+        return tuple(self._stage_outputs(x))
 
     def forward_features(self, x):
-        for downsample, stage in zip(self.downsample_layers, self.stages):
-            x = self._run_blocks(stage, downsample(x))
+        """Pooled pre-logits ``[B, projection_dim]``."""
+        for x in self._stage_outputs(x):
+            pass
         if self._fused_head_ok(x):
             return self._fused_head(x)
-        x = self.norm(x)
-        x = self.head_pre_logits(x)
-        x = self.head_norm(x)
-        x = self.head_act(x)
-        return x.mean(dim=[2, 3])
+        h = self.head_act(self.head_norm(self.head_pre_logits(self.norm(x))))
+        return h.mean(dim=(2, 3))
 
     def _fused_head_ok(self, x):
         """Prepared for inference, eval mode, bf16 autocast on a channels-last CUDA map,

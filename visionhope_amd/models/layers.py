@@ -1,4 +1,5 @@
-"""Normalization, feed-forward, embedding and downsampling layers (mirrors ``models/layers.py``)."""
+"""Layers of the VisionHOPE backbone around the blocks: channel LayerNorm, the MLP, the
+convolutional stem and the stage downsample (reference ``models/layers.py``)."""
 
 import torch
 from torch import nn
@@ -62,54 +63,62 @@ def build_norm(dim, norm_layer="group"):
 
 
 class FeedForwardNetwork(nn.Module):
-    """fc1 -> GELU -> (x + dwconv3(x)) -> GELU -> GRN -> fc2 (``layers.py:38-82``)."""
+    """Pointwise MLP on NCHW maps (reference ``models/layers.py:38-82``):
+
+        h = act(fc1(x));  h = act(h + dwconv3x3(h)) if use_dwconv;  h = grn(h) if use_grn
+        y = fc2(dropout(h)), then dropout
+
+    with 1x1 convolutions for fc1 / fc2 and a depthwise 3x3 ``dwconv``.
+    """
 
     def __init__(self, in_features, hidden_features=None, out_features=None, act_layer=nn.GELU,
                  drop=0.0, use_grn=False, use_dwconv=False):
         super().__init__()
-        hidden_features = hidden_features or in_features
-        out_features = out_features or in_features
-        self.fc1 = nn.Conv2d(in_features, hidden_features, kernel_size=1)
+        hidden = hidden_features or in_features
+        self.fc1 = nn.Conv2d(in_features, hidden, kernel_size=1)
         self.act = act_layer()
         self.use_dwconv = use_dwconv
-        self.dwconv = (
-            nn.Conv2d(hidden_features, hidden_features, kernel_size=3, padding=1, groups=hidden_features)
-            if use_dwconv else nn.Identity())
-        self.dwconv_act = act_layer() if use_dwconv else nn.Identity()
-        self.grn = GlobalResponseNorm(hidden_features) if use_grn else nn.Identity()
-        self.fc2 = nn.Conv2d(hidden_features, out_features, kernel_size=1)
+        if use_dwconv:
+            self.dwconv = nn.Conv2d(hidden, hidden, kernel_size=3, padding=1, groups=hidden)
+            self.dwconv_act = act_layer()
+        else:
+            self.dwconv = nn.Identity()
+            self.dwconv_act = nn.Identity()
+        self.grn = GlobalResponseNorm(hidden) if use_grn else nn.Identity()
+        self.fc2 = nn.Conv2d(hidden, out_features or in_features, kernel_size=1)
         self.drop = nn.Dropout(drop)
 
     def forward(self, x):
-        x = self.fc1(x)
-        x = self.act(x)
+        h = self.act(self.fc1(x))
         if self.use_dwconv:
-            x = self.dwconv_act(x + self.dwconv(x))
-        x = self.grn(x)
-        x = self.drop(x)
-        x = self.fc2(x)
-        x = self.drop(x)
-        return x
+            h = self.dwconv_act(h + self.dwconv(h))
+        return self.drop(self.fc2(self.drop(self.grn(h))))
+
+
+# Stem stages: (fraction of embed_dim as width divisor, stride, GELU after the BatchNorm).
+_STEM = ((2, 2, True), (2, 1, True), (1, 2, True), (1, 1, False))
 
 
 class PatchEmbedding(nn.Module):
-    """Stride-four convolutional stem (``layers.py:85-107``)."""
+    """Stride-4 convolutional stem (reference ``models/layers.py:85-107``): four 3x3
+    convolutions of widths embed_dim/2, embed_dim/2, embed_dim, embed_dim and strides 2,
+    1, 2, 1, each followed by BatchNorm and, except the last, GELU (``proj``, a
+    Sequential whose indices are the checkpoint keys)."""
 
     def __init__(self, in_chans, embed_dim, patch_size=4):
         super().__init__()
         if patch_size != 4:
             raise ValueError("The VisionHOPE stem requires patch_size=4")
-        widths = [embed_dim // 2, embed_dim // 2, embed_dim, embed_dim]
-        strides = [2, 1, 2, 1]
-        if min(widths) <= 0:
+        if embed_dim // 2 <= 0:
             raise ValueError("embed_dim is too small for the convolutional stem")
-        layers = []
-        for i, (width, stride) in enumerate(zip(widths, strides)):
-            layers.extend([nn.Conv2d(in_chans, width, 3, stride=stride, padding=1), nn.BatchNorm2d(width)])
-            if i < 3:
-                layers.append(nn.GELU())
-            in_chans = width
-        self.proj = nn.Sequential(*layers)
+        modules, channels = [], in_chans
+        for divisor, stride, gelu in _STEM:
+            width = embed_dim // divisor
+            modules += [nn.Conv2d(channels, width, 3, stride=stride, padding=1), nn.BatchNorm2d(width)]
+            if gelu:
+                modules.append(nn.GELU())
+            channels = width
+        self.proj = nn.Sequential(*modules)
         self.norm = nn.Identity()
 
     def forward(self, x):
@@ -159,7 +168,8 @@ class PatchEmbedding(nn.Module):
 
 
 class Downsample(nn.Module):
-    """Overlapping stride-two convolution followed by batch normalization (``layers.py:110-119``)."""
+    """Stage transition (reference ``models/layers.py:110-119``): a 3x3, stride-2 convolution
+    without bias, then BatchNorm."""
 
     def __init__(self, in_dim, out_dim):
         super().__init__()

@@ -12,9 +12,10 @@ import os
 import torch
 
 from ...utils import hip
+from ...utils.autograd import backward_unavailable
 from ...utils.cuda import on_tensor_device
 
-MAX_CHUNK = 64
+MAX_CHUNK = 64            # the reference's short-chunk kernel limit (chunk.py:31); the default standalone chunk
 BACKWARD_MAX_CHUNK = 256   # the backward kernel's longest chunk (the long-line range)
 SUPPORTED_HEAD_DIMS = (4, 8, 16, 32, 64)
 
@@ -138,77 +139,47 @@ def srnl_packed_backward(memories, x, q, chunk_sizes, dy, *, q_raw):
     return (*grads, dx.to(x.dtype), dq.to(q.dtype))
 
 
-class SRNLNormalizedQueryFunction(torch.autograd.Function):
-    """Forward of ``chunk.py:168-284``: normalised FP32 queries, chunks of at most 64."""
+class SRNLScanFunction(torch.autograd.Function):
+    """The packed recurrence with autograd, for every path that needs gradients.
+
+    One native forward (``srnl_packed_forward``) and one native backward
+    (``srnl_packed_backward``) cover what the reference splits over its short-chunk,
+    long-chunk and variable-line kernels (``chunk.py:168-588``, ``lines.py:183-671``):
+    the scan takes one chunk length per direction, any length in the forward and up to
+    ``BACKWARD_MAX_CHUNK`` in the backward.  ``q_raw``: queries are the unnormalised
+    ``[B, R, N, C]`` projections in x's dtype; otherwise unit FP32 ``[B, R, heads, N, d]``.
+    """
 
     @staticmethod
-    def forward(ctx, M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0, x, q, chunk_size):
+    def forward(ctx, M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0, x, q, chunks, q_raw):
         if torch.jit.is_tracing():
             raise RuntimeError("SRNL TorchScript tracing is unsupported; use eager or CUDA Graph inference.")
-        if not x.is_cuda:
-            raise RuntimeError("SRNL CUDA kernel requires CUDA tensors.")
-        if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-            raise RuntimeError(f"SRNL CUDA kernel supports fp16/bf16/fp32 x, got {x.dtype}.")
-        if q.dtype != torch.float32:
-            raise RuntimeError(f"SRNL normalized q path expects fp32 q, got {q.dtype}.")
-        head_dim = x.shape[-1]
-        if head_dim not in SUPPORTED_HEAD_DIMS:
-            raise AssertionError(
-                f"SRNL CUDA kernel requires head_dim in {SUPPORTED_HEAD_DIMS}, got {head_dim}.")
-        if chunk_size > MAX_CHUNK:
-            raise ValueError(f"chunk_size={chunk_size} exceeds MAX_CHUNK={MAX_CHUNK} in CUDA kernel")
         memories = (M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0)
-        chunks = [int(chunk_size)] * x.shape[1]
         ctx.save_for_backward(*memories, x, q)
-        ctx.chunks = chunks
-        return srnl_packed_forward(memories, x, q, chunks, q_raw=False)
+        ctx.chunks, ctx.q_raw = list(chunks), bool(q_raw)
+        return srnl_packed_forward(memories, x, q, ctx.chunks, q_raw=ctx.q_raw)
 
     @staticmethod
     def backward(ctx, dY):
-        """Reference ``chunk.py:289-359``: gradients of the memories, x and q."""
+        if max(ctx.chunks) > BACKWARD_MAX_CHUNK:
+            backward_unavailable(f"SRNL scan with a chunk of {max(ctx.chunks)} tokens")
         *memories, x, q = ctx.saved_tensors
-        grads = srnl_packed_backward(memories, x, q, ctx.chunks, dY, q_raw=False)
-        return (*grads, None)
+        grads = srnl_packed_backward(memories, x, q, ctx.chunks, dY, q_raw=ctx.q_raw)
+        return (*grads, None, None)
 
 
-class SRNLRawQueryFunction(torch.autograd.Function):
-    """Forward of ``chunk.py:362-505``: four directions, raw queries, chunks of at most 64."""
+def srnl_scan(memories, x, q, chunks, *, q_raw):
+    """Differentiable packed SRNL: y ``[B, R, heads, N, d]`` in x's dtype."""
+    return SRNLScanFunction.apply(*memories, x, q, tuple(int(c) for c in chunks), bool(q_raw))
 
-    @staticmethod
-    def forward(ctx, M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0, x, q_raw, chunk_size, num_heads, head_dim):
-        if torch.jit.is_tracing():
-            raise RuntimeError("SRNL TorchScript tracing is unsupported; use eager or CUDA Graph inference.")
-        if not x.is_cuda:
-            raise RuntimeError("SRNL qraw CUDA kernel requires CUDA tensors.")
-        if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-            raise RuntimeError(f"SRNL qraw CUDA kernel supports fp16/bf16/fp32 x, got {x.dtype}.")
-        if q_raw.dtype != x.dtype:
-            raise RuntimeError(
-                f"SRNL qraw CUDA kernel expects q_raw dtype to match x dtype, got {q_raw.dtype} vs {x.dtype}.")
-        batch, directions, x_num_heads, seq_len, x_head_dim = x.shape
-        num_heads, head_dim = int(num_heads), int(head_dim)
-        if directions != 4 or x_num_heads != num_heads or x_head_dim != head_dim:
-            raise AssertionError("Invalid x shape for SRNL qraw kernel.")
-        if q_raw.dim() != 4 or q_raw.shape[0] != batch or q_raw.shape[1] != 4 or q_raw.shape[2] != seq_len:
-            raise AssertionError("Invalid q_raw shape for SRNL qraw kernel.")
-        if q_raw.shape[3] != num_heads * head_dim:
-            raise AssertionError("q_raw channel count does not match num_heads * head_dim.")
-        if head_dim not in SUPPORTED_HEAD_DIMS:
-            raise AssertionError(
-                f"SRNL CUDA kernel requires head_dim in {SUPPORTED_HEAD_DIMS}, got {head_dim}.")
-        if chunk_size > MAX_CHUNK:
-            raise ValueError(f"chunk_size={chunk_size} exceeds MAX_CHUNK={MAX_CHUNK} in CUDA kernel")
-        memories = (M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0)
-        ctx.save_for_backward(*memories, x, q_raw)
-        ctx.chunks = [int(chunk_size)] * 4
-        return srnl_packed_forward(memories, x, q_raw, ctx.chunks, q_raw=True)
 
-    @staticmethod
-    def backward(ctx, dY):
-        """Reference ``chunk.py:510-588``: gradients of the memories, x and the raw queries."""
-        *memories, x, q_raw = ctx.saved_tensors
-        grads = srnl_packed_backward(memories, x, q_raw, ctx.chunks, dY, q_raw=True)
-        return (*grads, None, None, None)
+def _check_kernel_inputs(x, head_dim, what):
+    if not x.is_cuda:
+        raise RuntimeError(f"{what} requires CUDA tensors.")
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise RuntimeError(f"{what} supports fp16/bf16/fp32 x, got {x.dtype}.")
+    if head_dim not in SUPPORTED_HEAD_DIMS:
+        raise AssertionError(f"SRNL CUDA kernel requires head_dim in {SUPPORTED_HEAD_DIMS}, got {head_dim}.")
 
 
 def can_fuse_raw_query(x, q_raw, num_heads, head_dim):
@@ -233,13 +204,23 @@ def can_fuse_raw_query(x, q_raw, num_heads, head_dim):
 
 
 def srnl_raw_query(M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0, x, q_raw, chunk_size, num_heads, head_dim):
-    return SRNLRawQueryFunction.apply(
-        M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0, x, q_raw, chunk_size, int(num_heads), int(head_dim))
+    """Four directions with raw queries in x's dtype, one chunk length for all (reference
+    ``chunk.py:622-625``, chunks of at most 64 there; any length here)."""
+    _check_kernel_inputs(x, int(head_dim), "SRNL qraw CUDA kernel")
+    if q_raw.dtype != x.dtype:
+        raise RuntimeError(
+            f"SRNL qraw CUDA kernel expects q_raw dtype to match x dtype, got {q_raw.dtype} vs {x.dtype}.")
+    if not can_fuse_raw_query(x, q_raw, num_heads, head_dim):
+        raise AssertionError("Invalid x shape for SRNL qraw kernel.")
+    return srnl_scan((M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0), x, q_raw, [int(chunk_size)] * 4, q_raw=True)
 
 
 def srnl_normalized_query(M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0, x, q, chunk_size):
+    """Unit FP32 queries ``[B, R, heads, N, d]`` (reference ``chunk.py:628-634``)."""
     if x.dtype in (torch.float16, torch.bfloat16, torch.float32) and q.dtype == torch.float32:
-        return SRNLNormalizedQueryFunction.apply(M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0, x, q, chunk_size)
+        _check_kernel_inputs(x, int(x.shape[-1]), "SRNL CUDA kernel")
+        return srnl_scan((M_m_0, M_v_0, M_k_0, M_eta_0, M_alpha_0), x, q, [int(chunk_size)] * x.shape[1],
+                         q_raw=False)
     raise RuntimeError("The release HOPE CUDA path expects fp16/bf16/fp32 x and fp32 normalized q.")
 
 

@@ -1,20 +1,29 @@
-"""Device guard for native launches (mirrors ``utils/cuda.py:10-22`` of the reference)."""
+"""Device selection for native launches (reference ``utils/cuda.py:10-22``)."""
 
-from functools import wraps
+import functools
 
 import torch
 
 
+def _first_tensor(args, kwargs):
+    for value in args:
+        if isinstance(value, torch.Tensor):
+            return value
+    for value in kwargs.values():
+        if isinstance(value, torch.Tensor):
+            return value
+    return None
+
+
 def on_tensor_device(function):
-    """Run custom launches on the first tensor argument's device, preserving its current stream."""
-    @wraps(function)
-    def wrapped(*args, **kwargs):
-        tensor = next((value for value in (*args, *kwargs.values())
-                       if isinstance(value, torch.Tensor)), None)
-        if tensor is None or not tensor.is_cuda:
-            return function(*args, **kwargs)
-        if tensor.device.index == torch.cuda.current_device():
+    """Decorator: run ``function`` with the device of its first tensor argument current,
+    so the native calls it makes launch on that device's current stream.  CPU tensors,
+    and tensors already on the current device, run it unchanged."""
+    @functools.wraps(function)
+    def run_on_device(*args, **kwargs):
+        tensor = _first_tensor(args, kwargs)
+        if tensor is None or not tensor.is_cuda or tensor.get_device() == torch.cuda.current_device():
             return function(*args, **kwargs)
         with torch.cuda.device(tensor.device):
             return function(*args, **kwargs)
-    return wrapped
+    return run_on_device
