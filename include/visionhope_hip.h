@@ -91,6 +91,21 @@ int vh_srnl_spatial_forward(
     const int64_t chunks[4], const vh_srnl_consts* consts,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* vh_srnl_spatial_forward without a workspace argument: the chunk-start memories go to
+ * a fixed 96 MiB device array of the library (one per GPU, held from the first call on that
+ * GPU until the process ends), so the call allocates nothing.  No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc).  A call whose
+ * vh_srnl_workspace_bytes exceeds 96 MiB returns VH_ERR_WORKSPACE.  Calls that overlap on
+ * one GPU (several streams or host threads) share the array and race. */
+int vh_srnl_spatial_forward_noalloc(
+    const void* x, const void* q, int32_t io_dtype,
+    const float* M_m, const float* M_v, const float* M_k,
+    const float* M_eta, const float* M_alpha,
+    const float* d_skip, int32_t skip_per_direction, const float* dir_weight,
+    float* out, int64_t B, int64_t H, int64_t W, int64_t C, int32_t head_dim,
+    const int64_t chunks[4], const vh_srnl_consts* consts, void* stream);
+
 /* The two halves of vh_srnl_spatial_forward, for callers that overlap other work with
  * the scan (the readout needs q; the scan does not).  vh_srnl_spatial_scan writes the
  * chunk-start memories of every line into the workspace; vh_srnl_spatial_readout reads

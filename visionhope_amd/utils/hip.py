@@ -25,6 +25,7 @@ _DTYPE_CODES = {torch.float32: VH_DTYPE_F32, torch.bfloat16: VH_DTYPE_BF16, torc
 # Symbols declared in include/visionhope_hip.h (tests check the library exports all of them).
 EXPORTED_SYMBOLS = (
     "vh_abi_version", "vh_last_error", "vh_srnl_workspace_bytes", "vh_srnl_spatial_forward",
+    "vh_srnl_spatial_forward_noalloc",
     "vh_srnl_spatial_scan", "vh_srnl_spatial_readout",
     "vh_srnl_line_forward_seq_noatomic", "vh_srnl_sequence_forward", "vh_srnl_forward",
     "vh_postprocess_scale_forward", "vh_grn_workspace_bytes", "vh_grn_forward",
@@ -67,6 +68,9 @@ _SIGNATURES = {
     "vh_srnl_spatial_forward": (ctypes.c_int, [
         _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
         _i64, _i64, _i64, _i64, _i32, _I64P, _CP, _vp, _sz, _vp]),
+    "vh_srnl_spatial_forward_noalloc": (ctypes.c_int, [
+        _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
+        _i64, _i64, _i64, _i64, _i32, _I64P, _CP, _vp]),
     "vh_srnl_spatial_scan": (ctypes.c_int, [
         _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _I64P, _CP, _vp, _sz, _vp]),
     "vh_srnl_spatial_readout": (ctypes.c_int, [
