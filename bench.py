@@ -350,7 +350,7 @@ def profile_config3(device):
     import torch
 
     op, x = _config3_operator(device)
-    with torch.autocast("cuda", dtype=torch.bfloat16):
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
         for i in range(3):
             op(x)
             torch.cuda.synchronize()

@@ -45,7 +45,7 @@ def test_stage1_full_line_length(oracle, device, kind, dtype, tol):
     mems = memories(4, heads, 16, kind=kind, seed=512)
     x = randn(batch, hw, hw, channels, seed=5121).to(dtype)
     q = randn(batch, hw, hw, channels, seed=5122).to(dtype)
-    skip = randn(channels, seed=5123, scale=0.1)
+    skip = randn(channels, seed=5123, scale=0.01)   # small: the recurrence's output dominates
     wts = 1 + randn(4, channels, seed=5124, scale=0.1)
     t0 = time.time()
     got = _spatial(device, x, q, mems, skip, wts, (hw,) * 4)
@@ -65,7 +65,7 @@ def test_rectangular_chunks_above_256(oracle, device, dtype, tol):
     mems = memories(4, heads, 16, kind="perturbed", seed=320)
     x = randn(1, height, width, channels, seed=3201).to(dtype)
     q = randn(1, height, width, channels, seed=3202).to(dtype)
-    skip = randn(4 * channels, seed=3203, scale=0.1)
+    skip = randn(4 * channels, seed=3203, scale=0.01)
     wts = 1 + randn(4, channels, seed=3204, scale=0.1)
     got = _spatial(device, x, q, mems, skip, wts, (width, width, height, height))
     expected = oracle.operator_forward(x.float().numpy(), q.float().numpy(), mems, skip.numpy(), wts.numpy(), 16)

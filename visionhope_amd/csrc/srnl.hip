@@ -30,56 +30,9 @@
 #include <cstdlib>
 #include <type_traits>
 
-#include "vh_common.h"
+#include "srnl_device.h"
 
 namespace vh {
-
-struct Consts {
-    float eta_scale, alpha_min, alpha_bias, stab_mu;
-    int clamp;
-    float factor;
-};
-
-// Element (b, r, head, t, i) of a line-major input.  spatial = 1: t is a scan
-// index of direction r, mapped to a pixel of a channels-last image whose pixel
-// stride is st; otherwise st is the token stride of direction r.
-struct LineInput {
-    const void* ptr;
-    int64_t sb, sr, sh, st;
-    int spatial;
-    int64_t H, W;
-    float inv_h;  // 1.0f / H (spatial inputs, H * W < 2^24)
-};
-
-// Chunk length of direction r.  Constant indices only: a runtime index into a
-// kernel-argument array makes the compiler copy the whole argument block to
-// scratch memory (and demotes every pointer in it to flat addressing).
-__device__ __forceinline__ int chunk_of(const int (&chunk)[4], int r) {
-    return r == 0 ? chunk[0] : r == 1 ? chunk[1] : r == 2 ? chunk[2] : chunk[3];
-}
-
-template <typename T>
-__device__ __forceinline__ const T* line_ptr(const LineInput& in, int64_t b, int r, int64_t head,
-                                             int64_t t) {
-    const T* base = static_cast<const T*>(in.ptr);
-    if (in.spatial) return base + b * in.sb + scan_to_pixel(r, t, in.H, in.W, in.inv_h) * in.st + head * in.sh;
-    return base + b * in.sb + r * in.sr + head * in.sh + t * in.st;
-}
-
-struct ScanParams {
-    LineInput x;
-    const float *Mm, *Mv, *Mk, *Me, *Ma;
-    int64_t B, R, heads, L;
-    int chunk[4];
-    int64_t max_chunks;
-    float* states;  // [lines, max_chunks, D, D]: chunk-start M_m
-    int per_line_state;  // 1: memories hold one state per line (chunk.cu:287, StateCount == N)
-    int x_vec;           // input rows are aligned for vector loads
-    int lines_per_wave;  // head_dim 16: lines packed into one wave (1, 2 or 4)
-    int tiles_per_wave;  // head_dim 16: 16-slot column tiles per wave (2 or 4, >= lines_per_wave)
-    int aligned;         // spatial input with chunks (W, W, H, H): chunk c of scan r is a row/column
-    Consts k;
-};
 
 template <int D>
 struct ScanCfg {
@@ -151,16 +104,6 @@ __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
     for (int off = 1; off < N; off <<= 1) v += __shfl_xor(v, off);
     return v;
-}
-
-// Butterfly steps inside a quad of lanes, on the VALU (DPP quad_perm).
-// Quad permutes read only lanes of the same quad, so bound_ctrl never applies; setting
-// it lets the compiler fold the move into the consuming add (v_add_f32_dpp).
-__device__ __forceinline__ float quad_swap1(float v) {  // lanes (1,0,3,2)
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float quad_swap2(float v) {  // lanes (2,3,0,1)
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
 }
 
 template <int D, typename T>
@@ -415,120 +358,6 @@ __global__ __launch_bounds__(4 * D) void srnl_scan_kernel(const ScanParams p) {
 //   refresh      S (64 x 16, 50 rows used) <- S . G
 // The serial gain recurrence stays on the VALU (4 lanes per row of G).
 // ---------------------------------------------------------------------------
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-// bf16 matrix cores for bf16 activations.  v_mfma_f32_16x16x16_bf16 takes from lane l
-// the 4 consecutive k values 4(l/16)..4(l/16)+3 of A row l%16 and of B column l%16 (the
-// same operands one lane gives the four 16x16x4 fp32 steps above) and accumulates in
-// fp32.  An fp32 operand v enters as hi + lo, hi = bf16(v), lo = bf16(v - hi), which
-// leaves |v - hi - lo| <= 2^-16 |v|; bf16 activations enter exactly.
-typedef short v4s __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v4f mfma_bf16(v4s a, v4s b, v4f c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
-
-typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
-typedef float v4fl __attribute__((ext_vector_type(4)));
-
-// Hardware round-to-nearest-even conversions (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ void split_bf16(const float (&v)[4], v4s& hi, v4s& lo) {
-    const v4fl f = {v[0], v[1], v[2], v[3]};
-    const v4bf h = __builtin_convertvector(f, v4bf);
-    const v4bf l = __builtin_convertvector(f - __builtin_convertvector(h, v4fl), v4bf);
-    hi = __builtin_bit_cast(v4s, h);
-    lo = __builtin_bit_cast(v4s, l);
-}
-
-__device__ __forceinline__ v4s bf16x4_bits(uint2 r) {
-    v4s s;
-    s[0] = static_cast<short>(r.x & 0xffffu);
-    s[1] = static_cast<short>(r.x >> 16);
-    s[2] = static_cast<short>(r.y & 0xffffu);
-    s[3] = static_cast<short>(r.y >> 16);
-    return s;
-}
-
-// Four consecutive elements of a row as fp32 (8- or 16-byte load when `vec`).
-template <typename T>
-__device__ __forceinline__ void load4(const T* p, bool vec, float (&out)[4]) {
-    if (vec) {
-        if constexpr (sizeof(T) == 4) {
-            const float4 v = *reinterpret_cast<const float4*>(p);
-            out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
-        } else {
-            const uint2 v = *reinterpret_cast<const uint2*>(p);
-            out[0] = to_f32(T{static_cast<uint16_t>(v.x & 0xffffu)});
-            out[1] = to_f32(T{static_cast<uint16_t>(v.x >> 16)});
-            out[2] = to_f32(T{static_cast<uint16_t>(v.y & 0xffffu)});
-            out[3] = to_f32(T{static_cast<uint16_t>(v.y >> 16)});
-        }
-        return;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = to_f32(p[j]);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float quad_perm(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
-}
-
-__device__ __forceinline__ float readlane_f(float v, int lane) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
-// Sum over lanes l, l^16, l^32, l^48 with the gfx950 row-swap permutes (VALU, no LDS):
-// permlane16_swap(v, v) yields rows (r0, r0, r2, r2) and (r1, r1, r3, r3), so their sum
-// holds the xor-16 pair sums; permlane32_swap does the same for the two halves.
-__device__ __forceinline__ float xor16_32_sum(float v) {
-    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
-    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
-}
-
-// Element offset of scan token `tok` of direction r from the start of its line.
-template <bool SPATIAL>
-__device__ __forceinline__ int64_t token_offset(const LineInput& in, int r, int64_t tok) {
-    if constexpr (SPATIAL) return scan_to_pixel(r, tok, in.H, in.W, in.inv_h) * in.st;
-    else return tok * in.st;
-}
-
-// Gates of one token from its pre-activations pe = x.e and pa = x.a, ||k - v||^2 and
-// ||k||^2 (reference chunk.cu:382-393, memory.cuh:219-233):
-//   eta = ETA_SCALE softplus(clamp(pe)), alpha = ALPHA_MIN + (1 - ALPHA_MIN) sigmoid(clamp(pa + bias)),
-//   cap = STAB_MU (1 - alpha) / (sqrt(||k - v||^2 + 1e-12) + 1e-6), eff = cap (1 - exp(-eta / cap)),
-//   eff = min(eff, nextafter(FACTOR alpha / max(||k||^2, 1e-20), 0)) with the spectral clamp.
-// On the hardware exp2, log2, reciprocal and square root (about one ulp each), as the
-// reference's --use_fast_math build evaluates them with approximate intrinsics of its
-// own.  pe <= 10 after the clamp, so the reference's softplus branch for inputs above 20
-// never applies.  1 - exp(-r) is its Taylor series below r = 1/4 (relative error under
-// 2e-8 there, where 1 - exp2 would cancel) and 1 - exp2(-r log2 e) above.  The bound is
-// positive (alpha > 0), so nextafter toward 0 is one less in its bit pattern.
-__device__ __forceinline__ void token_gates_fast(const Consts& k, float pe, float pa, float dsq, float ksq,
-                                                 float& alpha, float& eff) {
-    constexpr float kLog2e = 1.44269504088896341f, kLn2 = 0.69314718055994531f;
-    const float ep = fminf(10.f, fmaxf(-10.f, pe));
-    const float ap = fminf(10.f, fmaxf(-10.f, pa + k.alpha_bias));
-    const float eta = k.eta_scale * (kLn2 * __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(kLog2e * ep)));
-    alpha = k.alpha_min + (1.f - k.alpha_min) * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-kLog2e * ap));
-    const float dn = __builtin_amdgcn_sqrtf(dsq + 1e-12f);
-    const float cap = k.stab_mu * (1.f - alpha) * __builtin_amdgcn_rcpf(dn + 1e-6f);
-    const float r = eta * __builtin_amdgcn_rcpf(cap);
-    const float series =
-        r * (1.f - r * (0.5f - r * (1.f / 6.f - r * (1.f / 24.f - r * (1.f / 120.f - r * (1.f / 720.f))))));
-    eff = cap * (r < 0.25f ? series : 1.f - __builtin_amdgcn_exp2f(-kLog2e * r));
-    if (k.clamp) {
-        const float bound = k.factor * alpha * __builtin_amdgcn_rcpf(fmaxf(ksq, 1e-20f));
-        eff = fminf(eff, __uint_as_float(__float_as_uint(bound) - 1u));
-    }
-}
-
 // NL lines per wave (NL in {1, 2, 4}) and TCW column tiles of 16 token slots per wave
 // (TCW in {2, 4}, NL <= TCW): the NL lines share (b, r) and take consecutive heads.
 // Each tile gives every line S = 16 TCW / NL token slots; lane l < 16 TCW owns slot
@@ -970,21 +799,6 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
 // ---------------------------------------------------------------------------
 // Spatial readout + four-direction fusion, one thread per output element.
 // ---------------------------------------------------------------------------
-struct FuseParams {
-    const void* x;
-    const void* q;
-    int per_direction;  // 1: x, q are serialized stacks [B, 4, L, C]; 0: channels-last [B, L, C]
-    const float* states;
-    int64_t max_chunks;
-    const float* skip;
-    int skip_per_dir;
-    const float* wgt;
-    void* out;          // [B, H, W, C], fp32 or the io dtype (see the kernel's TO)
-    const void* aux;    // optional [B, H, W, C] io-dtype addend of the fused result
-    int64_t B, H, W, C, heads;
-    int chunk[4];
-};
-
 template <int D, typename T, typename TO>
 __global__ __launch_bounds__(256) void srnl_fuse_readout_kernel(const FuseParams p) {
     const int64_t L = p.H * p.W;
@@ -1064,7 +878,6 @@ __global__ __launch_bounds__(256) void srnl_fuse_readout_kernel(const FuseParams
 template <typename T>
 struct Pix4 {   // 4 channels of one pixel as raw bits
     using Raw = typename std::conditional<sizeof(T) == 4, uint4, uint2>::type;
-    Raw q, x;
 };
 
 template <typename T>
@@ -1079,30 +892,58 @@ __device__ __forceinline__ void raw4_to_f32(const typename Pix4<T>::Raw& r, floa
     }
 }
 
-// y = M q~ for 16 pixels (lane n: pixel n, channels 4g..4g+3 of the result); q~ raw bits.
-template <typename T>
-__device__ __forceinline__ v4f readout_mfma(const float4& m, const typename Pix4<T>::Raw& qr, const float (&qv)[4]) {
+// Sum of squares of a lane's D/4 query channels (raw bits).
+template <typename T, int D>
+__device__ __forceinline__ float xraw_sumsq(const XRaw<T, D>& r) {
+    float s = 0.f;
+    float v[D / 4];
+    decode_x<T, D>(r, v);
+#pragma unroll
+    for (int j = 0; j < D / 4; ++j) s += v[j] * v[j];
+    return s;
+}
+
+// y = M q~ for 16 pixels on the matrix cores: lane l = 16 g + n gives M row n (of the
+// 16-channel half) and pixel n's query over the K-range [g D/4, (g+1) D/4), and receives
+// channels 4g..4g+3 of the half for pixel n.  bf16: M as hi + lo, q exact.
+template <typename T, int D>
+__device__ __forceinline__ v4f readout_mfma(const float (&m)[D / 4], const XRaw<T, D>& qr) {
     v4f y = {0.f, 0.f, 0.f, 0.f};
     if constexpr (std::is_same<T, bf16_t>::value) {
-        const v4s qs = bf16x4_bits(qr);
-        const float a[4] = {m.x, m.y, m.z, m.w};
-        v4s hi, lo;
-        split_bf16(a, hi, lo);
-        y = mfma_bf16(hi, qs, y);
-        y = mfma_bf16(lo, qs, y);
+        using Bf = BfOp<D>;
+        typename Bf::type hi, lo;
+        Bf::split(m, hi, lo);
+        const auto qs = Bf::exact(qr);
+        y = Bf::mma(hi, qs, y);
+        y = Bf::mma(lo, qs, y);
     } else {
-        y = mfma4(m.x, qv[0], y);
-        y = mfma4(m.y, qv[1], y);
-        y = mfma4(m.z, qv[2], y);
-        y = mfma4(m.w, qv[3], y);
+        float qv[D / 4];
+        decode_x<T, D>(qr, qv);
+#pragma unroll
+        for (int j = 0; j < D / 4; ++j) y = mfma4(m[j], qv[j], y);
     }
     return y;
 }
 
-template <typename T, typename TO>
-__global__ __launch_bounds__(256) void srnl_readout16_kernel(const FuseParams p, const int64_t tiles_h,
-                                                             const int64_t tiles_w) {
-    constexpr int D = 16, REC = 20, PER = 4;   // 16 channels + 4 padding floats per pixel record
+// ---------------------------------------------------------------------------
+// Spatial readout + fusion for head_dim 16 or 32 with row/column chunks (W, W, H, H).
+//
+// One workgroup of four waves per 16x16-pixel tile of one (image, head).  Every pixel of
+// a tile row reads the same direction-0/1 states (chunks h and H-1-h) and every pixel of
+// a tile column the same direction-2/3 states (chunks w and W-1-w), so each y = M q over
+// 16 pixels and a 16-channel half of the head is one matrix-core product (K = head_dim).
+// Wave v takes tile columns 4v..4v+3 (directions 2, 3) and then tile rows 4v..4v+3
+// (directions 0, 1); column contributions go through LDS to move pixels onto the row
+// layout; each output is (c0 + c1) + (c2 + c3) with c_r = w_r (y_r + skip_r x), stored
+// once.  Loads are branch-free (positions past the image edge read the edge pixel and
+// are never stored), so every load of a wave's four columns or rows is in flight at
+// once, and the row loads are issued before the column work.  head_dim 32 runs the two
+// halves one after the other.
+// ---------------------------------------------------------------------------
+template <typename T, typename TO, int D>
+__global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams p, const int64_t tiles_h,
+                                                                const int64_t tiles_w) {
+    constexpr int REC = 20, PER = 4, KQ = D / 4;   // 16 channels + 4 padding floats per pixel record
     using Raw = typename Pix4<T>::Raw;
     __shared__ __align__(16) float col[256 * REC];
     // Tile indices fit 32 bits (the host checks the grid size).
@@ -1116,115 +957,123 @@ __global__ __launch_bounds__(256) void srnl_readout16_kernel(const FuseParams p,
     const int H = static_cast<int>(p.H), W = static_cast<int>(p.W);
     const int64_t C = p.C, L = p.H * p.W;
     const int h0 = static_cast<int>(th) * 16, w0 = static_cast<int>(tw) * 16;
-    const int64_t cbase = head * D + 4 * g;
-    const T* xb = static_cast<const T*>(p.x) + b * L * C + cbase;
-    const T* qb = static_cast<const T*>(p.q) + b * L * C + cbase;
+    const T* qb = static_cast<const T*>(p.q) + b * L * C + head * D + KQ * g;
     const float* st[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-        st[r] = p.states + ((b * 4 + r) * p.heads + head) * p.max_chunks * (D * D) + n * D + 4 * g;
-    auto load_pix = [&](int h, int w) {
-        Pix4<T> v;
-        const int64_t at = (static_cast<int64_t>(h) * W + w) * C;
-        v.q = *reinterpret_cast<const Raw*>(qb + at);
-        v.x = *reinterpret_cast<const Raw*>(xb + at);
-        return v;
+        st[r] = p.states + ((b * 4 + r) * p.heads + head) * p.max_chunks * (D * D) + KQ * g;
+    auto load_q = [&](int h, int w) {
+        return load_xraw<T, D>(qb + (static_cast<int64_t>(h) * W + w) * C);
     };
-
-    // Row pass operands (directions 0, 1): tile row hh = 4 wv + k, lane n holds pixel
-    // (h0 + hh, w0 + n).  Issued first; consumed after the column pass.
-    const int wr = min(w0 + n, W - 1);
-    Pix4<T> rp[PER];
-    float4 m0[PER], m1[PER];
-    [[maybe_unused]] Raw ra[PER];
+    auto load_m = [&](const float* base, int chunk, int row, float (&m)[KQ]) {
+        const float* src = base + static_cast<int64_t>(chunk) * (D * D) + row * D;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int h = min(h0 + 4 * wv + k, H - 1);
-        rp[k] = load_pix(h, wr);
-        m0[k] = *reinterpret_cast<const float4*>(st[0] + h * (D * D));
-        m1[k] = *reinterpret_cast<const float4*>(st[1] + (H - 1 - h) * (D * D));
-        if (p.aux) ra[k] = *reinterpret_cast<const Raw*>(static_cast<const T*>(p.aux) + (b * L + static_cast<int64_t>(h) * W + wr) * C + cbase);
-    }
-
-    // Column pass (directions 2, 3): tile column ww = 4 wv + k, lane n holds pixel
-    // (h0 + n, w0 + ww).
-    float wt[4][4], sk[4][4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            wt[r][j] = p.wgt[r * C + cbase + j];
-            sk[r][j] = p.skip[(p.skip_per_dir ? r * C : 0) + cbase + j];
+        for (int j = 0; j < KQ; j += 4) {
+            const float4 f = *reinterpret_cast<const float4*>(src + j);
+            m[j] = f.x; m[j + 1] = f.y; m[j + 2] = f.z; m[j + 3] = f.w;
         }
-    {
-        const int hc = min(h0 + n, H - 1);
-        Pix4<T> cp[PER];
-        float4 m2[PER], m3[PER];
+    };
+    const int wr = min(w0 + n, W - 1), hc = min(h0 + n, H - 1);
+#pragma unroll
+    for (int half = 0; half < D / 16; ++half) {
+        const int64_t cbase = head * D + 16 * half + 4 * g;   // this lane's 4 output channels
+        const T* xb = static_cast<const T*>(p.x) + b * L * C + cbase;
+        const int mrow = 16 * half + n;                        // M row of this lane (A operand)
+
+        // Row pass operands (directions 0, 1): tile row hh = 4 wv + k, lane n holds pixel
+        // (h0 + hh, w0 + n).  Issued first; consumed after the column pass.
+        XRaw<T, D> rq[PER];
+        Raw rx[PER];
+        float m0[PER][KQ], m1[PER][KQ];
+        [[maybe_unused]] Raw ra[PER];
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int w = min(w0 + 4 * wv + k, W - 1);
-            cp[k] = load_pix(hc, w);
-            m2[k] = *reinterpret_cast<const float4*>(st[2] + w * (D * D));
-            m3[k] = *reinterpret_cast<const float4*>(st[3] + (W - 1 - w) * (D * D));
+            const int h = min(h0 + 4 * wv + k, H - 1);
+            rq[k] = load_q(h, wr);
+            rx[k] = *reinterpret_cast<const Raw*>(xb + (static_cast<int64_t>(h) * W + wr) * C);
+            load_m(st[0], h, mrow, m0[k]);
+            load_m(st[1], H - 1 - h, mrow, m1[k]);
+            if (p.aux) ra[k] = *reinterpret_cast<const Raw*>(static_cast<const T*>(p.aux) + (b * L + static_cast<int64_t>(h) * W + wr) * C + cbase);
         }
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            float qv[4], xv[4];
-            raw4_to_f32<T>(cp[k].q, qv);
-            raw4_to_f32<T>(cp[k].x, xv);
-            const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] +
-                                                            qv[3] * qv[3])), 1e-12f);
-            const v4f y2 = readout_mfma<T>(m2[k], cp[k].q, qv);
-            const v4f y3 = readout_mfma<T>(m3[k], cp[k].q, qv);
-            float c23[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                c23[j] = wt[2][j] * (y2[j] * inv + sk[2][j] * xv[j]) + wt[3][j] * (y3[j] * inv + sk[3][j] * xv[j]);
-            *reinterpret_cast<float4*>(col + ((4 * wv + k) * 16 + n) * REC + 4 * g) =
-                make_float4(c23[0], c23[1], c23[2], c23[3]);
-        }
-    }
-    __syncthreads();
 
-    const int w = w0 + n;
+        // Column pass (directions 2, 3): tile column ww = 4 wv + k, lane n holds pixel
+        // (h0 + n, w0 + ww).
+        float wt[4][4], sk[4][4];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int hh = 4 * wv + k, h = h0 + hh;
-        float qv[4], xv[4];
-        raw4_to_f32<T>(rp[k].q, qv);
-        raw4_to_f32<T>(rp[k].x, xv);
-        const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] +
-                                                        qv[3] * qv[3])), 1e-12f);
-        const v4f y0 = readout_mfma<T>(m0[k], rp[k].q, qv);
-        const v4f y1 = readout_mfma<T>(m1[k], rp[k].q, qv);
-        const float4 c23 = *reinterpret_cast<const float4*>(col + (n * 16 + hh) * REC + 4 * g);
-        const float c23v[4] = {c23.x, c23.y, c23.z, c23.w};
-        float o[4];
+        for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            o[j] = (wt[0][j] * (y0[j] * inv + sk[0][j] * xv[j]) + wt[1][j] * (y1[j] * inv + sk[1][j] * xv[j])) +
-                   c23v[j];
-        if (p.aux) {
-            float a[4];
-            raw4_to_f32<T>(ra[k], a);
+            for (int j = 0; j < 4; ++j) {
+                wt[r][j] = p.wgt[r * C + cbase + j];
+                sk[r][j] = p.skip[(p.skip_per_dir ? r * C : 0) + cbase + j];
+            }
+        {
+            XRaw<T, D> cq[PER];
+            Raw cx[PER];
+            float m2[PER][KQ], m3[PER][KQ];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o[j] += a[j];
-        }
-        if (h < H && w < W) {
-            const int64_t at = (b * L + static_cast<int64_t>(h) * W + w) * C + cbase;
-            if constexpr (sizeof(TO) == 4) {
-                *reinterpret_cast<float4*>(static_cast<float*>(p.out) + at) = make_float4(o[0], o[1], o[2], o[3]);
-            } else if constexpr (std::is_same<TO, bf16_t>::value) {
-                *reinterpret_cast<uint2*>(static_cast<TO*>(p.out) + at) =
-                    make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
-            } else {
-                const uint32_t lo = static_cast<uint32_t>(from_f32<TO>(o[0]).bits) |
-                                    (static_cast<uint32_t>(from_f32<TO>(o[1]).bits) << 16);
-                const uint32_t hi = static_cast<uint32_t>(from_f32<TO>(o[2]).bits) |
-                                    (static_cast<uint32_t>(from_f32<TO>(o[3]).bits) << 16);
-                *reinterpret_cast<uint2*>(static_cast<TO*>(p.out) + at) = make_uint2(lo, hi);
+            for (int k = 0; k < PER; ++k) {
+                const int w = min(w0 + 4 * wv + k, W - 1);
+                cq[k] = load_q(hc, w);
+                cx[k] = *reinterpret_cast<const Raw*>(xb + (static_cast<int64_t>(hc) * W + w) * C);
+                load_m(st[2], w, mrow, m2[k]);
+                load_m(st[3], W - 1 - w, mrow, m3[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                float xv[4];
+                raw4_to_f32<T>(cx[k], xv);
+                const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(xraw_sumsq<T, D>(cq[k]))), 1e-12f);
+                const v4f y2 = readout_mfma<T, D>(m2[k], cq[k]);
+                const v4f y3 = readout_mfma<T, D>(m3[k], cq[k]);
+                float c23[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    c23[j] = wt[2][j] * (y2[j] * inv + sk[2][j] * xv[j]) + wt[3][j] * (y3[j] * inv + sk[3][j] * xv[j]);
+                *reinterpret_cast<float4*>(col + ((4 * wv + k) * 16 + n) * REC + 4 * g) =
+                    make_float4(c23[0], c23[1], c23[2], c23[3]);
             }
         }
+        __syncthreads();
+
+        const int w = w0 + n;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int hh = 4 * wv + k, h = h0 + hh;
+            float xv[4];
+            raw4_to_f32<T>(rx[k], xv);
+            const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(xraw_sumsq<T, D>(rq[k]))), 1e-12f);
+            const v4f y0 = readout_mfma<T, D>(m0[k], rq[k]);
+            const v4f y1 = readout_mfma<T, D>(m1[k], rq[k]);
+            const float4 c23 = *reinterpret_cast<const float4*>(col + (n * 16 + hh) * REC + 4 * g);
+            const float c23v[4] = {c23.x, c23.y, c23.z, c23.w};
+            float o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o[j] = (wt[0][j] * (y0[j] * inv + sk[0][j] * xv[j]) + wt[1][j] * (y1[j] * inv + sk[1][j] * xv[j])) +
+                       c23v[j];
+            if (p.aux) {
+                float a[4];
+                raw4_to_f32<T>(ra[k], a);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] += a[j];
+            }
+            if (h < H && w < W) {
+                const int64_t at = (b * L + static_cast<int64_t>(h) * W + w) * C + cbase;
+                if constexpr (sizeof(TO) == 4) {
+                    *reinterpret_cast<float4*>(static_cast<float*>(p.out) + at) = make_float4(o[0], o[1], o[2], o[3]);
+                } else if constexpr (std::is_same<TO, bf16_t>::value) {
+                    *reinterpret_cast<uint2*>(static_cast<TO*>(p.out) + at) =
+                        make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+                } else {
+                    const uint32_t lo = static_cast<uint32_t>(from_f32<TO>(o[0]).bits) |
+                                        (static_cast<uint32_t>(from_f32<TO>(o[1]).bits) << 16);
+                    const uint32_t hi = static_cast<uint32_t>(from_f32<TO>(o[2]).bits) |
+                                        (static_cast<uint32_t>(from_f32<TO>(o[3]).bits) << 16);
+                    *reinterpret_cast<uint2*>(static_cast<TO*>(p.out) + at) = make_uint2(lo, hi);
+                }
+            }
+        }
+        if (half + 1 < D / 16) __syncthreads();   // the next half rewrites the column buffer
     }
 }
 
@@ -1284,9 +1133,33 @@ int check_memories(const float* a, const float* b, const float* c, const float* 
     return VH_OK;
 }
 
+template <typename T>
+constexpr int dtype_code_of() {
+    return std::is_same<T, float>::value ? VH_DTYPE_F32 : std::is_same<T, bf16_t>::value ? VH_DTYPE_BF16 : VH_DTYPE_F16;
+}
+
+// Waves per line of the wide scan for this call: 0 = use the single-wave kernels.  Every
+// head_dim-32 scan and head_dim-16 scans with fewer lines than SIMDs use it.
+// VH_SCAN_WIDE = 0 | 1 | 2 | 4 forces the choice (1 only for head_dim 16); VH_SCAN_PACK
+// (a forced head_dim-16 packing) selects the single-wave kernels.
+int wide_waves(int64_t lines, int d) {
+    if (const char* env = std::getenv("VH_SCAN_WIDE")) {
+        const int w = std::atoi(env);
+        if (w == 0) return 0;
+        if (w == 2 || w == 4 || (w == 1 && d == 16)) return w;
+    }
+    if (std::getenv("VH_SCAN_PACK")) return 0;   // a forced single-wave packing
+    if (d == 32 || (d == 16 && lines < 1024)) return scan_wide_waves(lines, d);
+    return 0;
+}
+
 template <int D, typename T>
 void launch_scan(const ScanParams& sp, hipStream_t stream) {
     const int64_t lines = sp.B * sp.R * sp.heads;
+    if constexpr (D == 16 || D == 32) {
+        const int waves = wide_waves(lines, D);
+        if (waves > 0 && launch_scan_wide(sp, dtype_code_of<T>(), D, waves, stream)) return;
+    }
     if constexpr (D == 16) {
         const int nl = sp.lines_per_wave, tcw = sp.tiles_per_wave;
         const unsigned grid = static_cast<unsigned>(lines / nl);
@@ -1446,22 +1319,27 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
                             reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sp.states) |
                             reinterpret_cast<uintptr_t>(aux);
     const bool out_f32 = out_dtype == VH_DTYPE_F32;
-    if (d == 16 && !per_direction && sp.chunk[0] == W && sp.chunk[1] == W && sp.chunk[2] == H &&
-        sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0) {
+    if ((d == 16 || (d == 32 && io_dtype != VH_DTYPE_F16)) && !per_direction && sp.chunk[0] == W &&
+        sp.chunk[1] == W && sp.chunk[2] == H && sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0) {
         const int64_t tiles_h = (H + 15) / 16, tiles_w = (W + 15) / 16;
         const int64_t n_tiles = sp.B * sp.heads * tiles_h * tiles_w;
         VH_REQUIRE(n_tiles <= 0x7fffffff, VH_ERR_SHAPE, "SRNL readout grid too large");
-        int rc = dispatch_t(io_dtype, [&](auto tv) {
+        auto go = [&](auto tv, auto dc) {
             using T = decltype(tv);
+            constexpr int DD = decltype(dc)::value;
             if (out_f32)
-                hipLaunchKernelGGL((srnl_readout16_kernel<T, float>), dim3(static_cast<unsigned>(n_tiles)),
+                hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD>), dim3(static_cast<unsigned>(n_tiles)),
                                    dim3(256), 0, stream, fp, tiles_h, tiles_w);
             else
-                hipLaunchKernelGGL((srnl_readout16_kernel<T, T>), dim3(static_cast<unsigned>(n_tiles)),
+                hipLaunchKernelGGL((srnl_readout_tile_kernel<T, T, DD>), dim3(static_cast<unsigned>(n_tiles)),
                                    dim3(256), 0, stream, fp, tiles_h, tiles_w);
-        });
+        };
+        int rc;
+        if (d == 16) rc = dispatch_t(io_dtype, [&](auto tv) { go(tv, std::integral_constant<int, 16>{}); });
+        else if (io_dtype == VH_DTYPE_BF16) rc = (go(bf16_t{}, std::integral_constant<int, 32>{}), VH_OK);
+        else rc = (go(float{}, std::integral_constant<int, 32>{}), VH_OK);
         if (rc) return rc;
-        return check_launch("srnl_readout16_kernel");
+        return check_launch("srnl_readout_tile_kernel");
     }
     const int64_t total = sp.B * H * W * C;
     const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
