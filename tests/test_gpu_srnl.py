@@ -282,17 +282,25 @@ def test_full_config3_properties(device):
     assert err.item() < 1e-4, err.item()
 
 
-WIDE_CASES = [(16, 1), (16, 2), (16, 4), (32, 2), (32, 4)]   # (head_dim, waves per line)
+# (head_dim, waves per line, mode): "rows" splits the rows of the gain over the waves,
+# "blocks" also splits each segment's tokens into blocks composed afterwards.
+WIDE_CASES = [(16, 1, "rows"), (16, 2, "rows"), (16, 2, "blocks"), (16, 4, "rows"), (16, 4, "blocks"),
+              (32, 2, "rows"), (32, 4, "rows"), (32, 4, "blocks")]
 
 
-@pytest.mark.parametrize("head_dim,waves", WIDE_CASES)
+def _wide_env(monkeypatch, waves, mode):
+    monkeypatch.setenv("VH_SCAN_WIDE", str(waves))
+    monkeypatch.setenv("VH_SCAN_TB", "1" if mode == "rows" else "2")
+
+
+@pytest.mark.parametrize("head_dim,waves,mode", WIDE_CASES)
 @pytest.mark.parametrize("height,width", [(7, 7), (14, 14), (19, 37), (56, 56)])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL)])
-def test_spatial_scan_wide(oracle, device, monkeypatch, head_dim, waves, height, width, dtype, tol):
+def test_spatial_scan_wide(oracle, device, monkeypatch, head_dim, waves, mode, height, width, dtype, tol):
     """The scan with one line per workgroup of 1, 2 or 4 waves (rows of the gain split over
     the waves): square and rectangular maps, chunks of 7 to 56 (one to four 16-token tiles,
     ragged last tiles), strong memories (active soft cap and spectral clamp)."""
-    monkeypatch.setenv("VH_SCAN_WIDE", str(waves))
+    _wide_env(monkeypatch, waves, mode)
     heads = 2
     channels = heads * head_dim
     mems = memories(4, heads, head_dim, kind="strong", seed=height * 7 + width + head_dim)
@@ -303,22 +311,22 @@ def test_spatial_scan_wide(oracle, device, monkeypatch, head_dim, waves, height,
     got = _spatial(device, x, q, mems, skip, wts, (width, width, height, height))
     expected = oracle.operator_forward(x.float().numpy(), q.float().numpy(), mems, skip.numpy(), wts.numpy(),
                                        head_dim)
-    assert_close(got, expected, tol, f"wide scan d={head_dim} W={waves} {height}x{width} {dtype}")
+    assert_close(got, expected, tol, f"wide scan d={head_dim} W={waves} {mode} {height}x{width} {dtype}")
 
 
-@pytest.mark.parametrize("head_dim,waves", WIDE_CASES)
+@pytest.mark.parametrize("head_dim,waves,mode", WIDE_CASES)
 @pytest.mark.parametrize("chunks", [(5, 16, 64, 3), (65, 128, 100, 200)])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL)])
-def test_sequence_scan_wide(oracle, device, monkeypatch, head_dim, waves, chunks, dtype, tol):
+def test_sequence_scan_wide(oracle, device, monkeypatch, head_dim, waves, mode, chunks, dtype, tol):
     """Packed sequences through the wide scan: chunks shorter than a tile, spanning several
     64-token segments, and ragged last chunks (length 263 = 2*128 + 7)."""
     from visionhope_amd.models.srnl_core.chunk import srnl_packed_forward
 
-    monkeypatch.setenv("VH_SCAN_WIDE", str(waves))
+    _wide_env(monkeypatch, waves, mode)
     batch, directions, heads, length = 1, 4, 2, 263
     mems = memories(directions, heads, head_dim, kind="perturbed", seed=head_dim + waves)
     x, q = _packed_case(batch, directions, heads, length, head_dim, dtype, seed=95)
     y = srnl_packed_forward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device),
                             q.to(device), list(chunks), q_raw=True)
     expected = oracle.sequence_forward(x.float().numpy(), q.float().numpy(), mems, list(chunks))
-    assert_close(y.float().cpu().numpy(), expected, tol, f"wide sequence d={head_dim} W={waves} {chunks}")
+    assert_close(y.float().cpu().numpy(), expected, tol, f"wide sequence d={head_dim} W={waves} {mode} {chunks}")

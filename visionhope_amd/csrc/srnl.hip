@@ -1158,7 +1158,14 @@ void launch_scan(const ScanParams& sp, hipStream_t stream) {
     const int64_t lines = sp.B * sp.R * sp.heads;
     if constexpr (D == 16 || D == 32) {
         const int waves = wide_waves(lines, D);
-        if (waves > 0 && launch_scan_wide(sp, dtype_code_of<T>(), D, waves, stream)) return;
+        // Token blocks (head_dim 16, chunks of 64 tokens or more, several waves): measured
+        // faster than the row split there, slower for shorter chunks and for head_dim 32.
+        // VH_SCAN_TB = 1 | 2 forces the row split or the blocks.
+        int max_chunk = 0;
+        for (int r = 0; r < sp.R; ++r) max_chunk = std::max(max_chunk, sp.chunk[r]);
+        int token_blocks = (D == 16 && max_chunk >= 64) ? 2 : 1;
+        if (const char* tbenv = std::getenv("VH_SCAN_TB")) token_blocks = std::atoi(tbenv) == 1 ? 1 : 2;
+        if (waves > 0 && launch_scan_wide(sp, dtype_code_of<T>(), D, waves, token_blocks, stream)) return;
     }
     if constexpr (D == 16) {
         const int nl = sp.lines_per_wave, tcw = sp.tiles_per_wave;

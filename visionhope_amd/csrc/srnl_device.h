@@ -305,8 +305,10 @@ struct FuseParams {
 
 // Scan with one line per workgroup of `waves` waves (srnl_wide.hip): head_dim 16 or 32,
 // fp32 or bf16 activations, vector-aligned rows.  Returns false (nothing launched) for
-// any other case.  scan_wide_waves picks the waves per line for a line count.
+// any other case.  scan_wide_waves picks the waves per line for a line count;
+// token_blocks > 1 selects the token-block mode (blocks of the chunk composed).
 int scan_wide_waves(int64_t lines, int head_dim);
-bool launch_scan_wide(const ScanParams& sp, int io_dtype, int head_dim, int waves, hipStream_t stream);
+bool launch_scan_wide(const ScanParams& sp, int io_dtype, int head_dim, int waves, int token_blocks,
+                      hipStream_t stream);
 
 }  // namespace vh

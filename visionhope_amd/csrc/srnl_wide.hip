@@ -32,16 +32,29 @@
 namespace vh {
 namespace {
 
-template <typename T, int D, int W, bool SPATIAL>
+// TB token blocks: TB = 1 splits the rows of G over the W waves (every wave walks every
+// token); TB > 1 also splits the tokens of a segment into TB contiguous blocks, one per
+// group of W/TB waves.  The gain update is linear in (G, k - v), so block b maps the gain at
+// its start to G X_b + Y_b, where X_b is the recurrence over the block started from the
+// identity with k - v taken as zero and Y_b the recurrence started from zero with the
+// actual k - v: both are the same row recurrence on 2D rows (rows of G are independent),
+// computed for every block at once.  The blocks are then composed in order,
+// G <- G X_b + Y_b, as D x D products on the fp32 matrix cores, which shortens the serial
+// chain of a segment by the factor TB.
+template <typename T, int D, int W, int TB, bool SPATIAL>
 __global__ __launch_bounds__(64 * W) void srnl_scanw_kernel(const ScanParams p) {
-    static_assert((D == 16 || D == 32) && (W == 1 || W == 2 || W == 4), "scan shape");
+    static_assert((D == 16 || D == 32) && (W == 1 || W == 2 || W == 4) && W % TB == 0, "scan shape");
     constexpr int KQ = D / 4;                       // K-range of a lane group
     constexpr int NRT = D / 16;                     // 16-row tiles of a D x D matrix
     constexpr int ROWS = 3 * D + 2;                 // M_m, M_v, M_k rows, then e, a
     constexpr int RT = (ROWS + 1 + 15) / 16;        // state row tiles, with a zero row after a
     constexpr int SR = RT * 16 * D;                 // floats of one state buffer
-    constexpr int SEG = 64, TPW = 4 / W;            // tokens per segment; tiles per wave
-    constexpr int RW = D / W, RL = 64 / RW, E = D / RL;   // recurrence: rows per wave, lanes per row, entries
+    constexpr int SEG = (TB > 1 && D == 16) ? 128 : 64;   // tokens per segment
+    constexpr int NBUF = TB > 1 ? 1 : 2;            // segment buffers (double-buffered rows mode)
+    constexpr int TPW = SEG / 16 / W;               // tiles per wave per segment
+    constexpr int RB = W / TB;                      // row groups
+    constexpr int RW = (TB > 1 ? 2 * D : D) / RB;   // recurrence rows per wave (X and Y rows when TB > 1)
+    constexpr int RL = 64 / RW, E = D / RL;         // lanes per row, entries per lane
     static_assert(RL >= 2 && RL <= 16 && E >= 1, "recurrence layout");
     constexpr int GS = D + 1, DKS = SEG + 4;
     constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
@@ -50,10 +63,11 @@ __global__ __launch_bounds__(64 * W) void srnl_scanw_kernel(const ScanParams p) 
     using Half = typename Bf::type;
 
     __shared__ __align__(16) float St[2 * SR];          // state, double-buffered across chunks
-    __shared__ __align__(16) float Gs[D * GS];          // the chunk's gain
-    __shared__ __align__(16) float kk[2][SEG * D];      // normalised keys [slot][D]
-    __shared__ __align__(16) float dkT[2][D * DKS];     // (k - v)[row][slot]
-    __shared__ __align__(16) float cf[2][SEG * 8];      // block coefficients per slot
+    __shared__ __align__(16) float Gs[2][D * GS];       // the chunk's gain (TB > 1: ping-pong while composing)
+    __shared__ __align__(16) float kk[NBUF][SEG * D];   // normalised keys [slot][D]
+    __shared__ __align__(16) float dkT[NBUF][D * DKS];  // (k - v)[row][slot]
+    __shared__ __align__(16) float cf[NBUF][SEG * 8];   // block coefficients per slot
+    __shared__ __align__(16) float XY[TB > 1 ? TB * 2 * D * GS : 1];   // X_b rows, then Y_b rows, per block
 
     const int64_t lines = p.B * p.R * p.heads;
     const int64_t line = xcd_remap(blockIdx.x, lines);
@@ -81,7 +95,11 @@ __global__ __launch_bounds__(64 * W) void srnl_scanw_kernel(const ScanParams p) 
 
     const int C = chunk_of(p.chunk, r);
     const int64_t nc = (p.L + C - 1) / C;
-    const int grow = wv * RW + lane / RL, c0 = (lane % RL) * E;   // recurrence: row of G, first column
+    // Recurrence layout: lane -> (row, first column).  TB = 1: row grow of G.  TB > 1: wave
+    // (tb, rb) holds pseudo-row prow of block tb: X_b row prow (< D) or Y_b row prow - D.
+    const int tb = wv % TB, prow = (wv / TB) * RW + lane / RL, c0 = (lane % RL) * E;
+    const int grow = TB > 1 ? prow % D : prow;                   // row of G (and of k - v) it follows
+    const bool use_dk = TB == 1 || prow >= D;                    // X rows see k - v as zero
     const T* xcol = static_cast<const T*>(p.x.ptr) + b * p.x.sb + r * p.x.sr + head * p.x.sh + q * KQ;
     // Row/column chunks (spatial operator): token i of chunk cc is pixel pa*cc + pb*i + pc
     // (32-bit: the host allows this only when H*W*pixel_stride < 2^31).
@@ -258,7 +276,8 @@ __global__ __launch_bounds__(64 * W) void srnl_scanw_kernel(const ScanParams p) 
             o.c1v[u][0] = w2.x; o.c1v[u][1] = w2.y;
         }
         const float4 d4 = *reinterpret_cast<const float4*>(&dkT[buf][grow * DKS + t]);
-        o.df[0] = d4.x; o.df[1] = d4.y; o.df[2] = d4.z; o.df[3] = d4.w;
+        o.df[0] = use_dk ? d4.x : 0.f; o.df[1] = use_dk ? d4.y : 0.f;
+        o.df[2] = use_dk ? d4.z : 0.f; o.df[3] = use_dk ? d4.w : 0.f;
     };
     auto step = [&](float (&g)[E], const StepOps& o) {
         float pdot[4];
@@ -301,6 +320,37 @@ __global__ __launch_bounds__(64 * W) void srnl_scanw_kernel(const ScanParams p) 
         }
     };
 
+    // G <- Gin X_bb + Y_bb (or X_0 + Y_0 when Gin is null): the 16x16 output tiles over the
+    // waves (head_dim 16: one tile, wave 0), fp32 matrix cores.
+    // `first`, `stride`: the threads taking part (one wave: lane, 64; the workgroup: tid, 64 W).
+    auto compose = [&](const float* Gin, int bb, float* Gout, int first, int stride) {
+        const float* X = XY + bb * 2 * D * GS;
+        const float* Y = X + D * GS;
+        if (Gin == nullptr) {
+            for (int idx = first; idx < D * D; idx += stride) {
+                const int rr = idx / D, cc = idx - rr * D;
+                Gout[rr * GS + cc] = X[rr * GS + cc] + Y[rr * GS + cc];
+            }
+            return;
+        }
+        for (int tile = wv; tile < NRT * NRT; tile += W) {
+            const int rt = tile / NRT, ct = tile - rt * NRT;
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kh = 0; kh < NRT; ++kh)
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const int k = 16 * kh + 4 * q + st;
+                    acc = mfma4(Gin[(16 * rt + i16) * GS + k], X[k * GS + 16 * ct + i16], acc);
+                }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int rr = 16 * rt + 4 * q + j, cc = 16 * ct + i16;
+                Gout[rr * GS + cc] = acc[j] + Y[rr * GS + cc];
+            }
+        }
+    };
+
     bool have_next = false;
     int buf = 0;
     for (int64_t c = 0; c < nc; ++c) {
@@ -314,8 +364,11 @@ __global__ __launch_bounds__(64 * W) void srnl_scanw_kernel(const ScanParams p) 
         // The last chunk's gain only feeds a refresh that no output reads.
         if (c == nc - 1) break;
         float g[E];
+        int gcur = -1;   // TB > 1: buffer of Gs holding the composed gain so far (-1: identity)
+        if constexpr (TB == 1) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) g[e] = (c0 + e == grow) ? 1.f : 0.f;
+            for (int e = 0; e < E; ++e) g[e] = (c0 + e == grow) ? 1.f : 0.f;
+        }
         for (int sbase = 0; sbase < C; sbase += SEG) {
             const int scnt = min(SEG, C - sbase);
             if (!have_next) issue(c, sbase, scnt);
@@ -332,43 +385,123 @@ __global__ __launch_bounds__(64 * W) void srnl_scanw_kernel(const ScanParams p) 
                 if (have_next) issue(ncc, nbase, min(SEG, C - nbase));
             }
             __syncthreads();
-            StepOps opA, opB;
-            fetch(buf, 0, opA);
-            for (int t0 = 0; t0 < scnt; t0 += 8) {
-                fetch(buf, min(t0 + 4, SEG - 4), opB);
-                __builtin_amdgcn_sched_barrier(0);
-                step(g, opA);
-                pin(opB);
-                if (t0 + 4 >= scnt) break;
-                fetch(buf, min(t0 + 8, SEG - 4), opA);
-                __builtin_amdgcn_sched_barrier(0);
-                step(g, opB);
-                pin(opA);
+            // Slots [t_begin, t_end) of this wave's block, in 4-slot steps (slots past the
+            // segment's count act as the identity, so the count rounds up to a multiple of 4).
+            int t_begin = 0, t_end = scnt;
+            if constexpr (TB > 1) {
+                const int cnt4 = (scnt + 3) & ~3;
+                const int span = ((cnt4 + 4 * TB - 1) / (4 * TB)) * 4;
+                t_begin = min(tb * span, cnt4);
+                t_end = min(t_begin + span, cnt4);
+#pragma unroll
+                for (int e = 0; e < E; ++e) g[e] = (prow < D && c0 + e == prow) ? 1.f : 0.f;
             }
-            buf ^= 1;
+            if (t_begin < t_end) {
+                StepOps opA, opB;
+                fetch(buf, t_begin, opA);
+                for (int t0 = t_begin; t0 < t_end; t0 += 8) {
+                    fetch(buf, min(t0 + 4, SEG - 4), opB);
+                    __builtin_amdgcn_sched_barrier(0);
+                    step(g, opA);
+                    pin(opB);
+                    if (t0 + 4 >= t_end) break;
+                    fetch(buf, min(t0 + 8, SEG - 4), opA);
+                    __builtin_amdgcn_sched_barrier(0);
+                    step(g, opB);
+                    pin(opA);
+                }
+            }
+            if constexpr (TB > 1) {
+                // block maps to LDS, then compose them onto the gain so far
+#pragma unroll
+                for (int e = 0; e < E; ++e) XY[(tb * 2 * D + prow) * GS + c0 + e] = g[e];
+                __syncthreads();
+                if constexpr (NRT == 1) {
+                    // One 16x16 tile: wave 0 composes every block with the gain held transposed
+                    // in accumulator layout (lane 16q + n holds G[n][4q..4q+3]):
+                    //   G X + Y  ->  (G X + Y)^T = X^T G^T + Y^T,
+                    // so G^T is the B operand as it stands and only X and Y are read from LDS
+                    // (independent of the chain, all issued up front).
+                    if (wv == 0) {
+                        float xa[TB][4], yt[TB][4];
+#pragma unroll
+                        for (int bb = 0; bb < TB; ++bb) {
+                            const float* X = XY + bb * 2 * D * GS;
+#pragma unroll
+                            for (int st = 0; st < 4; ++st) {
+                                xa[bb][st] = X[(4 * q + st) * GS + i16];          // X^T[n][4q + st]
+                                yt[bb][st] = X[(D + i16) * GS + 4 * q + st];      // Y^T[4q + st][n]
+                            }
+                        }
+                        v4f gt;
+                        int bb0 = 0;
+                        if (gcur < 0) {
+                            const float* X0 = XY;
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) gt[j] = X0[i16 * GS + 4 * q + j] + yt[0][j];
+                            bb0 = 1;
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) gt[j] = Gs[gcur][i16 * GS + 4 * q + j];
+                        }
+#pragma unroll
+                        for (int bb = 0; bb < TB; ++bb) {
+                            if (bb < bb0) continue;
+                            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int st = 0; st < 4; ++st) acc = mfma4(xa[bb][st], gt[st], acc);
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) gt[j] = acc[j] + yt[bb][j];
+                        }
+                        const int out = gcur < 0 ? 0 : gcur ^ 1;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) Gs[out][i16 * GS + 4 * q + j] = gt[j];
+                    }
+                    gcur = gcur < 0 ? 0 : gcur ^ 1;
+                } else {
+                    for (int bb = 0; bb < TB; ++bb) {
+                        const int out = gcur < 0 ? 0 : gcur ^ 1;
+                        compose(gcur < 0 ? nullptr : Gs[gcur], bb, Gs[out], tid, 64 * W);
+                        gcur = out;
+                        __syncthreads();
+                    }
+                }
+                if constexpr (NRT == 1) __syncthreads();
+            } else {
+                buf ^= 1;
+            }
         }
         // ---- refresh: Sn <- Sc G, 16-row tiles over the waves ----
+        const float* Gf = Gs[TB > 1 ? gcur : 0];
+        if constexpr (TB == 1) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) Gs[grow * GS + c0 + e] = g[e];
-        __syncthreads();
+            for (int e = 0; e < E; ++e) Gs[0][grow * GS + c0 + e] = g[e];
+            __syncthreads();
+        }
+        // The columns of G this lane supplies (K-range of its lane group), read and split once.
+        float bg[NRT][KQ];
+        [[maybe_unused]] Half bh[NRT], bl[NRT];
+#pragma unroll
+        for (int ct = 0; ct < NRT; ++ct) {
+#pragma unroll
+            for (int s = 0; s < KQ; ++s) bg[ct][s] = Gf[(q * KQ + s) * GS + 16 * ct + i16];
+            if constexpr (kRefreshBf16) Bf::split(bg[ct], bh[ct], bl[ct]);
+        }
         for (int rt = wv; rt < RT; rt += W) {
+            float a[KQ];
+            lds_vec<KQ>(Sc + (16 * rt + i16) * D + q * KQ, a);
+            [[maybe_unused]] Half ah, al;
+            if constexpr (kRefreshBf16) Bf::split(a, ah, al);
 #pragma unroll
             for (int ct = 0; ct < NRT; ++ct) {
                 v4f acc = {0.f, 0.f, 0.f, 0.f};
-                float a[KQ], bg[KQ];
-                lds_vec<KQ>(Sc + (16 * rt + i16) * D + q * KQ, a);
-#pragma unroll
-                for (int s = 0; s < KQ; ++s) bg[s] = Gs[(q * KQ + s) * GS + 16 * ct + i16];
                 if constexpr (kRefreshBf16) {
-                    Half ah, al, bh, bl;
-                    Bf::split(a, ah, al);
-                    Bf::split(bg, bh, bl);
-                    acc = Bf::mma(ah, bh, acc);
-                    acc = Bf::mma(al, bh, acc);
-                    acc = Bf::mma(ah, bl, acc);
+                    acc = Bf::mma(ah, bh[ct], acc);
+                    acc = Bf::mma(al, bh[ct], acc);
+                    acc = Bf::mma(ah, bl[ct], acc);
                 } else {
 #pragma unroll
-                    for (int s = 0; s < KQ; ++s) acc = mfma4(a[s], bg[s], acc);
+                    for (int s = 0; s < KQ; ++s) acc = mfma4(a[s], bg[ct][s], acc);
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) Sn[(16 * rt + 4 * q + j) * D + 16 * ct + i16] = acc[j];
@@ -379,28 +512,29 @@ __global__ __launch_bounds__(64 * W) void srnl_scanw_kernel(const ScanParams p) 
 }
 
 template <typename T, int D, bool SPATIAL>
-void launch_w(const ScanParams& sp, int waves, hipStream_t stream) {
+void launch_w(const ScanParams& sp, int waves, int token_blocks, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(sp.B * sp.R * sp.heads);
-    switch (waves) {
-        case 1:
-            if constexpr (D == 16) {
-                hipLaunchKernelGGL((srnl_scanw_kernel<T, D, 1, SPATIAL>), dim3(grid), dim3(64), 0, stream, sp);
-                break;
-            }
-            [[fallthrough]];
-        case 2:
-            hipLaunchKernelGGL((srnl_scanw_kernel<T, D, 2, SPATIAL>), dim3(grid), dim3(128), 0, stream, sp);
-            break;
-        default:
-            hipLaunchKernelGGL((srnl_scanw_kernel<T, D, 4, SPATIAL>), dim3(grid), dim3(256), 0, stream, sp);
-            break;
+    auto go = [&](auto wc, auto tc) {
+        constexpr int Wc = decltype(wc)::value, TBc = decltype(tc)::value;
+        hipLaunchKernelGGL((srnl_scanw_kernel<T, D, Wc, TBc, SPATIAL>), dim3(grid), dim3(64 * Wc), 0, stream, sp);
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    if constexpr (D == 16) {
+        if (waves == 1) go(I1{}, I1{});
+        else if (waves == 2) token_blocks > 1 ? go(I2{}, I2{}) : go(I2{}, I1{});
+        else token_blocks > 1 ? go(I4{}, I4{}) : go(I4{}, I1{});
+    } else {
+        if (waves <= 2) go(I2{}, I1{});
+        else token_blocks > 1 ? go(I4{}, I2{}) : go(I4{}, I1{});
     }
 }
 
 template <typename T, int D>
-void launch_t(const ScanParams& sp, int waves, hipStream_t stream) {
-    if (sp.x.spatial) launch_w<T, D, true>(sp, waves, stream);
-    else launch_w<T, D, false>(sp, waves, stream);
+void launch_t(const ScanParams& sp, int waves, int token_blocks, hipStream_t stream) {
+    if (sp.x.spatial) launch_w<T, D, true>(sp, waves, token_blocks, stream);
+    else launch_w<T, D, false>(sp, waves, token_blocks, stream);
 }
 
 }  // namespace
@@ -413,14 +547,15 @@ int scan_wide_waves(int64_t lines, int head_dim) {
     return w;
 }
 
-bool launch_scan_wide(const ScanParams& sp, int io_dtype, int head_dim, int waves, hipStream_t stream) {
+bool launch_scan_wide(const ScanParams& sp, int io_dtype, int head_dim, int waves, int token_blocks,
+                      hipStream_t stream) {
     if (!sp.x_vec || (head_dim != 16 && head_dim != 32) || io_dtype == VH_DTYPE_F16) return false;
     if (head_dim == 16) {
-        if (io_dtype == VH_DTYPE_BF16) launch_t<bf16_t, 16>(sp, waves, stream);
-        else launch_t<float, 16>(sp, waves, stream);
+        if (io_dtype == VH_DTYPE_BF16) launch_t<bf16_t, 16>(sp, waves, token_blocks, stream);
+        else launch_t<float, 16>(sp, waves, token_blocks, stream);
     } else {
-        if (io_dtype == VH_DTYPE_BF16) launch_t<bf16_t, 32>(sp, waves, stream);
-        else launch_t<float, 32>(sp, waves, stream);
+        if (io_dtype == VH_DTYPE_BF16) launch_t<bf16_t, 32>(sp, waves, token_blocks, stream);
+        else launch_t<float, 32>(sp, waves, token_blocks, stream);
     }
     return true;
 }
