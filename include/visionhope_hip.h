@@ -199,7 +199,11 @@ int vh_postprocess_scale_forward(
     float* out, int64_t B, int64_t heads, int64_t H, int64_t W, int32_t head_dim,
     int32_t channels_last, void* stream);
 
-/* Workspace of vh_grn_forward: B * ceil(H*W / rows_per_slab) * C fp32 partial sums. */
+/* Workspace of vh_grn_forward and vh_grn_scale_forward: a 32 KiB header of
+ * synchronisation words, then B * pieces * C fp32 partial sums.
+ * The synchronisation words must be zero when a workspace is first used (zero the whole
+ * workspace once); every call leaves them zero, so the workspace can be reused as is.
+ * Calls that share a workspace must not overlap (use one workspace per stream). */
 size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W);
 
 /* GRN on channels-last x [B, H, W, C] (io_dtype): gx = ||x||_2 over H*W,

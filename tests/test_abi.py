@@ -55,8 +55,13 @@ def test_abi_version_matches_header(lib):
 def test_workspace_queries(lib):
     assert lib.vh_srnl_workspace_bytes(10, 7, 16) == 10 * 7 * 16 * 16 * 4
     assert lib.vh_srnl_workspace_bytes(0, 7, 16) == 0
-    # 100 pixels, B=2: the statistics pass splits each image into 13 slabs of 8 pixels
-    assert lib.vh_grn_workspace_bytes(2, 8, 10, 10) == 2 * 13 * 8 * 4
+    # 100 pixels, B=2: the 32 KiB synchronisation header, then the partial sums of the
+    # two-pass statistics, which split each image into 13 slabs of 8 pixels (the one-pass
+    # kernel needs one piece per image here)
+    assert lib.vh_grn_workspace_bytes(2, 8, 10, 10) == 32768 + 2 * 13 * 8 * 4
+    # 56x56x96, B=128: the scalar statistics' 49 slabs of 64 pixels exceed the one-pass
+    # kernel's 19 pieces of 21 x 8 rows
+    assert lib.vh_grn_workspace_bytes(128, 96, 56, 56) == 32768 + 128 * 49 * 96 * 4
 
 
 def _consts():

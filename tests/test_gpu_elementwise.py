@@ -16,9 +16,10 @@ FP32_TOL = 1e-5
 @pytest.mark.parametrize("channels_last", [False, True])
 @pytest.mark.parametrize("per_direction", [False, True])
 @pytest.mark.parametrize("heads,head_dim,height,width", [(3, 16, 6, 9), (5, 8, 13, 17), (2, 64, 16, 8),
-                                                         (1, 4, 5, 3)])
+                                                         (1, 4, 5, 3), (8, 16, 7, 10), (4, 32, 5, 6)])
 def test_direction_fusion(oracle, device, dtype, channels_last, per_direction, heads, head_dim, height, width):
-    """Every fusion kernel (tiled 8x8 channels-last with partial edge tiles, scalar NCHW,
+    """Every fusion kernel (tiled 4x4 channels-last with partial edge tiles and a last chunk
+    of fewer heads than the others (8 heads of 16, 4 of 32), scalar NCHW,
     head_dim 4 below the 8-channel vectors) against the oracle."""
     from visionhope_amd.utils.direction_fusion import visionhope_postprocess_scale
 
@@ -88,6 +89,102 @@ def test_grn(oracle, device, dtype, channels, height, width, channels_last):
     assert y.dtype == torch.float32
     expected = oracle.grn(x.float().numpy(), gamma.numpy(), beta.numpy())
     assert_close(y.cpu().numpy(), expected, 2e-5, "GRN")
+
+
+def _grn_abi(lib, x, gamma, beta, ws):
+    """vh_grn_forward through the C-ABI on a channels-last [B, H, W, C] tensor: y, gx, inv_den."""
+    from visionhope_amd.utils import hip
+
+    batch, height, width, channels = x.shape
+    y = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    gx = torch.empty(batch, channels, device=x.device)
+    inv_den = torch.empty(batch, device=x.device)
+    hip.check(lib.vh_grn_forward(hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(gamma), hip.ptr(beta), hip.ptr(y),
+                                 hip.VH_DTYPE_F32, hip.ptr(gx), hip.ptr(inv_den), batch, channels, height, width,
+                                 1e-6, hip.ptr(ws), ws.numel() * 4, hip.stream_of(x)), "vh_grn_forward")
+    return y, gx, inv_den
+
+
+def _grn_stats(x):
+    """float64 gx and inv_den of a channels-last numpy map (utils/grn.py:26-38)."""
+    gx = np.sqrt((x.astype(np.float64) ** 2).sum(axis=(1, 2)))
+    return gx, 1.0 / (gx.mean(axis=1) + 1e-6)
+
+
+@pytest.mark.parametrize("batch,channels,height,width", [(16, 96, 100, 100), (5, 256, 14, 14), (3, 2048, 7, 7),
+                                                         (4, 96, 7, 5)])
+def test_grn_one_pass_pieces(oracle, device, batch, channels, height, width):
+    """The one-pass GRN (x held in registers while the pieces of an image exchange their
+    sums of squares) at 60, 4, 7 and 1 pieces per image through the C-ABI: y, gx and
+    inv_den against float64, and the workspace's 32 KiB synchronisation header is zero
+    again after the call (the contract that lets the next call reuse the workspace)."""
+    from visionhope_amd.utils import hip
+
+    lib = hip.load_library()
+    gen = torch.Generator(device=device).manual_seed(channels + height)
+    x = torch.randn(batch, height, width, channels, device=device, generator=gen).bfloat16()
+    gamma = torch.randn(channels, device=device, generator=gen) * 0.1
+    beta = torch.randn(channels, device=device, generator=gen) * 0.1
+    nbytes = lib.vh_grn_workspace_bytes(batch, channels, height, width)
+    ws = torch.zeros((nbytes + 3) // 4, device=device)
+    for _ in range(2):   # the second call runs on the counters the first one left
+        y, gx, inv_den = _grn_abi(lib, x, gamma, beta, ws)
+        torch.cuda.synchronize()
+        words = ws[:8192].view(torch.int32)
+        assert int(words.abs().sum()) == 0, "synchronisation words not left zero"
+        xn = x.float().cpu().numpy()
+        want_gx, want_inv = _grn_stats(xn)
+        assert_close(gx.cpu().numpy(), want_gx, 1e-5, "gx")
+        assert_close(inv_den.cpu().numpy(), want_inv, 1e-5, "inv_den")
+        expected = oracle.grn(xn.transpose(0, 3, 1, 2), gamma.cpu().numpy(), beta.cpu().numpy()).transpose(0, 2, 3, 1)
+        assert_close(y.cpu().numpy(), expected, 1e-5, "GRN one pass")
+
+
+def test_grn_one_pass_back_to_back_shapes(oracle, device):
+    """Calls with different batch, piece counts and dtypes in a row on one workspace, each
+    checked: a small batch followed by a larger one (whose counters must not sit where the
+    first call wrote partial sums), and a batch of 300 (two launches of at most 256
+    images)."""
+    from visionhope_amd.utils.grn_cuda import visionhope_grn
+
+    shapes = [(3, 96, 40, 40, torch.bfloat16), (8, 96, 56, 56, torch.bfloat16), (2, 192, 28, 28, torch.float32),
+              (33, 96, 20, 30, torch.float16), (1, 512, 9, 11, torch.bfloat16), (300, 64, 6, 6, torch.bfloat16)]
+    for i, (batch, channels, height, width, dtype) in enumerate(shapes):
+        x = randn(batch, channels, height, width, seed=40 + i).to(dtype).contiguous(memory_format=torch.channels_last)
+        gamma = randn(channels, seed=50 + i, scale=0.1)
+        beta = randn(channels, seed=60 + i, scale=0.1)
+        y = visionhope_grn(x.to(device), gamma.to(device), beta.to(device), 1e-6)
+        expected = oracle.grn(x.float().numpy(), gamma.numpy(), beta.numpy())
+        assert_close(y.cpu().numpy(), expected, 2e-5, f"GRN call {i}")
+
+
+def test_grn_one_pass_graph_replays(device):
+    """The one-pass GRN captured in a HIP graph three times over: every replay, with eager
+    GRN calls of another shape and synchronisations between replays, equals the eager
+    result bit for bit."""
+    from visionhope_amd.utils.grn_cuda import visionhope_grn
+
+    gen = torch.Generator(device=device).manual_seed(77)
+    x = torch.randn(32, 28, 28, 192, device=device, generator=gen).bfloat16().permute(0, 3, 1, 2)
+    other = torch.randn(3, 14, 14, 256, device=device, generator=gen).bfloat16().permute(0, 3, 1, 2)
+    gamma = torch.randn(192, device=device, generator=gen) * 0.1
+    beta = torch.randn(192, device=device, generator=gen) * 0.1
+    g2, b2 = gamma[:128].repeat(2), beta[:128].repeat(2)
+    eager = visionhope_grn(x, gamma, beta, 1e-6)
+    eager_other = visionhope_grn(other, g2, b2, 1e-6)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [visionhope_grn(x, gamma, beta, 1e-6) for _ in range(3)]
+    for replay in range(3):
+        for o in outs:
+            o.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o in outs:
+            assert torch.equal(o, eager), f"replay {replay} differs from eager"
+        assert torch.equal(visionhope_grn(other, g2, b2, 1e-6), eager_other)
+        torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])

@@ -96,6 +96,38 @@ __device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
     }
 }
 
+// The same eight elements kept as loaded (16 bytes of a 16-bit type, 32 of fp32) so a
+// kernel can issue many loads before it spends registers on the fp32 values.
+template <typename T> struct Pack8 { uint4 u; };
+template <> struct Pack8<float> { float4 a, b; };
+
+template <typename T>
+__device__ __forceinline__ Pack8<T> load_pack8(const T* p) {
+    Pack8<T> r;
+    if constexpr (sizeof(T) == 4) {
+        r.a = *reinterpret_cast<const float4*>(p);
+        r.b = *reinterpret_cast<const float4*>(p + 4);
+    } else {
+        r.u = *reinterpret_cast<const uint4*>(p);
+    }
+    return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void pack8_to_f32(const Pack8<T>& r, float (&v)[8]) {
+    if constexpr (sizeof(T) == 4) {
+        v[0] = r.a.x; v[1] = r.a.y; v[2] = r.a.z; v[3] = r.a.w;
+        v[4] = r.b.x; v[5] = r.b.y; v[6] = r.b.z; v[7] = r.b.w;
+    } else {
+        const uint32_t w[4] = {r.u.x, r.u.y, r.u.z, r.u.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            v[2 * h] = to_f32(T{static_cast<uint16_t>(w[h] & 0xffffu)});
+            v[2 * h + 1] = to_f32(T{static_cast<uint16_t>(w[h] >> 16)});
+        }
+    }
+}
+
 typedef __bf16 vh_bf16x2 __attribute__((ext_vector_type(2)));
 typedef float vh_f32x2 __attribute__((ext_vector_type(2)));
 

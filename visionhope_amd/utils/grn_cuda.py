@@ -1,13 +1,29 @@
 """Native GRN forward on MI355X (replaces ``utils/grn_cuda.py`` + ``utils/csrc/grn_cuda.cu``).
 
-Three launches on the current stream: per-slab partial sums of x^2, per-image
-statistics (gx, 1/(mean gx + eps)), and the FP32 affine output.
+For C % 8 == 0 maps whose images split into at most 64 register-resident pieces, one
+launch on the current stream reads x once: each piece publishes its per-channel sums of
+x^2, waits for the other pieces of its image, then applies the FP32 affine output to the
+rows it holds.  Other maps take two or three launches (partial sums, statistics, apply).
 """
 import torch
 from torch.autograd import Function
 
 from . import hip
 from .cuda import on_tensor_device
+
+# One GRN workspace per (device, stream): its leading synchronisation words must be zero
+# when a workspace is first used, and every call leaves them zero, so a zero-filled
+# buffer is kept and reused; calls on one stream never overlap.
+_STREAM_WORKSPACES = {}
+
+
+def _stream_workspace(nbytes, device):
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _STREAM_WORKSPACES.get(key)
+    if ws is None or ws.numel() * 4 < nbytes:
+        ws = torch.zeros(max(1, (int(nbytes) + 255) // 256 * 64), dtype=torch.float32, device=device)
+        _STREAM_WORKSPACES[key] = ws
+    return ws
 
 
 class _VisionHOPEGRNFunction(Function):
@@ -24,8 +40,7 @@ class _VisionHOPEGRNFunction(Function):
         gx = torch.empty((batch, channels), device=x.device, dtype=torch.float32)
         inv_den = torch.empty((batch,), device=x.device, dtype=torch.float32)
         lib = hip.load_library()
-        nbytes = lib.vh_grn_workspace_bytes(batch, channels, height, width)
-        ws = hip.workspace(nbytes, x.device)
+        ws = _stream_workspace(lib.vh_grn_workspace_bytes(batch, channels, height, width), x.device)
         hip.check(lib.vh_grn_forward(
             hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(gamma), hip.ptr(beta), hip.ptr(y),
             hip.dtype_code(out_dtype), hip.ptr(gx), hip.ptr(inv_den), batch, channels, height, width,
