@@ -75,6 +75,27 @@ def _np(t):
     return t.detach().numpy()
 
 
+def test_residual_add_special_cases(oracle):
+    """oracle.residual_add pinned without a second restatement: gamma = 0 or a dropped
+    sample (drop scale 0) returns the residual bit for bit; gamma = drop = 1 is the fp32
+    sum; scaling the branch by 2 scales the increment by exactly 2 (powers of two are exact
+    in fp32); the drop scale applies per sample, not per channel."""
+    rng = np.random.default_rng(3)
+    res = rng.normal(size=(3, 4, 5, 6)).astype(np.float32)
+    br = rng.normal(size=(3, 4, 5, 6)).astype(np.float32)
+    gamma = rng.normal(size=6).astype(np.float32)
+    ones = np.ones(3, np.float32)
+    np.testing.assert_array_equal(oracle.residual_add(res, br, np.zeros(6, np.float32), ones), res)
+    drop = np.array([1.0, 0.0, 2.0], np.float32)
+    out = oracle.residual_add(res, br, gamma, drop)
+    np.testing.assert_array_equal(out[1], res[1])
+    np.testing.assert_array_equal(oracle.residual_add(res, br, np.ones(6, np.float32), ones), res + br)
+    inc1 = oracle.residual_add(np.zeros_like(res), br, gamma, drop)
+    inc2 = oracle.residual_add(np.zeros_like(res), 2 * br, gamma, drop)
+    np.testing.assert_array_equal(inc2, 2 * inc1)
+    np.testing.assert_array_equal(inc1[2], 2 * oracle.residual_add(np.zeros_like(res), br, gamma, ones)[2])
+
+
 def test_torch_tail_forwards_match_numpy_oracle(oracle):
     """Each tail forward of the differentiable oracle against the NumPy restatement."""
     from oracle import oracle_torch as ot

@@ -5,6 +5,8 @@ The reference ships no golden vectors and its SRNL exists only as CUDA source
   * an independent NumPy fp64 formulation (chunk-level matrix algebra),
   * closed forms: first chunk = plain GEMM; zero key/value memories = pure decay by
     sigma(ln 9) = 0.9 per token; zero memories = zero output; chunk length 1 by hand,
+  * library routines: the gates at pre-activations on both sides of the +-10 clamp
+    against torch's softplus, sigmoid and clamp,
   * invariants: causality, padding invariance, non-expansion of every chunk gain,
     query scale invariance, and the operator's rot180 / transpose symmetries,
   * planted mistakes (oracle `mutation` switch): each is caught by one of the above.
@@ -124,6 +126,50 @@ def test_chunk_length_one_by_hand(oracle):
     zeros_v = np.zeros((1, d))
     y = _run(oracle, x[None], q[None], (m_m[None], m_v[None], m_k[None], zeros_v, zeros_v), 1)
     np.testing.assert_allclose(y[0, 1], _chunk_one_by_hand(m_m, m_v, m_k, x, q), rtol=1e-12)
+
+
+@pytest.mark.parametrize("pre_e", [-12.0, -3.0, 0.0, 3.0, 12.0])
+@pytest.mark.parametrize("pre_a", [-12.0, -3.0, 0.0, 3.0, 12.0])
+@pytest.mark.parametrize("min_retention", [0.0, 0.3])
+def test_gates_match_library_routines(oracle, pre_e, pre_a, min_retention):
+    """The gates at non-zero gate vectors, pinned by library routines: chunk length 1,
+    gate vectors chosen so that x.e = pre_e and x.a = pre_a (+-12 lies beyond the +-10
+    pre-activation clamp).  The learning rate is step_scale * softplus(clamp(x.e)) with
+    torch's softplus (beta 1, threshold 20) and the retention min_r + (1 - min_r) *
+    sigmoid(clamp(x.a + bias)) with torch's sigmoid, both in float64; the first step's
+    gain is then alpha I - eff (2k - v) k^T as in _chunk_one_by_hand."""
+    import torch
+    from oracle.oracle import Consts
+
+    consts = Consts(min_retention=min_retention)
+    m_m, m_v, m_k, x, q = _hand_case()
+    d = x.shape[-1]
+    e = pre_e * x[0] / (x[0] @ x[0])
+    a = pre_a * x[0] / (x[0] @ x[0])
+    y = _run(oracle, x[None], q[None], (m_m[None], m_v[None], m_k[None], e[None], a[None]), 1, consts=consts)
+
+    f64 = torch.float64
+    ep = torch.clamp(torch.tensor(pre_e, dtype=f64), -10.0, 10.0)
+    ap = torch.clamp(torch.tensor(pre_a, dtype=f64) + consts.retention_bias, -10.0, 10.0)
+    eta = consts.step_scale * torch.nn.functional.softplus(ep, beta=1.0, threshold=20.0)
+    alpha = min_retention + (1.0 - min_retention) * torch.sigmoid(ap)
+    kr = torch.from_numpy(m_k @ x[0])
+    k = kr / torch.sqrt(kr @ kr + 1e-6)
+    v = torch.from_numpy(m_v @ x[0])
+    dn = torch.sqrt(((k - v) ** 2).sum() + 1e-12)
+    cap = consts.injection_margin * (1 - alpha) / (dn + 1e-6)
+    eff = cap * -torch.expm1(-eta / cap)
+    lim = torch.nextafter(2 * consts.spectral_margin * alpha / torch.clamp_min(k @ k, 1e-20),
+                          torch.tensor(0.0, dtype=f64))
+    eff = torch.minimum(eff, lim)
+    gain = alpha * torch.eye(d, dtype=f64) - eff * torch.outer(2 * k - v, k)
+    q1 = torch.from_numpy(q[1] / np.linalg.norm(q[1]))
+    want = (torch.from_numpy(m_m) @ gain @ q1).numpy()
+    np.testing.assert_allclose(y[0, 1], want, rtol=1e-12, atol=1e-15)
+    if abs(pre_a + consts.retention_bias) > 10:   # clamped: any larger pre-activation gives the same output
+        a2 = 2 * a
+        y2 = _run(oracle, x[None], q[None], (m_m[None], m_v[None], m_k[None], e[None], a2[None]), 1, consts=consts)
+        np.testing.assert_array_equal(y2, y)
 
 
 def test_causality(oracle):
