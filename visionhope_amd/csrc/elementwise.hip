@@ -400,23 +400,28 @@ __global__ __launch_bounds__(256) void grn_partial8_wide_kernel(const T* __restr
     }
 }
 
-// gx[b, c] = sqrt(sum over the slabs), one thread per channel (grid: channel blocks x images,
-// so small batches still spread over the GPU).
+// gx[b, c] = sqrt(sum over the slabs): a workgroup takes 64 channels of one image and 4
+// threads per channel, thread j summing slabs j, j + 4, ... (two accumulators), and the four
+// partial sums meet in LDS in a fixed order (deterministic).  Grid: channel blocks x images.
 __global__ __launch_bounds__(256) void grn_gx_kernel(const float* __restrict__ partial, float* __restrict__ gx, int C,
                                                     int nslab) {
-    const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
-    if (c >= C) return;
-    const float* pc = partial + static_cast<int64_t>(b) * nslab * C + c;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    int s = 0;
-    for (; s + 4 <= nslab; s += 4) {
-        a0 += pc[s * C];
-        a1 += pc[(s + 1) * C];
-        a2 += pc[(s + 2) * C];
-        a3 += pc[(s + 3) * C];
+    __shared__ float part[4][64];
+    const int cl = threadIdx.x & 63, j = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl, b = blockIdx.y;
+    float a0 = 0.f, a1 = 0.f;
+    if (c < C) {
+        const float* pc = partial + static_cast<int64_t>(b) * nslab * C + c;
+        int s = j;
+        for (; s + 4 < nslab; s += 8) {
+            a0 += pc[static_cast<int64_t>(s) * C];
+            a1 += pc[static_cast<int64_t>(s + 4) * C];
+        }
+        if (s < nslab) a0 += pc[static_cast<int64_t>(s) * C];
     }
-    for (; s < nslab; ++s) a0 += pc[s * C];
-    gx[static_cast<int64_t>(b) * C + c] = sqrtf((a0 + a1) + (a2 + a3));
+    part[j][cl] = a0 + a1;
+    __syncthreads();
+    if (j == 0 && c < C)
+        gx[static_cast<int64_t>(b) * C + c] = sqrtf((part[0][cl] + part[1][cl]) + (part[2][cl] + part[3][cl]));
 }
 
 // Apply for wide maps: every workgroup of image b forms inv_den from gx (fixed order, so all
@@ -1117,12 +1122,16 @@ static size_t grn_sync_bytes() {
 }
 
 // Pieces per image of the one-pass kernel (0 when the map does not qualify): R = 256 / (C/8)
-// rows per pass, v rows per thread.
-static int64_t grn_onepass_pieces(int64_t C, int64_t S, int v = kGrnVec) {
+// rows per pass, v rows per thread.  Every piece reads the pieces x C partial sums of its
+// image, so the map qualifies only while those reads stay within 1/8 of the piece's own x
+// bytes (R v C elem_bytes); wide maps with few rows per piece (e.g. 32x32x1792, 64 pieces
+// of 16 rows) take the two-pass kernels instead.
+static int64_t grn_onepass_pieces(int64_t C, int64_t S, int elem_bytes, int v = kGrnVec) {
     if (C % 8 != 0 || C / 8 > 256) return 0;
     const int64_t rows = (256 / (C / 8)) * v;
     const int64_t pieces = (S + rows - 1) / rows;
-    return pieces <= kGrnMaxPieces ? pieces : 0;
+    if (pieces > kGrnMaxPieces || pieces * 4 * 8 > rows * elem_bytes) return 0;
+    return pieces;
 }
 
 size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W) {
@@ -1131,7 +1140,9 @@ size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W) {
     const int64_t S = H * W;
     const int64_t rows = grn_rows_per_slab(B, S);
     int64_t nslab = std::max<int64_t>((S + rows - 1) / rows, (S + kGrnRowsPerSlab - 1) / kGrnRowsPerSlab);
-    nslab = std::max(nslab, grn_onepass_pieces(C, S));
+    // the one-pass kernel's pieces at either rows-per-thread choice (fp32 qualifies whenever a
+    // 16-bit type does)
+    nslab = std::max({nslab, grn_onepass_pieces(C, S, 4, kGrnVec), grn_onepass_pieces(C, S, 4, 2 * kGrnVec)});
     return grn_sync_bytes() + static_cast<size_t>(B * nslab * C) * sizeof(float);
 }
 
@@ -1158,9 +1169,10 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
     const int64_t total = B * S * C;
     // 16 rows per thread (half the pieces, half the synchronisations; measured 5% faster at
     // 56x56x96 and 28x28x192) unless the image would then be a single piece
+    const int eb = dtype_bytes(io_dtype);
     int vrows = 2 * kGrnVec;
-    int64_t pieces = grn_onepass_pieces(C, S, vrows);
-    if (pieces < 2) pieces = grn_onepass_pieces(C, S, vrows = kGrnVec);
+    int64_t pieces = grn_onepass_pieces(C, S, eb, vrows);
+    if (pieces < 2) pieces = grn_onepass_pieces(C, S, eb, vrows = kGrnVec);
     if (pieces > 0 && grn_vectorised(C, x, y) && B * S * C < (int64_t(1) << 31)) {
         const int G = static_cast<int>(C / 8);
         const unsigned threads = static_cast<unsigned>((G * (256 / G) + 63) / 64 * 64);
@@ -1204,7 +1216,7 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
             // partial sums (vslab x C floats) stays small next to its share of x
             const bool fold = static_cast<int64_t>(vslab) * C <= 8192;
             if (!fold)
-                hipLaunchKernelGGL(grn_gx_kernel, dim3(static_cast<unsigned>((C + 255) / 256), static_cast<unsigned>(B)),
+                hipLaunchKernelGGL(grn_gx_kernel, dim3(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>(B)),
                                    dim3(256), 0, s, partial, gx, static_cast<int>(C), vslab);
             dispatch_t(y_dtype, [&](auto ov) {
                 using TO = decltype(ov);
@@ -1234,7 +1246,7 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
             hipLaunchKernelGGL((grn_partial8_wide_kernel<T>), dim3(static_cast<unsigned>(vslab), static_cast<unsigned>(B)),
                                dim3(256), 0, s, static_cast<const T*>(x), partial, static_cast<int>(C),
                                static_cast<int>(S), rows, vslab);
-            hipLaunchKernelGGL(grn_gx_kernel, dim3(static_cast<unsigned>((C + 255) / 256), static_cast<unsigned>(B)),
+            hipLaunchKernelGGL(grn_gx_kernel, dim3(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>(B)),
                                dim3(256), 0, s, partial, gx, static_cast<int>(C), vslab);
             dispatch_t(y_dtype, [&](auto ov) {
                 using TO = decltype(ov);
