@@ -121,3 +121,31 @@ def test_checkpoint_round_trip_prepared_gpu(tiny_case, device, tmp_path):
     err = rel_err(got, expected[:8])
     print(f"checkpoint round trip: logits normwise {err:.3e}", flush=True)
     assert err <= 1e-4
+
+
+def test_graph_replays_match_eager_forward(tiny_case, device):
+    """The prepared Tiny forward as the bench runs it (bf16 autocast, inference mode, every
+    block forking a side stream for the query projection and the position encoding and
+    joining it before the readout) captured in one HIP graph: three replays, with an eager
+    forward and a synchronisation between replays, give the eager logits bit for bit, and
+    the eager forwards agree with each other."""
+    from visionhope_amd.inference.prepare import prepare_for_inference
+
+    model, images, _ = tiny_case
+    gpu = copy.deepcopy(model).to(device).to(memory_format=torch.channels_last)
+    prepare_for_inference(gpu)
+    batch = images[:16].to(device).contiguous(memory_format=torch.channels_last)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        eager = gpu(batch)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            captured = gpu(batch)
+        for replay in range(3):
+            captured.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(captured, eager), f"replay {replay} differs from the eager forward"
+            again = gpu(batch)
+            torch.cuda.synchronize()
+            assert torch.equal(again, eager), f"eager forward after replay {replay} differs"

@@ -22,9 +22,10 @@
 //   * readout kernels — y = M_m^c q_hat for every token, fully parallel.  For
 //     the spatial operator the readout also restores the four scan orders and
 //     fuses sum_r w_r (y_r + skip_r x) per pixel, so no per-direction output
-//     ever reaches HBM and no atomics are used.  head_dim 16 with row/column
-//     chunks uses 16x16-pixel MFMA tiles (srnl_readout16_kernel); every other
-//     case one thread per output in the reference's summation order.
+//     ever reaches HBM and no atomics are used.  head_dim 16, and 32 with fp32
+//     or bf16 activations, with row/column chunks use 16x16-pixel MFMA tiles
+//     (srnl_readout_tile_kernel); every other case one thread per output in the
+//     reference's summation order.
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
