@@ -1154,6 +1154,8 @@ int wide_waves(int64_t lines, int d) {
     return 0;
 }
 
+void scan16_ut_packing(int64_t lines, int64_t heads, int* nl, int* tcw);
+
 template <int D, typename T>
 void launch_scan(const ScanParams& sp, hipStream_t stream) {
     const int64_t lines = sp.B * sp.R * sp.heads;
@@ -1167,6 +1169,16 @@ void launch_scan(const ScanParams& sp, hipStream_t stream) {
         int token_blocks = (D == 16 && max_chunk >= 64) ? 2 : 1;
         if (const char* tbenv = std::getenv("VH_SCAN_TB")) token_blocks = std::atoi(tbenv) == 1 ? 1 : 2;
         if (waves > 0 && launch_scan_wide(sp, dtype_code_of<T>(), D, waves, token_blocks, stream)) return;
+    }
+    if constexpr (D == 16 && std::is_same<T, bf16_t>::value) {
+        // bf16 activations: the block form (srnl_ut.hip).  VH_SCAN_UT = 0 selects the
+        // stepped form below instead.
+        const char* ut = std::getenv("VH_SCAN_UT");
+        if (!(ut && ut[0] == '0')) {
+            ScanParams up = sp;
+            scan16_ut_packing(lines, sp.heads, &up.lines_per_wave, &up.tiles_per_wave);
+            if (launch_scan16_ut(up, stream)) return;
+        }
     }
     if constexpr (D == 16) {
         const int nl = sp.lines_per_wave, tcw = sp.tiles_per_wave;
@@ -1245,6 +1257,28 @@ void scan16_packing(int64_t lines, int64_t heads, int* nl, int* tcw) {
     }
     if (heads % 2 == 0 && lines >= 4 * 1024) {
         *nl = 2;
+        *tcw = 2;
+    } else {
+        *nl = 1;
+        *tcw = 4;
+    }
+}
+
+// Packing of the block-form scan (srnl_ut.hip, 200-310 VGPRs: one or two waves per SIMD).
+// Measured on MI355X at the Tiny stages (B = 128, scan launches alone): 1 x 4 for 1024
+// lines (chunk 56: 270 us; 1 x 2 301 us), 1 x 2 for 2048 (chunk 28: 104 us; 1 x 4 217 us),
+// 2 x 2 for 4096 and 8192 (chunks 14 and 7: 56.5 and 53 us; 4 x 4 71 and 68 us).
+// VH_SCAN_PACK overrides it as for the stepped form.
+void scan16_ut_packing(int64_t lines, int64_t heads, int* nl, int* tcw) {
+    if (std::getenv("VH_SCAN_PACK")) {
+        scan16_packing(lines, heads, nl, tcw);
+        return;
+    }
+    if (heads % 2 == 0 && lines >= 4 * 1024) {
+        *nl = 2;
+        *tcw = 2;
+    } else if (lines >= 2 * 1024) {
+        *nl = 1;
         *tcw = 2;
     } else {
         *nl = 1;

@@ -308,6 +308,9 @@ struct FuseParams {
 // any other case.  scan_wide_waves picks the waves per line for a line count;
 // token_blocks > 1 selects the token-block mode (blocks of the chunk composed).
 int scan_wide_waves(int64_t lines, int head_dim);
+// Scan for head_dim 16 with bf16 activations in the block form (srnl_ut.hip), packed as
+// sp.lines_per_wave x sp.tiles_per_wave like srnl_scan16_kernel.
+bool launch_scan16_ut(const ScanParams& sp, hipStream_t stream);
 bool launch_scan_wide(const ScanParams& sp, int io_dtype, int head_dim, int waves, int token_blocks,
                       hipStream_t stream);
 
