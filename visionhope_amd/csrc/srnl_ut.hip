@@ -89,8 +89,8 @@ __global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) 
     static_assert((TCW == 2 || TCW == 4) && NL <= TCW, "tile packing");
     constexpr int D = 16, TT = 16 * TCW, S = TT / NL, TPL = TCW / NL, DKS = TT + 4;
     __shared__ __align__(16) float kT[D * DKS];     // normalised keys [feature][slot]
-    __shared__ __align__(16) float dT[D * DKS];     // k - v [feature][slot]
-    __shared__ __align__(16) float tk[5 * TT];      // per slot: eta^, cl, cl - log2 alpha, a_{t-1}, w
+    __shared__ __align__(16) float ndT[D * DKS];    // v - k [feature][slot]
+    __shared__ __align__(16) float tk[4 * TT];      // per slot: rho, kappa, -a_{t-1}, w
     __shared__ __align__(16) float Lc[TCW * 256];   // per tile: L[s][t] at [t][s]
     __shared__ __align__(16) float Zs[TCW * 256];   // per tile: Z[s][f] at [f][s]
     __shared__ __align__(16) float gr[NL * 2 * D];  // per line: e, a (gate operand rows)
@@ -232,11 +232,11 @@ __global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) 
                 const int t = 16 * tc + i16;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float kv = kacc[tc][j] * inv, df = kv - vacc[tc][j];
+                    const float kv = kacc[tc][j] * inv, nd = vacc[tc][j] - kv;
                     kn4[tc][j] = kv;
-                    dsq[tc] += df * df;
+                    dsq[tc] += nd * nd;
                     kT[(4 * q + j) * DKS + t] = kv;
-                    dT[(4 * q + j) * DKS + t] = df;
+                    ndT[(4 * q + j) * DKS + t] = nd;
                 }
             }
 #pragma unroll
@@ -246,8 +246,13 @@ __global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) 
                              : (q == 1 ? v[1 % TCW] : v[0]))
             float alpha, eff;
             token_gates_fast(p.k, VH_OWN(pe), VH_OWN(pq), VH_OWN(dsq), VH_OWN(ksq), alpha, eff);
-            // per-slot scalars; a tile is one DPP row, where cl is the inclusive prefix sum
-            // of log2 alpha and the block decay a_15 is 2^cl at its last slot
+            // Per-slot scalars.  A tile is one DPP row, where cl is the inclusive prefix sum
+            // of log2 alpha; the block decay a_15 is 2^cl at its last slot (tot).  The
+            // triangle's ratio a_{t-1} / a_s = 2^(clx_t - cl_s) (clx = cl - log2 alpha) is
+            // split into a row factor rho_s = eta^_s 2^(m - cl_s) and a column factor
+            // kappa_t = 2^(clx_t - m) about the block's midpoint m = tot / 2: both exponents
+            // stay within |tot| / 2 <= 116 (alpha >= sigmoid(-10) per token), so neither
+            // factor overflows.
             const bool valid = slot_lane && my_slot < cnt;
             const float la = valid ? __builtin_amdgcn_logf(alpha) : 0.f;
             const float eh = valid ? eff : 0.f;
@@ -256,20 +261,19 @@ __global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) 
             cl += row_shr<2>(cl);
             cl += row_shr<4>(cl);
             cl += row_shr<8>(cl);
-            float tot[TCW], decay[TCW];
+            float decay[TCW], tots[TCW];
 #pragma unroll
             for (int tc = 0; tc < TCW; ++tc) {
-                tot[tc] = readlane_f(cl, 16 * tc + 15);
-                decay[tc] = __builtin_amdgcn_exp2f(tot[tc]);
+                tots[tc] = readlane_f(cl, 16 * tc + 15);
+                decay[tc] = __builtin_amdgcn_exp2f(tots[tc]);
             }
-            const float my_tot = VH_OWN(tot);
+            const float tot = VH_OWN(tots), mid = 0.5f * tot, clx = cl - la;
 #undef VH_OWN
             if (slot_lane) {
-                tk[lane] = eh;
-                tk[TT + lane] = cl;
-                tk[2 * TT + lane] = cl - la;
-                tk[3 * TT + lane] = __builtin_amdgcn_exp2f(cl - la);
-                tk[4 * TT + lane] = eh * __builtin_amdgcn_exp2f(my_tot - cl);
+                tk[lane] = eh * __builtin_amdgcn_exp2f(mid - cl);            // rho
+                tk[TT + lane] = __builtin_amdgcn_exp2f(clx - mid);           // kappa
+                tk[2 * TT + lane] = -__builtin_amdgcn_exp2f(clx);            // -a_{t-1}
+                tk[3 * TT + lane] = eh * __builtin_amdgcn_exp2f(tot - cl);   // w
             }
             // prefetch the next tile's x operands
             {
@@ -280,27 +284,25 @@ __global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) 
                 if (have_next) issue_tile(ncc, nbase, min(S, C - nbase), xr, xvalid);
             }
             __syncthreads();
-            // ---- Gram tiles P = K^T K (lane 16 q + t, entry j: P[4q + j][t]) and L ----
-            {
-                v4s kh[TCW], kl[TCW];
+            // ---- L = diag(rho) K^T K diag(kappa), strict upper triangle (lane 16 q + t,
+            //      entry j: L[4q + j][t]), stored by columns: Lc[tc][t][s] = L[s][t] ----
 #pragma unroll
-                for (int tc = 0; tc < TCW; ++tc) split4(kn4[tc], kh[tc], kl[tc]);
+            for (int tc = 0; tc < TCW; ++tc) {
+                const float rho = tk[16 * tc + i16], kap = tk[TT + 16 * tc + i16];
+                float ka[4], kb[4];
 #pragma unroll
-                for (int tc = 0; tc < TCW; ++tc) {
-                    const v4f P = mma3(kh[tc], kl[tc], kh[tc], kl[tc], v4f{0.f, 0.f, 0.f, 0.f});
-                    const float4 eh4 = ld4(tk + 16 * tc + 4 * q);
-                    const float4 cl4 = ld4(tk + TT + 16 * tc + 4 * q);
-                    const float clx = tk[2 * TT + 16 * tc + i16];
-                    const float ehs[4] = {eh4.x, eh4.y, eh4.z, eh4.w}, cls[4] = {cl4.x, cl4.y, cl4.z, cl4.w};
-                    float lv[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float ratio = __builtin_amdgcn_exp2f(clx - cls[j]);   // <= 1 where used
-                        const float val = ehs[j] * ratio * P[j];
-                        lv[j] = (4 * q + j < i16) ? val : 0.f;
-                    }
-                    *reinterpret_cast<float4*>(Lc + (16 * tc + i16) * 16 + 4 * q) = make_float4(lv[0], lv[1], lv[2], lv[3]);
+                for (int j = 0; j < 4; ++j) {
+                    ka[j] = kn4[tc][j] * rho;
+                    kb[j] = kn4[tc][j] * kap;
                 }
+                v4s kah, kal, kbh, kbl;
+                split4(ka, kah, kal);
+                split4(kb, kbh, kbl);
+                const v4f P = mma3(kah, kal, kbh, kbl, v4f{0.f, 0.f, 0.f, 0.f});
+                float lv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) lv[j] = (4 * q + j < i16) ? P[j] : 0.f;
+                *reinterpret_cast<float4*>(Lc + (16 * tc + i16) * 16 + 4 * q) = make_float4(lv[0], lv[1], lv[2], lv[3]);
             }
             __syncthreads();
             // ---- Z = (I + L)^-1 W K^T: lane 16 b + f solves column f of tile b from the last
@@ -310,7 +312,7 @@ __global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) 
 #pragma unroll
                 for (int s0 = 0; s0 < 16; s0 += 4) {
                     const float4 k4 = ld4(kT + i16 * DKS + 16 * q + s0);
-                    const float4 w4 = ld4(tk + 4 * TT + 16 * q + s0);
+                    const float4 w4 = ld4(tk + 3 * TT + 16 * q + s0);
                     acc[s0] = k4.x * w4.x; acc[s0 + 1] = k4.y * w4.y;
                     acc[s0 + 2] = k4.z * w4.z; acc[s0 + 3] = k4.w * w4.w;
                 }
@@ -353,11 +355,11 @@ __global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) 
                 // -(k a_{t-1}) and -delta with slot 4q + j and feature f
                 const float4 z4 = ld4(Zs + (16 * tc + i16) * 16 + 4 * q);
                 const float4 k4 = ld4(kT + i16 * DKS + 16 * tc + 4 * q);
-                const float4 d4 = ld4(dT + i16 * DKS + 16 * tc + 4 * q);
-                const float4 a4 = ld4(tk + 3 * TT + 16 * tc + 4 * q);
+                const float4 d4 = ld4(ndT + i16 * DKS + 16 * tc + 4 * q);
+                const float4 a4 = ld4(tk + 2 * TT + 16 * tc + 4 * q);
                 const float zv[4] = {z4.x, z4.y, z4.z, z4.w};
-                const float nka[4] = {-k4.x * a4.x, -k4.y * a4.y, -k4.z * a4.z, -k4.w * a4.w};
-                const float ndl[4] = {-d4.x, -d4.y, -d4.z, -d4.w};
+                const float nka[4] = {k4.x * a4.x, k4.y * a4.y, k4.z * a4.z, k4.w * a4.w};
+                const float ndl[4] = {d4.x, d4.y, d4.z, d4.w};
                 v4s zh, zl;
                 split4(zv, zh, zl);
                 const v4f dI = diag4(decay[tc], q, i16);
