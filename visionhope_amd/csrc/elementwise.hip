@@ -6,6 +6,7 @@
 // write fp32 results once.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "vh_common.h"
 
@@ -569,8 +570,8 @@ __global__ __launch_bounds__(256) void grn_onepass8_kernel(const T* __restrict__
                                                           const float* __restrict__ beta, float* __restrict__ gx,
                                                           float* __restrict__ inv_den, TO* __restrict__ y,
                                                           uint32_t* __restrict__ sync, float* __restrict__ partial,
-                                                          int C, int S, int pieces, int b0, float eps) {
-    extern __shared__ float red[];   // [R][C] partial sums, then [C] gx
+                                                          int C, int S, int pieces, int b0, float eps, int piece_rows) {
+    extern __shared__ __align__(16) float red[];   // [R][C] partial sums, then [C] gx; FP32 staging
     __shared__ uint32_t word;
     __shared__ float wsum[4];
     const int t = static_cast<int>(threadIdx.x);
@@ -583,7 +584,7 @@ __global__ __launch_bounds__(256) void grn_onepass8_kernel(const T* __restrict__
     uint32_t* const done = counted + kGrnSyncWords / 2;
     const int g = t % G, rr = t / G;
     const bool lane_rows = rr < R;
-    const int s0 = piece * R * V, s1 = min(S, s0 + R * V);
+    const int s0 = piece * piece_rows, s1 = min(S, s0 + piece_rows);   // piece_rows <= R * V
     const T* xb = x + static_cast<int64_t>(b) * S * C + g * 8;
     Pack8<T> raw[V];
 #pragma unroll
@@ -664,7 +665,45 @@ __global__ __launch_bounds__(256) void grn_onepass8_kernel(const T* __restrict__
         for (int c = t; c < C; c += nt) gx[static_cast<int64_t>(b) * C + c] = gsh[c];
         if (t == 0) inv_den[b] = inv;
     }
-    if (lane_rows) {
+    if constexpr (sizeof(TO) == 4) {
+        // FP32 output: thread t = rr * G + g writes bytes [32 t, 32 t + 32) of the R * C
+        // outputs of step v, so a wave's outputs are one contiguous 2 KB range.  They go
+        // through the wave's own 2 KB of LDS and out in two stores whose 64 lanes write
+        // consecutive 16-byte chunks (one contiguous 1 KB run per instruction); the
+        // exchange stays inside the wave.
+        float sc[8], bt[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = lane_rows ? g * 8 + j : j;
+            sc[j] = 1.f + gamma[c] * (gsh[c] * inv);
+            bt[j] = beta[c];
+        }
+        float4* const wst = reinterpret_cast<float4*>(red + ((R * C + 3) & ~3)) + (t >> 6) * 128;
+        const int wl = t & 63;
+        char* const yb = reinterpret_cast<char*>(y + static_cast<int64_t>(b) * S * C);
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const int sv = s0 + v * R;
+            if (sv >= s1) break;
+            float f[8];
+            pack8_to_f32<T>(raw[v], f);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = f[j] * sc[j] + bt[j];
+            wst[2 * wl] = make_float4(f[0], f[1], f[2], f[3]);
+            wst[2 * wl + 1] = make_float4(f[4], f[5], f[6], f[7]);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int64_t nbytes = static_cast<int64_t>(min(R, s1 - sv)) * C * 4;
+            const int64_t o0 = static_cast<int64_t>(t >> 6) * 2048 + 16 * wl;
+            const float4 c0 = wst[wl], c1 = wst[64 + wl];
+            if (o0 < nbytes) *reinterpret_cast<float4*>(yb + static_cast<int64_t>(sv) * C * 4 + o0) = c0;
+            if (o0 + 1024 < nbytes) *reinterpret_cast<float4*>(yb + static_cast<int64_t>(sv) * C * 4 + o0 + 1024) = c1;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    } else if (lane_rows) {
         float sc[8], bt[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -753,7 +792,12 @@ __global__ __launch_bounds__(256) void layernorm_nhwc_kernel(const T* __restrict
 // ADD: the normalised row is x + r rounded to T (a residual add), which is also stored
 // to x_sum, so the sum is read once instead of being written by one kernel and read by
 // the next.
-template <typename T, typename TO, int GP, bool ADD = false>
+// STAGE: the workgroup's output rows (one contiguous range of rows * C values) are
+// assembled in LDS and stored in 16-byte chunks by consecutive lanes, so every store
+// instruction of a wave writes one contiguous 1 KB run (a lane's own 8 outputs would
+// leave 16-byte gaps in each instruction's footprint).  Dynamic LDS of
+// (256 / LPR) * C * sizeof(TO) bytes.
+template <typename T, typename TO, int GP, bool ADD = false, bool STAGE = false>
 __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                              const float* __restrict__ bias, TO* __restrict__ y,
                                                              float* __restrict__ mean_out,
@@ -792,16 +836,39 @@ __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restric
         }
     for (int off = LPR / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
     const float rstd = 1.f / sqrtf(sq / static_cast<float>(C) + eps);
-    if (!active) return;
+    if constexpr (STAGE) {
+        extern __shared__ __align__(16) unsigned char ln_stage[];
+        TO* st = reinterpret_cast<TO*>(ln_stage) + (threadIdx.x >> lpr_log2) * C;
 #pragma unroll
-    for (int k = 0; k < GP; ++k) {
-        const int c = (k * LPR + lane) * 8;
-        float wv[8], bv[8], o[8];
-        load8<float>(w + c, wv);
-        load8<float>(bias + c, bv);
+        for (int k = 0; k < GP; ++k) {
+            const int c = (k * LPR + lane) * 8;
+            float wv[8], bv[8], o[8];
+            load8<float>(w + c, wv);
+            load8<float>(bias + c, bv);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = v[k][j] * rstd * wv[j] + bv[j];
-        store8<TO>(y + row * C + c, o);
+            for (int j = 0; j < 8; ++j) o[j] = v[k][j] * rstd * wv[j] + bv[j];
+            store8<TO>(st + c, o);
+        }
+        __syncthreads();
+        const int64_t row0 = static_cast<int64_t>(blockIdx.x) * (256 >> lpr_log2);
+        const int64_t nr = min(static_cast<int64_t>(256 >> lpr_log2), rows - row0);
+        const int n16 = static_cast<int>(nr * C * static_cast<int64_t>(sizeof(TO)) / 16);
+        const uint4* src = reinterpret_cast<const uint4*>(ln_stage);
+        uint4* dst = reinterpret_cast<uint4*>(y + row0 * C);
+        for (int m = threadIdx.x; m < n16; m += 256) dst[m] = src[m];
+        if (!active) return;
+    } else {
+        if (!active) return;
+#pragma unroll
+        for (int k = 0; k < GP; ++k) {
+            const int c = (k * LPR + lane) * 8;
+            float wv[8], bv[8], o[8];
+            load8<float>(w + c, wv);
+            load8<float>(bias + c, bv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = v[k][j] * rstd * wv[j] + bv[j];
+            store8<TO>(y + row * C + c, o);
+        }
     }
     if (lane == 0) {
         if (mean_out) mean_out[row] = mean;
@@ -929,6 +996,20 @@ bool launch_ln_nhwc8(const void* x, const float* w, const float* b, void* yv, fl
     const unsigned blocks = static_cast<unsigned>((rows + (256 >> lg) - 1) / (256 >> lg));
     const T* xp = static_cast<const T*>(x);
     TO* y = static_cast<TO*>(yv);
+    // Staged stores while the workgroup's rows fit in 32 KB of LDS (GP <= 4 for FP32 out).
+    const size_t stage = static_cast<size_t>(256 >> lg) * C * sizeof(TO);
+    const char* env = std::getenv("VH_LN_STAGE");
+    if (stage <= 32768 && !(env && env[0] == '0')) {
+        switch (gp) {
+#define VH_LN8S(G)                                                                                              \
+    case G:                                                                                                     \
+        hipLaunchKernelGGL((layernorm_nhwc8_kernel<T, TO, G, false, true>), dim3(blocks), dim3(256), stage, s, xp, \
+                           w, b, y, mean, rstd, rows, C, lg, eps);                                              \
+        return true;
+            VH_LN8S(1) VH_LN8S(2) VH_LN8S(3) VH_LN8S(4)
+#undef VH_LN8S
+        }
+    }
     switch (gp) {
 #define VH_LN8(G)                                                                                        \
     case G:                                                                                              \
@@ -1126,11 +1207,25 @@ static size_t grn_sync_bytes() {
 // image, so the map qualifies only while those reads stay within 1/8 of the piece's own x
 // bytes (R v C elem_bytes); wide maps with few rows per piece (e.g. 32x32x1792, 64 pieces
 // of 16 rows) take the two-pass kernels instead.
-static int64_t grn_onepass_pieces(int64_t C, int64_t S, int elem_bytes, int v = kGrnVec) {
+// Pieces per image of the one-pass kernel: at least 5 and as few as 32 rows per thread
+// allow, balanced (every piece but the last holds *piece_rows rows, *vrows >= rows per
+// thread).  Fewer pieces mean fewer workgroups waiting on each other, more mean more
+// workgroups in flight; measured on MI355X (B = 128, bf16 in, FP32 out): 56x56x96 at 5
+// pieces (32 rows per thread) 0.78 of the HBM peak against 0.68 at 10 and 0.56 at 19;
+// 28x28x192 0.60 / 0.64 / 0.65 / 0.65 at 3 / 4 / 5 / 8.  Returns 0 where the one-pass
+// kernel does not apply (fewer than 2 pieces, or the other pieces' partial sums a piece
+// reads would not be small next to its own x).
+static int64_t grn_onepass_plan(int64_t C, int64_t S, int elem_bytes, int64_t* piece_rows, int* vrows) {
     if (C % 8 != 0 || C / 8 > 256) return 0;
-    const int64_t rows = (256 / (C / 8)) * v;
+    const int64_t R = 256 / (C / 8);
+    const int64_t want = std::min<int64_t>(std::max<int64_t>(5, (S + 4 * kGrnVec * R - 1) / (4 * kGrnVec * R)),
+                                           (S + R - 1) / R);
+    const int64_t rows = (S + want - 1) / want;
     const int64_t pieces = (S + rows - 1) / rows;
-    if (pieces > kGrnMaxPieces || pieces * 4 * 8 > rows * elem_bytes) return 0;
+    const int64_t v = (rows + R - 1) / R;
+    if (pieces < 2 || pieces > kGrnMaxPieces || v > 4 * kGrnVec || pieces * 4 * 8 > rows * elem_bytes) return 0;
+    if (piece_rows) *piece_rows = rows;
+    if (vrows) *vrows = v <= kGrnVec ? kGrnVec : v <= 2 * kGrnVec ? 2 * kGrnVec : 4 * kGrnVec;
     return pieces;
 }
 
@@ -1140,9 +1235,8 @@ size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W) {
     const int64_t S = H * W;
     const int64_t rows = grn_rows_per_slab(B, S);
     int64_t nslab = std::max<int64_t>((S + rows - 1) / rows, (S + kGrnRowsPerSlab - 1) / kGrnRowsPerSlab);
-    // the one-pass kernel's pieces at either rows-per-thread choice (fp32 qualifies whenever a
-    // 16-bit type does)
-    nslab = std::max({nslab, grn_onepass_pieces(C, S, 4, kGrnVec), grn_onepass_pieces(C, S, 4, 2 * kGrnVec)});
+    // the one-pass kernel's pieces (fp32 qualifies whenever a 16-bit type does)
+    nslab = std::max(nslab, grn_onepass_plan(C, S, 4, nullptr, nullptr));
     return grn_sync_bytes() + static_cast<size_t>(B * nslab * C) * sizeof(float);
 }
 
@@ -1167,32 +1261,36 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
     uint32_t* sync = static_cast<uint32_t*>(workspace);
     float* partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + grn_sync_bytes());
     const int64_t total = B * S * C;
-    // 16 rows per thread (half the pieces, half the synchronisations; measured 5% faster at
-    // 56x56x96 and 28x28x192) unless the image would then be a single piece
-    const int eb = dtype_bytes(io_dtype);
-    int vrows = 2 * kGrnVec;
-    int64_t pieces = grn_onepass_pieces(C, S, eb, vrows);
-    if (pieces < 2) pieces = grn_onepass_pieces(C, S, eb, vrows = kGrnVec);
+    int vrows = 0;
+    int64_t piece_rows = 0;
+    const int64_t pieces = grn_onepass_plan(C, S, dtype_bytes(io_dtype), &piece_rows, &vrows);
     if (pieces > 0 && grn_vectorised(C, x, y) && B * S * C < (int64_t(1) << 31)) {
         const int G = static_cast<int>(C / 8);
         const unsigned threads = static_cast<unsigned>((G * (256 / G) + 63) / 64 * 64);
-        const size_t lds = static_cast<size_t>(256 / G) * static_cast<size_t>(C) * sizeof(float);
+        // [R][C] partial sums (rounded up to 16 bytes), then 2 KB of staging per wave for FP32 output
+        const size_t lds = ((static_cast<size_t>(256 / G) * static_cast<size_t>(C) + 3) & ~size_t(3)) * sizeof(float) +
+                           static_cast<size_t>(threads / 64) * 2048;
         int rc = dispatch_t(io_dtype, [&](auto tv) {
             using T = decltype(tv);
             dispatch_t(y_dtype, [&](auto ov) {
                 using TO = decltype(ov);
                 for (int64_t b0 = 0; b0 < B; b0 += kGrnSyncImages) {
                     const int64_t nb = std::min<int64_t>(kGrnSyncImages, B - b0);
-                    if (vrows == 2 * kGrnVec)
+                    if (vrows == 4 * kGrnVec)
+                        hipLaunchKernelGGL((grn_onepass8_kernel<T, TO, 4 * kGrnVec>), dim3(static_cast<unsigned>(nb * pieces)),
+                                           dim3(threads), lds, s, static_cast<const T*>(x), gamma, beta, gx, inv_den,
+                                           static_cast<TO*>(y), sync, partial, static_cast<int>(C), static_cast<int>(S),
+                                           static_cast<int>(pieces), static_cast<int>(b0), eps, static_cast<int>(piece_rows));
+                    else if (vrows == 2 * kGrnVec)
                         hipLaunchKernelGGL((grn_onepass8_kernel<T, TO, 2 * kGrnVec>), dim3(static_cast<unsigned>(nb * pieces)),
                                            dim3(threads), lds, s, static_cast<const T*>(x), gamma, beta, gx, inv_den,
                                            static_cast<TO*>(y), sync, partial, static_cast<int>(C), static_cast<int>(S),
-                                           static_cast<int>(pieces), static_cast<int>(b0), eps);
+                                           static_cast<int>(pieces), static_cast<int>(b0), eps, static_cast<int>(piece_rows));
                     else
                         hipLaunchKernelGGL((grn_onepass8_kernel<T, TO, kGrnVec>), dim3(static_cast<unsigned>(nb * pieces)),
                                            dim3(threads), lds, s, static_cast<const T*>(x), gamma, beta, gx, inv_den,
                                            static_cast<TO*>(y), sync, partial, static_cast<int>(C), static_cast<int>(S),
-                                           static_cast<int>(pieces), static_cast<int>(b0), eps);
+                                           static_cast<int>(pieces), static_cast<int>(b0), eps, static_cast<int>(piece_rows));
                 }
             });
         });
