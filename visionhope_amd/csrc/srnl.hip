@@ -847,8 +847,13 @@ __global__ __launch_bounds__(256) void srnl_fuse_readout_kernel(const FuseParams
         const int64_t ch = t / chunk_of(p.chunk, r);
         const float* m = p.states + (((b * 4 + r) * p.heads + head) * p.max_chunks + ch) * D * D + i * D;
         float dot = 0.f;
+        if (p.split_states) {
 #pragma unroll
-        for (int j = 0; j < D; ++j) dot += m[j] * qv[j];
+            for (int j = 0; j < D; ++j) dot += split_state_at(m, j) * qv[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < D; ++j) dot += m[j] * qv[j];
+        }
         const float y = dot * qinv;
         const float contrib = y + p.skip[(p.skip_per_dir ? r * p.C : 0) + c] * xval;
         const float weighted = p.wgt[r * p.C + c] * contrib;
@@ -907,10 +912,18 @@ __device__ __forceinline__ float xraw_sumsq(const XRaw<T, D>& r) {
 // y = M q~ for 16 pixels on the matrix cores: lane l = 16 g + n gives M row n (of the
 // 16-channel half) and pixel n's query over the K-range [g D/4, (g+1) D/4), and receives
 // channels 4g..4g+3 of the half for pixel n.  bf16: M as hi + lo, q exact.
-template <typename T, int D>
+// SPLIT (bf16, D = 16): m holds the bits of the stored bf16 hi[4], lo[4] pair.
+template <typename T, int D, bool SPLIT = false>
 __device__ __forceinline__ v4f readout_mfma(const float (&m)[D / 4], const XRaw<T, D>& qr) {
     v4f y = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (std::is_same<T, bf16_t>::value) {
+    if constexpr (SPLIT) {
+        static_assert(std::is_same<T, bf16_t>::value && D == 16, "split states: bf16, head_dim 16");
+        const v4s hi = __builtin_bit_cast(v4s, make_uint2(__float_as_uint(m[0]), __float_as_uint(m[1])));
+        const v4s lo = __builtin_bit_cast(v4s, make_uint2(__float_as_uint(m[2]), __float_as_uint(m[3])));
+        const v4s qs = bf16x4_bits(qr.v);
+        y = mfma_bf16(hi, qs, y);
+        y = mfma_bf16(lo, qs, y);
+    } else if constexpr (std::is_same<T, bf16_t>::value) {
         using Bf = BfOp<D>;
         typename Bf::type hi, lo;
         Bf::split(m, hi, lo);
@@ -941,7 +954,7 @@ __device__ __forceinline__ v4f readout_mfma(const float (&m)[D / 4], const XRaw<
 // once, and the row loads are issued before the column work.  head_dim 32 runs the two
 // halves one after the other.
 // ---------------------------------------------------------------------------
-template <typename T, typename TO, int D>
+template <typename T, typename TO, int D, bool SPLIT = false>
 __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams p, const int64_t tiles_h,
                                                                 const int64_t tiles_w) {
     constexpr int REC = 20, PER = 4, KQ = D / 4;   // 16 channels + 4 padding floats per pixel record
@@ -957,17 +970,19 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
     const int H = static_cast<int>(p.H), W = static_cast<int>(p.W);
     const int64_t C = p.C, L = p.H * p.W;
+    const int Ci = static_cast<int>(C);
     const int h0 = static_cast<int>(th) * 16, w0 = static_cast<int>(tw) * 16;
-    const T* qb = static_cast<const T*>(p.q) + b * L * C + head * D + KQ * g;
+    // Workgroup-uniform bases and 32-bit lane offsets (the host requires H * W * C < 2^31
+    // and per-line state blocks below 2^31 floats), so loads take a scalar base.
+    const int64_t img = b * L * C + head * D;
+    const T* qb = static_cast<const T*>(p.q) + img;
     const float* st[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-        st[r] = p.states + ((b * 4 + r) * p.heads + head) * p.max_chunks * (D * D) + KQ * g;
-    auto load_q = [&](int h, int w) {
-        return load_xraw<T, D>(qb + (static_cast<int64_t>(h) * W + w) * C);
-    };
+    for (int r = 0; r < 4; ++r) st[r] = p.states + ((b * 4 + r) * p.heads + head) * p.max_chunks * (D * D);
+    auto pix = [&](int h, int w) { return (h * W + w) * Ci; };
+    auto load_q = [&](int h, int w) { return load_xraw<T, D>(qb + (pix(h, w) + KQ * g)); };
     auto load_m = [&](const float* base, int chunk, int row, float (&m)[KQ]) {
-        const float* src = base + static_cast<int64_t>(chunk) * (D * D) + row * D;
+        const float* src = base + (chunk * (D * D) + row * D + KQ * g);
 #pragma unroll
         for (int j = 0; j < KQ; j += 4) {
             const float4 f = *reinterpret_cast<const float4*>(src + j);
@@ -978,7 +993,8 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
 #pragma unroll
     for (int half = 0; half < D / 16; ++half) {
         const int64_t cbase = head * D + 16 * half + 4 * g;   // this lane's 4 output channels
-        const T* xb = static_cast<const T*>(p.x) + b * L * C + cbase;
+        const int cl = 16 * half + 4 * g;                      // ... relative to the head
+        const T* xb = static_cast<const T*>(p.x) + img;
         const int mrow = 16 * half + n;                        // M row of this lane (A operand)
 
         // Row pass operands (directions 0, 1): tile row hh = 4 wv + k, lane n holds pixel
@@ -991,22 +1007,22 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
         for (int k = 0; k < PER; ++k) {
             const int h = min(h0 + 4 * wv + k, H - 1);
             rq[k] = load_q(h, wr);
-            rx[k] = *reinterpret_cast<const Raw*>(xb + (static_cast<int64_t>(h) * W + wr) * C);
+            rx[k] = *reinterpret_cast<const Raw*>(xb + (pix(h, wr) + cl));
             load_m(st[0], h, mrow, m0[k]);
             load_m(st[1], H - 1 - h, mrow, m1[k]);
-            if (p.aux) ra[k] = *reinterpret_cast<const Raw*>(static_cast<const T*>(p.aux) + (b * L + static_cast<int64_t>(h) * W + wr) * C + cbase);
+            if (p.aux) ra[k] = *reinterpret_cast<const Raw*>(static_cast<const T*>(p.aux) + img + (pix(h, wr) + cl));
         }
 
         // Column pass (directions 2, 3): tile column ww = 4 wv + k, lane n holds pixel
         // (h0 + n, w0 + ww).
         float wt[4][4], sk[4][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                wt[r][j] = p.wgt[r * C + cbase + j];
-                sk[r][j] = p.skip[(p.skip_per_dir ? r * C : 0) + cbase + j];
-            }
+        for (int r = 0; r < 4; ++r) {
+            const float4 w4 = *reinterpret_cast<const float4*>(p.wgt + r * C + cbase);
+            const float4 s4 = *reinterpret_cast<const float4*>(p.skip + (p.skip_per_dir ? r * C : 0) + cbase);
+            wt[r][0] = w4.x; wt[r][1] = w4.y; wt[r][2] = w4.z; wt[r][3] = w4.w;
+            sk[r][0] = s4.x; sk[r][1] = s4.y; sk[r][2] = s4.z; sk[r][3] = s4.w;
+        }
         {
             XRaw<T, D> cq[PER];
             Raw cx[PER];
@@ -1015,7 +1031,7 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
             for (int k = 0; k < PER; ++k) {
                 const int w = min(w0 + 4 * wv + k, W - 1);
                 cq[k] = load_q(hc, w);
-                cx[k] = *reinterpret_cast<const Raw*>(xb + (static_cast<int64_t>(hc) * W + w) * C);
+                cx[k] = *reinterpret_cast<const Raw*>(xb + (pix(hc, w) + cl));
                 load_m(st[2], w, mrow, m2[k]);
                 load_m(st[3], W - 1 - w, mrow, m3[k]);
             }
@@ -1023,9 +1039,10 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
             for (int k = 0; k < PER; ++k) {
                 float xv[4];
                 raw4_to_f32<T>(cx[k], xv);
-                const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(xraw_sumsq<T, D>(cq[k]))), 1e-12f);
-                const v4f y2 = readout_mfma<T, D>(m2[k], cq[k]);
-                const v4f y3 = readout_mfma<T, D>(m3[k], cq[k]);
+                // 1 / max(|q|, 1e-12) = rsqrt(max(|q|^2, 1e-24)) (hardware reciprocal square root)
+                const float inv = __builtin_amdgcn_rsqf(fmaxf(xor16_32_sum(xraw_sumsq<T, D>(cq[k])), 1e-24f));
+                const v4f y2 = readout_mfma<T, D, SPLIT>(m2[k], cq[k]);
+                const v4f y3 = readout_mfma<T, D, SPLIT>(m3[k], cq[k]);
                 float c23[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
@@ -1042,9 +1059,9 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
             const int hh = 4 * wv + k, h = h0 + hh;
             float xv[4];
             raw4_to_f32<T>(rx[k], xv);
-            const float inv = 1.f / fmaxf(sqrtf(xor16_32_sum(xraw_sumsq<T, D>(rq[k]))), 1e-12f);
-            const v4f y0 = readout_mfma<T, D>(m0[k], rq[k]);
-            const v4f y1 = readout_mfma<T, D>(m1[k], rq[k]);
+            const float inv = __builtin_amdgcn_rsqf(fmaxf(xor16_32_sum(xraw_sumsq<T, D>(rq[k])), 1e-24f));
+            const v4f y0 = readout_mfma<T, D, SPLIT>(m0[k], rq[k]);
+            const v4f y1 = readout_mfma<T, D, SPLIT>(m1[k], rq[k]);
             const float4 c23 = *reinterpret_cast<const float4*>(col + (n * 16 + hh) * REC + 4 * g);
             const float c23v[4] = {c23.x, c23.y, c23.z, c23.w};
             float o[4];
@@ -1059,7 +1076,7 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
                 for (int j = 0; j < 4; ++j) o[j] += a[j];
             }
             if (h < H && w < W) {
-                const int64_t at = (b * L + static_cast<int64_t>(h) * W + w) * C + cbase;
+                const int64_t at = img + (pix(h, w) + cl);
                 if constexpr (sizeof(TO) == 4) {
                     *reinterpret_cast<float4*>(static_cast<float*>(p.out) + at) = make_float4(o[0], o[1], o[2], o[3]);
                 } else if constexpr (std::is_same<TO, bf16_t>::value) {
@@ -1156,6 +1173,18 @@ int wide_waves(int64_t lines, int d) {
 
 void scan16_ut_packing(int64_t lines, int64_t heads, int* nl, int* tcw);
 
+// The block-form scan (bf16 activations, head_dim 16, at least 1024 lines; fewer take the
+// wide kernel) on channels-last maps stores its chunk-start states split into bf16 hi + lo
+// pairs for the readouts (split_state_at, readout_mfma).  The scan and the readout entry
+// points both decide the format here, from the same arguments.
+bool scan_ut_enabled() {
+    const char* ut = std::getenv("VH_SCAN_UT");
+    return !(ut && ut[0] == '0');
+}
+bool state_split_bf16(int io_dtype, int d, int64_t lines, bool spatial) {
+    return io_dtype == VH_DTYPE_BF16 && d == 16 && lines >= 1024 && spatial && scan_ut_enabled();
+}
+
 template <int D, typename T>
 void launch_scan(const ScanParams& sp, hipStream_t stream) {
     const int64_t lines = sp.B * sp.R * sp.heads;
@@ -1173,8 +1202,7 @@ void launch_scan(const ScanParams& sp, hipStream_t stream) {
     if constexpr (D == 16 && std::is_same<T, bf16_t>::value) {
         // bf16 activations: the block form (srnl_ut.hip).  VH_SCAN_UT = 0 selects the
         // stepped form below instead.
-        const char* ut = std::getenv("VH_SCAN_UT");
-        if (!(ut && ut[0] == '0')) {
+        if (scan_ut_enabled()) {
             ScanParams up = sp;
             scan16_ut_packing(lines, sp.heads, &up.lines_per_wave, &up.tiles_per_wave);
             if (launch_scan16_ut(up, stream)) return;
@@ -1335,6 +1363,7 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
     scan16_packing(lines, heads, &sp.lines_per_wave, &sp.tiles_per_wave);
     sp.aligned = x.spatial && R == 4 && chunks[0] == x.W && chunks[1] == x.W && chunks[2] == x.H &&
                  chunks[3] == x.H && x.H * x.W * x.st < (int64_t(1) << 31);
+    sp.split_states = state_split_bf16(io_dtype, d, lines, x.spatial != 0) ? 1 : 0;
     rc = dispatch_d(d, [&](auto dc) {
         constexpr int D = decltype(dc)::value;
         dispatch_t(io_dtype, [&](auto tv) { launch_scan<D, decltype(tv)>(sp, stream); });
@@ -1357,18 +1386,32 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
     fp.skip = skip; fp.skip_per_dir = skip_per_dir; fp.wgt = wgt; fp.out = out; fp.aux = aux;
     fp.B = sp.B; fp.H = H; fp.W = W; fp.C = C; fp.heads = sp.heads;
     for (int r = 0; r < 4; ++r) fp.chunk[r] = sp.chunk[r];
+    fp.split_states = sp.split_states;
     const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q) |
                             reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sp.states) |
-                            reinterpret_cast<uintptr_t>(aux);
+                            reinterpret_cast<uintptr_t>(aux) | reinterpret_cast<uintptr_t>(skip) |
+                            reinterpret_cast<uintptr_t>(wgt);
     const bool out_f32 = out_dtype == VH_DTYPE_F32;
     if ((d == 16 || (d == 32 && io_dtype != VH_DTYPE_F16)) && !per_direction && sp.chunk[0] == W &&
-        sp.chunk[1] == W && sp.chunk[2] == H && sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0) {
+        sp.chunk[1] == W && sp.chunk[2] == H && sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0 &&
+        H * W * C < (int64_t(1) << 31) && sp.max_chunks * d * d < (int64_t(1) << 31)) {
         const int64_t tiles_h = (H + 15) / 16, tiles_w = (W + 15) / 16;
         const int64_t n_tiles = sp.B * sp.heads * tiles_h * tiles_w;
         VH_REQUIRE(n_tiles <= 0x7fffffff, VH_ERR_SHAPE, "SRNL readout grid too large");
         auto go = [&](auto tv, auto dc) {
             using T = decltype(tv);
             constexpr int DD = decltype(dc)::value;
+            if constexpr (std::is_same<T, bf16_t>::value && DD == 16) {
+                if (fp.split_states) {
+                    if (out_f32)
+                        hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD, true>),
+                                           dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0, stream, fp, tiles_h, tiles_w);
+                    else
+                        hipLaunchKernelGGL((srnl_readout_tile_kernel<T, T, DD, true>),
+                                           dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0, stream, fp, tiles_h, tiles_w);
+                    return;
+                }
+            }
             if (out_f32)
                 hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD>), dim3(static_cast<unsigned>(n_tiles)),
                                    dim3(256), 0, stream, fp, tiles_h, tiles_w);
@@ -1518,6 +1561,7 @@ int vh_srnl_spatial_readout(const void* x, const void* q, int32_t io_dtype, cons
     VH_REQUIRE(workspace_bytes >= need, VH_ERR_WORKSPACE, "SRNL workspace needs %zu bytes, got %zu", need,
                workspace_bytes);
     sp.states = const_cast<float*>(static_cast<const float*>(workspace));
+    sp.split_states = state_split_bf16(io_dtype, head_dim, B * 4 * sp.heads, true) ? 1 : 0;
     return run_fuse(sp, x, q, 0, io_dtype, d_skip, skip_per_direction, dir_weight, out, H, W, C, head_dim,
                     static_cast<hipStream_t>(stream), aux, out_dtype);
 }

@@ -53,6 +53,7 @@ struct ScanParams {
     int lines_per_wave;  // head_dim 16: lines packed into one wave (1, 2 or 4)
     int tiles_per_wave;  // head_dim 16: 16-slot column tiles per wave (2 or 4, >= lines_per_wave)
     int aligned;         // spatial input with chunks (W, W, H, H): chunk c of scan r is a row/column
+    int split_states;    // chunk-start states stored as bf16 hi + lo pairs (see state_split_bf16)
     Consts k;
 };
 
@@ -301,7 +302,17 @@ struct FuseParams {
     const void* aux;    // optional [B, H, W, C] io-dtype addend of the fused result
     int64_t B, H, W, C, heads;
     int chunk[4];
+    int split_states;   // states stored as bf16 hi + lo pairs (see state_split_bf16)
 };
+
+// Chunk-start states in the split format: the 16 bytes that hold M[i][4g..4g+3] in FP32
+// hold instead bf16 hi[4] then bf16 lo[4] with hi = bf16(v), lo = bf16(v - hi), the
+// operand pair the bf16 matrix-core readout multiplies (same size, same addressing).
+__device__ __forceinline__ float split_state_at(const float* row, int col) {
+    const uint16_t* u = reinterpret_cast<const uint16_t*>(row + 4 * (col >> 2));
+    const int j = col & 3;
+    return __uint_as_float(static_cast<uint32_t>(u[j]) << 16) + __uint_as_float(static_cast<uint32_t>(u[4 + j]) << 16);
+}
 
 // Scan with one line per workgroup of `waves` waves (srnl_wide.hip): head_dim 16 or 32,
 // fp32 or bf16 activations, vector-aligned rows.  Returns false (nothing launched) for
