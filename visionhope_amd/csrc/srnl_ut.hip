@@ -84,8 +84,11 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 
 }  // namespace
 
+// Two-tile packings run two waves per SIMD (their line counts give 2048 or more waves), so
+// they are held to 256 VGPRs; four-tile packings run one wave per SIMD.
 template <int NL, int TCW, bool SPATIAL>
-__global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(TCW == 2 ? 2 : 1)))
+void srnl_scan16_ut_kernel(const ScanParams p) {
     static_assert((TCW == 2 || TCW == 4) && NL <= TCW, "tile packing");
     constexpr int D = 16, TT = 16 * TCW, S = TT / NL, TPL = TCW / NL, DKS = TT + 4;
     __shared__ __align__(16) float kT[D * DKS];     // normalised keys [feature][slot]
@@ -325,25 +328,40 @@ __global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) 
                     acc[s0] = k4.x * w4.x; acc[s0 + 1] = k4.y * w4.y;
                     acc[s0 + 2] = k4.z * w4.z; acc[s0 + 3] = k4.w * w4.w;
                 }
-                // four columns of L at a time (rows s < v of column v)
-#pragma unroll
-                for (int v0 = 12; v0 >= 0; v0 -= 4) {
-                    float lcol[4][16];
+                // four columns of L at a time (rows s < v of column v); the next group's
+                // loads are issued before the current group's arithmetic
+                float lA[4][16], lB[4][16];
+                auto load_group = [&](int v0, float (&buf)[4][16]) {
 #pragma unroll
                     for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
                         for (int s0 = 0; s0 < v0 + dv; s0 += 4) {
                             const float4 l4 = ld4(Lc + (16 * q + v0 + dv) * 16 + s0);
-                            lcol[dv][s0] = l4.x; lcol[dv][s0 + 1] = l4.y; lcol[dv][s0 + 2] = l4.z; lcol[dv][s0 + 3] = l4.w;
+                            buf[dv][s0] = l4.x; buf[dv][s0 + 1] = l4.y; buf[dv][s0 + 2] = l4.z; buf[dv][s0 + 3] = l4.w;
                         }
+                };
+                auto solve_group = [&](int v0, const float (&buf)[4][16]) {
 #pragma unroll
                     for (int dv = 3; dv >= 0; --dv) {
                         const int v = v0 + dv;
                         zc[v] = acc[v];
 #pragma unroll
-                        for (int s = 0; s < v; ++s) acc[s] -= lcol[dv][s] * zc[v];
+                        for (int s2 = 0; s2 < v; ++s2) acc[s2] -= buf[dv][s2] * zc[v];
                     }
-                }
+                };
+                load_group(12, lA);
+                load_group(8, lB);
+                __builtin_amdgcn_sched_barrier(0);
+                solve_group(12, lA);
+                __builtin_amdgcn_sched_barrier(0);
+                load_group(4, lA);
+                __builtin_amdgcn_sched_barrier(0);
+                solve_group(8, lB);
+                __builtin_amdgcn_sched_barrier(0);
+                load_group(0, lB);
+                __builtin_amdgcn_sched_barrier(0);
+                solve_group(4, lA);
+                solve_group(0, lB);
                 float* dst = Zs + (16 * q + i16) * 16;
 #pragma unroll
                 for (int s = 0; s < 16; s += 4)
@@ -351,57 +369,64 @@ __global__ __launch_bounds__(64) void srnl_scan16_ut_kernel(const ScanParams p) 
             }
             __syncthreads();
             // ---- per block X_b (and Y_b or Y_b^T) on the matrix cores, all tiles at once;
-            //      then the composition G <- G X_b + Y_b, the only serial step ----
+            //      then the composition G <- G X_b + Y_b, the only serial step.  ONE: the
+            //      chunk is this single full pass (first block: tile 0 of each line, last:
+            //      tile TPL - 1), so each block's products are fixed at compile time. ----
             const int nblk = (cnt + 15) / 16;
-            v4s xh[TCW], xl[TCW];
-            v4f yc[TCW];
-#pragma unroll
-            for (int tc = 0; tc < TCW; ++tc) {
-                const int bt = tc % TPL, lam = tc / TPL;
-                if (bt >= nblk) continue;
-                const bool first = g_identity && bt == 0, last = last_pass && bt == nblk - 1;
-                // D(Z): lane 16 q + f holds Z[4q + j][f]; feature-major operands of the block:
-                // -(k a_{t-1}) and -delta with slot 4q + j and feature f
-                const float4 z4 = ld4(Zs + (16 * tc + i16) * 16 + 4 * q);
-                const float4 k4 = ld4(kT + i16 * DKS + 16 * tc + 4 * q);
-                const float4 d4 = ld4(ndT + i16 * DKS + 16 * tc + 4 * q);
-                const float4 a4 = ld4(tk + 2 * TT + 16 * tc + 4 * q);
-                const float zv[4] = {z4.x, z4.y, z4.z, z4.w};
-                const float nka[4] = {k4.x * a4.x, k4.y * a4.y, k4.z * a4.z, k4.w * a4.w};
-                const float ndl[4] = {d4.x, d4.y, d4.z, d4.w};
-                v4s zh, zl;
-                split4(zv, zh, zl);
-                const v4f dI = diag4(decay[tc], q, i16);
-                if (first) {
-                    // G_b = I: G_{b+1} = X_b + Y_b = a_15 I - (K D_a + Delta) Z, or its transpose
-                    const float nb[4] = {nka[0] + ndl[0], nka[1] + ndl[1], nka[2] + ndl[2], nka[3] + ndl[3]};
-                    v4s nbh, nbl;
-                    split4(nb, nbh, nbl);
-                    if (last) gD[lam] = mma3(nbh, nbl, zh, zl, dI);
-                    else gT[lam] = mma3(zh, zl, nbh, nbl, dI);
-                } else {
-                    v4s kah, kal, dlh, dll;
-                    split4(nka, kah, kal);
-                    split4(ndl, dlh, dll);
-                    split4(mma3(kah, kal, zh, zl, dI), xh[tc], xl[tc]);                 // D(X_b)
-                    yc[tc] = last ? mma3(dlh, dll, zh, zl, v4f{0.f, 0.f, 0.f, 0.f})     // D(Y_b)
-                                  : mma3(zh, zl, dlh, dll, v4f{0.f, 0.f, 0.f, 0.f});    // D(Y_b^T)
-                }
-            }
+            auto blocks = [&](auto one_c) {
+            constexpr bool ONE = decltype(one_c)::value;
+            // block bt's X/Y products are issued right before its composition step, so they
+            // overlap the previous step's matrix-core latency
 #pragma unroll
             for (int bt = 0; bt < TPL; ++bt) {
-                if (bt >= nblk) break;
-                if (g_identity && bt == 0) continue;
-                const bool last = last_pass && bt == nblk - 1;
+                if (!ONE && bt >= nblk) break;
+                const bool first = ONE ? bt == 0 : (g_identity && bt == 0);
+                const bool last = ONE ? bt == TPL - 1 : (last_pass && bt == nblk - 1);
+                v4s xh[NL], xl[NL];
+                v4f yc[NL];
 #pragma unroll
                 for (int lam = 0; lam < NL; ++lam) {
                     const int tc = lam * TPL + bt;
+                    // D(Z): lane 16 q + f holds Z[4q + j][f]; feature-major operands of the
+                    // block (slot 4q + j, feature f): -(k a_{t-1}) and -delta
+                    const float4 z4 = ld4(Zs + (16 * tc + i16) * 16 + 4 * q);
+                    const float4 k4 = ld4(kT + i16 * DKS + 16 * tc + 4 * q);
+                    const float4 d4 = ld4(ndT + i16 * DKS + 16 * tc + 4 * q);
+                    const float4 a4 = ld4(tk + 2 * TT + 16 * tc + 4 * q);
+                    const float zv[4] = {z4.x, z4.y, z4.z, z4.w};
+                    const float nka[4] = {k4.x * a4.x, k4.y * a4.y, k4.z * a4.z, k4.w * a4.w};
+                    const float ndl[4] = {d4.x, d4.y, d4.z, d4.w};
+                    v4s zh, zl;
+                    split4(zv, zh, zl);
+                    const v4f dI = diag4(decay[tc], q, i16);
+                    if (first) {
+                        // G_b = I: G_{b+1} = X_b + Y_b = a_15 I - (K D_a + Delta) Z, or its transpose
+                        const float nb[4] = {nka[0] + ndl[0], nka[1] + ndl[1], nka[2] + ndl[2], nka[3] + ndl[3]};
+                        v4s nbh, nbl;
+                        split4(nb, nbh, nbl);
+                        if (last) gD[lam] = mma3(nbh, nbl, zh, zl, dI);
+                        else gT[lam] = mma3(zh, zl, nbh, nbl, dI);
+                    } else {
+                        v4s kah, kal, dlh, dll;
+                        split4(nka, kah, kal);
+                        split4(ndl, dlh, dll);
+                        split4(mma3(kah, kal, zh, zl, dI), xh[lam], xl[lam]);               // D(X_b)
+                        if (last) yc[lam] = mma3(dlh, dll, zh, zl, v4f{0.f, 0.f, 0.f, 0.f});    // D(Y_b)
+                        else yc[lam] = mma3(zh, zl, dlh, dll, v4f{0.f, 0.f, 0.f, 0.f});         // D(Y_b^T)
+                    }
+                }
+                if (first) continue;
+#pragma unroll
+                for (int lam = 0; lam < NL; ++lam) {
                     v4s gh, gl;
                     split4(gT[lam], gh, gl);
-                    if (last) gD[lam] = mma3(gh, gl, xh[tc], xl[tc], yc[tc]);      // G_b X_b + Y_b
-                    else gT[lam] = mma3(xh[tc], xl[tc], gh, gl, yc[tc]);           // X_b^T G_b^T + Y_b^T
+                    if (last) gD[lam] = mma3(gh, gl, xh[lam], xl[lam], yc[lam]);      // G_b X_b + Y_b
+                    else gT[lam] = mma3(xh[lam], xl[lam], gh, gl, yc[lam]);           // X_b^T G_b^T + Y_b^T
                 }
             }
+            };
+            if (g_identity && last_pass && nblk == TPL) blocks(std::true_type{});
+            else blocks(std::false_type{});
             g_identity = false;
             __syncthreads();
         }
