@@ -592,7 +592,7 @@ def main(argv=None):
                    "wall_s_timed_region": round(wall, 3)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 5), "traffic": srnl_bytes,
-                     "kernel": "vh_srnl_spatial_forward (srnl_scan16_kernel + srnl_readout_tile_kernel)",
+                     "kernel": "vh_srnl_spatial_forward (srnl_scan16_ut_kernel + srnl_readout_tile_kernel)",
                      "scope": "sum over the 29 SRNL launches of one forward (3/4/18/4 blocks at "
                               "56/28/14/7); achieved = reference FLOP count / event-timed duration; "
                               "traffic = rocprofv3 FETCH_SIZE+WRITE_SIZE bytes, calibrated",

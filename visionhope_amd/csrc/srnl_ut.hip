@@ -105,6 +105,12 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
     const int64_t b = line0 / (p.heads * p.R);
     const int lane = threadIdx.x;
     const int i16 = lane & 15, q = lane >> 4;
+    // Four-tile packings: reserve the whole 256-entry architected VGPR file, so that two
+    // waves of this kernel never share a SIMD (more than 256 of its 512 registers each).
+    // With fewer registers the workgroup dispatcher was seen to put two waves on ~90 SIMDs
+    // and leave as many idle, which made the launch 20 % longer (the doubled waves finish
+    // last); waves of other kernels can still share the SIMD.
+    if constexpr (TCW == 4) asm volatile("" ::: "v255");
 
     // State in A-operand layout: sA[lam][R][j] = S[16 R + i16][4 q + j].
     float sA[NL][4][4];
