@@ -39,8 +39,13 @@ def _dw_reference(x, conv, epilogue, gate=None, acc=None):
 @pytest.mark.parametrize("ksize", [3, 5, 7])
 @pytest.mark.parametrize("epilogue", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
-def test_depthwise_epilogues(device, ksize, epilogue, dtype, tol):
+@pytest.mark.parametrize("tile", ["0", "2"])
+def test_depthwise_epilogues(device, monkeypatch, ksize, epilogue, dtype, tol, tile):
+    """Both kernels (the per-thread window one, VH_DW_TILE=0, and the LDS-tiled one
+    wherever it applies, VH_DW_TILE=2; FP32 maps always take the first)."""
     from visionhope_amd.utils import dwconv
+
+    monkeypatch.setenv("VH_DW_TILE", tile)
 
     channels = 24
     conv = torch.nn.Conv2d(channels, channels, ksize, padding=ksize // 2, groups=channels)
@@ -67,6 +72,34 @@ def test_depthwise_epilogues(device, ksize, epilogue, dtype, tol):
     assert_close(got.double().cpu().numpy(), expected.numpy(), tol, f"dwconv K={ksize} epi={epilogue}")
 
 
+@pytest.mark.parametrize("ksize", [3, 5, 7])
+@pytest.mark.parametrize("epilogue", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("shape", [(3, 40, 14, 14), (2, 16, 28, 28), (1, 64, 7, 7), (2, 8, 5, 19), (1, 128, 9, 16)])
+def test_depthwise_tiled_kernel_matches_window_kernel(device, monkeypatch, ksize, epilogue, shape):
+    """The LDS-tiled kernel accumulates each window in the order of the per-thread one,
+    so on bf16 maps the two give identical bits (shapes: Tiny-like maps, a map narrower
+    than one segment, rows that do not fill the last band, several channel slabs)."""
+    from visionhope_amd.utils import dwconv
+
+    b, c, h, w = shape
+    conv = torch.nn.Conv2d(c, c, ksize, padding=ksize // 2, groups=c)
+    with torch.no_grad():
+        conv.weight.copy_(randn(*conv.weight.shape, seed=61, scale=0.3))
+        conv.bias.copy_(randn(c, seed=62, scale=0.1))
+    conv = conv.to(device)
+    x = randn(b, c, h, w, seed=63).bfloat16().to(device).contiguous(memory_format=torch.channels_last)
+    gate = randn(b, c, h, w, seed=64).bfloat16().to(device).contiguous(memory_format=torch.channels_last)
+    acc = randn(b, h, w, c, seed=65).to(device)
+    aux = gate if epilogue == dwconv.EPI_GATE else acc if epilogue == dwconv.EPI_ADD_F32_AUX else None
+    results = []
+    for tile in ("0", "2"):
+        monkeypatch.setenv("VH_DW_TILE", tile)
+        out = acc.clone() if epilogue == dwconv.EPI_ACCUM_F32 else None
+        results.append(dwconv.depthwise_conv(x, conv, epilogue, aux=aux, out=out))
+    torch.cuda.synchronize()
+    assert torch.equal(results[0], results[1])
+
+
 @pytest.mark.parametrize("ksize,epilogue", [(3, 3), (7, 2), (5, 5)])
 def test_depthwise_split_launches_match_one_launch(device, monkeypatch, ksize, epilogue):
     """Inputs above the per-launch buffer limit go in several launches of whole images;
@@ -79,6 +112,7 @@ def test_depthwise_split_launches_match_one_launch(device, monkeypatch, ksize, e
         conv.weight.copy_(randn(*conv.weight.shape, seed=41, scale=0.3))
         conv.bias.copy_(randn(channels, seed=42, scale=0.1))
     conv = conv.to(device)
+    monkeypatch.setenv("VH_DW_TILE", "0")   # the split applies to the per-thread window kernel
     x = randn(5, channels, h, w, seed=43).bfloat16().to(device).contiguous(memory_format=torch.channels_last)
     gate = randn(5, channels, h, w, seed=44).bfloat16().to(device).contiguous(memory_format=torch.channels_last)
     acc = randn(5, h, w, channels, seed=45).to(device)
@@ -198,15 +232,17 @@ def test_fused_block_falls_back_for_odd_layouts(device):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape", [(2, 64, 16, 16), (3, 256, 8, 24), (2, 1024, 14, 14)])
-def test_depthwise_gelu_grn_statistics(device, dtype, shape):
+@pytest.mark.parametrize("ksize,tile", [(3, "1"), (7, "1"), (3, "2")])
+def test_depthwise_gelu_grn_statistics(device, monkeypatch, dtype, shape, ksize, tile):
     """The FFN middle with GRN statistics taken in the depthwise pass: the map equals the
     plain fused depthwise + GELU (same arithmetic) and the scale matches the separate GRN
     statistics pass on that map (FP32 sums in another order)."""
     from visionhope_amd.utils import dwconv
     from visionhope_amd.utils.grn_cuda import grn_scale
 
+    monkeypatch.setenv("VH_DW_TILE", tile)
     b, c, h, w = shape
-    conv = torch.nn.Conv2d(c, c, 3, padding=1, groups=c)
+    conv = torch.nn.Conv2d(c, c, ksize, padding=ksize // 2, groups=c)
     with torch.no_grad():
         conv.weight.copy_(randn(*conv.weight.shape, seed=51, scale=0.3))
         conv.bias.copy_(randn(c, seed=52, scale=0.1))

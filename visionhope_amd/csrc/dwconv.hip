@@ -69,6 +69,50 @@ __device__ __forceinline__ void decode8(const Raw8<T>& r, float (&v)[8]) {
     }
 }
 
+// Epilogue of one output pixel (8 channels at element offset `at`): the fused
+// elementwise work of EPI on the accumulated window `acc` (bias included) and the
+// input value `center` at the same position, then one store; DW_ADD_GELU_SUMSQ also
+// adds the squares of the stored values to `sumsq`.
+template <int EPI, typename T>
+__device__ __forceinline__ void dw_store_pixel(const DwParams& p, int64_t at, float (&acc)[8],
+                                               [[maybe_unused]] const float (&center)[8],
+                                               [[maybe_unused]] float (&sumsq)[8]) {
+    if constexpr (EPI == DW_ACCUM_F32) {
+        float* o = static_cast<float*>(p.out) + at;
+        float prev[8];
+        load8<float>(o, prev);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = prev[j] + acc[j];
+        store8<float>(o, acc);
+    } else {
+        if constexpr (EPI == DW_ADD_F32_AUX) {
+            float a[8];
+            load8<float>(static_cast<const float*>(p.aux) + at, a);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = a[j] + acc[j];
+        } else if constexpr (EPI == DW_GATE) {
+            float gv[8];
+            load8<T>(static_cast<const T*>(p.aux) + at, gv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = center[j] + sigmoid_fast(gv[j]) * acc[j];
+        } else if constexpr (EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = gelu_fast(center[j] + acc[j]);
+            if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float r = to_f32(from_f32<T>(acc[j]));   // the stored value
+                    sumsq[j] += r * r;
+                }
+            }
+        } else if constexpr (EPI == DW_ADD_INPUT) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = center[j] + acc[j];
+        }
+        store8<T>(static_cast<T*>(p.out) + at, acc);
+    }
+}
+
 // One thread per (image, row, segment of P pixels, 8 channels): each kernel row loads
 // the P+K-1 input vectors of the segment once and reuses them for all K horizontal
 // taps of the P outputs, so a K x K window costs (P+K-1)/P input loads per tap row
@@ -169,41 +213,7 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
 #pragma unroll
     for (int px = 0; px < P; ++px) {
         if (w0 + px >= W) break;
-        const int64_t at = (pix0 + px) * C + c;
-        if constexpr (EPI == DW_ACCUM_F32) {
-            float* o = static_cast<float*>(p.out) + at;
-            float prev[8];
-            load8<float>(o, prev);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[px][j] = prev[j] + acc[px][j];
-            store8<float>(o, acc[px]);
-        } else {
-            if constexpr (EPI == DW_ADD_F32_AUX) {
-                float a[8];
-                load8<float>(static_cast<const float*>(p.aux) + at, a);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[px][j] = a[j] + acc[px][j];
-            } else if constexpr (EPI == DW_GATE) {
-                float gv[8];
-                load8<T>(static_cast<const T*>(p.aux) + at, gv);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[px][j] = center[px][j] + sigmoid_fast(gv[j]) * acc[px][j];
-            } else if constexpr (EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[px][j] = gelu_fast(center[px][j] + acc[px][j]);
-                if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const float r = to_f32(from_f32<T>(acc[px][j]));   // the stored value
-                        sumsq[j] += r * r;
-                    }
-                }
-            } else if constexpr (EPI == DW_ADD_INPUT) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[px][j] = center[px][j] + acc[px][j];
-            }
-            store8<T>(static_cast<T*>(p.out) + at, acc[px]);
-        }
+        dw_store_pixel<EPI, T>(p, (pix0 + px) * C + c, acc[px], center[px], sumsq);
     }
     if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
         // GRN partial sums: this block's threads cover whole channel groups of one image
@@ -228,12 +238,176 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
     }
 }
 
+// LDS-tiled variant.  A block owns one image, a band of RB output rows and a slab of
+// CS = 8 CG channels: it copies the band's input rows with their K/2-row halo (zeros
+// outside the image, and K/2 zero columns either side) and the slab's taps into LDS
+// once, then each thread computes P consecutive pixels x 8 channels of one output row
+// from LDS.  Global memory sees each input vector of the band once (plus the halo)
+// instead of once per tap row and segment, and every (pixel segment, channel group) of
+// the map is a thread, which small maps need to fill the chip.  Per output the window
+// is accumulated in the order of dwconv_nhwc_kernel (tap rows top to bottom, inputs
+// left to right), so both kernels produce the same bits.
+struct DwTile {
+    int P;             // pixels per thread (7 or 8)
+    int CG;            // 8-channel groups per block
+    int segs;          // P-pixel segments per row
+    int RB;            // output rows per band
+    int bands;         // bands per image
+    int slabs;         // channel slabs, C / (8 CG)
+    int WP;            // tile row length in pixels: segs P + K - 1
+    int TR;            // tile rows: RB + K - 1
+    uint32_t x_bytes;  // LDS bytes of the input tile (at least the 8 KB reduction buffer)
+    uint32_t lds_bytes;
+    FastDiv wp_div, cg_div;
+};
+
+template <int K, int EPI, typename T, int P>
+__global__ __launch_bounds__(256) void dwconv_tile_kernel(const DwParams p, const DwTile t) {
+    constexpr int R = K / 2, NI = P + K - 1, VB = 8 * static_cast<int>(sizeof(T));
+    extern __shared__ __align__(16) unsigned char dw_lds[];
+    const int CG = t.CG, CS = 8 * CG, H = static_cast<int>(p.H), W = static_cast<int>(p.W);
+    const int64_t C = p.C;
+    // Slabs of one (image, band) are adjacent blocks (they read the same input lines),
+    // then the bands of one image (they share halo rows).
+    const uint32_t l = xcd_remap_any(blockIdx.x, gridDim.x);
+    const uint32_t slab = l % static_cast<uint32_t>(t.slabs), l1 = l / static_cast<uint32_t>(t.slabs);
+    const int band = static_cast<int>(l1 % static_cast<uint32_t>(t.bands));
+    const int64_t b = l1 / static_cast<uint32_t>(t.bands);
+    const int h0 = band * t.RB;
+    const int c0 = static_cast<int>(slab) * CS;
+    const int tid = threadIdx.x;
+    unsigned char* xs = dw_lds;
+    float* tps = reinterpret_cast<float*>(dw_lds + t.x_bytes);
+
+    // Stage the tile: vector e = (tile row, tile column, group) in that order, so the
+    // LDS address is 16 e (or 32 e for FP32) and consecutive lanes copy consecutive
+    // 16-byte pieces of one pixel's slab.
+    const T* xb = static_cast<const T*>(p.x) + b * H * W * C + c0;
+    const int nvec = t.TR * t.WP * CG;
+    constexpr int NB = 4;
+    for (int base = tid; base < nvec; base += 256 * NB) {
+        Raw8<T> v[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int e = base + 256 * u;
+            const uint32_t pix = fast_div(static_cast<uint32_t>(e), t.cg_div);
+            const int g = e - static_cast<int>(pix) * CG;
+            const uint32_t tr = fast_div(pix, t.wp_div);
+            const int hh = h0 - R + static_cast<int>(tr), ww = static_cast<int>(pix - tr * t.WP) - R;
+            const bool inside = e < nvec && static_cast<unsigned>(hh) < static_cast<unsigned>(H) &&
+                                static_cast<unsigned>(ww) < static_cast<unsigned>(W);
+#pragma unroll
+            for (int n = 0; n < Raw8<T>::N; ++n) {
+                uint4 q = make_uint4(0u, 0u, 0u, 0u);
+                if (inside) q = *reinterpret_cast<const uint4*>(xb + (static_cast<int64_t>(hh) * W + ww) * C + 8 * g + 4 * n);
+                v[u].w[4 * n] = q.x; v[u].w[4 * n + 1] = q.y; v[u].w[4 * n + 2] = q.z; v[u].w[4 * n + 3] = q.w;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int e = base + 256 * u;
+            if (e < nvec) {
+#pragma unroll
+                for (int n = 0; n < Raw8<T>::N; ++n)
+                    *reinterpret_cast<uint4*>(xs + e * VB + 16 * n) =
+                        make_uint4(v[u].w[4 * n], v[u].w[4 * n + 1], v[u].w[4 * n + 2], v[u].w[4 * n + 3]);
+            }
+        }
+    }
+    for (int e = tid; e < K * K * 2 * CG; e += 256) {
+        const int tap = e / (2 * CG), qd = e - tap * 2 * CG;
+        *reinterpret_cast<float4*>(tps + tap * CS + 4 * qd) =
+            *reinterpret_cast<const float4*>(p.taps + tap * C + c0 + 4 * qd);
+    }
+    __syncthreads();
+
+    const int g = tid % CG, rs = tid / CG, s = rs % t.segs, r = rs / t.segs;
+    const int h = h0 + r, w0 = s * P, c = c0 + 8 * g;
+    [[maybe_unused]] float sumsq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    auto vec_at = [&](int tr, int wc) {   // decoded input vector at tile (row, column)
+        Raw8<T> raw;
+        const unsigned char* src = xs + ((tr * t.WP + wc) * CG + g) * VB;
+#pragma unroll
+        for (int n = 0; n < Raw8<T>::N; ++n) {
+            const uint4 q = *reinterpret_cast<const uint4*>(src + 16 * n);
+            raw.w[4 * n] = q.x; raw.w[4 * n + 1] = q.y; raw.w[4 * n + 2] = q.z; raw.w[4 * n + 3] = q.w;
+        }
+        return raw;
+    };
+    if (r < t.RB && h < H) {
+        float acc[P][8];
+        {
+            float b8[8];
+            if (p.bias) load8<float>(p.bias + c, b8);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float bj = p.bias ? b8[j] : 0.f;
+#pragma unroll
+                for (int px = 0; px < P; ++px) acc[px][j] = bj;
+            }
+        }
+        // Tap rows one at a time for 5x5 and 7x7 (unrolled, their taps and inputs would
+        // take the whole register file).
+        constexpr int DY_UNROLL = K == 3 ? K : 1;
+#pragma unroll DY_UNROLL
+        for (int dy = 0; dy < K; ++dy) {
+            float tp[K][8];
+#pragma unroll
+            for (int dx = 0; dx < K; ++dx) {
+                const float4 a = *reinterpret_cast<const float4*>(tps + (dy * K + dx) * CS + 8 * g);
+                const float4 bq = *reinterpret_cast<const float4*>(tps + (dy * K + dx) * CS + 8 * g + 4);
+                tp[dx][0] = a.x; tp[dx][1] = a.y; tp[dx][2] = a.z; tp[dx][3] = a.w;
+                tp[dx][4] = bq.x; tp[dx][5] = bq.y; tp[dx][6] = bq.z; tp[dx][7] = bq.w;
+            }
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                float v[8];
+                decode8<T>(vec_at(r + dy, w0 + i), v);
+#pragma unroll
+                for (int dx = 0; dx < K; ++dx) {
+                    const int px = i - dx;
+                    if (px >= 0 && px < P) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) acc[px][j] += v[j] * tp[dx][j];
+                    }
+                }
+            }
+        }
+        const int64_t pix0 = (b * H + h) * W + w0;
+#pragma unroll
+        for (int px = 0; px < P; ++px) {
+            if (w0 + px >= W) break;
+            float center[8];
+            if constexpr (EPI == DW_ADD_INPUT || EPI == DW_GATE || EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ)
+                decode8<T>(vec_at(r + R, w0 + px + R), center);
+            dw_store_pixel<EPI, T>(p, (pix0 + px) * C + c, acc[px], center, sumsq);
+        }
+    }
+    if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
+        // GRN partial sums of this (image, band, slab): group g's threads in order; the
+        // partial row of (image, band) is [b * bands + band][C].
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(xs);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red[tid * 8 + j] = sumsq[j];
+        __syncthreads();
+        if (tid < CG) {
+            float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int k = 0; k < 256 / CG; ++k)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) tot[j] += red[(k * CG + tid) * 8 + j];
+            float* dst = p.partial + (b * t.bands + band) * C + c0 + 8 * tid;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dst[j] = tot[j];
+        }
+    }
+}
+
 namespace {
 
-// Pixels per thread (register blocking along W).  VH_DW_PIXELS = 1, 2, 4 or 8 overrides
-// the default for measurements.
-// Measured on MI355X at the Tiny shapes (B=128; W = 56, 14 and 7): 8 pixels for 3x3,
-// 4 for 5x5, 2 for 7x7 on wide maps and 8 on narrow ones.
+// Pixels per thread (register blocking along W) of dwconv_nhwc_kernel, measured on
+// MI355X at the Tiny shapes (B=128; W = 56, 14 and 7): 8 pixels for 3x3, 4 for 5x5,
+// 2 for 7x7 on wide maps and 8 on narrow ones.
 inline int dw_default_pixels(int K, int64_t W) {
     if (K == 3) return 8;
     if (K == 5) return 4;
@@ -278,14 +452,7 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
     }
 }
 
-inline int dw_pixels(int K, int64_t W) {
-    int px = dw_default_pixels(K, W);
-    if (const char* env = std::getenv("VH_DW_PIXELS")) {
-        const int v = std::atoi(env);
-        if (v == 1 || v == 2 || v == 4 || v == 8) px = v;
-    }
-    return px;
-}
+inline int dw_pixels(int K, int64_t W) { return dw_default_pixels(K, W); }
 
 // Blocks per image of the depthwise grid, or 0 when blocks do not tile whole images
 // and whole channel groups (the condition of the GRN partial-sum epilogue).
@@ -295,14 +462,92 @@ inline int64_t dw_blocks_per_image(int K, int64_t H, int64_t W, int64_t C) {
     return H * segs * G / 256;
 }
 
+// Plan of dwconv_tile_kernel for a map of `es`-byte elements (2-byte maps: bf16 and
+// fp16), or false when it does not apply (FP32, a row's segments x channel groups above one block, a tile above 64 KB of LDS,
+// more than 2^31 blocks); dwconv_nhwc_kernel covers those.  The slab width trades the
+// halo re-read (K - 1 extra rows per band: wide bands want narrow slabs) against the
+// bytes of one pixel a load covers contiguously (64 bf16 channels fill a 128-byte
+// line): the lowest (RB + K - 1) / RB x sqrt(128 / min(128, slab bytes)) wins, the
+// wider slab on ties.  VH_DW_TILE=0 turns the variant off and VH_DW_TILE=2 uses it
+// wherever it applies (tests compare the kernels); VH_DW_TILE_CS=<channels> forces a
+// slab width (measurements).
+inline bool dw_tile_plan(int K, int64_t B, int64_t H, int64_t W, int64_t C, int es, DwTile& t) {
+    const char* mode = std::getenv("VH_DW_TILE");
+    if (mode && mode[0] == '0') return false;
+    const bool everywhere = mode && mode[0] == '2';
+    int force = 0;
+    if (const char* env = std::getenv("VH_DW_TILE_CS")) force = std::atoi(env);
+    if (es != 2 || B <= 0 || H <= 0 || W <= 0 || C % 8 != 0) return false;
+    // Measured on MI355X at the Tiny shapes (B = 128, bf16): faster than the per-thread
+    // window kernel for 7x7 at every map size (56x56: 37 vs 64 us, 28x28: 20 vs 37 us)
+    // and for 5x5 from 28x28 up; slower for 3x3, whose staging is not overlapped with
+    // computation (memory-bound there), and for 5x5 on 14x14 and 7x7 maps.
+    if (!everywhere && (K == 3 || (K == 5 && W < 28))) return false;
+    const int P = (W % 7 == 0) ? 7 : 8;
+    const int64_t segs = (W + P - 1) / P;
+    bool found = false;
+    double best = 0.0;
+    for (int cs : {64, 32, 16, 8}) {
+        if (C % cs != 0 || (force && cs != force)) continue;
+        const int64_t cg = cs / 8;
+        if (segs * cg > 256) continue;
+        const int64_t rb = std::min<int64_t>(H, 256 / (segs * cg));
+        const int64_t wp = segs * P + K - 1, tr = rb + K - 1;
+        const int64_t xb = std::max<int64_t>(tr * wp * cs * es, 256 * 8 * 4);
+        const int64_t lds = xb + int64_t(K) * K * cs * 4;
+        if (lds > 64 * 1024) continue;
+        const double score = double(tr) / double(rb) * std::sqrt(128.0 / std::min<int64_t>(128, cs * es));
+        if (found && score >= best - 1e-9) continue;
+        found = true;
+        best = score;
+        t.P = P; t.CG = static_cast<int>(cg); t.segs = static_cast<int>(segs); t.RB = static_cast<int>(rb);
+        t.WP = static_cast<int>(wp); t.TR = static_cast<int>(tr);
+        t.x_bytes = static_cast<uint32_t>(xb); t.lds_bytes = static_cast<uint32_t>(lds);
+    }
+    if (!found) return false;
+    t.bands = static_cast<int>((H + t.RB - 1) / t.RB);
+    t.slabs = static_cast<int>(C / (8 * t.CG));
+    if (B * t.bands * t.slabs >= (int64_t(1) << 31)) return false;
+    t.wp_div = make_fastdiv(static_cast<uint32_t>(t.WP));
+    t.cg_div = make_fastdiv(static_cast<uint32_t>(t.CG));
+    return true;
+}
+
+template <int K, typename T, int P>
+void launch_dw_tile(int epi, const DwParams& dp, const DwTile& t, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(dp.B * t.bands * t.slabs));
+    switch (epi) {
+#define VH_DWT(E)                                                                                           \
+    case E: hipLaunchKernelGGL((dwconv_tile_kernel<K, E, T, P>), grid, dim3(256), t.lds_bytes, s, dp, t); \
+        break;
+        VH_DWT(DW_PLAIN) VH_DWT(DW_ADD_INPUT) VH_DWT(DW_GATE) VH_DWT(DW_ADD_GELU) VH_DWT(DW_ACCUM_F32)
+        VH_DWT(DW_ADD_F32_AUX) VH_DWT(DW_ADD_GELU_SUMSQ)
+#undef VH_DWT
+    }
+}
+
+// Rows of GRN partial sums per image that the launch for this map writes (the bands of
+// the tiled kernel, else the blocks of dwconv_nhwc_kernel), 0 when neither covers it.
+inline int64_t dw_partial_rows(int K, int64_t B, int64_t H, int64_t W, int64_t C, int es) {
+    DwTile t;
+    if (dw_tile_plan(K, B, H, W, C, es, t)) return t.bands;
+    return dw_blocks_per_image(K, H, W, C);
+}
+
 template <int K, typename T>
 void launch_dw(int epi, const DwParams& dp, hipStream_t s) {
-    switch (dw_pixels(K, dp.W)) {
-        case 1: launch_dw_p<K, T, 1>(epi, dp, s); break;
-        case 2: launch_dw_p<K, T, 2>(epi, dp, s); break;
-        case 4: launch_dw_p<K, T, 4>(epi, dp, s); break;
-        default: launch_dw_p<K, T, 8>(epi, dp, s); break;
+    if constexpr (sizeof(T) == 2) {
+        DwTile t;
+        if (dw_tile_plan(K, dp.B, dp.H, dp.W, dp.C, 2, t)) {
+            if (t.P == 7) launch_dw_tile<K, T, 7>(epi, dp, t, s);
+            else launch_dw_tile<K, T, 8>(epi, dp, t, s);
+            return;
+        }
     }
+    if constexpr (K == 3) launch_dw_p<K, T, 8>(epi, dp, s);
+    else if constexpr (K == 5) launch_dw_p<K, T, 4>(epi, dp, s);
+    else if (dw_pixels(K, dp.W) == 2) launch_dw_p<K, T, 2>(epi, dp, s);
+    else launch_dw_p<K, T, 8>(epi, dp, s);
 }
 
 }  // namespace
@@ -346,7 +591,11 @@ extern "C" int vh_dwconv2d_nhwc_forward(const void* x, int32_t io_dtype, const f
 
 extern "C" size_t vh_dwconv2d_gelu_grn_workspace_bytes(int64_t B, int64_t H, int64_t W, int64_t C, int32_t ksize) {
     if (B <= 0 || H <= 0 || W <= 0 || (ksize != 3 && ksize != 5 && ksize != 7)) return 0;
-    return static_cast<size_t>(B * dw_blocks_per_image(ksize, H, W, C) * C) * sizeof(float);
+    // One size for every io dtype: the larger of the 2- and 4-byte launches' needs, 0
+    // unless both are covered.
+    const int64_t rows2 = dw_partial_rows(ksize, B, H, W, C, 2), rows4 = dw_partial_rows(ksize, B, H, W, C, 4);
+    if (rows2 == 0 || rows4 == 0) return 0;
+    return static_cast<size_t>(B * std::max(rows2, rows4) * C) * sizeof(float);
 }
 
 extern "C" int vh_dwconv2d_gelu_grn_forward(const void* x, int32_t io_dtype, const float* taps, const float* bias,
@@ -359,8 +608,9 @@ extern "C" int vh_dwconv2d_gelu_grn_forward(const void* x, int32_t io_dtype, con
                "depthwise conv + GRN statistics expects nonempty NHWC input and B <= 65535");
     VH_REQUIRE(ksize == 3 || ksize == 5 || ksize == 7, VH_ERR_ARG, "kernel size must be 3, 5 or 7, got %d", ksize);
     VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);
-    VH_REQUIRE(dw_blocks_per_image(ksize, H, W, C) > 0, VH_ERR_SHAPE,
-               "GRN partial sums need C/8 dividing 256 and whole 256-thread blocks per image");
+    const int64_t rows = dw_partial_rows(ksize, B, H, W, C, dtype_bytes(io_dtype));
+    VH_REQUIRE(rows > 0 && vh_dwconv2d_gelu_grn_workspace_bytes(B, H, W, C, ksize) > 0, VH_ERR_SHAPE,
+               "GRN partial sums do not cover this map (C %% 8, or a row too wide for one block)");
     VH_REQUIRE(H * W * C * dtype_bytes(io_dtype) < (int64_t(1) << 31), VH_ERR_SHAPE,
                "depthwise conv image too large (one image must be below 2 GiB)");
     const size_t need = vh_dwconv2d_gelu_grn_workspace_bytes(B, H, W, C, ksize);
@@ -385,6 +635,5 @@ extern "C" int vh_dwconv2d_gelu_grn_forward(const void* x, int32_t io_dtype, con
     }
     int rc = check_launch("dwconv_nhwc_kernel (GRN partial sums)");
     if (rc) return rc;
-    return launch_grn_finalize(static_cast<const float*>(workspace), gx, inv_den, B, C,
-                               dw_blocks_per_image(ksize, H, W, C), eps, gamma, scale, s);
+    return launch_grn_finalize(static_cast<const float*>(workspace), gx, inv_den, B, C, rows, eps, gamma, scale, s);
 }
