@@ -57,6 +57,37 @@ def test_pointwise_gelu(device, k, n):
     assert_close(got.double().cpu().numpy(), expected.double().numpy(), 5e-3, "pw gelu")
 
 
+@pytest.mark.parametrize("k,n,m", [(64, 256, 98309), (128, 512, 40007), (256, 1024, 25088), (192, 128, 70001),
+                                   (256, 128, 64 * 512 * 5), (128, 256, 129)])
+@pytest.mark.parametrize("epilogue", [0, 1, 3])
+def test_pointwise_resident_weights_match_tiled_kernel(device, monkeypatch, k, n, m, epilogue):
+    """The resident-weight kernel (shallow products: weights held in registers, pixel
+    tiles streamed through an LDS ring, several tiles per block at these sizes, a ragged
+    last tile) accumulates k in the order of the LDS-tiled kernels, so the bf16 outputs
+    are identical; both match the FP64 reference."""
+    from visionhope_amd.utils import pointwise
+
+    lin = nn.Linear(k, n)
+    with torch.no_grad():
+        lin.weight.copy_(randn(n, k, seed=71, scale=k ** -0.5))
+        lin.bias.copy_(randn(n, seed=72, scale=0.5))
+    lin = lin.to(device)
+    x = _bf16(randn(m, k, seed=73)).to(device)
+    monkeypatch.setenv("VH_PW_RESIDENT", "2")
+    got = pointwise.pointwise_conv(x, lin, epilogue)
+    monkeypatch.setenv("VH_PW_RESIDENT", "0")
+    other = pointwise.pointwise_conv(x, lin, epilogue)
+    torch.cuda.synchronize()
+    assert torch.equal(got, other)
+    rows = torch.arange(0, m, max(1, m // 997), device=device)   # a sample of rows against FP64
+    ref = _linear_ref(x[rows].cpu(), lin.cpu())
+    if epilogue == pointwise.EPI_GELU:
+        ref = _bf16(F.gelu(ref.double()))
+    elif epilogue == pointwise.EPI_SILU:
+        ref = _bf16(F.silu(ref.double()))
+    assert_close(got[rows].double().cpu().numpy(), ref.double().numpy(), 5e-3, f"resident K={k} N={n} M={m}")
+
+
 @pytest.mark.parametrize("k,n", [(256, 64), (1024, 256), (64, 32), (512, 128), (128, 512)])
 @pytest.mark.parametrize("with_grn", [False, True])
 @pytest.mark.parametrize("hw", [(5, 7), (16, 20)])

@@ -320,6 +320,129 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Resident weights (K = 64 .. 256 in steps of 64, N a multiple of BN, epilogues without
+// a residual): a block owns BN output channels and walks pixel tiles of BM rows with a
+// stride of the blocks that share its channels.  Each wave keeps the weight fragments
+// of its BN/4 channels in registers for the whole launch (TN x K/32 16-byte fragments
+// per lane), so per pixel tile only x moves: global -> LDS directly
+// (global_load_lds_dwordx4), two tiles in a ring, the copies of tile i+2 issued as soon
+// as every wave has read tile i, so they overlap tile i's epilogue and tile i+1's
+// products.  Pixel rows past M are clamped to row M - 1 (loads and stores), so every
+// lane issues the same stores on every tile and the wait for tile i+1 is an exact
+// count: 2 S + D younger operations (S stores per tile, D copies per tile), vector
+// memory operations completing in issue order.  The blocks that share a pixel tile
+// are adjacent (consecutive on one XCD), so x is read from HBM about once.
+// LDS layout as in pointwise_dma_kernel: 16-byte chunk c of tile row r at slot
+// K/8 r + ((c & ~7) | ((c ^ r) & 7)).
+// ---------------------------------------------------------------------------
+template <int K, int BN, int BM, int EPI>
+__global__ __launch_bounds__(256, 2) void pointwise_resident_kernel(const PwParams p, const int blocks_per_slice) {
+    static_assert(K % 64 == 0 && K <= 256 && BN % 128 == 0 && BM % 64 == 0, "resident tile shape");
+    static_assert(EPI != PW_ADD, "no residual in this kernel");
+    constexpr int WN = BN / 4, TN = WN / 16, TM = BM / 16, KS = K / 32, CPR = K / 8;
+    constexpr int TILE = BM * K * 2;                 // bytes
+    constexpr int D = BM * CPR / 256;                // copies per lane per tile
+    constexpr int S = TM * TN / 2;                   // stores per lane per tile
+    static_assert(D * 256 == BM * CPR && D >= 1, "whole copy instructions");
+    __shared__ __align__(16) unsigned char lds[2 * TILE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
+    const uint32_t slices = static_cast<uint32_t>(p.N / BN);
+    const uint32_t l = xcd_remap_any(blockIdx.x, gridDim.x);
+    const int n0 = static_cast<int>(l % slices) * BN + wv * WN;   // this wave's first channel
+    const int64_t g = l / slices;
+    const int64_t mtiles = (p.M + BM - 1) / BM;
+    const int ntiles = g < mtiles ? static_cast<int>((mtiles - 1 - g) / blocks_per_slice + 1) : 0;
+    if (ntiles == 0) return;   // uniform per block, before any barrier
+
+    // Weights and bias of the wave's channels, held for the whole launch.
+    uint4 wf[TN][KS];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            wf[tn][ks] = *reinterpret_cast<const uint4*>(p.w + static_cast<int64_t>(n0 + pw_wrow(tn, i16)) * K +
+                                                          32 * ks + 8 * kg);
+    float bv[TN / 2][8];
+#pragma unroll
+    for (int q = 0; q < TN / 2; ++q) pw_bias8(p, n0 + 32 * q + 8 * kg, bv[q]);
+
+    typedef __attribute__((address_space(3))) unsigned char lds_byte;
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_byte*)lds));
+    auto issue = [&](int i) {   // copies of this block's i-th tile into ring slot i % 2
+        const int64_t m0 = (g + static_cast<int64_t>(i) * blocks_per_slice) * BM;
+        const uint32_t sb = lds0 + (i & 1) * TILE;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int slot = (wv * D + d) * 64 + lane, r = slot / CPR, sc = slot % CPR;
+            const int c = (sc & ~7) | ((sc ^ r) & 7);
+            const int64_t m = std::min<int64_t>(m0 + r, p.M - 1);
+            lds_dma16(p.x + m * K + 8 * c, __builtin_amdgcn_readfirstlane(sb + (wv * D + d) * 1024));
+        }
+    };
+    auto slot = [](int r, int c) { return (r * CPR + ((c & ~7) | ((c ^ r) & 7))) * 16; };
+
+    // Weights and bias in registers before the copies start: the empty statements make
+    // the compiler wait for these loads here, outside the loop (it does not see the
+    // copies, which the waits below count by hand).
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            asm volatile("" ::"v"(wf[tn][ks].x), "v"(wf[tn][ks].y), "v"(wf[tn][ks].z), "v"(wf[tn][ks].w));
+#pragma unroll
+    for (int q = 0; q < TN / 2; ++q)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(bv[q][j]));
+    issue(0);
+    if (ntiles > 1) issue(1);
+    for (int i = 0; i < ntiles; ++i) {
+        // Wait for tile i's copies.  Younger operations: for i = 0 tile 1's copies; for
+        // i = 1 tile 2's copies and tile 0's stores; for i >= 2 tile i-2's stores, tile
+        // i+1's copies and tile i-1's stores (copies only where those tiles exist).
+        if (i == 0) {
+            if (ntiles > 1) wait_vmem<D>();
+            else wait_vmem<0>();
+        } else if (i == 1) {
+            if (ntiles > 2) wait_vmem<S + D>();
+            else wait_vmem<S>();
+        } else {
+            if (i + 1 < ntiles) wait_vmem<2 * S + D>();
+            else wait_vmem<2 * S>();
+        }
+        block_barrier();
+        const unsigned char* a = lds + (i & 1) * TILE;
+        v4f_pw acc[TN][TM];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = v4f_pw{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            uint4 xf[TM];
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) xf[tm] = *reinterpret_cast<const uint4*>(a + slot(16 * tm + i16, 4 * ks + kg));
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = mfma_16x16x32(wf[tn][ks], xf[tm], acc[tn][tm]);
+        }
+        if (i + 2 < ntiles) {
+            block_barrier();   // every wave has read slot i % 2
+            issue(i + 2);
+        }
+        const int64_t m0 = (g + static_cast<int64_t>(i) * blocks_per_slice) * BM;
+#pragma unroll
+        for (int q = 0; q < TN / 2; ++q)
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const int64_t m = std::min<int64_t>(m0 + 16 * tm + i16, p.M - 1);
+                pw_store8<EPI>(p, m, n0 + 32 * q + 8 * kg, bv[q], acc[2 * q][tm], acc[2 * q + 1][tm]);
+            }
+    }
+}
+
 // Narrow outputs (N = 32 or 64) with K <= 256: no LDS.  A wave owns 16 TM pixels and
 // every output channel; it issues all loads of its x rows at once (TM * KS 16-byte
 // fragments), reads the small weight fragments through L1 and writes each pixel's
@@ -435,6 +558,39 @@ int launch_pw(const PwParams& p, hipStream_t s) {
             VH_PWT(64, 128, 2, 32, 2) VH_PWT(64, 128, 2, 32, 4) VH_PWT(64, 128, 2, 64, 2) VH_PWT(64, 128, 2, 64, 3)
             VH_PWT(128, 64, 2, 32, 4) VH_PWT(256, 128, 4, 32, 2) VH_PWT(128, 256, 2, 32, 1)
 #undef VH_PWT
+        }
+    }
+    // Resident weights for the shallow products without residual or GRN prologue
+    // (fc1 + GELU, the projections): K = 64 .. 256, N a multiple of 128.  Channel
+    // slices of 256 up to K = 128, else 128 (the weight fragments take 64 VGPRs), and
+    // about 512 blocks (two per CU, one round).  It pays when every block streams a
+    // few pixel tiles past its weights: measured on MI355X (Tiny, B = 128) fc1 + GELU
+    // 56x56 98 -> 86 us, 28x28 56 -> 49 us, 14x14 42 -> 35 us, proj_out 28x28 11.5 ->
+    // 9.6 us, but slower where the pixel tiles x channel slices are fewer than 1024
+    // (14x14 and 7x7 projections: the weights are loaded for one or two tiles).
+    // VH_PW_RESIDENT=0 turns it off, =2 takes it wherever the shape allows (tests).
+    if constexpr (!PRO_ON && EPI != PW_ADD) {
+        const char* res_env = std::getenv("VH_PW_RESIDENT");
+        const bool res_off = res_env && res_env[0] == '0', res_all = res_env && res_env[0] == '2';
+        if (!res_off && bk == 0 && p.K % 64 == 0 && p.K <= 256 && p.N % 128 == 0) {
+            const bool wide = p.N % 256 == 0 && p.K <= 128;
+            const int64_t slices = p.N / (wide ? 256 : 128), mtiles = (p.M + 63) / 64;
+            const int64_t bps = std::max<int64_t>(1, std::min<int64_t>(mtiles, 512 / std::max<int64_t>(1, slices)));
+            if ((res_all || mtiles * slices >= 1024) && slices * bps < (int64_t(1) << 31)) {
+                const dim3 grid(static_cast<unsigned>(slices * bps));
+                auto run = [&](auto kern) {
+                    hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, p, static_cast<int>(bps));
+                    return check_launch("pointwise_resident_kernel");
+                };
+                switch (p.K) {
+                    case 64: return wide ? run(pointwise_resident_kernel<64, 256, 64, EPI>)
+                                         : run(pointwise_resident_kernel<64, 128, 64, EPI>);
+                    case 128: return wide ? run(pointwise_resident_kernel<128, 256, 64, EPI>)
+                                          : run(pointwise_resident_kernel<128, 128, 64, EPI>);
+                    case 192: return run(pointwise_resident_kernel<192, 128, 64, EPI>);
+                    default: return run(pointwise_resident_kernel<256, 128, 64, EPI>);
+                }
+            }
         }
     }
     // The GRN prologue is staged in LDS (PRO 2) when every block spans at most two
