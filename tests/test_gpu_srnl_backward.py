@@ -52,6 +52,48 @@ def test_srnl_backward_matches_oracle(device, head_dim, q_raw, kind):
     _check(got, want, f"d={head_dim} q_raw={q_raw} {kind}")
 
 
+@pytest.mark.parametrize("heads", [4, 8])
+@pytest.mark.parametrize("head_dim", [4, 8, 16])
+@pytest.mark.parametrize("q_raw", [True, False])
+def test_srnl_backward_packed_lines_match_oracle(device, heads, head_dim, q_raw):
+    """Head counts divisible by 4 run the variant that packs 4 lines (consecutive heads of
+    one image and direction) into a workgroup for head_dim 4, 8 and 16 with chunks of 64
+    or less; raw and normalised queries, ragged chunks, perturbed memories."""
+    from visionhope_amd.models.srnl_core.chunk import srnl_packed_backward
+
+    batch, directions, length = 2, 4, 21
+    chunks = [6, 4, 8, 5]
+    mems = memories(directions, heads, head_dim, kind="perturbed", seed=100 + heads + head_dim)
+    x = randn(batch, directions, heads, length, head_dim, seed=31)
+    if q_raw:
+        q = randn(batch, directions, length, heads * head_dim, seed=32)
+    else:
+        q = randn(batch, directions, heads, length, head_dim, seed=32)
+        q = q / q.norm(dim=-1, keepdim=True)
+    dy = randn(batch, directions, heads, length, head_dim, seed=33)
+    want = _oracle_grads(x, q, mems, chunks, dy, q_raw)
+    got = srnl_packed_backward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device), q.to(device),
+                               chunks, dy.to(device), q_raw=q_raw)
+    _check(got, want, f"heads={heads} d={head_dim} q_raw={q_raw}")
+
+
+def test_srnl_backward_tiny_stage3_shape(device):
+    """The Tiny stage-3 operator shape the packed variant trains on: 8 heads of d = 16 on
+    a 14 x 14 map (196-token lines, chunks of 14), one image, raw queries."""
+    from visionhope_amd.models.srnl_core.chunk import srnl_packed_backward
+
+    batch, directions, heads, length, d = 1, 4, 8, 196, 16
+    chunks = [14, 14, 14, 14]
+    mems = memories(directions, heads, d, kind="perturbed", seed=77)
+    x = randn(batch, directions, heads, length, d, seed=34)
+    q = randn(batch, directions, length, heads * d, seed=35)
+    dy = randn(batch, directions, heads, length, d, seed=36)
+    want = _oracle_grads(x, q, mems, chunks, dy, True)
+    got = srnl_packed_backward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device), q.to(device),
+                               chunks, dy.to(device), q_raw=True)
+    _check(got, want, "Tiny stage 3")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_srnl_backward_low_precision_inputs(device, dtype):
     """bf16 / fp16 x and raw q: the kernel reads the rounded values and computes in fp32;
