@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
 // is accumulated in the order of dwconv_nhwc_kernel (tap rows top to bottom, inputs
 // left to right), so both kernels produce the same bits.
 struct DwTile {
-    int P;             // pixels per thread (7 or 8)
+    int P;             // pixels per thread (7 or 8; 2 for 7x7 windows on maps up to 14 wide)
     int CG;            // 8-channel groups per block
     int segs;          // P-pixel segments per row
     int RB;            // output rows per band
@@ -483,7 +483,13 @@ inline bool dw_tile_plan(int K, int64_t B, int64_t H, int64_t W, int64_t C, int 
     // and for 5x5 from 28x28 up; slower for 3x3, whose staging is not overlapped with
     // computation (memory-bound there), and for 5x5 on 14x14 and 7x7 maps.
     if (!everywhere && (K == 3 || (K == 5 && W < 28))) return false;
-    const int P = (W % 7 == 0) ? 7 : 8;
+    int P = (W % 7 == 0) ? 7 : 8;
+    if (K == 7 && W <= 14) P = 2;   // small maps: 3.5x the threads for (P + 6) / P input reads
+    if (const char* env = std::getenv("VH_DW_TILE_P")) {
+        const int v = std::atoi(env);
+        if (v == 2 || (v == 7 && W % 7 == 0) || v == 8) P = v;
+    }
+    if (P == 2 && K != 7) P = (W % 7 == 0) ? 7 : 8;
     const int64_t segs = (W + P - 1) / P;
     bool found = false;
     double best = 0.0;
@@ -540,7 +546,10 @@ void launch_dw(int epi, const DwParams& dp, hipStream_t s) {
         DwTile t;
         if (dw_tile_plan(K, dp.B, dp.H, dp.W, dp.C, 2, t)) {
             if (t.P == 7) launch_dw_tile<K, T, 7>(epi, dp, t, s);
-            else launch_dw_tile<K, T, 8>(epi, dp, t, s);
+            else if constexpr (K == 7) {
+                if (t.P == 2) launch_dw_tile<K, T, 2>(epi, dp, t, s);
+                else launch_dw_tile<K, T, 8>(epi, dp, t, s);
+            } else launch_dw_tile<K, T, 8>(epi, dp, t, s);
             return;
         }
     }
