@@ -113,7 +113,10 @@ int vh_srnl_spatial_forward_noalloc(
  * = sum_r dir_weight[r, c] (y_r + d_skip[r, c] x) + aux, with aux an optional io-dtype
  * [B, H, W, C] addend (NULL: none) and out stored as out_dtype (fp32 or io_dtype).  No
  * counterpart in the reference (its fused kernel does both, fused.cu:307-351); the
- * prepared block uses aux for the local position encoding (models/block.py:77-78). */
+ * prepared block uses aux for the local position encoding (models/block.py:77-78).
+ * The workspace contents are private to the pair: for bf16 maps with head_dim 16 and at
+ * least 1024 lines (B*4*heads) each 16-byte slot of a state holds four entries as bf16
+ * hi then lo halves (the same size as FP32), otherwise FP32. */
 int vh_srnl_spatial_scan(
     const void* x, int32_t io_dtype, const float* M_m, const float* M_v, const float* M_k,
     const float* M_eta, const float* M_alpha, int64_t B, int64_t H, int64_t W, int64_t C,
