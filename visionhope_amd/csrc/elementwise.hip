@@ -797,6 +797,29 @@ __global__ __launch_bounds__(256) void layernorm_nhwc_kernel(const T* __restrict
 // instruction of a wave writes one contiguous 1 KB run (a lane's own 8 outputs would
 // leave 16-byte gaps in each instruction's footprint).  Dynamic LDS of
 // (256 / LPR) * C * sizeof(TO) bytes.
+// Sum over aligned groups of 2^lg consecutive lanes (lg = 0 .. 6, uniform), on the VALU:
+// DPP quad permutes and half-row / row mirrors inside a 16-lane row, then the gfx950
+// row-swap permutes for the 16- and 32-lane steps (no LDS round trips).
+template <int CTRL>
+__device__ __forceinline__ float ln_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float ln_lane_sum(float v, int lg) {
+    if (lg >= 1) v += ln_dpp<0xB1>(v);    // lanes (1, 0, 3, 2)
+    if (lg >= 2) v += ln_dpp<0x4E>(v);    // lanes (2, 3, 0, 1)
+    if (lg >= 3) v += ln_dpp<0x141>(v);   // i <-> 7 - i within 8 lanes
+    if (lg >= 4) v += ln_dpp<0x140>(v);   // i <-> 15 - i within 16 lanes
+    if (lg >= 5) {
+        const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+    }
+    if (lg >= 6) {
+        const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+    }
+    return v;
+}
+
 template <typename T, typename TO, int GP, bool ADD = false, bool STAGE = false>
 __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                              const float* __restrict__ bias, TO* __restrict__ y,
@@ -809,6 +832,14 @@ __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restric
     const int lane = threadIdx.x & (LPR - 1);
     const bool active = row < rows;
     const T* xr = x + (active ? row : 0) * C;
+    // The affine parameters of this lane's channels are loaded first, so their latency
+    // overlaps the row's loads and reductions.
+    float wv[GP][8], bv[GP][8];
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+        load8<float>(w + (k * LPR + lane) * 8, wv[k]);
+        load8<float>(bias + (k * LPR + lane) * 8, bv[k]);
+    }
     float v[GP][8];
     float sum = 0.f;
 #pragma unroll
@@ -824,7 +855,7 @@ __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restric
 #pragma unroll
         for (int j = 0; j < 8; ++j) sum += v[k][j];
     }
-    for (int off = LPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    sum = ln_lane_sum(sum, lpr_log2);
     const float mean = sum / static_cast<float>(C);
     float sq = 0.f;
 #pragma unroll
@@ -834,7 +865,7 @@ __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restric
             v[k][j] -= mean;
             sq += v[k][j] * v[k][j];
         }
-    for (int off = LPR / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+    sq = ln_lane_sum(sq, lpr_log2);
     const float rstd = 1.f / sqrtf(sq / static_cast<float>(C) + eps);
     if constexpr (STAGE) {
         extern __shared__ __align__(16) unsigned char ln_stage[];
@@ -842,11 +873,9 @@ __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restric
 #pragma unroll
         for (int k = 0; k < GP; ++k) {
             const int c = (k * LPR + lane) * 8;
-            float wv[8], bv[8], o[8];
-            load8<float>(w + c, wv);
-            load8<float>(bias + c, bv);
+            float o[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = v[k][j] * rstd * wv[j] + bv[j];
+            for (int j = 0; j < 8; ++j) o[j] = v[k][j] * rstd * wv[k][j] + bv[k][j];
             store8<TO>(st + c, o);
         }
         __syncthreads();
@@ -862,11 +891,9 @@ __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restric
 #pragma unroll
         for (int k = 0; k < GP; ++k) {
             const int c = (k * LPR + lane) * 8;
-            float wv[8], bv[8], o[8];
-            load8<float>(w + c, wv);
-            load8<float>(bias + c, bv);
+            float o[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = v[k][j] * rstd * wv[j] + bv[j];
+            for (int j = 0; j < 8; ++j) o[j] = v[k][j] * rstd * wv[k][j] + bv[k][j];
             store8<TO>(y + row * C + c, o);
         }
     }
