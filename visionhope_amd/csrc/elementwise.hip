@@ -168,6 +168,16 @@ __global__ __launch_bounds__(256) void direction_fusion_tile_kernel(const Fusion
     };
     fetch(0);
     fetch(1);
+    // Per-channel skip and scale of all four directions, loaded behind the data so their
+    // latency is not paid after the phase barrier.
+    float sk[4][8], sc[4][8];
+    if (k < items) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            load8<float>(p.skip + (p.skip_per_dir ? r * C : 0) + c0, sk[r]);
+            load8<float>(p.scale + r * C + c0, sc[r]);
+        }
+    }
 #pragma unroll
     for (int phase = 0; phase < 2; ++phase) {
         if (live[phase]) {
@@ -180,15 +190,13 @@ __global__ __launch_bounds__(256) void direction_fusion_tile_kernel(const Fusion
 #pragma unroll
             for (int rr = 0; rr < 2; ++rr) {
                 const int r = 2 * phase + rr;
-                float yv[8], xv[8], sk[8], sc[8];
+                float yv[8], xv[8];
                 pack8_to_f32<T>(ry[r], yv);
                 pack8_to_f32<T>(rx[r], xv);
-                load8<float>(p.skip + (p.skip_per_dir ? r * C : 0) + c0, sk);
-                load8<float>(p.scale + r * C + c0, sc);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float v = yv[j] + sk[j] * xv[j];
-                    out[j] = r == 0 ? sc[j] * v : out[j] + sc[j] * v;
+                    const float v = yv[j] + sk[r][j] * xv[j];
+                    out[j] = r == 0 ? sc[r][j] * v : out[j] + sc[r][j] * v;
                 }
             }
 #pragma unroll
