@@ -59,6 +59,38 @@ def test_conv3x3(device, cin, cout, stride, hw, act, in_dtype):
                  f"conv3x3 cin={cin} cout={cout} s={stride} hw={hw} act={act}")
 
 
+@pytest.mark.parametrize("batch,cin,cout,stride,hw,act,in_dtype", [
+    (2, 3, 32, 2, (224, 224), 1, torch.float32),    # Tiny stem, first convolution
+    (2, 3, 64, 2, (9, 12), 0, torch.bfloat16),
+    (2, 32, 32, 1, (112, 112), 1, torch.bfloat16),  # stem convolution 2
+    (2, 32, 64, 2, (112, 112), 1, torch.bfloat16),  # stem convolution 3
+    (2, 64, 64, 1, (56, 56), 0, torch.bfloat16),    # stem convolution 4
+    (2, 64, 128, 2, (56, 56), 0, torch.bfloat16),   # downsample 1
+    (3, 32, 32, 1, (13, 29), 0, torch.bfloat16),    # tiles across row ends, partial last band
+    (3, 64, 96, 2, (15, 17), 1, torch.bfloat16),    # odd map at stride 2, three 32-channel slices
+    (2, 32, 64, 1, (1, 1), 1, torch.bfloat16),      # one pixel: every neighbour in the padding
+    (1, 64, 64, 1, (97, 5), 0, torch.bfloat16),     # narrow, tall map
+])
+def test_conv3x3_band_kernel_matches_tiled_kernel(device, monkeypatch, batch, cin, cout, stride, hw, act, in_dtype):
+    """The band kernel (input rows staged in LDS once per band, weights in registers) runs
+    the products in the tiled kernel's k order with the same operands, so both give the
+    same bits; VH_CONV_BAND=0 selects the tiled kernel."""
+    from visionhope_amd.utils.conv_bn import conv3x3_bias_act
+
+    conv = nn.Conv2d(cin, cout, 3, stride=stride, padding=1)
+    x = randn(batch, cin, *hw, seed=81).to(in_dtype).to(device).contiguous(memory_format=torch.channels_last)
+    wd = randn(cout, cin, 3, 3, seed=82, scale=(9 * cin) ** -0.5).to(device).contiguous(memory_format=torch.channels_last)
+    bias = randn(cout, seed=83, scale=0.5).to(device)
+    monkeypatch.setenv("VH_CONV_BAND", "1")
+    band = conv3x3_bias_act(x, conv, wd, bias, act)
+    monkeypatch.setenv("VH_CONV_BAND", "0")
+    tiled = conv3x3_bias_act(x, conv, wd, bias, act)
+    assert torch.equal(band, tiled), f"band vs tiled: max diff {(band.float() - tiled.float()).abs().max().item()}"
+    if hw[0] * hw[1] <= 4096:
+        expected = _reference(x.float().cpu(), wd.float().cpu(), bias.cpu(), stride, act)
+        assert_close(band.double().cpu().numpy(), expected.numpy(), BF16_TOL, "band kernel vs fp64")
+
+
 def test_conv3x3_cached_weight_follows_the_folded_weight(device):
     """The GEMM operand is rebuilt when the folded weight changes."""
     from visionhope_amd.utils.conv_bn import conv3x3_bias_act

@@ -159,6 +159,239 @@ __global__ __launch_bounds__(256, OCC) void conv3x3_kernel(const ConvParams cp) 
     pw_epilogue<EPI, TN, TM, WM, WN>(p, m0, n0, wm, wn, kg, i16, acc);
 }
 
+// ---------------------------------------------------------------------------
+// Band kernel for narrow inputs (Cin = 32 or 64, or the RGB image).  A work item is one
+// image's band of TH full-width output rows for BN output channels.  Its input rows
+// (S (TH-1) + 3 rows, zero rows outside the image and a zero column either side) are
+// copied into LDS once, so every input pixel leaves global memory once per band rather
+// than once per tap, and the products read only LDS.  Blocks are persistent: each
+// keeps the weight fragments of its channels in registers for the whole launch (one
+// wave: 16 channels, all of K) and walks the bands with a stride of the grid, loading
+// the next band's rows into registers while the current band computes.  The outputs
+// of a band are assembled in LDS and written as contiguous pixel rows.
+//
+// LDS layout: patch pixel (row r, column p) at slot r PW + pos(p), PW = W + 2; with
+// stride 2 the even columns come first and the odd ones after them (pos(p) = p/2 or
+// HALF + p/2), so the pixels that one tap reads for consecutive outputs are
+// consecutive slots.  A slot holds Cin/8 16-byte chunks plus one spare, so the 16
+// slots of a fragment read start in distinct bank groups.  For the image a slot is 8
+// bytes: three channels and a zero, rounded to bf16.
+//
+// The k steps run in the order of conv3x3_kernel (tap-major, 32 channels per step,
+// the same operands to the same MFMA), so both kernels produce the same bits.
+struct BandParams {
+    ConvParams cp;
+    int TH, IR, PW, HALF, nbands, nslices, items;   // items = images x bands
+    uint32_t patch_bytes;
+    FastDiv pw_div, nb_div;
+};
+
+template <int CIN, int S, int WGN, int MT, int PRE, int MODE, int EPI>
+__global__ __launch_bounds__(256, 2) void conv3x3_band_kernel(const BandParams bp) {
+    constexpr bool RGB = MODE != CONV_TAPS;
+    static_assert(RGB ? CIN == 4 : (CIN == 32 || CIN == 64), "band kernel channels");
+    constexpr int KS = RGB ? 2 : 9 * CIN / 32;            // k steps of 32
+    constexpr int CPP = CIN / 8;                          // 16-byte chunks per input pixel
+    constexpr int PSTRIDE = RGB ? 8 : (CPP + 1) * 16;     // bytes per patch slot
+    constexpr int WGM = 4 / WGN, BN = WGN * 16;
+    constexpr int OSTR = 2 * BN + 16;                     // bytes per output-stage pixel
+    extern __shared__ __align__(16) unsigned char band_lds[];
+    unsigned char* const ost = band_lds + bp.patch_bytes;
+    const ConvParams& cp = bp.cp;
+    const PwParams& p = cp.g;
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
+    const int wm = wv % WGM, wn = wv / WGM;
+    const int slice = static_cast<int>(blockIdx.x % static_cast<uint32_t>(bp.nslices));
+    const int stride_items = static_cast<int>(gridDim.x / static_cast<uint32_t>(bp.nslices));
+    const int H = cp.H, W = cp.W, PW = bp.PW, Wo = cp.Wo, TH = bp.TH;
+    const int nw = slice * BN + wn * 16;   // this wave's first output channel
+
+    // Weight fragments: channel nw + i16, k = 32 ks + 8 kg .. + 7.
+    uint4 wf[KS];
+    {
+        const bf16_t* wr = p.w + static_cast<int64_t>(nw + i16) * p.K + 8 * kg;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) wf[ks] = *reinterpret_cast<const uint4*>(wr + 32 * ks);
+    }
+    float bv[4];
+    {
+        const float4 b4 = p.bias ? *reinterpret_cast<const float4*>(p.bias + nw + 4 * kg) : make_float4(0.f, 0.f, 0.f, 0.f);
+        bv[0] = b4.x; bv[1] = b4.y; bv[2] = b4.z; bv[3] = b4.w;
+    }
+
+    auto pos = [&](int pc) { return S == 1 ? pc : ((pc & 1) ? bp.HALF + (pc >> 1) : (pc >> 1)); };
+    // Staging of one band's input rows: PRE units per thread (16-byte chunks, or image
+    // pixels), loaded into registers by fetch and written to the patch by commit.  A
+    // unit's patch position is the same in every band; it keeps its LDS destination,
+    // its patch row (-1024 for the zero columns, so the row test rejects them) and its
+    // byte offset from the band's first input row.
+    const int total = RGB ? bp.IR * PW : bp.IR * PW * CPP;
+    [[maybe_unused]] uint4 rv[PRE];
+    [[maybe_unused]] float rf[PRE][3];
+    uint32_t rdst[PRE];
+    int rrow[PRE], rrel[PRE];
+#pragma unroll
+    for (int j = 0; j < PRE; ++j) {
+        const int idx = std::min(256 * j + tid, total - 1);
+        const int slot = RGB ? idx : idx / CPP, c = RGB ? 0 : idx % CPP;
+        const int r = static_cast<int>(fast_div(static_cast<uint32_t>(slot), bp.pw_div)), pc = slot - r * PW;
+        const int iw = pc - 1;
+        rrow[j] = static_cast<unsigned>(iw) < static_cast<unsigned>(W) ? r : -1024;
+        rrel[j] = RGB ? (r * W + iw) * 12 : ((r * W + iw) * CIN + 8 * c) * 2;
+        rdst[j] = static_cast<uint32_t>((r * PW + pos(pc)) * PSTRIDE + 16 * c);
+    }
+    // Image bytes as one buffer: positions outside it read zeros.
+    const uint32_t img_bytes = static_cast<uint32_t>(H * W) * (RGB ? (MODE == CONV_RGB_F32 ? 12u : 6u) : 2u * CIN);
+    auto fetch = [&](int item) {
+        const int b = static_cast<int>(fast_div(static_cast<uint32_t>(item), bp.nb_div));
+        const int ih0 = S * (item - b * bp.nbands) * TH - 1;
+        if constexpr (!RGB) {
+            const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<bf16_t*>(p.x + static_cast<int64_t>(b) * H * W * CIN), 0, img_bytes, 0x00020000);
+            const int rowb = ih0 * W * CIN * 2;
+#pragma unroll
+            for (int j = 0; j < PRE; ++j) {
+                const bool ok = static_cast<unsigned>(ih0 + rrow[j]) < static_cast<unsigned>(H);
+                const uint32_t off = ok ? static_cast<uint32_t>(rowb + rrel[j]) : 0x80000000u;
+                const auto raw = __builtin_amdgcn_raw_buffer_load_b128(xr, static_cast<int>(off), 0, 0);
+                rv[j] = make_uint4(raw[0], raw[1], raw[2], raw[3]);
+            }
+        } else if constexpr (MODE == CONV_RGB_F32) {
+            const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(cp.xf + static_cast<int64_t>(b) * H * W * 3), 0, img_bytes, 0x00020000);
+            const int rowb = ih0 * W * 12;
+#pragma unroll
+            for (int j = 0; j < PRE; ++j) {
+                const bool ok = static_cast<unsigned>(ih0 + rrow[j]) < static_cast<unsigned>(H);
+                const int off = ok ? rowb + rrel[j] : static_cast<int>(0x80000000u);
+#pragma unroll
+                for (int q = 0; q < 3; ++q)
+                    rf[j][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, off + 4 * q, 0, 0));
+            }
+        } else {
+            const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<bf16_t*>(p.x + static_cast<int64_t>(b) * H * W * 3), 0, img_bytes, 0x00020000);
+            const int rowb = ih0 * W * 6;
+#pragma unroll
+            for (int j = 0; j < PRE; ++j) {
+                const bool ok = static_cast<unsigned>(ih0 + rrow[j]) < static_cast<unsigned>(H);
+                const int off = ok ? rowb + rrel[j] / 2 : static_cast<int>(0x80000000u);
+#pragma unroll
+                for (int q = 0; q < 3; ++q)
+                    rf[j][q] = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(xr, off + 2 * q, 0, 0)) << 16);
+            }
+        }
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int j = 0; j < PRE; ++j) {
+            if (256 * j + tid >= total) break;
+            if constexpr (!RGB)
+                *reinterpret_cast<uint4*>(band_lds + rdst[j]) = rv[j];
+            else
+                *reinterpret_cast<uint2*>(band_lds + rdst[j]) =
+                    make_uint2(pack_bf16x2(rf[j][0], rf[j][1]), pack_bf16x2(rf[j][2], 0.f));
+        }
+    };
+
+    // Byte offset of tap (kh, kw) from the slot of tap (0, 0).
+    auto tapoff = [&](int t) {
+        const int kh = t / 3, kw = t - 3 * (t / 3);
+        return (kh * PW + (S == 1 ? kw : (kw == 1 ? bp.HALF : kw / 2))) * PSTRIDE;
+    };
+    // The image's k = 4 tap + c: lane kg holds taps 2 kg and 2 kg + 1 in step 0 and
+    // tap 8 (kg = 0) or zeros in step 1.
+    [[maybe_unused]] int roff0 = 0, roff1 = 0, roff8 = 0;
+    if constexpr (RGB) {
+        roff0 = tapoff(2 * kg);
+        roff1 = tapoff(2 * kg + 1);
+        roff8 = tapoff(8);
+    }
+
+    int item = static_cast<int>(blockIdx.x / static_cast<uint32_t>(bp.nslices));
+    if (item >= bp.items) return;
+    fetch(item);
+    commit();
+    __syncthreads();
+    for (; item < bp.items; item += stride_items) {
+        const int next = item + stride_items;
+        if (next < bp.items) fetch(next);
+        const int b = static_cast<int>(fast_div(static_cast<uint32_t>(item), bp.nb_div));
+        const int oh0 = (item - b * bp.nbands) * TH;
+        const int valid = std::min(TH, cp.Ho - oh0) * Wo;
+        const int mtiles = (valid + 15) / 16, per = (mtiles + WGM - 1) / WGM;
+        const int mt_end = std::min(mtiles, (wm + 1) * per);
+        // A group of CNT pixel tiles (16 consecutive output pixels each, wrapping across
+        // rows) starting at tile g: products over all k steps, then the epilogue into
+        // the output stage.
+        auto group = [&](int g, auto cnt_c) {
+            constexpr int CNT = decltype(cnt_c)::value;
+            uint32_t vb[CNT];
+#pragma unroll
+            for (int t = 0; t < CNT; ++t) {
+                const int m = std::min((g + t) * 16 + i16, valid - 1);
+                const int r = static_cast<int>(fast_div(static_cast<uint32_t>(m), cp.wo)), ow = m - r * Wo;
+                vb[t] = static_cast<uint32_t>((S * r * PW + ow) * PSTRIDE + (RGB ? 0 : 16 * kg));
+            }
+            v4f_pw acc[CNT];
+#pragma unroll
+            for (int t = 0; t < CNT; ++t) acc[t] = v4f_pw{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                uint4 a[CNT];
+#pragma unroll
+                for (int t = 0; t < CNT; ++t) {
+                    if constexpr (!RGB) {
+                        const int tap = CIN == 32 ? ks : ks / 2;
+                        const int off = tapoff(tap) + (CIN == 32 ? 0 : 64 * (ks % 2));
+                        a[t] = *reinterpret_cast<const uint4*>(band_lds + vb[t] + off);
+                    } else if (ks == 0) {
+                        const uint2 lo = *reinterpret_cast<const uint2*>(band_lds + vb[t] + roff0);
+                        const uint2 hi = *reinterpret_cast<const uint2*>(band_lds + vb[t] + roff1);
+                        a[t] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                    } else {
+                        const uint2 lo = *reinterpret_cast<const uint2*>(band_lds + vb[t] + roff8);
+                        a[t] = kg == 0 ? make_uint4(lo.x, lo.y, 0u, 0u) : make_uint4(0u, 0u, 0u, 0u);
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < CNT; ++t) acc[t] = mfma_16x16x32(wf[ks], a[t], acc[t]);
+            }
+            // Lane holds channels nw + 4 kg .. + 3 of pixel 16 (g + t) + i16.
+#pragma unroll
+            for (int t = 0; t < CNT; ++t) {
+                const int m = (g + t) * 16 + i16;
+                if (m >= valid) continue;
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    v[j] = round_bf16(acc[t][j] + bv[j]);
+                    if constexpr (EPI == PW_GELU) v[j] = gelu_fast(v[j]);
+                }
+                *reinterpret_cast<uint2*>(ost + m * OSTR + 2 * (wn * 16 + 4 * kg)) =
+                    make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+            }
+        };
+        int g = wm * per;
+        for (; g + MT <= mt_end; g += MT) group(g, std::integral_constant<int, MT>{});
+        for (; g < mt_end; ++g) group(g, std::integral_constant<int, 1>{});
+        __syncthreads();
+        // The band's outputs: valid pixels x BN channels, 16-byte chunks in address order.
+        {
+            constexpr int CPX = BN / 8;
+            bf16_t* out = p.out + ((static_cast<int64_t>(b) * cp.Ho + oh0) * Wo) * p.N + slice * BN;
+            for (int c = tid; c < valid * CPX; c += 256) {
+                const int m = c / CPX, q = c % CPX;
+                *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * p.N + 8 * q) =
+                    *reinterpret_cast<const uint4*>(ost + m * OSTR + 16 * q);
+            }
+        }
+        if (next < bp.items) commit();
+        __syncthreads();
+    }
+}
+
 namespace {
 
 template <int EPI, int MODE>
@@ -186,9 +419,81 @@ int launch_conv(const ConvParams& cp, hipStream_t s) {
     }
 }
 
+// Band kernel launch, or -1 when it does not cover the shape (Cin other than 3, 32, 64;
+// N not a multiple of 32; more than 64 KB of LDS or 10 staging units per thread) or
+// VH_CONV_BAND=0 asks for conv3x3_kernel.  The band height aims at 7 pixel tiles per
+// wave (one pass of the product loop); the grid is the number of blocks that fit on
+// the GPU at once (a multiple of the channel slices).
+template <int EPI, int MODE>
+int launch_band(const ConvParams& cp, hipStream_t s) {
+    if (const char* env = std::getenv("VH_CONV_BAND"))
+        if (env[0] == '0') return -1;
+    const int cin = MODE == CONV_TAPS ? cp.Cin : 4;
+    if (!(cin == 4 || cin == 32 || cin == 64) || cp.g.N % 32 != 0) return -1;
+    if (static_cast<int64_t>(cp.H) * cp.W * (cin == 4 ? 12 : 2 * cin) >= (int64_t(1) << 31)) return -1;
+    const int wgn = cp.g.N % 64 == 0 ? 4 : 2, wgm = 4 / wgn, bn = 16 * wgn;
+    const int pstride = cin == 4 ? 8 : (cin / 8 + 1) * 16;
+    const int units_per_slot = cin == 4 ? 1 : cin / 8;
+    BandParams bp{};
+    bp.cp = cp;
+    bp.PW = cp.W + 2;
+    bp.HALF = (bp.PW + 1) / 2;
+    auto rows_of = [&](int t) { return cp.stride * (t - 1) + 3; };
+    auto lds_of = [&](int t) {
+        return static_cast<int64_t>(rows_of(t)) * bp.PW * pstride + static_cast<int64_t>(t) * cp.Wo * (2 * bn + 16);
+    };
+    auto units_of = [&](int t) { return static_cast<int64_t>(rows_of(t)) * bp.PW * units_per_slot; };
+    int th = std::max(1, std::min(cp.Ho, (112 * wgm + cp.Wo - 1) / cp.Wo));
+    while (th > 1 && (lds_of(th) > 65536 || units_of(th) > 10 * 256)) --th;
+    if (lds_of(th) > 65536 || units_of(th) > 10 * 256) return -1;
+    const int pre = static_cast<int>((units_of(th) + 255) / 256);
+    bp.TH = th;
+    bp.IR = rows_of(th);
+    bp.nbands = (cp.Ho + th - 1) / th;
+    bp.nslices = cp.g.N / bn;
+    const int64_t batch = cp.g.M / (static_cast<int64_t>(cp.Ho) * cp.Wo);
+    if (batch * bp.nbands >= (int64_t(1) << 31)) return -1;
+    bp.items = static_cast<int>(batch * bp.nbands);
+    bp.patch_bytes = static_cast<uint32_t>(static_cast<int64_t>(bp.IR) * bp.PW * pstride);
+    bp.pw_div = make_fastdiv(static_cast<uint32_t>(bp.PW));
+    bp.nb_div = make_fastdiv(static_cast<uint32_t>(bp.nbands));
+    const size_t lds = static_cast<size_t>(lds_of(th));
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    auto go = [&](auto kern) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds) != hipSuccess || per_cu <= 0) per_cu = 1;
+        const int64_t streams = std::min<int64_t>(bp.items, static_cast<int64_t>(per_cu) * cus / bp.nslices);
+        const dim3 grid(static_cast<unsigned>(std::max<int64_t>(1, streams) * bp.nslices));
+        hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, bp);
+        return check_launch("conv3x3_band_kernel");
+    };
+#define VH_BAND(CIN_, S_, WGN_, PRE_)                                                            \
+    if (cin == CIN_ && cp.stride == S_ && wgn == WGN_ && pre <= PRE_)                            \
+        return go(conv3x3_band_kernel<CIN_, S_, WGN_, 7, PRE_, MODE, EPI>);
+    if constexpr (MODE == CONV_TAPS) {
+        VH_BAND(32, 1, 2, 8) VH_BAND(32, 1, 4, 8) VH_BAND(32, 2, 2, 10) VH_BAND(32, 2, 4, 10)
+        VH_BAND(64, 1, 2, 8) VH_BAND(64, 1, 4, 8) VH_BAND(64, 2, 2, 10) VH_BAND(64, 2, 4, 10)
+    } else {
+        VH_BAND(4, 1, 2, 5) VH_BAND(4, 1, 4, 5) VH_BAND(4, 2, 2, 5) VH_BAND(4, 2, 4, 5)
+    }
+#undef VH_BAND
+    return -1;
+}
+
 template <int MODE>
 int launch_conv_act(const ConvParams& cp, int act, hipStream_t s) {
-    return act == 1 ? launch_conv<PW_GELU, MODE>(cp, s) : launch_conv<PW_BIAS, MODE>(cp, s);
+    if (act == 1) {
+        const int rc = launch_band<PW_GELU, MODE>(cp, s);
+        return rc != -1 ? rc : launch_conv<PW_GELU, MODE>(cp, s);
+    }
+    const int rc = launch_band<PW_BIAS, MODE>(cp, s);
+    return rc != -1 ? rc : launch_conv<PW_BIAS, MODE>(cp, s);
 }
 
 }  // namespace
