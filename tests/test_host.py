@@ -239,6 +239,67 @@ def test_invariant_divisor_multiplication_is_exact():
             assert n * m < (1 << 64)
 
 
+def _bf16_round(x64):
+    """float64 -> nearest-even bfloat16, returned as float64 (finite inputs)."""
+    b = np.asarray(x64, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16 << 16
+    return b.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def test_gelu_table_header_matches_generator(tmp_path):
+    """gelu_table.h is what gen_gelu_table.py writes (the committed header is not stale)."""
+    import subprocess
+    import sys
+
+    csrc = Path(__file__).resolve().parents[1] / "visionhope_amd" / "csrc"
+    out = tmp_path / "gelu_table.h"
+    subprocess.run([sys.executable, str(csrc / "gen_gelu_table.py"), str(out)], check=True)
+    assert out.read_text() == (csrc / "gelu_table.h").read_text()
+
+
+def test_gelu_table_gives_the_bf16_gelu():
+    """The device's tabulated GELU (gelu_bf16_tab: x * Phi[clamp(x)] in float32, then the
+    output rounding to bf16), emulated with the entries parsed from gelu_table.h, against
+    the bf16 rounding of x Phi(x) in float64 (scipy's ndtr) for every finite bf16 x with
+    |x| < 64: equal except where the float64 value lies within float32 rounding of a bf16
+    rounding boundary.  Tiny inputs give x/2 and |x| >= 8 gives x (positive) or a
+    magnitude below 1e-15 |x| (negative; the exact value is below 7e-15)."""
+    import re
+    from scipy.special import ndtr
+
+    src = (Path(__file__).resolve().parents[1] / "visionhope_amd" / "csrc" / "gelu_table.h").read_text()
+    lo, hi, n = (int(v, 0) for v in re.search(r"GELU_TAB_LO = (0x[0-9A-F]+)u, GELU_TAB_HI = (0x[0-9A-F]+)u, "
+                                               r"GELU_TAB_N = ([0-9]+)u", src).groups())
+    vals = [float.fromhex(v) for v in re.findall(r"(-?0x[0-9a-fp.+-]+)f,", src)]
+    assert n == hi - lo + 1 and len(vals) == 2 * n
+    tab = np.array(vals, dtype=np.float32)
+    bits = np.arange(0, 0x7F80, dtype=np.uint32)            # +0 .. largest finite bf16 magnitude
+    bits = np.concatenate([bits, bits | 0x8000])
+    x32 = (bits << 16).view(np.float32)
+    keep = np.abs(x32) < 64
+    bits, x32 = bits[keep], x32[keep]
+    a = np.clip(bits & 0x7FFF, lo, hi)
+    got = _bf16_round((x32 * tab[a - lo + (bits >> 15) * n]).astype(np.float32).astype(np.float64))
+    x = x32.astype(np.float64)
+    exact = x * ndtr(x)
+    want = _bf16_round(exact)
+    normal = (np.abs(x) >= 2.0 ** -100) & (x > -8)   # away from float32 subnormals and the far tail
+    differ = (got != want) & normal
+    # each difference is a one-unit flip at a near tie of the float64 value
+    assert differ.mean() < 1e-4, differ.sum()
+    gap = np.abs(exact[differ] - 0.5 * (got[differ] + want[differ]))
+    assert (gap <= 1e-6 * np.abs(exact[differ]) + 1e-30).all()
+    tiny = (np.abs(x) < 2.0 ** -10) & (np.abs(x) >= 2.0 ** -100)
+    assert (got[tiny] == _bf16_round(x[tiny] / 2)).all()
+    assert (got[x >= 8] == x[x >= 8]).all()
+    far = x <= -8
+    assert (np.abs(got[far]) <= 1e-15 * np.abs(x[far])).all() and (np.abs(exact[far]) < 7e-15).all()
+    # a table shifted by one entry fails
+    shifted = np.roll(tab, 1)
+    bad = _bf16_round((x32 * shifted[a - lo + (bits >> 15) * n]).astype(np.float32).astype(np.float64))
+    assert (bad != want).mean() > 0.05
+
+
 def test_gelu_fit_accuracy():
     """The device GELU's erfc fit, evaluated step by step in float32 with the constants
     read from the kernel header, against x * Phi(x) in float64 (scipy's ndtr)."""

@@ -51,6 +51,8 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
     constexpr int A_CHUNKS = (A_TOTAL + 255) / 256, B_CHUNKS = (B_TOTAL + 255) / 256;
     __shared__ __align__(16) bf16_t lds[2][(BM + BN) * PW_LDS_ROW];
     __shared__ __align__(16) float grn_s[2][PRO == 2 ? 3 * BK : 4];
+    __shared__ float gtab[EPI == PW_GELU ? 2 * GELU_TAB_N : 1];
+    if constexpr (EPI == PW_GELU) gelu_tab_fill(gtab, static_cast<int>(threadIdx.x), 256);   // published by the first barrier
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const int wm = wv % WGM, wn = wv / WGM;
@@ -180,7 +182,7 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
             const int64_t m = m0 + wm * WM + 16 * tm + i16;
-            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm]);
+            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm], EPI == PW_GELU ? gtab : nullptr);
         }
     }
 }
@@ -217,6 +219,11 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
     constexpr int GRN_BYTES = PRO ? 3 * BK * 4 : 0;
     constexpr int STAGE = (BM + BN) * BK * 2 + GRN_BYTES;
     __shared__ __align__(16) unsigned char lds[3 * STAGE];
+    __shared__ float gtab[EPI == PW_GELU ? 2 * GELU_TAB_N : 1];
+    if constexpr (EPI == PW_GELU) {
+        gelu_tab_fill(gtab, static_cast<int>(threadIdx.x), 256);
+        __syncthreads();   // before the copies: their waits below are counted by hand
+    }
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const int wm = wv % WGM, wn = wv / WGM;
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
             const int64_t m = m0 + wm * WM + 16 * tm + i16;
-            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm]);
+            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm], EPI == PW_GELU ? gtab : nullptr);
         }
     }
 }
@@ -346,6 +353,7 @@ __global__ __launch_bounds__(256, 2) void pointwise_resident_kernel(const PwPara
     constexpr int S = TM * TN / 2;                   // stores per lane per tile
     static_assert(D * 256 == BM * CPR && D >= 1, "whole copy instructions");
     __shared__ __align__(16) unsigned char lds[2 * TILE];
+    __shared__ float gtab[EPI == PW_GELU ? 2 * GELU_TAB_N : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const uint32_t slices = static_cast<uint32_t>(p.N / BN);
@@ -367,6 +375,10 @@ __global__ __launch_bounds__(256, 2) void pointwise_resident_kernel(const PwPara
     float bv[TN / 2][8];
 #pragma unroll
     for (int q = 0; q < TN / 2; ++q) pw_bias8(p, n0 + 32 * q + 8 * kg, bv[q]);
+    if constexpr (EPI == PW_GELU) {
+        gelu_tab_fill(gtab, tid, 256);
+        __syncthreads();
+    }
 
     typedef __attribute__((address_space(3))) unsigned char lds_byte;
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_byte*)lds));
@@ -438,7 +450,8 @@ __global__ __launch_bounds__(256, 2) void pointwise_resident_kernel(const PwPara
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm) {
                 const int64_t m = std::min<int64_t>(m0 + 16 * tm + i16, p.M - 1);
-                pw_store8<EPI>(p, m, n0 + 32 * q + 8 * kg, bv[q], acc[2 * q][tm], acc[2 * q + 1][tm]);
+                pw_store8<EPI>(p, m, n0 + 32 * q + 8 * kg, bv[q], acc[2 * q][tm], acc[2 * q + 1][tm],
+                               EPI == PW_GELU ? gtab : nullptr);
             }
     }
 }
@@ -492,7 +505,7 @@ __global__ __launch_bounds__(256) void pointwise_narrow_kernel(const PwParams p)
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
             const int64_t m = m_wave + 16 * tm + i16;
-            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm]);
+            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm], EPI == PW_GELU ? gelu_phi_table : nullptr);
         }
     }
 }

@@ -49,15 +49,13 @@ __device__ __forceinline__ uint4 grn_apply8(uint4 v, const float* s, const float
     return r;
 }
 
-__device__ __forceinline__ float round_bf16(float v) {
-    return __uint_as_float(static_cast<uint32_t>(from_f32<bf16_t>(v).bits) << 16);
-}
 
 // Epilogue of one tile pair: lane holds channels n .. n+7 (from acc0 = tile 2q,
 // acc1 = tile 2q+1) of pixel m.
+// gtab: the GELU table (gelu_bf16_tab) or null for the erfc form (gelu_fast).
 template <int EPI>
 __device__ __forceinline__ void pw_store8(const PwParams& p, int64_t m, int n, const float (&bv)[8], const v4f_pw& acc0,
-                                          const v4f_pw& acc1) {
+                                          const v4f_pw& acc1, const float* gtab = nullptr) {
     float v[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -65,8 +63,13 @@ __device__ __forceinline__ void pw_store8(const PwParams& p, int64_t m, int n, c
         v[4 + j] = round_bf16(acc1[j] + bv[4 + j]);
     }
     if constexpr (EPI == PW_GELU) {
+        if (gtab) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = gelu_fast(v[j]);
+            for (int j = 0; j < 8; ++j) v[j] = gelu_bf16_tab(v[j], gtab);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = gelu_fast(v[j]);
+        }
     } else if constexpr (EPI == PW_SILU) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = v[j] * sigmoid_fast(v[j]);
@@ -112,7 +115,7 @@ __device__ __forceinline__ void pw_tile(const PwParams& p, int64_t& m0, int& n0)
 // n0 + wn WN + 32 q + 8 kg + (0..7) of pixel m0 + wm WM + 16 tm + i16.
 template <int EPI, int TN, int TM, int WM, int WN>
 __device__ __forceinline__ void pw_epilogue(const PwParams& p, int64_t m0, int n0, int wm, int wn, int kg, int i16,
-                                            const v4f_pw (&acc)[TN][TM]) {
+                                            const v4f_pw (&acc)[TN][TM], const float* gtab = nullptr) {
 #pragma unroll
     for (int q = 0; q < TN / 2; ++q) {
         const int n = n0 + wn * WN + 32 * q + 8 * kg;
@@ -121,7 +124,7 @@ __device__ __forceinline__ void pw_epilogue(const PwParams& p, int64_t m0, int n
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
             const int64_t m = m0 + wm * WM + 16 * tm + i16;
-            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm]);
+            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm], gtab);
         }
     }
 }

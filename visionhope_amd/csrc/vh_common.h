@@ -10,6 +10,7 @@
 #include <type_traits>
 
 #include "../../include/visionhope_hip.h"
+#include "gelu_table.h"
 
 namespace vh {
 
@@ -264,6 +265,27 @@ __device__ __forceinline__ float gelu_fast(float x) {
     const float half_erfc = t * __builtin_amdgcn_exp2f(p - (0.72134752044448170f * x) * x);
     // x Phi(x) = max(x, 0) - |x| erfc(|x| / sqrt(2)) / 2 on both sides of 0
     return fmaf(-fabsf(x), half_erfc, fmaxf(x, 0.f));
+}
+
+// v rounded to bf16 (nearest even), as an fp32.
+__device__ __forceinline__ float round_bf16(float v) {
+    return __uint_as_float(static_cast<uint32_t>(from_f32<bf16_t>(v).bits) << 16);
+}
+
+// GELU of a bf16 value v (an fp32 whose low 16 bits are zero) through the table of
+// Phi in gelu_table.h: v * Phi(v) with |v| clamped to the table's range [2^-10, 8);
+// the float32 product is within one float32 rounding of the exact GELU inside the
+// range, and outside it rounds to the same bf16 (v/2 below, v or a magnitude under
+// 7e-15 above).  tab is the table (2 GELU_TAB_N floats), normally copied to LDS by
+// gelu_tab_fill.
+__device__ __forceinline__ float gelu_bf16_tab(float v, const float* tab) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t m = (b >> 16) & 0x7fffu;
+    const uint32_t a = m < GELU_TAB_LO ? GELU_TAB_LO : (m > GELU_TAB_HI ? GELU_TAB_HI : m);
+    return v * tab[a - GELU_TAB_LO + (b >> 31) * GELU_TAB_N];
+}
+__device__ __forceinline__ void gelu_tab_fill(float* tab, int tid, int nthreads) {
+    for (int i = tid; i < static_cast<int>(2 * GELU_TAB_N); i += nthreads) tab[i] = gelu_phi_table[i];
 }
 
 }  // namespace vh
