@@ -258,12 +258,13 @@ def test_gelu_table_header_matches_generator(tmp_path):
 
 
 def test_gelu_table_gives_the_bf16_gelu():
-    """The device's tabulated GELU (gelu_bf16_tab: x * Phi[clamp(x)] in float32, then the
-    output rounding to bf16), emulated with the entries parsed from gelu_table.h, against
-    the bf16 rounding of x Phi(x) in float64 (scipy's ndtr) for every finite bf16 x with
-    |x| < 64: equal except where the float64 value lies within float32 rounding of a bf16
-    rounding boundary.  Tiny inputs give x/2 and |x| >= 8 gives x (positive) or a
-    magnitude below 1e-15 |x| (negative; the exact value is below 7e-15)."""
+    """The device's tabulated GELU (gelu_bf16_tab: fma(-|x|, Q[clamp(|x|)], max(x, 0)) in
+    float32 with Q(a) = Phi(-a), then the output rounding to bf16), emulated with the
+    entries parsed from gelu_table.h, against the bf16 rounding of x Phi(x) in float64
+    (scipy's ndtr) for every finite bf16 x with |x| < 64: equal except where the float64
+    value lies within float32 rounding of a bf16 rounding boundary.  Tiny inputs give
+    x/2 and |x| >= 8 gives x (positive) or a magnitude below 1e-15 |x| (negative; the
+    exact value is below 7e-15)."""
     import re
     from scipy.special import ndtr
 
@@ -271,16 +272,22 @@ def test_gelu_table_gives_the_bf16_gelu():
     lo, hi, n = (int(v, 0) for v in re.search(r"GELU_TAB_LO = (0x[0-9A-F]+)u, GELU_TAB_HI = (0x[0-9A-F]+)u, "
                                                r"GELU_TAB_N = ([0-9]+)u", src).groups())
     vals = [float.fromhex(v) for v in re.findall(r"(-?0x[0-9a-fp.+-]+)f,", src)]
-    assert n == hi - lo + 1 and len(vals) == 2 * n
+    assert n == hi - lo + 1 and len(vals) == n
     tab = np.array(vals, dtype=np.float32)
+
+    def device(table):
+        q = table[np.clip(bits & 0x7FFF, lo, hi) - lo].astype(np.float64)
+        # fma: the float64 product of two float32 values is exact; one rounding to float32
+        r = (np.maximum(x, 0) - np.abs(x) * q).astype(np.float32).astype(np.float64)
+        return _bf16_round(r)
+
     bits = np.arange(0, 0x7F80, dtype=np.uint32)            # +0 .. largest finite bf16 magnitude
     bits = np.concatenate([bits, bits | 0x8000])
     x32 = (bits << 16).view(np.float32)
     keep = np.abs(x32) < 64
     bits, x32 = bits[keep], x32[keep]
-    a = np.clip(bits & 0x7FFF, lo, hi)
-    got = _bf16_round((x32 * tab[a - lo + (bits >> 15) * n]).astype(np.float32).astype(np.float64))
     x = x32.astype(np.float64)
+    got = device(tab)
     exact = x * ndtr(x)
     want = _bf16_round(exact)
     normal = (np.abs(x) >= 2.0 ** -100) & (x > -8)   # away from float32 subnormals and the far tail
@@ -294,10 +301,9 @@ def test_gelu_table_gives_the_bf16_gelu():
     assert (got[x >= 8] == x[x >= 8]).all()
     far = x <= -8
     assert (np.abs(got[far]) <= 1e-15 * np.abs(x[far])).all() and (np.abs(exact[far]) < 7e-15).all()
-    # a table shifted by one entry fails
-    shifted = np.roll(tab, 1)
-    bad = _bf16_round((x32 * shifted[a - lo + (bits >> 15) * n]).astype(np.float32).astype(np.float64))
-    assert (bad != want).mean() > 0.05
+    # a table shifted by one entry, or Phi(+a) in place of Phi(-a), fails
+    assert (device(np.roll(tab, 1)) != want).mean() > 0.05
+    assert (device((1 - tab).astype(np.float32)) != want).mean() > 0.05
 
 
 def test_gelu_fit_accuracy():

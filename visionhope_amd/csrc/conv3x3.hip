@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256, OCC) void conv3x3_kernel(const ConvParams cp) 
     constexpr int CPR = BK / 8, A_CHUNKS = BM * CPR / 256, B_CHUNKS = (BN * CPR + 255) / 256;
     static_assert(BM * CPR % 256 == 0, "whole A chunks per thread");
     __shared__ __align__(16) bf16_t lds[2][(BM + BN) * LROW];
-    __shared__ float gtab[EPI == PW_GELU ? 2 * GELU_TAB_N : 1];
+    __shared__ float gtab[EPI == PW_GELU ? GELU_TAB_N : 1];
     if constexpr (EPI == PW_GELU) gelu_tab_fill(gtab, static_cast<int>(threadIdx.x), 256);   // published by the first barrier
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void conv3x3_band_kernel(const BandParams b
     constexpr int WGM = 4 / WGN, BN = WGN * 16;
     constexpr int OSTR = 2 * BN + 16;                     // bytes per output-stage pixel
     extern __shared__ __align__(16) unsigned char band_lds[];
-    __shared__ float gtab[EPI == PW_GELU ? 2 * GELU_TAB_N : 1];
+    __shared__ float gtab[EPI == PW_GELU ? GELU_TAB_N : 1];
     if constexpr (EPI == PW_GELU) gelu_tab_fill(gtab, static_cast<int>(threadIdx.x), 256);   // published by the first barrier
     unsigned char* const ost = band_lds + bp.patch_bytes;
     const ConvParams& cp = bp.cp;
@@ -369,9 +369,14 @@ __global__ __launch_bounds__(256, 2) void conv3x3_band_kernel(const BandParams b
                 if (m >= valid) continue;
                 float v[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    v[j] = round_bf16(acc[t][j] + bv[j]);
-                    if constexpr (EPI == PW_GELU) v[j] = gelu_bf16_tab(v[j], gtab);
+                for (int j = 0; j < 4; j += 2) {
+                    const uint32_t w = pack_bf16x2(acc[t][j] + bv[j], acc[t][j + 1] + bv[j + 1]);
+                    v[j] = bf16_lo(w);
+                    v[j + 1] = bf16_hi(w);
+                }
+                if constexpr (EPI == PW_GELU) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) v[j] = gelu_bf16_tab(v[j], gtab);
                 }
                 *reinterpret_cast<uint2*>(ost + m * OSTR + 2 * (wn * 16 + 4 * kg)) =
                     make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));

@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256, OCC) void pointwise_gemm_kernel(const PwParams
     constexpr int A_CHUNKS = (A_TOTAL + 255) / 256, B_CHUNKS = (B_TOTAL + 255) / 256;
     __shared__ __align__(16) bf16_t lds[2][(BM + BN) * PW_LDS_ROW];
     __shared__ __align__(16) float grn_s[2][PRO == 2 ? 3 * BK : 4];
-    __shared__ float gtab[EPI == PW_GELU ? 2 * GELU_TAB_N : 1];
+    __shared__ float gtab[EPI == PW_GELU ? GELU_TAB_N : 1];
     if constexpr (EPI == PW_GELU) gelu_tab_fill(gtab, static_cast<int>(threadIdx.x), 256);   // published by the first barrier
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
     constexpr int GRN_BYTES = PRO ? 3 * BK * 4 : 0;
     constexpr int STAGE = (BM + BN) * BK * 2 + GRN_BYTES;
     __shared__ __align__(16) unsigned char lds[3 * STAGE];
-    __shared__ float gtab[EPI == PW_GELU ? 2 * GELU_TAB_N : 1];
+    __shared__ float gtab[EPI == PW_GELU ? GELU_TAB_N : 1];
     if constexpr (EPI == PW_GELU) {
         gelu_tab_fill(gtab, static_cast<int>(threadIdx.x), 256);
         __syncthreads();   // before the copies: their waits below are counted by hand
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void pointwise_resident_kernel(const PwPara
     constexpr int S = TM * TN / 2;                   // stores per lane per tile
     static_assert(D * 256 == BM * CPR && D >= 1, "whole copy instructions");
     __shared__ __align__(16) unsigned char lds[2 * TILE];
-    __shared__ float gtab[EPI == PW_GELU ? 2 * GELU_TAB_N : 1];
+    __shared__ float gtab[EPI == PW_GELU ? GELU_TAB_N : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, i16 = lane & 15, kg = lane >> 4;
     const uint32_t slices = static_cast<uint32_t>(p.N / BN);
@@ -505,7 +505,7 @@ __global__ __launch_bounds__(256) void pointwise_narrow_kernel(const PwParams p)
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
             const int64_t m = m_wave + 16 * tm + i16;
-            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm], EPI == PW_GELU ? gelu_phi_table : nullptr);
+            if (m < p.M) pw_store8<EPI>(p, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm], EPI == PW_GELU ? gelu_tail_table : nullptr);
         }
     }
 }

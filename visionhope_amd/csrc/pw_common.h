@@ -56,11 +56,14 @@ __device__ __forceinline__ uint4 grn_apply8(uint4 v, const float* s, const float
 template <int EPI>
 __device__ __forceinline__ void pw_store8(const PwParams& p, int64_t m, int n, const float (&bv)[8], const v4f_pw& acc0,
                                           const v4f_pw& acc1, const float* gtab = nullptr) {
+    // acc + bias rounded to bf16, two values per conversion.
     float v[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        v[j] = round_bf16(acc0[j] + bv[j]);
-        v[4 + j] = round_bf16(acc1[j] + bv[4 + j]);
+    for (int j = 0; j < 4; j += 2) {
+        const uint32_t w0 = pack_bf16x2(acc0[j] + bv[j], acc0[j + 1] + bv[j + 1]);
+        const uint32_t w1 = pack_bf16x2(acc1[j] + bv[4 + j], acc1[j + 1] + bv[5 + j]);
+        v[j] = bf16_lo(w0); v[j + 1] = bf16_hi(w0);
+        v[4 + j] = bf16_lo(w1); v[5 + j] = bf16_hi(w1);
     }
     if constexpr (EPI == PW_GELU) {
         if (gtab) {

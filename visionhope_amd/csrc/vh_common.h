@@ -272,20 +272,20 @@ __device__ __forceinline__ float round_bf16(float v) {
     return __uint_as_float(static_cast<uint32_t>(from_f32<bf16_t>(v).bits) << 16);
 }
 
-// GELU of a bf16 value v (an fp32 whose low 16 bits are zero) through the table of
-// Phi in gelu_table.h: v * Phi(v) with |v| clamped to the table's range [2^-10, 8);
-// the float32 product is within one float32 rounding of the exact GELU inside the
-// range, and outside it rounds to the same bf16 (v/2 below, v or a magnitude under
-// 7e-15 above).  tab is the table (2 GELU_TAB_N floats), normally copied to LDS by
+// GELU of a bf16 value v (an fp32 whose low 16 bits are zero) through the table of the
+// tail Q(a) = Phi(-a) in gelu_table.h: max(v, 0) - |v| Q(|v|) with |v| clamped to the
+// table's range [2^-10, 8) (the form of gelu_fast, Q read instead of evaluated).  Inside
+// the range the result is within one float32 rounding of each term of the exact GELU;
+// outside it the bf16-rounded result is the exact one's (v/2 below, v or a magnitude
+// under 7e-15 above).  tab is the table (GELU_TAB_N floats), normally copied to LDS by
 // gelu_tab_fill.
 __device__ __forceinline__ float gelu_bf16_tab(float v, const float* tab) {
-    const uint32_t b = __float_as_uint(v);
-    const uint32_t m = (b >> 16) & 0x7fffu;
+    const uint32_t m = (__float_as_uint(v) >> 16) & 0x7fffu;
     const uint32_t a = m < GELU_TAB_LO ? GELU_TAB_LO : (m > GELU_TAB_HI ? GELU_TAB_HI : m);
-    return v * tab[a - GELU_TAB_LO + (b >> 31) * GELU_TAB_N];
+    return fmaf(-fabsf(v), tab[a - GELU_TAB_LO], fmaxf(v, 0.f));
 }
 __device__ __forceinline__ void gelu_tab_fill(float* tab, int tid, int nthreads) {
-    for (int i = tid; i < static_cast<int>(2 * GELU_TAB_N); i += nthreads) tab[i] = gelu_phi_table[i];
+    for (int i = tid; i < static_cast<int>(GELU_TAB_N); i += nthreads) tab[i] = gelu_tail_table[i];
 }
 
 }  // namespace vh
