@@ -52,7 +52,7 @@ __device__ __forceinline__ uint4 grn_apply8(uint4 v, const float* s, const float
 
 // Epilogue of one tile pair: lane holds channels n .. n+7 (from acc0 = tile 2q,
 // acc1 = tile 2q+1) of pixel m.
-// gtab: the GELU table (gelu_bf16_tab) or null for the erfc form (gelu_fast).
+// gtab: the GELU table (gelu_bf16_tab), required for PW_GELU.
 template <int EPI>
 __device__ __forceinline__ void pw_store8(const PwParams& p, int64_t m, int n, const float (&bv)[8], const v4f_pw& acc0,
                                           const v4f_pw& acc1, const float* gtab = nullptr) {
@@ -66,13 +66,8 @@ __device__ __forceinline__ void pw_store8(const PwParams& p, int64_t m, int n, c
         v[4 + j] = bf16_lo(w1); v[5 + j] = bf16_hi(w1);
     }
     if constexpr (EPI == PW_GELU) {
-        if (gtab) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = gelu_bf16_tab(v[j], gtab);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = gelu_fast(v[j]);
-        }
+        for (int j = 0; j < 8; ++j) v[j] = gelu_bf16_tab(v[j], gtab);
     } else if constexpr (EPI == PW_SILU) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = v[j] * sigmoid_fast(v[j]);

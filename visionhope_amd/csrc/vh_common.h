@@ -282,7 +282,11 @@ __device__ __forceinline__ float round_bf16(float v) {
 __device__ __forceinline__ float gelu_bf16_tab(float v, const float* tab) {
     const uint32_t m = (__float_as_uint(v) >> 16) & 0x7fffu;
     const uint32_t a = m < GELU_TAB_LO ? GELU_TAB_LO : (m > GELU_TAB_HI ? GELU_TAB_HI : m);
-    return fmaf(-fabsf(v), tab[a - GELU_TAB_LO], fmaxf(v, 0.f));
+    // max(v, 0) as one instruction: fmaxf would first canonicalize v (v is a bit pattern
+    // from a shift or mask, which the compiler cannot prove canonical).
+    float pos;
+    asm("v_max_f32 %0, 0, %1" : "=v"(pos) : "v"(v));
+    return fmaf(-fabsf(v), tab[a - GELU_TAB_LO], pos);
 }
 __device__ __forceinline__ void gelu_tab_fill(float* tab, int tid, int nthreads) {
     for (int i = tid; i < static_cast<int>(GELU_TAB_N); i += nthreads) tab[i] = gelu_tail_table[i];
