@@ -243,8 +243,14 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
         const int64_t m = std::min<int64_t>(m0 + (wv * A_INS + i) * 8 + lrow, p.M - 1);
         asrc[i] = p.x + m * K + 8 * lchunk;
     }
+    // B rows in fragment order: LDS row wn WN + 16 tn + i16 holds weight row
+    // wn WN + pw_wrow(tn, i16), so a fragment reads 16 consecutive swizzled rows (the
+    // permuted rows read in place conflict in the LDS banks).
 #pragma unroll
-    for (int i = 0; i < B_INS; ++i) bsrc[i] = p.w + static_cast<int64_t>(n0 + (wv * B_INS + i) * 8 + lrow) * K + 8 * lchunk;
+    for (int i = 0; i < B_INS; ++i) {
+        const int R = (wv * B_INS + i) * 8 + lrow, rn = R / WN, rr = R % WN;
+        bsrc[i] = p.w + static_cast<int64_t>(n0 + rn * WN + pw_wrow(rr / 16, rr % 16)) * K + 8 * lchunk;
+    }
     [[maybe_unused]] const float* gsrc = nullptr;
     [[maybe_unused]] int64_t img0 = 0;
     if constexpr (PRO) {
@@ -270,7 +276,7 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
     auto slot = [](int r, int c) { return (r * 8 + (c ^ (r & 7))) * 16; };
     int brow[TN];
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) brow[tn] = wn * WN + pw_wrow(tn, i16);
+    for (int tn = 0; tn < TN; ++tn) brow[tn] = wn * WN + 16 * tn + i16;
     [[maybe_unused]] int rel[TM];
     if constexpr (PRO) {
 #pragma unroll
@@ -341,7 +347,10 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
 // memory operations completing in issue order.  The blocks that share a pixel tile
 // are adjacent (consecutive on one XCD), so x is read from HBM about once.
 // LDS layout as in pointwise_dma_kernel: 16-byte chunk c of tile row r at slot
-// K/8 r + ((c & ~7) | ((c ^ r) & 7)).
+// K/8 r + ((c & ~X) | ((c ^ r) & X)), X = 15 for rows of 16 or 32 chunks (K = 128, 256),
+// else 7: measured on gfx950 (bank-conflict counter, 16 consecutive rows read at one
+// chunk), rows of 256 or 512 bytes conflict with the 3-bit swizzle and not with the
+// 4-bit one.
 // ---------------------------------------------------------------------------
 template <int K, int BN, int BM, int EPI>
 __global__ __launch_bounds__(256, 2) void pointwise_resident_kernel(const PwParams p, const int blocks_per_slice) {
@@ -351,6 +360,7 @@ __global__ __launch_bounds__(256, 2) void pointwise_resident_kernel(const PwPara
     constexpr int TILE = BM * K * 2;                 // bytes
     constexpr int D = BM * CPR / 256;                // copies per lane per tile
     constexpr int S = TM * TN / 2;                   // stores per lane per tile
+    constexpr int SWZ = CPR % 16 == 0 ? 15 : 7;      // chunk swizzle mask
     static_assert(D * 256 == BM * CPR && D >= 1, "whole copy instructions");
     __shared__ __align__(16) unsigned char lds[2 * TILE];
     __shared__ float gtab[EPI == PW_GELU ? GELU_TAB_N : 1];
@@ -388,12 +398,12 @@ __global__ __launch_bounds__(256, 2) void pointwise_resident_kernel(const PwPara
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int slot = (wv * D + d) * 64 + lane, r = slot / CPR, sc = slot % CPR;
-            const int c = (sc & ~7) | ((sc ^ r) & 7);
+            const int c = (sc & ~SWZ) | ((sc ^ r) & SWZ);
             const int64_t m = std::min<int64_t>(m0 + r, p.M - 1);
             lds_dma16(p.x + m * K + 8 * c, __builtin_amdgcn_readfirstlane(sb + (wv * D + d) * 1024));
         }
     };
-    auto slot = [](int r, int c) { return (r * CPR + ((c & ~7) | ((c ^ r) & 7))) * 16; };
+    auto slot = [](int r, int c) { return (r * CPR + ((c & ~SWZ) | ((c ^ r) & SWZ))) * 16; };
 
     // Weights and bias in registers before the copies start: the empty statements make
     // the compiler wait for these loads here, outside the loop (it does not see the
