@@ -283,6 +283,17 @@ __global__ __launch_bounds__(kGrnFinalizeThreads) void grn_finalize_kernel(const
         if (sg < SG) {
             const float* pc = partial + b * nslab * C + c;
             int64_t s = sg;
+            // Eight loads in flight, added in the order of the loop below.
+            for (; s + 7 * SG < nslab; s += 8 * SG) {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = pc[(s + j * SG) * C];
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    a0 += v[j];
+                    a1 += v[j + 1];
+                }
+            }
             for (; s + SG < nslab; s += 2 * SG) {
                 a0 += pc[s * C];
                 a1 += pc[(s + SG) * C];
@@ -300,17 +311,29 @@ __global__ __launch_bounds__(kGrnFinalizeThreads) void grn_finalize_kernel(const
         }
     } else {
         for (int64_t c = t; c < C; c += NT) {
-            // Four independent partial sums keep four loads in flight.
+            // Four independent partial sums (a0 takes slabs 0, 4, 8, ...).
             const float* pc = partial + b * nslab * C + c;
             float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-            int64_t s = 0;
-            for (; s + 4 <= nslab; s += 4) {
-                a0 += pc[s * C];
-                a1 += pc[(s + 1) * C];
-                a2 += pc[(s + 2) * C];
-                a3 += pc[(s + 3) * C];
+            // Slab s goes to a(s % 4) below the last multiple of 4 and to a0 after it; the
+            // slabs are loaded sixteen at a time, all in flight, and added in that order.
+            const int64_t full = nslab & ~int64_t(3);
+            for (int64_t s = 0; s < nslab; s += 16) {
+                float v[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = s + j < nslab ? pc[(s + j) * C] : 0.f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int64_t g = s + j;
+                    if (g < full) {
+                        if (j % 4 == 0) a0 += v[j];
+                        else if (j % 4 == 1) a1 += v[j];
+                        else if (j % 4 == 2) a2 += v[j];
+                        else a3 += v[j];
+                    } else if (g < nslab) {
+                        a0 += v[j];
+                    }
+                }
             }
-            for (; s < nslab; ++s) a0 += pc[s * C];
             const float acc = (a0 + a1) + (a2 + a3);
             const float g = sqrtf(acc);
             gx[b * C + c] = g;
