@@ -281,6 +281,20 @@ int vh_dwconv2d_nhwc_forward(
     int32_t epilogue, const void* aux, void* out, int64_t B, int64_t H, int64_t W, int64_t C,
     void* stream);
 
+/* The block's CPE and the LayerNorm after it on a channels-last x [B, H, W, C]
+ * (io_dtype): out = x + conv(x) + b as epilogue 1 of vh_dwconv2d_nhwc_forward
+ * (ksize 3), and out_norm = LayerNorm over the C channels of out as stored, with
+ * ln_weight / ln_bias [C] fp32 and eps, the bits that vh_layernorm2d_forward gives on
+ * out (same reduction order).  C = 8 * 2^k <= 256; 16-byte aligned tensors.  No
+ * counterpart in the reference's native code: it runs the CPE (a depthwise Conv2d plus
+ * the residual add, models/block.py:102-103) and norm1 (LayerNorm2d,
+ * models/block.py:104, utils/layer_norm_cuda.py) as separate modules; this fuses them
+ * on the prepared inference path. */
+int vh_dwconv2d_add_layernorm2d_forward(
+    const void* x, int32_t io_dtype, const float* taps, const float* bias, int32_t ksize,
+    const float* ln_weight, const float* ln_bias, float eps, void* out, void* out_norm,
+    int64_t B, int64_t H, int64_t W, int64_t C, void* stream);
+
 /* Workspace of vh_dwconv2d_gelu_grn_forward: B * (blocks per image) * C fp32 partial
  * sums, or 0 when the shape is not covered (C/8 must divide 256 and the kernel's
  * 256-thread blocks must tile whole images). */

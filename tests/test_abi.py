@@ -218,6 +218,24 @@ def test_dwconv_grn_workspace_query(lib):
     assert rc == hip.VH_ERR_SHAPE
 
 
+def test_dwconv_add_layernorm_validates(lib):
+    """The fused CPE + LayerNorm takes kernel size 3 and C = 8 * 2^k <= 256 only."""
+    p = ctypes.c_void_p(0x1000)
+
+    def call(C=256, ksize=3, x=p, eps=1e-6, dtype=hip.VH_DTYPE_BF16):
+        return lib.vh_dwconv2d_add_layernorm2d_forward(x, dtype, p, p, ksize, p, p, ctypes.c_float(eps), p, p,
+                                                       2, 14, 14, C, None)
+
+    assert call(C=96) == hip.VH_ERR_SHAPE      # C/8 = 12 is not a power of two
+    assert call(C=512) == hip.VH_ERR_SHAPE     # 64 groups: more than one 32-lane row group
+    assert call(ksize=5) == hip.VH_ERR_ARG
+    assert call(x=None) == hip.VH_ERR_ARG
+    assert call(eps=0.0) == hip.VH_ERR_ARG
+    assert call(dtype=7) == hip.VH_ERR_DTYPE
+    assert call(x=ctypes.c_void_p(0x1008)) == hip.VH_ERR_ARG   # misaligned
+    assert b"aligned" in lib.vh_last_error()
+
+
 def test_check_raises_with_message(lib):
     assert _spatial(lib, head_dim=12) == hip.VH_ERR_HEAD_DIM
     with pytest.raises(RuntimeError, match="head_dim"):

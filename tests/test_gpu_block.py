@@ -257,6 +257,45 @@ def test_depthwise_gelu_grn_statistics(device, monkeypatch, dtype, shape, ksize,
     assert_close(scale.cpu().numpy(), grn_scale(plain, gamma, 1e-6).cpu().numpy(), 1e-5, "fused GRN scale")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(2, 64, 56, 56), (3, 128, 28, 28), (2, 256, 14, 14), (4, 256, 7, 7),
+                                   (2, 128, 9, 13), (2, 8, 5, 6), (1, 32, 1, 17)])
+def test_depthwise_add_layernorm_matches_separate_kernels(device, dtype, shape):
+    """The block's CPE with norm1 in one pass gives the bits of the depthwise CPE kernel
+    followed by the channels-last LayerNorm kernel (same sums in the same lane order)."""
+    from visionhope_amd.utils import dwconv
+    from visionhope_amd.utils.layer_norm_cuda import visionhope_layernorm2d
+
+    b, c, h, w = shape
+    conv = torch.nn.Conv2d(c, c, 3, padding=1, groups=c)
+    with torch.no_grad():
+        conv.weight.copy_(randn(*conv.weight.shape, seed=91, scale=0.3))
+        conv.bias.copy_(randn(c, seed=92, scale=0.1))
+    conv = conv.to(device)
+    weight = (1 + randn(c, seed=93, scale=0.2)).to(device)
+    bias = randn(c, seed=94, scale=0.1).to(device)
+    x = randn(b, c, h, w, seed=95, scale=2.0).to(dtype).to(device).contiguous(memory_format=torch.channels_last)
+    fused = dwconv.depthwise_conv_add_layernorm(x, conv, weight, bias, 1e-6)
+    assert fused is not None
+    y, yn = fused
+    ref_y = dwconv.depthwise_conv(x, conv, dwconv.EPI_ADD_INPUT)
+    with torch.no_grad():
+        ref_n = visionhope_layernorm2d(ref_y, weight, bias, 1e-6, force_channels_last=True, out_dtype=dtype)
+    assert y.dtype == yn.dtype == dtype
+    assert torch.equal(y, ref_y)
+    assert torch.equal(yn, ref_n), (yn.float() - ref_n.float()).abs().max().item()
+
+
+def test_depthwise_add_layernorm_declines_uncovered_shapes(device):
+    from visionhope_amd.utils import dwconv
+
+    for c in (96, 512):
+        conv = torch.nn.Conv2d(c, c, 3, padding=1, groups=c).to(device)
+        x = torch.zeros(1, c, 4, 4, device=device, dtype=torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        ones = torch.ones(c, device=device)
+        assert dwconv.depthwise_conv_add_layernorm(x, conv, ones, ones, 1e-6) is None
+
+
 def test_depthwise_gelu_grn_declines_uncovered_shapes(device):
     from visionhope_amd.utils import dwconv
 

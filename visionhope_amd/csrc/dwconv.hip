@@ -18,7 +18,8 @@
 namespace vh {
 
 enum DwEpilogue { DW_PLAIN = 0, DW_ADD_INPUT = 1, DW_GATE = 2, DW_ADD_GELU = 3, DW_ACCUM_F32 = 4, DW_ADD_F32_AUX = 5,
-                  DW_ADD_GELU_SUMSQ = 6 };   // 6: internal, DW_ADD_GELU + GRN partial sums (see below)
+                  DW_ADD_GELU_SUMSQ = 6,     // 6: internal, DW_ADD_GELU + GRN partial sums (see below)
+                  DW_ADD_INPUT_LN = 7 };     // 7: internal, DW_ADD_INPUT + the LayerNorm of the result
 
 struct DwParams {
     const void* x;
@@ -28,6 +29,13 @@ struct DwParams {
     void* out;           // io dtype, or fp32 for DW_ACCUM_F32
     int64_t B, H, W, C;
     float* partial;      // DW_ADD_GELU_SUMSQ: [B, blocks per image, C] sums of squares of out
+    // DW_ADD_INPUT_LN: LayerNorm affine [C] fp32, eps, output [B, H, W, C] (io dtype) and
+    // log2 of the lanes per pixel (C / 8, a power of two <= 32)
+    const float* ln_w = nullptr;
+    const float* ln_b = nullptr;
+    float ln_eps = 0.f;
+    void* out_norm = nullptr;
+    int ln_lg = 0;
 };
 
 // Launch geometry: thread index -> (image, row, segment, channel group), with the
@@ -171,7 +179,8 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
         for (int i = 0; i < NI; ++i) {
             float v[8];
             decode8<T>(r[i], v);
-            if constexpr (EPI == DW_ADD_INPUT || EPI == DW_GATE || EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ) {
+            if constexpr (EPI == DW_ADD_INPUT || EPI == DW_GATE || EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ ||
+                          EPI == DW_ADD_INPUT_LN) {
                 if (i >= R && i < R + P && dy == R) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) center[i - R][j] = v[j];
@@ -210,10 +219,63 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
     }
     const int64_t pix0 = (static_cast<int64_t>(row0) + h) * W + w0;
     [[maybe_unused]] float sumsq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if constexpr (EPI == DW_ADD_INPUT_LN) {
+        // x + conv(x) as stored (rounded to T), then its LayerNorm over the pixel's C
+        // channels: the C/8 lanes of one pixel segment are consecutive lanes (cg = lane
+        // within the group), so the sums run as in layernorm_nhwc8_kernel with one group
+        // of 8 channels per lane, and both outputs are the bits that the separate
+        // kernels give.  A segment's lanes share w0, so the loop exit is uniform in a group.
+        float lw[8], lb[8];
+        load8<float>(p.ln_w + c, lw);
+        load8<float>(p.ln_b + c, lb);
+        const float inv_c = 1.f / static_cast<float>(C);   // exact for power-of-two C
 #pragma unroll
-    for (int px = 0; px < P; ++px) {
-        if (w0 + px >= W) break;
-        dw_store_pixel<EPI, T>(p, (pix0 + px) * C + c, acc[px], center[px], sumsq);
+        for (int px = 0; px < P; ++px) {
+            if (w0 + px >= W) break;
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = center[px][j] + acc[px][j];
+            if constexpr (std::is_same_v<T, bf16_t>) {
+                // one conversion per pair, stored, then read back as the stored values
+                uint32_t wv[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) wv[k] = pack_bf16x2(v[2 * k], v[2 * k + 1]);
+                *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + (pix0 + px) * C + c) =
+                    make_uint4(wv[0], wv[1], wv[2], wv[3]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    v[2 * k] = __uint_as_float(wv[k] << 16);
+                    v[2 * k + 1] = __uint_as_float(wv[k] & 0xffff0000u);
+                }
+            } else {
+                store8<T>(static_cast<T*>(p.out) + (pix0 + px) * C + c, v);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = to_f32(from_f32<T>(v[j]));
+            }
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sum += v[j];
+            sum = ln_lane_sum(sum, p.ln_lg);
+            const float mean = sum * inv_c;
+            float sq = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                v[j] -= mean;
+                sq += v[j] * v[j];
+            }
+            sq = ln_lane_sum(sq, p.ln_lg);
+            const float rstd = __builtin_amdgcn_rsqf(sq * inv_c + p.ln_eps);
+            float o[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = v[j] * rstd * lw[j] + lb[j];
+            store8<T>(static_cast<T*>(p.out_norm) + (pix0 + px) * C + c, o);
+        }
+    } else {
+#pragma unroll
+        for (int px = 0; px < P; ++px) {
+            if (w0 + px >= W) break;
+            dw_store_pixel<EPI, T>(p, (pix0 + px) * C + c, acc[px], center[px], sumsq);
+        }
     }
     if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
         // GRN partial sums: this block's threads cover whole channel groups of one image
@@ -434,6 +496,7 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
         q.out = static_cast<char*>(dp.out) + skip * out_size;
         if (dp.aux) q.aux = static_cast<const char*>(dp.aux) + skip * aux_size;
         if (dp.partial) q.partial = dp.partial + b0 * (dp.H * segs * (dp.C / 8) / 256) * dp.C;
+        if (dp.out_norm) q.out_norm = static_cast<char*>(dp.out_norm) + skip * sizeof(T);
         DwGrid g;
         g.total = static_cast<uint32_t>(q.B * q.H * segs * (q.C / 8));
         g.G = make_fastdiv(static_cast<uint32_t>(q.C / 8));
@@ -448,6 +511,10 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
             VH_DW(DW_PLAIN) VH_DW(DW_ADD_INPUT) VH_DW(DW_GATE) VH_DW(DW_ADD_GELU) VH_DW(DW_ACCUM_F32)
             VH_DW(DW_ADD_F32_AUX) VH_DW(DW_ADD_GELU_SUMSQ)
 #undef VH_DW
+            case DW_ADD_INPUT_LN:
+                if constexpr (K == 3)
+                    hipLaunchKernelGGL((dwconv_nhwc_kernel<K, DW_ADD_INPUT_LN, T, P>), grid, dim3(256), 0, s, q, g, x_bytes);
+                break;
         }
     }
 }
@@ -544,7 +611,7 @@ template <int K, typename T>
 void launch_dw(int epi, const DwParams& dp, hipStream_t s) {
     if constexpr (sizeof(T) == 2) {
         DwTile t;
-        if (dw_tile_plan(K, dp.B, dp.H, dp.W, dp.C, 2, t)) {
+        if (epi != DW_ADD_INPUT_LN && dw_tile_plan(K, dp.B, dp.H, dp.W, dp.C, 2, t)) {
             if (t.P == 7) launch_dw_tile<K, T, 7>(epi, dp, t, s);
             else if constexpr (K == 7) {
                 if (t.P == 2) launch_dw_tile<K, T, 2>(epi, dp, t, s);
@@ -596,6 +663,43 @@ extern "C" int vh_dwconv2d_nhwc_forward(const void* x, int32_t io_dtype, const f
         default: go(f16_t{}); break;
     }
     return check_launch("dwconv_nhwc_kernel");
+}
+
+extern "C" int vh_dwconv2d_add_layernorm2d_forward(const void* x, int32_t io_dtype, const float* taps,
+                                                  const float* bias, int32_t ksize, const float* ln_weight,
+                                                  const float* ln_bias, float eps, void* out, void* out_norm,
+                                                  int64_t B, int64_t H, int64_t W, int64_t C, void* stream) {
+    VH_REQUIRE(x && taps && out && out_norm && ln_weight && ln_bias, VH_ERR_ARG,
+               "depthwise conv + LayerNorm pointers must not be null");
+    VH_REQUIRE(B > 0 && H > 0 && W > 0 && C > 0, VH_ERR_SHAPE, "depthwise conv + LayerNorm expects nonempty NHWC input");
+    VH_REQUIRE(ksize == 3, VH_ERR_ARG, "depthwise conv + LayerNorm takes kernel size 3, got %d", ksize);
+    const int64_t ng = C / 8;
+    VH_REQUIRE(C % 8 == 0 && ng <= 32 && (ng & (ng - 1)) == 0, VH_ERR_SHAPE,
+               "depthwise conv + LayerNorm needs C = 8 * 2^k <= 256, got %lld", (long long)C);
+    VH_REQUIRE(valid_dtype(io_dtype), VH_ERR_DTYPE, "unsupported io dtype code %d", io_dtype);
+    VH_REQUIRE(eps > 0.f, VH_ERR_ARG, "LayerNorm eps must be positive");
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                            reinterpret_cast<uintptr_t>(out_norm) | reinterpret_cast<uintptr_t>(taps) |
+                            reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(ln_weight) |
+                            reinterpret_cast<uintptr_t>(ln_bias);
+    VH_REQUIRE(align % 16 == 0, VH_ERR_ARG, "depthwise conv + LayerNorm tensors must be 16-byte aligned");
+    VH_REQUIRE(H * W * C * dtype_bytes(io_dtype) < (int64_t(1) << 31), VH_ERR_SHAPE,
+               "depthwise conv image too large (one image must be below 2 GiB)");
+    DwParams dp{x, taps, bias, nullptr, out, B, H, W, C, nullptr};
+    dp.ln_w = ln_weight;
+    dp.ln_b = ln_bias;
+    dp.ln_eps = eps;
+    dp.out_norm = out_norm;
+    int lg = 0;
+    while ((int64_t(1) << lg) < ng) ++lg;
+    dp.ln_lg = lg;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (io_dtype) {
+        case VH_DTYPE_F32: launch_dw<3, float>(DW_ADD_INPUT_LN, dp, s); break;
+        case VH_DTYPE_BF16: launch_dw<3, bf16_t>(DW_ADD_INPUT_LN, dp, s); break;
+        default: launch_dw<3, f16_t>(DW_ADD_INPUT_LN, dp, s); break;
+    }
+    return check_launch("dwconv_nhwc_kernel (add + LayerNorm)");
 }
 
 extern "C" size_t vh_dwconv2d_gelu_grn_workspace_bytes(int64_t B, int64_t H, int64_t W, int64_t C, int32_t ksize) {

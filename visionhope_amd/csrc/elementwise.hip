@@ -827,30 +827,8 @@ __global__ __launch_bounds__(256) void layernorm_nhwc_kernel(const T* __restrict
 // assembled in LDS and stored in 16-byte chunks by consecutive lanes, so every store
 // instruction of a wave writes one contiguous 1 KB run (a lane's own 8 outputs would
 // leave 16-byte gaps in each instruction's footprint).  Dynamic LDS of
-// (256 / LPR) * C * sizeof(TO) bytes.
-// Sum over aligned groups of 2^lg consecutive lanes (lg = 0 .. 6, uniform), on the VALU:
-// DPP quad permutes and half-row / row mirrors inside a 16-lane row, then the gfx950
-// row-swap permutes for the 16- and 32-lane steps (no LDS round trips).
-template <int CTRL>
-__device__ __forceinline__ float ln_dpp(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float ln_lane_sum(float v, int lg) {
-    if (lg >= 1) v += ln_dpp<0xB1>(v);    // lanes (1, 0, 3, 2)
-    if (lg >= 2) v += ln_dpp<0x4E>(v);    // lanes (2, 3, 0, 1)
-    if (lg >= 3) v += ln_dpp<0x141>(v);   // i <-> 7 - i within 8 lanes
-    if (lg >= 4) v += ln_dpp<0x140>(v);   // i <-> 15 - i within 16 lanes
-    if (lg >= 5) {
-        const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
-    }
-    if (lg >= 6) {
-        const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
-    }
-    return v;
-}
-
+// (256 / LPR) * C * sizeof(TO) bytes.  The row sums run on the VALU (ln_lane_sum: DPP
+// and row-swap permutes, no LDS round trips).
 template <typename T, typename TO, int GP, bool ADD = false, bool STAGE = false>
 __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                              const float* __restrict__ bias, TO* __restrict__ y,
@@ -887,7 +865,8 @@ __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restric
         for (int j = 0; j < 8; ++j) sum += v[k][j];
     }
     sum = ln_lane_sum(sum, lpr_log2);
-    const float mean = sum / static_cast<float>(C);
+    const float inv_c = 1.f / static_cast<float>(C);   // exact for power-of-two C
+    const float mean = sum * inv_c;
     float sq = 0.f;
 #pragma unroll
     for (int k = 0; k < GP; ++k)
@@ -897,7 +876,7 @@ __global__ __launch_bounds__(256) void layernorm_nhwc8_kernel(const T* __restric
             sq += v[k][j] * v[k][j];
         }
     sq = ln_lane_sum(sq, lpr_log2);
-    const float rstd = 1.f / sqrtf(sq / static_cast<float>(C) + eps);
+    const float rstd = __builtin_amdgcn_rsqf(sq * inv_c + eps);   // hardware reciprocal square root
     if constexpr (STAGE) {
         extern __shared__ __align__(16) unsigned char ln_stage[];
         TO* st = reinterpret_cast<TO*>(ln_stage) + (threadIdx.x >> lpr_log2) * C;

@@ -267,6 +267,29 @@ __device__ __forceinline__ float gelu_fast(float x) {
     return fmaf(-fabsf(x), half_erfc, fmaxf(x, 0.f));
 }
 
+// Sum of v over aligned groups of 2^lg consecutive lanes (lg <= 6), every lane of a
+// group receiving the group's sum: DPP quad permutes and row mirrors, then the
+// 16- and 32-lane row swaps.
+template <int CTRL>
+__device__ __forceinline__ float ln_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float ln_lane_sum(float v, int lg) {
+    if (lg >= 1) v += ln_dpp<0xB1>(v);    // lanes (1, 0, 3, 2)
+    if (lg >= 2) v += ln_dpp<0x4E>(v);    // lanes (2, 3, 0, 1)
+    if (lg >= 3) v += ln_dpp<0x141>(v);   // i <-> 7 - i within 8 lanes
+    if (lg >= 4) v += ln_dpp<0x140>(v);   // i <-> 15 - i within 16 lanes
+    if (lg >= 5) {
+        const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+    }
+    if (lg >= 6) {
+        const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+    }
+    return v;
+}
+
 // v rounded to bf16 (nearest even), as an fp32.
 __device__ __forceinline__ float round_bf16(float v) {
     return __uint_as_float(static_cast<uint32_t>(from_f32<bf16_t>(v).bits) << 16);

@@ -2,6 +2,7 @@
 ``models/block.py``), its reference-order forward, and the fused inference forward that
 prepared models run on the GPU."""
 
+import os
 import torch
 from torch import nn
 from torch.nn import functional as F
@@ -178,11 +179,21 @@ class VisionHOPEBlock(nn.Module):
         def nchw(t_nhwc):
             return t_nhwc.permute(0, 3, 1, 2)
 
+        # CPE and norm1: one pass (the sum and its LayerNorm) where the map allows
+        # (VH_CPE_LN=0 runs the two kernels, for measurements).
+        h = None
         if self.cpe is not None:
-            x = dwconv.depthwise_conv(x, self.cpe, dwconv.EPI_ADD_INPUT)
+            fused = (dwconv.depthwise_conv_add_layernorm(x, self.cpe, self.norm1.weight, self.norm1.bias,
+                                                         self.norm1.eps)
+                     if x.dtype == act and os.environ.get("VH_CPE_LN", "1") != "0" else None)
+            if fused is not None:
+                x, h = fused
+            else:
+                x = dwconv.depthwise_conv(x, self.cpe, dwconv.EPI_ADD_INPUT)
         # Token-mixer branch.
-        h = visionhope_layernorm2d(x, self.norm1.weight, self.norm1.bias, self.norm1.eps,
-                                   force_channels_last=True, out_dtype=act)
+        if h is None:
+            h = visionhope_layernorm2d(x, self.norm1.weight, self.norm1.bias, self.norm1.eps,
+                                       force_channels_last=True, out_dtype=act)
         inner = project(h.permute(0, 2, 3, 1), self.proj_in)
         if self.local_mode == "gated_dwconv7":
             gate = project(inner, self.local_gate)

@@ -108,6 +108,35 @@ def depthwise_conv(x, conv, epilogue=EPI_PLAIN, aux=None, out=None):
 
 
 @on_tensor_device
+def depthwise_conv_add_layernorm(x, conv, weight, bias, eps):
+    """``x + conv(x)`` (``EPI_ADD_INPUT``, the block CPE) and the LayerNorm over the
+    channels of that sum (``visionhope_layernorm2d(..., force_channels_last=True,
+    out_dtype=x.dtype)`` with ``weight``, ``bias``, ``eps``), both channels-last in x's
+    dtype, from one pass and with the same bits as the two separate kernels; ``None``
+    when the shape is not covered (kernel size 3 and C = 8 * 2^k <= 256, FP32 contiguous
+    affine parameters), then use ``depthwise_conv`` and ``visionhope_layernorm2d``."""
+    if not x.is_cuda or x.dtype not in _DTYPES or not is_depthwise(conv):
+        raise ValueError("depthwise_conv_add_layernorm expects a CUDA map and a depthwise Conv2d")
+    batch, channels, height, width = x.shape
+    groups = channels // 8
+    if (conv.kernel_size[0] != 3 or channels % 8 or groups > 32 or groups & (groups - 1)
+            or weight.dtype != torch.float32 or bias.dtype != torch.float32
+            or not weight.is_contiguous() or not bias.is_contiguous()
+            or weight.numel() != channels or bias.numel() != channels
+            or weight.data_ptr() % 16 or bias.data_ptr() % 16):
+        return None
+    taps, conv_bias = depthwise_taps(conv)
+    x = _channels_last(x)
+    out = torch.empty_like(x, memory_format=torch.channels_last)
+    out_norm = torch.empty_like(x, memory_format=torch.channels_last)
+    lib = hip.load_library()
+    hip.check(lib.vh_dwconv2d_add_layernorm2d_forward(
+        hip.ptr(x), hip.dtype_code(x.dtype), hip.ptr(taps), hip.ptr(conv_bias), 3, hip.ptr(weight),
+        hip.ptr(bias), float(eps), hip.ptr(out), hip.ptr(out_norm), batch, height, width, channels,
+        hip.stream_of(x)), "vh_dwconv2d_add_layernorm2d_forward")
+    return out, out_norm
+
+
 def depthwise_conv_gelu_grn(x, conv, gamma, eps):
     """``gelu(x + conv(x))`` (``EPI_ADD_GELU``) and the GRN scale ``[B, C]`` of that output
     (``1 + gamma * nx``, ``utils/grn.py:26-38``) from one pass over the map; ``None`` when
