@@ -257,6 +257,55 @@ def test_gelu_table_header_matches_generator(tmp_path):
     assert out.read_text() == (csrc / "gelu_table.h").read_text()
 
 
+def _gelu_interp(x32, pairs):
+    """gelu_qi in float32 (vh_common.h): s = min(128 |x|, 1024 - 2^-14), i = floor(s),
+    f = s - i, Q = fma(f, step[i], value[i]), GELU = fma(-|x|, Q, max(x, 0))."""
+    a = np.abs(x32)
+    s = np.minimum(a * np.float32(128), np.float32(1024 - 2.0 ** -14)).astype(np.float32)
+    i = s.astype(np.int64)
+    f = (s - i.astype(np.float32)).astype(np.float32)
+    # fma: the float64 product of two float32 values is exact; one rounding to float32
+    q = (f.astype(np.float64) * pairs[i, 1] + pairs[i, 0]).astype(np.float32)
+    return (np.maximum(x32, 0).astype(np.float64) - a.astype(np.float64) * q).astype(np.float32).astype(np.float64)
+
+
+def test_gelu_interpolation_table_accuracy():
+    """The interpolated GELU of the depthwise kernels (gelu_qi), emulated with the pairs
+    parsed from gelu_table.h, against x Phi(x) in float64 (scipy's ndtr) on a dense grid
+    of float32 inputs: within 2.3e-6 absolute everywhere and 2.1e-4 relative where
+    |GELU| > 1e-6 (the bounds the header states), x/2 near 0, x at large positive x.
+    A table shifted by one entry, or with the steps dropped, fails the bounds."""
+    import re
+    from scipy.special import ndtr
+
+    src = (Path(__file__).resolve().parents[1] / "visionhope_amd" / "csrc" / "gelu_table.h").read_text()
+    n = int(re.search(r"GELU_QI_N = ([0-9]+)u", src).group(1))
+    body = src.split("gelu_interp_table[2 * GELU_QI_N]")[1].split("{")[1].split("};")[0]
+    vals = [float.fromhex(v) for v in re.findall(r"(-?0x[0-9a-fp.+-]+)f,", body)]
+    assert n == 1024 and len(vals) == 2 * n
+    pairs = np.array(vals, dtype=np.float32).reshape(n, 2).astype(np.float64)
+    x32 = np.concatenate([np.linspace(-12, 12, 600001), np.linspace(-1e-3, 1e-3, 2001),
+                          np.array([0.0, 7.999, 8.0, 30.0, -7.999, -8.0])]).astype(np.float32)
+    x = x32.astype(np.float64)
+    exact = x * ndtr(x)
+
+    def errors(table):
+        err = np.abs(_gelu_interp(x32, table) - exact)
+        big = np.abs(exact) > 1e-6
+        return err.max(), (err[big] / np.abs(exact[big])).max()
+
+    ab, rel = errors(pairs)
+    assert ab < 2.3e-6 and rel < 2.1e-4, (ab, rel)
+    small = (np.abs(x) < 1e-4) & (x != 0)
+    assert np.allclose(_gelu_interp(x32[small], pairs), x[small] / 2, rtol=1e-4, atol=0)
+    assert _gelu_interp(np.float32([30.0]), pairs)[0] == 30.0
+    shifted = np.roll(pairs, 1, axis=0)
+    assert errors(shifted)[0] > 1e-3
+    no_step = pairs.copy()
+    no_step[:, 1] = 0
+    assert errors(no_step)[0] > 1e-4
+
+
 def test_gelu_table_gives_the_bf16_gelu():
     """The device's tabulated GELU (gelu_bf16_tab: fma(-|x|, Q[clamp(|x|)], max(x, 0)) in
     float32 with Q(a) = Phi(-a), then the output rounding to bf16), emulated with the
@@ -271,7 +320,8 @@ def test_gelu_table_gives_the_bf16_gelu():
     src = (Path(__file__).resolve().parents[1] / "visionhope_amd" / "csrc" / "gelu_table.h").read_text()
     lo, hi, n = (int(v, 0) for v in re.search(r"GELU_TAB_LO = (0x[0-9A-F]+)u, GELU_TAB_HI = (0x[0-9A-F]+)u, "
                                                r"GELU_TAB_N = ([0-9]+)u", src).groups())
-    vals = [float.fromhex(v) for v in re.findall(r"(-?0x[0-9a-fp.+-]+)f,", src)]
+    body = src.split("gelu_tail_table[GELU_TAB_N] = {")[1].split("};")[0]
+    vals = [float.fromhex(v) for v in re.findall(r"(-?0x[0-9a-fp.+-]+)f,", body)]
     assert n == hi - lo + 1 and len(vals) == n
     tab = np.array(vals, dtype=np.float32)
 

@@ -84,7 +84,8 @@ __device__ __forceinline__ void decode8(const Raw8<T>& r, float (&v)[8]) {
 template <int EPI, typename T>
 __device__ __forceinline__ void dw_store_pixel(const DwParams& p, int64_t at, float (&acc)[8],
                                                [[maybe_unused]] const float (&center)[8],
-                                               [[maybe_unused]] float (&sumsq)[8]) {
+                                               [[maybe_unused]] float (&sumsq)[8],
+                                               [[maybe_unused]] const float2* gq = nullptr) {
     if constexpr (EPI == DW_ACCUM_F32) {
         float* o = static_cast<float*>(p.out) + at;
         float prev[8];
@@ -104,8 +105,15 @@ __device__ __forceinline__ void dw_store_pixel(const DwParams& p, int64_t at, fl
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[j] = center[j] + sigmoid_fast(gv[j]) * acc[j];
         } else if constexpr (EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ) {
+            // the interpolated GELU (gq: its table in LDS) for 2-byte outputs, else the
+            // erfc form
+            if (sizeof(T) == 2 && gq) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = gelu_fast(center[j] + acc[j]);
+                for (int j = 0; j < 8; ++j) acc[j] = gelu_qi(center[j] + acc[j], gq);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = gelu_fast(center[j] + acc[j]);
+            }
             if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -133,6 +141,14 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
     constexpr int R = K / 2, NI = P + K - 1;
     constexpr uint32_t OUTSIDE = 0x80000000u;
     const uint32_t idx = xcd_remap_any(blockIdx.x, gridDim.x) * 256u + threadIdx.x;
+    // GELU table of 2-byte outputs, copied to LDS by every thread before any returns
+    [[maybe_unused]] const float2* gq = nullptr;
+    if constexpr ((EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ) && sizeof(T) == 2) {
+        __shared__ float4 gq4[GELU_QI_N / 2];
+        gelu_qi_fill(gq4, static_cast<int>(threadIdx.x), 256);
+        __syncthreads();
+        gq = reinterpret_cast<const float2*>(gq4);
+    }
     if (idx >= g.total) return;
     const uint32_t t0 = fast_div(idx, g.G);
     const uint32_t cg = idx - t0 * g.G.d;
@@ -274,7 +290,7 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
 #pragma unroll
         for (int px = 0; px < P; ++px) {
             if (w0 + px >= W) break;
-            dw_store_pixel<EPI, T>(p, (pix0 + px) * C + c, acc[px], center[px], sumsq);
+            dw_store_pixel<EPI, T>(p, (pix0 + px) * C + c, acc[px], center[px], sumsq, gq);
         }
     }
     if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
@@ -327,6 +343,13 @@ template <int K, int EPI, typename T, int P>
 __global__ __launch_bounds__(256) void dwconv_tile_kernel(const DwParams p, const DwTile t) {
     constexpr int R = K / 2, NI = P + K - 1, VB = 8 * static_cast<int>(sizeof(T));
     extern __shared__ __align__(16) unsigned char dw_lds[];
+    // GELU table of 2-byte outputs (visible after the staging barrier below)
+    [[maybe_unused]] const float2* gq = nullptr;
+    if constexpr ((EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ) && sizeof(T) == 2) {
+        __shared__ float4 gq4[GELU_QI_N / 2];
+        gelu_qi_fill(gq4, static_cast<int>(threadIdx.x), 256);
+        gq = reinterpret_cast<const float2*>(gq4);
+    }
     const int CG = t.CG, CS = 8 * CG, H = static_cast<int>(p.H), W = static_cast<int>(p.W);
     const int64_t C = p.C;
     // Slabs of one (image, band) are adjacent blocks (they read the same input lines),
@@ -442,7 +465,7 @@ __global__ __launch_bounds__(256) void dwconv_tile_kernel(const DwParams p, cons
             float center[8];
             if constexpr (EPI == DW_ADD_INPUT || EPI == DW_GATE || EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ)
                 decode8<T>(vec_at(r + R, w0 + px + R), center);
-            dw_store_pixel<EPI, T>(p, (pix0 + px) * C + c, acc[px], center, sumsq);
+            dw_store_pixel<EPI, T>(p, (pix0 + px) * C + c, acc[px], center, sumsq, gq);
         }
     }
     if constexpr (EPI == DW_ADD_GELU_SUMSQ) {

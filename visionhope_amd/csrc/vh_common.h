@@ -315,4 +315,20 @@ __device__ __forceinline__ void gelu_tab_fill(float* tab, int tid, int nthreads)
     for (int i = tid; i < static_cast<int>(GELU_TAB_N); i += nthreads) tab[i] = gelu_tail_table[i];
 }
 
+// GELU of a float32 value through the interpolation table of Q(a) = Phi(-a) in
+// gelu_table.h (GELU_QI_N (value, step) pairs on the grid a = i / 128, normally copied to
+// LDS by gelu_qi_fill): max(v, 0) - |v| Q(|v|) with Q(|v|) = fma(f, step[i], value[i]),
+// s = min(128 |v|, 1024 - 2^-14), i = floor(s), f = s - i (exact).  Within 2.3e-6
+// absolute and 2.1e-4 relative (where |GELU| > 1e-6) of x Phi(x).
+__device__ __forceinline__ float gelu_qi(float v, const float2* tab) {
+    const float a = fabsf(v);
+    const float s = fminf(a * GELU_QI_SCALE, 1023.99993896484375f);
+    const float2 e = tab[static_cast<int>(s)];
+    return fmaf(-a, fmaf(__builtin_amdgcn_fractf(s), e.y, e.x), fmaxf(v, 0.f));
+}
+__device__ __forceinline__ void gelu_qi_fill(float4* tab, int tid, int nthreads) {
+    const float4* src = reinterpret_cast<const float4*>(gelu_interp_table);
+    for (int i = tid; i < static_cast<int>(GELU_QI_N / 2); i += nthreads) tab[i] = src[i];
+}
+
 }  // namespace vh
