@@ -59,6 +59,28 @@ typedef struct vh_srnl_consts {
 int vh_abi_version(void);
 const char* vh_last_error(void);
 
+/* Dispatch overrides, for tests and measurements only.  No counterpart in the
+ * reference (its only environment reads are the numerics constants,
+ * models/srnl_core/chunk.py:34-58).  Every entry point chooses its kernel
+ * variant from its own arguments; nothing is read from the environment.
+ * vh_set_dispatch_override(name, value) forces one choice for every later call
+ * in this process until it is cleared (value NULL or ""); an unknown name or a
+ * malformed value returns VH_ERR_ARG and changes nothing.  Names and values:
+ *   scan_ut          "0" | "1"        SRNL head_dim-16 bf16: stepped form / block form
+ *   scan_wide        "0"|"1"|"2"|"4"  SRNL: waves per line of the wide scan (0: none)
+ *   scan_tb          "1" | "2"        wide scan: row split / token blocks
+ *   scan_pack        "<L>x<T>"        head_dim-16 scans: lines and 16-slot tiles per wave
+ *   pw_cfg, pw_resident               1x1 convolution kernel variants
+ *   dw_tile, dw_tile_cs, dw_tile_p, dw_launch_bytes   depthwise kernel variants
+ *   ln_stage         "0" | "1"        LayerNorm staged stores
+ *   conv_band        "0" | "1"        3x3 convolution band kernel
+ *   grn_spin_limit   1 .. 2^20        one-pass GRN: sleeps before a piece stops waiting
+ *                                     for the other pieces of its image
+ * Results stay within each kernel's stated tolerance under every override: an
+ * override changes which kernel runs, never what it computes. */
+int vh_set_dispatch_override(const char* name, const char* value);
+void vh_clear_dispatch_overrides(void);
+
 /* ---------------------------------------------------------------------------
  * SRNL recurrence.  Every SRNL entry point runs the same two kernels: a scan
  * over the chunks of each (batch, direction, head) line that writes the
@@ -208,6 +230,14 @@ int vh_postprocess_scale_forward(
  * workspace once); every call leaves them zero, so the workspace can be reused as is.
  * Calls that share a workspace must not overlap (use one workspace per stream). */
 size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W);
+
+/* Diagnostic, not for graph capture: synchronises `stream`, then sets *count to the
+ * number of times a workgroup of vh_grn_forward's one-pass kernel on this workspace
+ * stopped waiting for the other workgroups of its image and computed the image's
+ * statistics from x itself (its output is still correct; the count only shows that
+ * the wait gave up).  The count is never reset by the library.  No counterpart in
+ * the reference, whose GRN has no cross-workgroup wait (grn_cuda.cu:290-320). */
+int vh_grn_workspace_fallbacks(const void* workspace, size_t workspace_bytes, void* stream, int64_t* count);
 
 /* GRN on channels-last x [B, H, W, C] (io_dtype): gx = ||x||_2 over H*W,
  * nx = gx / (mean_c gx + eps), y = x (1 + gamma nx) + beta, y [B, H, W, C] computed

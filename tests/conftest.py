@@ -36,6 +36,22 @@ def oracle():
     return module
 
 
+@pytest.fixture
+def dispatch():
+    """Forces kernel choices of the library for one test (``vh_set_dispatch_override``,
+    e.g. ``dispatch(scan_pack="2x2")``); every override is cleared when the test ends."""
+    from visionhope_amd.utils import hip
+
+    lib = hip.load_library()
+
+    def force(**values):
+        for name, value in values.items():
+            hip.check(lib.vh_set_dispatch_override(name.encode(), str(value).encode()), "vh_set_dispatch_override")
+
+    yield force
+    lib.vh_clear_dispatch_overrides()
+
+
 @pytest.fixture(scope="session")
 def device():
     import torch

@@ -270,3 +270,37 @@ def test_srnl_backward_validates_directions_and_constants(lib):
         assert name in lib.vh_last_error()
     bad_margin = hip.make_consts(0.025, 0.0, 2.197224577, 0.999, True, 0.0)
     assert _spatial(lib, consts=bad_margin) == hip.VH_ERR_ARG
+
+
+def test_dispatch_overrides_are_validated(lib):
+    """Kernel choices are forced only through vh_set_dispatch_override, which rejects unknown
+    names and malformed values; nothing is read from the environment."""
+    assert lib.vh_set_dispatch_override(b"no_such_knob", b"1") == hip.VH_ERR_ARG
+    assert b"unknown" in lib.vh_last_error()
+    for name, bad in ((b"scan_wide", b"3"), (b"scan_pack", b"3x4"), (b"scan_pack", b"4x2"), (b"scan_ut", b"yes"),
+                      (b"grn_spin_limit", b"0"), (b"grn_spin_limit", b"2000000"), (b"pw_cfg", b"q1"),
+                      (b"dw_launch_bytes", b"-5"), (b"scan_tb", b"12345678901234567890123456789012345")):
+        assert lib.vh_set_dispatch_override(name, bad) == hip.VH_ERR_ARG, (name, bad)
+    for name, good in ((b"scan_wide", b"2"), (b"scan_pack", b"2x4"), (b"grn_spin_limit", b"64"),
+                       (b"pw_cfg", b"t128x128k32o2"), (b"dw_launch_bytes", b"4097")):
+        assert lib.vh_set_dispatch_override(name, good) == hip.VH_OK, (name, good)
+        assert lib.vh_set_dispatch_override(name, None) == hip.VH_OK
+    lib.vh_clear_dispatch_overrides()
+
+
+def test_no_environment_reads_in_the_library():
+    """The shipped sources choose kernels from their arguments (and the dispatch overrides);
+    the only environment variables read anywhere are the reference's numerics constants."""
+    sources = list((ROOT / "visionhope_amd" / "csrc").glob("*.hip")) + list((ROOT / "visionhope_amd" / "csrc").glob("*.h"))
+    for path in sources:
+        assert "getenv" not in path.read_text(), path.name
+    for path in (ROOT / "visionhope_amd").rglob("*.py"):
+        text = path.read_text()
+        if "os.environ" in text:
+            assert path.name in ("chunk.py", "build.py"), path
+
+
+def test_grn_fallback_query_validates(lib):
+    count = ctypes.c_int64(-1)
+    assert lib.vh_grn_workspace_fallbacks(None, 1 << 20, None, ctypes.byref(count)) == hip.VH_ERR_ARG
+    assert lib.vh_grn_workspace_fallbacks(ctypes.c_void_p(0x1000), 100, None, ctypes.byref(count)) == hip.VH_ERR_WORKSPACE

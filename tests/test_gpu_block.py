@@ -40,12 +40,12 @@ def _dw_reference(x, conv, epilogue, gate=None, acc=None):
 @pytest.mark.parametrize("epilogue", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
 @pytest.mark.parametrize("tile", ["0", "2"])
-def test_depthwise_epilogues(device, monkeypatch, ksize, epilogue, dtype, tol, tile):
-    """Both kernels (the per-thread window one, VH_DW_TILE=0, and the LDS-tiled one
-    wherever it applies, VH_DW_TILE=2; FP32 maps always take the first)."""
+def test_depthwise_epilogues(device, dispatch, ksize, epilogue, dtype, tol, tile):
+    """Both kernels (the per-thread window one, dw_tile="0", and the LDS-tiled one
+    wherever it applies, dw_tile="2"; FP32 maps always take the first)."""
     from visionhope_amd.utils import dwconv
 
-    monkeypatch.setenv("VH_DW_TILE", tile)
+    dispatch(dw_tile=tile)
 
     channels = 24
     conv = torch.nn.Conv2d(channels, channels, ksize, padding=ksize // 2, groups=channels)
@@ -75,7 +75,7 @@ def test_depthwise_epilogues(device, monkeypatch, ksize, epilogue, dtype, tol, t
 @pytest.mark.parametrize("ksize", [3, 5, 7])
 @pytest.mark.parametrize("epilogue", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("shape", [(3, 40, 14, 14), (2, 16, 28, 28), (1, 64, 7, 7), (2, 8, 5, 19), (1, 128, 9, 16)])
-def test_depthwise_tiled_kernel_matches_window_kernel(device, monkeypatch, ksize, epilogue, shape):
+def test_depthwise_tiled_kernel_matches_window_kernel(device, dispatch, ksize, epilogue, shape):
     """The LDS-tiled kernel accumulates each window in the order of the per-thread one,
     so on bf16 maps the two give identical bits (shapes: Tiny-like maps, a map narrower
     than one segment, rows that do not fill the last band, several channel slabs)."""
@@ -93,7 +93,7 @@ def test_depthwise_tiled_kernel_matches_window_kernel(device, monkeypatch, ksize
     aux = gate if epilogue == dwconv.EPI_GATE else acc if epilogue == dwconv.EPI_ADD_F32_AUX else None
     results = []
     for tile in ("0", "2"):
-        monkeypatch.setenv("VH_DW_TILE", tile)
+        dispatch(dw_tile=tile)
         out = acc.clone() if epilogue == dwconv.EPI_ACCUM_F32 else None
         results.append(dwconv.depthwise_conv(x, conv, epilogue, aux=aux, out=out))
     torch.cuda.synchronize()
@@ -101,7 +101,7 @@ def test_depthwise_tiled_kernel_matches_window_kernel(device, monkeypatch, ksize
 
 
 @pytest.mark.parametrize("ksize,epilogue", [(3, 3), (7, 2), (5, 5)])
-def test_depthwise_split_launches_match_one_launch(device, monkeypatch, ksize, epilogue):
+def test_depthwise_split_launches_match_one_launch(device, dispatch, ksize, epilogue):
     """Inputs above the per-launch buffer limit go in several launches of whole images;
     the result is bit-identical to one launch (the limit is lowered to one image here)."""
     from visionhope_amd.utils import dwconv
@@ -112,13 +112,13 @@ def test_depthwise_split_launches_match_one_launch(device, monkeypatch, ksize, e
         conv.weight.copy_(randn(*conv.weight.shape, seed=41, scale=0.3))
         conv.bias.copy_(randn(channels, seed=42, scale=0.1))
     conv = conv.to(device)
-    monkeypatch.setenv("VH_DW_TILE", "0")   # the split applies to the per-thread window kernel
+    dispatch(dw_tile="0")   # the split applies to the per-thread window kernel
     x = randn(5, channels, h, w, seed=43).bfloat16().to(device).contiguous(memory_format=torch.channels_last)
     gate = randn(5, channels, h, w, seed=44).bfloat16().to(device).contiguous(memory_format=torch.channels_last)
     acc = randn(5, h, w, channels, seed=45).to(device)
     aux = gate if epilogue == dwconv.EPI_GATE else acc if epilogue == dwconv.EPI_ADD_F32_AUX else None
     whole = dwconv.depthwise_conv(x, conv, epilogue, aux=aux)
-    monkeypatch.setenv("VH_DW_LAUNCH_BYTES", str(h * w * channels * 2 + 7))
+    dispatch(dw_launch_bytes=str(h * w * channels * 2 + 7))
     split = dwconv.depthwise_conv(x, conv, epilogue, aux=aux)
     torch.cuda.synchronize()
     assert torch.equal(split, whole)
@@ -156,8 +156,11 @@ def _cpu_block_reference(block, x, oracle):
 
 
 @pytest.mark.parametrize("local_mode", ["gated_dwconv7", "residual_dwconv"])
-@pytest.mark.parametrize("autocast", [False, True])
+@pytest.mark.parametrize("autocast", [None, torch.bfloat16, torch.float16])
 def test_fused_block_matches_oracle(oracle, device, local_mode, autocast):
+    """The fused inference path of a block (FP32, bf16 and fp16 autocast; fp16 takes the
+    library GEMM for the 1x1 projections and the fp16 scan and readout kernels) against
+    the prepared block on the CPU with the FP64 oracle operator."""
     from visionhope_amd.inference.prepare import prepare_for_inference
     from visionhope_amd.models.block import VisionHOPEBlock
 
@@ -172,15 +175,15 @@ def test_fused_block_matches_oracle(oracle, device, local_mode, autocast):
     expected = _cpu_block_reference(reference, x, oracle).numpy()
 
     x_dev = x.to(device).contiguous(memory_format=torch.channels_last)
-    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
-        if autocast:
-            x_dev = x_dev.bfloat16()
+    with torch.no_grad(), torch.autocast("cuda", dtype=autocast or torch.bfloat16, enabled=autocast is not None):
+        if autocast is not None:
+            x_dev = x_dev.to(autocast)
         assert gpu._fused_eligible(x_dev)
         out = gpu(x_dev)
-    assert out.dtype == (torch.bfloat16 if autocast else torch.float32)
+    assert out.dtype == (autocast or torch.float32)
     assert out.is_contiguous(memory_format=torch.channels_last)
-    # FP32 tolerance 1e-4; bf16 autocast tolerance 2e-2, both normwise and elementwise.
-    assert_close(out.double().cpu().numpy(), expected, 2e-2 if autocast else 1e-4,
+    # FP32 tolerance 1e-4; bf16 / fp16 autocast tolerance 2e-2, both normwise and elementwise.
+    assert_close(out.double().cpu().numpy(), expected, 2e-2 if autocast is not None else 1e-4,
                  f"fused block {local_mode} autocast={autocast}")
 
 
@@ -233,14 +236,14 @@ def test_fused_block_falls_back_for_odd_layouts(device):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape", [(2, 64, 16, 16), (3, 256, 8, 24), (2, 1024, 14, 14)])
 @pytest.mark.parametrize("ksize,tile", [(3, "1"), (7, "1"), (3, "2")])
-def test_depthwise_gelu_grn_statistics(device, monkeypatch, dtype, shape, ksize, tile):
+def test_depthwise_gelu_grn_statistics(device, dispatch, dtype, shape, ksize, tile):
     """The FFN middle with GRN statistics taken in the depthwise pass: the map equals the
     plain fused depthwise + GELU (same arithmetic) and the scale matches the separate GRN
     statistics pass on that map (FP32 sums in another order)."""
     from visionhope_amd.utils import dwconv
     from visionhope_amd.utils.grn_cuda import grn_scale
 
-    monkeypatch.setenv("VH_DW_TILE", tile)
+    dispatch(dw_tile=tile)
     b, c, h, w = shape
     conv = torch.nn.Conv2d(c, c, ksize, padding=ksize // 2, groups=c)
     with torch.no_grad():

@@ -71,19 +71,19 @@ def test_conv3x3(device, cin, cout, stride, hw, act, in_dtype):
     (2, 32, 64, 1, (1, 1), 1, torch.bfloat16),      # one pixel: every neighbour in the padding
     (1, 64, 64, 1, (97, 5), 0, torch.bfloat16),     # narrow, tall map
 ])
-def test_conv3x3_band_kernel_matches_tiled_kernel(device, monkeypatch, batch, cin, cout, stride, hw, act, in_dtype):
+def test_conv3x3_band_kernel_matches_tiled_kernel(device, dispatch, batch, cin, cout, stride, hw, act, in_dtype):
     """The band kernel (input rows staged in LDS once per band, weights in registers) runs
     the products in the tiled kernel's k order with the same operands, so both give the
-    same bits; VH_CONV_BAND=0 selects the tiled kernel."""
+    same bits; the conv_band override "0" selects the tiled kernel."""
     from visionhope_amd.utils.conv_bn import conv3x3_bias_act
 
     conv = nn.Conv2d(cin, cout, 3, stride=stride, padding=1)
     x = randn(batch, cin, *hw, seed=81).to(in_dtype).to(device).contiguous(memory_format=torch.channels_last)
     wd = randn(cout, cin, 3, 3, seed=82, scale=(9 * cin) ** -0.5).to(device).contiguous(memory_format=torch.channels_last)
     bias = randn(cout, seed=83, scale=0.5).to(device)
-    monkeypatch.setenv("VH_CONV_BAND", "1")
+    dispatch(conv_band="1")
     band = conv3x3_bias_act(x, conv, wd, bias, act)
-    monkeypatch.setenv("VH_CONV_BAND", "0")
+    dispatch(conv_band="0")
     tiled = conv3x3_bias_act(x, conv, wd, bias, act)
     assert torch.equal(band, tiled), f"band vs tiled: max diff {(band.float() - tiled.float()).abs().max().item()}"
     if hw[0] * hw[1] <= 4096:

@@ -60,7 +60,7 @@ def test_pointwise_gelu(device, k, n):
 @pytest.mark.parametrize("k,n,m", [(64, 256, 98309), (128, 512, 40007), (256, 1024, 25088), (192, 128, 70001),
                                    (256, 128, 64 * 512 * 5), (128, 256, 129)])
 @pytest.mark.parametrize("epilogue", [0, 1, 3])
-def test_pointwise_resident_weights_match_tiled_kernel(device, monkeypatch, k, n, m, epilogue):
+def test_pointwise_resident_weights_match_tiled_kernel(device, dispatch, k, n, m, epilogue):
     """The resident-weight kernel (shallow products: weights held in registers, pixel
     tiles streamed through an LDS ring, several tiles per block at these sizes, a ragged
     last tile) accumulates k in the order of the LDS-tiled kernels, so the bf16 outputs
@@ -73,9 +73,9 @@ def test_pointwise_resident_weights_match_tiled_kernel(device, monkeypatch, k, n
         lin.bias.copy_(randn(n, seed=72, scale=0.5))
     lin = lin.to(device)
     x = _bf16(randn(m, k, seed=73)).to(device)
-    monkeypatch.setenv("VH_PW_RESIDENT", "2")
+    dispatch(pw_resident="2")
     got = pointwise.pointwise_conv(x, lin, epilogue)
-    monkeypatch.setenv("VH_PW_RESIDENT", "0")
+    dispatch(pw_resident="0")
     other = pointwise.pointwise_conv(x, lin, epilogue)
     torch.cuda.synchronize()
     assert torch.equal(got, other)

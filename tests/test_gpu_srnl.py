@@ -45,11 +45,11 @@ SCAN16_PACKINGS = ["1x4", "2x4", "4x4", "1x2", "2x2"]   # <lines per wave>x<16-s
 @pytest.mark.parametrize("packing", SCAN16_PACKINGS)
 @pytest.mark.parametrize("height,width", [(7, 7), (14, 14), (6, 9), (19, 37)])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL)])
-def test_spatial_scan16_packing(oracle, device, monkeypatch, packing, height, width, dtype, tol):
+def test_spatial_scan16_packing(oracle, device, dispatch, packing, height, width, dtype, tol):
     """head_dim 16 scan with 1, 2 or 4 lines and 2 or 4 token tiles per wave (forced; the
     library picks a packing by itself from the line count): short and long chunks (more
     than one tile per chunk), rectangular images."""
-    monkeypatch.setenv("VH_SCAN_PACK", packing)
+    dispatch(scan_pack=packing)
     heads = 4
     channels = heads * 16
     mems = memories(4, heads, 16, kind="strong", seed=height * 31 + width)
@@ -64,12 +64,12 @@ def test_spatial_scan16_packing(oracle, device, monkeypatch, packing, height, wi
 
 @pytest.mark.parametrize("packing", ["2x4", "4x4", "1x2", "2x2"])
 @pytest.mark.parametrize("chunks", [(5, 16), (17, 33)])
-def test_sequence_scan16_packing(oracle, device, monkeypatch, packing, chunks):
+def test_sequence_scan16_packing(oracle, device, dispatch, packing, chunks):
     """Packed sequences with head_dim 16 and 4 heads, lines and tiles packed per wave,
     padded chunks."""
     from visionhope_amd.models.srnl_core.chunk import srnl_packed_forward
 
-    monkeypatch.setenv("VH_SCAN_PACK", packing)
+    dispatch(scan_pack=packing)
     batch, directions, heads, length = 2, 2, 4, 83
     mems = memories(directions, heads, 16, kind="perturbed", seed=int(packing[0]))
     x, q = _packed_case(batch, directions, heads, length, 16, torch.float32, seed=81)
@@ -97,6 +97,46 @@ def test_config1_standalone_srnl(oracle, device):
     expected = oracle.sequence_forward(packed, x.view(2, 1, 196, 64).numpy(), mems, [14], q_raw=True)
     expected = expected[:, 0].transpose(0, 2, 1, 3).reshape(2, 196, 64)
     assert_close(y, expected, FP32_TOL, "config 1")
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL),
+                                       (torch.float16, HALF_TOL)])
+@pytest.mark.parametrize("head_dim", [16, 32])
+def test_srnl_module_fast_inference_sequence_path(oracle, device, dtype, tol, head_dim):
+    """SRNL(fast_inference=True) in eval mode without gradients takes the sequence inference
+    entry (reference ``fused.py:211-219`` via ``srnl.py:_inference_path``): config 1's
+    standalone shape, and the packed four-direction call with spatial chunks."""
+    from visionhope_amd.models import SRNL
+
+    torch.manual_seed(1234)
+    module = SRNL(64, head_dim=head_dim, chunk_size=14, fast_inference=True).to(device).eval()
+    with torch.no_grad():
+        module.M_eta_0.normal_(0, 0.1)
+        module.M_alpha_0.normal_(0, 0.1)
+    x = randn(2, 196, 64, seed=1234).to(dtype)
+    with torch.no_grad():
+        assert module.inference_status(x.to(device))["path"] == "sequence"
+        y = module(x.to(device))
+    assert y.dtype == dtype
+    mems = tuple(p.detach().cpu().numpy() for p in module.initial_memories)
+    heads = 64 // head_dim
+    packed = x.float().view(2, 1, 196, heads, head_dim).transpose(2, 3).numpy()
+    expected = oracle.sequence_forward(packed, x.float().view(2, 1, 196, 64).numpy(), mems, [14], q_raw=True)
+    expected = expected[:, 0].transpose(0, 2, 1, 3).reshape(2, 196, 64)
+    assert_close(y.float().cpu().numpy(), expected, tol, f"fast inference standalone {dtype} d={head_dim}")
+
+    four = SRNL(32, head_dim=head_dim, directions=4, fast_inference=True).to(device).eval()
+    with torch.no_grad():
+        four.M_eta_0.normal_(0, 0.1)
+        four.M_alpha_0.normal_(0, 0.1)
+    height, width = 6, 9
+    xp = randn(2, 4, 32 // head_dim, height * width, head_dim, seed=5).to(dtype)
+    qp = randn(2, 4, height * width, 32, seed=6).to(dtype)
+    with torch.no_grad():
+        yp = four(xp.to(device), qp.to(device), spatial_shape=(height, width))
+    mems = tuple(p.detach().cpu().numpy() for p in four.initial_memories)
+    expected = oracle.sequence_forward(xp.float().numpy(), qp.float().numpy(), mems, [width, width, height, height])
+    assert_close(yp.float().cpu().numpy(), expected, tol, f"fast inference packed {dtype} d={head_dim}")
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, HALF_TOL), (torch.float16, HALF_TOL)])
@@ -150,7 +190,8 @@ def test_spatial_forward_fp32(oracle, device, height, width, head_dim, heads, sk
 
 
 @pytest.mark.parametrize("height,width,heads", [(19, 37, 2), (16, 32, 1), (33, 17, 3), (56, 56, 2)])
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL)])
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL),
+                                       (torch.float16, HALF_TOL)])
 def test_spatial_readout_tiles(oracle, device, height, width, heads, dtype, tol):
     """head_dim 16 with row/column chunks: 16x16 tile readout, full and ragged edge tiles."""
     channels = heads * 16
@@ -178,19 +219,37 @@ def test_spatial_forward_other_chunks(oracle, device):
     assert_close(got, expected, FP32_TOL, "spatial other chunks")
 
 
-def test_spatial_forward_bf16_config3_shape(oracle, device):
-    """Operator workload shape at reduced batch (B=2, 56x56, C=96, 3 heads of 32), bf16."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_spatial_forward_half_config3_shape(oracle, device, dtype):
+    """Operator workload shape at reduced batch (B=2, 56x56, C=96, 3 heads of 32), bf16 and
+    fp16 activations (the reference builds every kernel for both, cuda_source.py:50-68)."""
     heads, head_dim, hw = 3, 32, 56
     channels = heads * head_dim
     mems = memories(4, heads, head_dim, kind="perturbed", seed=9)
-    x = randn(2, hw, hw, channels, seed=41).bfloat16()
-    q = randn(2, hw, hw, channels, seed=42).bfloat16()
+    x = randn(2, hw, hw, channels, seed=41).to(dtype)
+    q = randn(2, hw, hw, channels, seed=42).to(dtype)
     skip = randn(channels, seed=43, scale=0.1)
     wts = 1 + randn(4, channels, seed=44, scale=0.1)
     got = _spatial(device, x, q, mems, skip, wts, (hw, hw, hw, hw))
     expected = oracle.operator_forward(x.float().numpy(), q.float().numpy(), mems, skip.numpy(),
                                        wts.numpy(), head_dim)
-    assert_close(got, expected, HALF_TOL, "config3 bf16")
+    assert_close(got, expected, HALF_TOL, f"config3 {dtype}")
+
+
+@pytest.mark.parametrize("height,width,head_dim,heads", [(7, 7, 16, 2), (6, 9, 16, 3), (12, 5, 32, 1),
+                                                         (14, 14, 32, 2), (4, 4, 8, 2), (5, 3, 64, 1)])
+def test_spatial_forward_fp16(oracle, device, height, width, head_dim, heads):
+    """fp16 activations through the spatial operator at every head_dim path (the per-element
+    readout at head_dim 32, the matrix-core tile readout at 16)."""
+    channels = heads * head_dim
+    mems = memories(4, heads, head_dim, kind="strong", seed=height * width + 1)
+    x = randn(2, height, width, channels, seed=35).half()
+    q = randn(2, height, width, channels, seed=36).half()
+    skip = randn(channels, seed=37, scale=0.1)
+    wts = 1 + randn(4, channels, seed=38, scale=0.1)
+    got = _spatial(device, x, q, mems, skip, wts, (width, width, height, height))
+    expected = oracle.operator_forward(x.float().numpy(), q.float().numpy(), mems, skip.numpy(), wts.numpy(), head_dim)
+    assert_close(got, expected, HALF_TOL, f"spatial fp16 {height}x{width} d={head_dim}")
 
 
 def test_line_forward_seq_noatomic_reference_layout(oracle, device):
@@ -288,19 +347,18 @@ WIDE_CASES = [(16, 1, "rows"), (16, 2, "rows"), (16, 2, "blocks"), (16, 4, "rows
               (32, 2, "rows"), (32, 4, "rows"), (32, 4, "blocks")]
 
 
-def _wide_env(monkeypatch, waves, mode):
-    monkeypatch.setenv("VH_SCAN_WIDE", str(waves))
-    monkeypatch.setenv("VH_SCAN_TB", "1" if mode == "rows" else "2")
+def _wide_env(dispatch, waves, mode):
+    dispatch(scan_wide=waves, scan_tb="1" if mode == "rows" else "2")
 
 
 @pytest.mark.parametrize("head_dim,waves,mode", WIDE_CASES)
 @pytest.mark.parametrize("height,width", [(7, 7), (14, 14), (19, 37), (56, 56)])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL)])
-def test_spatial_scan_wide(oracle, device, monkeypatch, head_dim, waves, mode, height, width, dtype, tol):
+def test_spatial_scan_wide(oracle, device, dispatch, head_dim, waves, mode, height, width, dtype, tol):
     """The scan with one line per workgroup of 1, 2 or 4 waves (rows of the gain split over
     the waves): square and rectangular maps, chunks of 7 to 56 (one to four 16-token tiles,
     ragged last tiles), strong memories (active soft cap and spectral clamp)."""
-    _wide_env(monkeypatch, waves, mode)
+    _wide_env(dispatch, waves, mode)
     heads = 2
     channels = heads * head_dim
     mems = memories(4, heads, head_dim, kind="strong", seed=height * 7 + width + head_dim)
@@ -317,12 +375,12 @@ def test_spatial_scan_wide(oracle, device, monkeypatch, head_dim, waves, mode, h
 @pytest.mark.parametrize("head_dim,waves,mode", WIDE_CASES)
 @pytest.mark.parametrize("chunks", [(5, 16, 64, 3), (65, 128, 100, 200)])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, HALF_TOL)])
-def test_sequence_scan_wide(oracle, device, monkeypatch, head_dim, waves, mode, chunks, dtype, tol):
+def test_sequence_scan_wide(oracle, device, dispatch, head_dim, waves, mode, chunks, dtype, tol):
     """Packed sequences through the wide scan: chunks shorter than a tile, spanning several
     64-token segments, and ragged last chunks (length 263 = 2*128 + 7)."""
     from visionhope_amd.models.srnl_core.chunk import srnl_packed_forward
 
-    _wide_env(monkeypatch, waves, mode)
+    _wide_env(dispatch, waves, mode)
     batch, directions, heads, length = 1, 4, 2, 263
     mems = memories(directions, heads, head_dim, kind="perturbed", seed=head_dim + waves)
     x, q = _packed_case(batch, directions, heads, length, head_dim, dtype, seed=95)

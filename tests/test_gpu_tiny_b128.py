@@ -1,0 +1,121 @@
+"""The spatial SRNL kernels at the Tiny B = 128 stage shapes, where the library's own
+dispatch (no override) picks the block-form scan with its per-stage packings (1 x 4 tiles
+at 1024 lines, 1 x 2 at 2048, 2 x 2 at 4096 and 8192) and the matrix-core readout on
+split chunk states, checked against the C oracle on the same bf16 inputs:
+
+* the fused entry (``vh_srnl_spatial_forward``, FP32 output) at a bound the block form's
+  arithmetic supports: 2e-5, about one hi + lo rounding (2^-16 = 1.5e-5 relative) of the
+  output, a thousand times inside the 2e-2 budget of bf16 activations (observed on
+  MI355X: 5e-8 with the default-scale memories, up to 1.6e-6 with strong ones), so a
+  defect that costs even 1e-4 fails;
+* the scan / readout pair with bf16 output plus an addend, as the fused block path calls
+  it (``vh_srnl_spatial_scan`` + ``vh_srnl_spatial_readout``): the bf16 rounding of the
+  output, 2^-8 relative, bounds it;
+* the same shapes with a forced kernel choice (the wide scan at 1024 lines, the stepped
+  form at 4096): every scan kernel writes the state format the readout decodes.
+
+The observed errors are printed (``pytest -s``).
+"""
+
+import pytest
+import torch
+
+from tests.helpers import max_rel_err, memories, randn, rel_err
+
+pytestmark = pytest.mark.gpu
+
+BATCH = 128
+STAGES = [(56, 2), (28, 4), (14, 8), (7, 16)]      # (H = W, heads of 16): 1024 .. 8192 lines
+UT_TOL = 2e-5          # FP32 output of the block-form scan + split-state readout
+BF16_OUT_TOL = 5e-3    # bf16 output: one rounding (2^-8 relative) on top of UT_TOL
+_ORACLE = {}
+
+
+def _case(hw, heads, kind):
+    channels = heads * 16
+    seed = hw * 100 + heads
+    mems = memories(4, heads, 16, kind=kind, seed=seed)
+    x = randn(BATCH, hw, hw, channels, seed=seed + 1).bfloat16()
+    q = randn(BATCH, hw, hw, channels, seed=seed + 2).bfloat16()
+    skip = randn(channels, seed=seed + 3, scale=0.1)
+    wts = 1 + randn(4, channels, seed=seed + 4, scale=0.1)
+    return mems, x, q, skip, wts
+
+
+def _expected(oracle, hw, heads, kind):
+    key = (hw, heads, kind)
+    if key not in _ORACLE:
+        mems, x, q, skip, wts = _case(hw, heads, kind)
+        print(f"\n[oracle] B={BATCH} {hw}x{hw} heads={heads} {kind}", flush=True)
+        _ORACLE[key] = oracle.operator_forward(x.float().numpy(), q.float().numpy(), mems, skip.numpy(),
+                                               wts.numpy(), 16)
+    return _ORACLE[key]
+
+
+def _fused(device, mems, x, q, skip, wts, hw):
+    from visionhope_amd.models.srnl_core.fused import srnl_spatial_inference
+
+    return srnl_spatial_inference(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device), q.to(device),
+                                  skip.to(device), wts.to(device), (hw,) * 4).cpu().numpy()
+
+
+@pytest.mark.parametrize("hw,heads", STAGES)
+@pytest.mark.parametrize("kind", ["perturbed", "strong"])
+def test_tiny_b128_spatial_forward(oracle, device, hw, heads, kind):
+    mems, x, q, skip, wts = _case(hw, heads, kind)
+    lines = BATCH * 4 * heads
+    print(f"\n[case] fused B={BATCH} {hw}x{hw} lines={lines} {kind}", flush=True)
+    got = _fused(device, mems, x, q, skip, wts, hw)
+    expected = _expected(oracle, hw, heads, kind)
+    r, m = rel_err(got, expected), max_rel_err(got, expected)
+    print(f"[err] fused {hw}x{hw} {kind}: normwise {r:.2e} elementwise {m:.2e}", flush=True)
+    assert r <= UT_TOL and m <= UT_TOL, f"{hw}x{hw} {kind}: normwise {r:.3e}, elementwise {m:.3e}"
+
+
+@pytest.mark.parametrize("hw,heads", STAGES)
+@pytest.mark.parametrize("kind", ["perturbed", "strong"])
+def test_tiny_b128_scan_readout_bf16_aux(oracle, device, hw, heads, kind):
+    """The block path's call: bf16 output of the four fused directions plus a bf16 addend
+    (the position encoding), rounded once."""
+    from visionhope_amd.models.srnl_core.fused import srnl_spatial_readout, srnl_spatial_scan
+
+    mems, x, q, skip, wts = _case(hw, heads, kind)
+    aux = randn(*x.shape, seed=hw + 5, scale=0.5).bfloat16()
+    print(f"\n[case] scan+readout bf16+aux B={BATCH} {hw}x{hw} {kind}", flush=True)
+    xd = x.to(device)
+    ws = srnl_spatial_scan(tuple(torch.from_numpy(m).to(device) for m in mems), xd, (hw,) * 4)
+    got = srnl_spatial_readout(ws, xd, q.to(device), skip.to(device), wts.to(device), (hw,) * 4, 16,
+                               aux=aux.to(device), out_dtype=torch.bfloat16)
+    assert got.dtype == torch.bfloat16
+    got = got.float().cpu().numpy()
+    expected = _expected(oracle, hw, heads, kind) + aux.float().numpy()
+    r, m = rel_err(got, expected), max_rel_err(got, expected)
+    print(f"[err] scan+readout {hw}x{hw} {kind}: normwise {r:.2e} elementwise {m:.2e}", flush=True)
+    assert r <= BF16_OUT_TOL and m <= BF16_OUT_TOL, f"{hw}x{hw} {kind}: normwise {r:.3e}, elementwise {m:.3e}"
+
+
+@pytest.mark.parametrize("hw,heads,forced", [
+    (56, 2, {"scan_wide": 2}),                     # wide scan, row split, 1024 lines
+    (56, 2, {"scan_wide": 4, "scan_tb": 2}),       # wide scan, token blocks
+    (14, 8, {"scan_ut": 0}),                       # stepped form, 2 x 2 packing, 4096 lines
+    (14, 8, {"scan_pack": "4x4"}),                 # block form, 4 x 4 packing
+])
+def test_tiny_b128_forced_kernels_share_the_state_format(oracle, device, dispatch, hw, heads, forced):
+    """Whichever scan kernel runs, the readout decodes the states it wrote: the fused entry
+    and the scan / readout pair under each override, at the default dispatch's tolerance."""
+    from visionhope_amd.models.srnl_core.fused import srnl_spatial_readout, srnl_spatial_scan
+
+    dispatch(**forced)
+    mems, x, q, skip, wts = _case(hw, heads, "perturbed")
+    print(f"\n[case] forced {forced} B={BATCH} {hw}x{hw}", flush=True)
+    expected = _expected(oracle, hw, heads, "perturbed")
+    got = _fused(device, mems, x, q, skip, wts, hw)
+    r, m = rel_err(got, expected), max_rel_err(got, expected)
+    print(f"[err] forced {forced} fused: normwise {r:.2e} elementwise {m:.2e}", flush=True)
+    assert r <= UT_TOL and m <= UT_TOL, f"{forced}: normwise {r:.3e}, elementwise {m:.3e}"
+    xd = x.to(device)
+    ws = srnl_spatial_scan(tuple(torch.from_numpy(m_).to(device) for m_ in mems), xd, (hw,) * 4)
+    pair = srnl_spatial_readout(ws, xd, q.to(device), skip.to(device), wts.to(device), (hw,) * 4, 16)
+    r = rel_err(pair.cpu().numpy(), expected)
+    assert r <= UT_TOL, f"{forced} scan/readout pair: normwise {r:.3e}"
+

@@ -430,13 +430,13 @@ int launch_conv(const ConvParams& cp, hipStream_t s) {
 
 // Band kernel launch, or -1 when it does not cover the shape (Cin other than 3, 32, 64;
 // N not a multiple of 32; more than 64 KB of LDS or 10 staging units per thread) or
-// VH_CONV_BAND=0 asks for conv3x3_kernel.  The band height aims at 7 pixel tiles per
+// the conv_band override "0" asks for conv3x3_kernel.  The band height aims at 7 pixel tiles per
 // wave (one pass of the product loop); the grid is the number of blocks that fit on
 // the GPU at once (a multiple of the channel slices).
 template <int EPI, int MODE>
 int launch_band(const ConvParams& cp, hipStream_t s) {
-    if (const char* env = std::getenv("VH_CONV_BAND"))
-        if (env[0] == '0') return -1;
+    const Override band("conv_band");
+    if (band.set() && band.value[0] == '0') return -1;
     const int cin = MODE == CONV_TAPS ? cp.Cin : 4;
     if (!(cin == 4 || cin == 32 || cin == 64) || cp.g.N % 32 != 0) return -1;
     if (static_cast<int64_t>(cp.H) * cp.W * (cin == 4 ? 12 : 2 * cin) >= (int64_t(1) << 31)) return -1;

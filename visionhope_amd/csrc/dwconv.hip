@@ -503,9 +503,11 @@ template <int K, typename T, int P>
 void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
     // The input of one launch is addressed as one buffer below 2^31 bytes: large batches
     // go in several launches of whole images.
-    // VH_DW_LAUNCH_BYTES lowers the per-launch limit (tests use it to exercise the split).
+    // The dw_launch_bytes override lowers the per-launch limit (tests use it to exercise
+    // the split).
     int64_t limit = (int64_t(1) << 31) - 1;
-    if (const char* env = std::getenv("VH_DW_LAUNCH_BYTES")) limit = std::min(limit, std::max<int64_t>(1, std::atoll(env)));
+    const Override forced_limit("dw_launch_bytes");
+    if (forced_limit.set()) limit = std::min<int64_t>(limit, std::max<int64_t>(1, forced_limit.as_i64()));
     const int64_t image_elems = dp.H * dp.W * dp.C;
     const int64_t per_launch = std::max<int64_t>(1, limit / (image_elems * int64_t(sizeof(T))));
     const int64_t segs = (dp.W + P - 1) / P;
@@ -558,15 +560,15 @@ inline int64_t dw_blocks_per_image(int K, int64_t H, int64_t W, int64_t C) {
 // halo re-read (K - 1 extra rows per band: wide bands want narrow slabs) against the
 // bytes of one pixel a load covers contiguously (64 bf16 channels fill a 128-byte
 // line): the lowest (RB + K - 1) / RB x sqrt(128 / min(128, slab bytes)) wins, the
-// wider slab on ties.  VH_DW_TILE=0 turns the variant off and VH_DW_TILE=2 uses it
-// wherever it applies (tests compare the kernels); VH_DW_TILE_CS=<channels> forces a
-// slab width (measurements).
+// wider slab on ties.  The dw_tile override "0" turns the variant off and "2" uses it
+// wherever it applies (tests compare the kernels); dw_tile_cs=<channels> forces a slab
+// width and dw_tile_p=<pixels> the pixels per thread (measurements).
 inline bool dw_tile_plan(int K, int64_t B, int64_t H, int64_t W, int64_t C, int es, DwTile& t) {
-    const char* mode = std::getenv("VH_DW_TILE");
-    if (mode && mode[0] == '0') return false;
-    const bool everywhere = mode && mode[0] == '2';
-    int force = 0;
-    if (const char* env = std::getenv("VH_DW_TILE_CS")) force = std::atoi(env);
+    const Override mode("dw_tile");
+    if (mode.set() && mode.value[0] == '0') return false;
+    const bool everywhere = mode.set() && mode.value[0] == '2';
+    const Override forced_cs("dw_tile_cs");
+    const int force = forced_cs.set() ? forced_cs.as_int() : 0;
     if (es != 2 || B <= 0 || H <= 0 || W <= 0 || C % 8 != 0) return false;
     // Measured on MI355X at the Tiny shapes (B = 128, bf16): faster than the per-thread
     // window kernel for 7x7 at every map size (56x56: 37 vs 64 us, 28x28: 20 vs 37 us)
@@ -575,8 +577,9 @@ inline bool dw_tile_plan(int K, int64_t B, int64_t H, int64_t W, int64_t C, int 
     if (!everywhere && (K == 3 || (K == 5 && W < 28))) return false;
     int P = (W % 7 == 0) ? 7 : 8;
     if (K == 7 && W <= 14) P = 2;   // small maps: 3.5x the threads for (P + 6) / P input reads
-    if (const char* env = std::getenv("VH_DW_TILE_P")) {
-        const int v = std::atoi(env);
+    const Override forced_p("dw_tile_p");
+    if (forced_p.set()) {
+        const int v = forced_p.as_int();
         if (v == 2 || (v == 7 && W % 7 == 0) || v == 8) P = v;
     }
     if (P == 2 && K != 7) P = (W % 7 == 0) ? 7 : 8;

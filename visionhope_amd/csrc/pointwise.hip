@@ -523,8 +523,8 @@ __global__ __launch_bounds__(256) void pointwise_narrow_kernel(const PwParams p)
 namespace {
 
 // Narrow outputs (N = 32, 64) with K <= 64 take the LDS-free kernel with 64 pixels per
-// wave; the rest the LDS-tiled one with the tile chosen below.  VH_PW_CFG selects a
-// variant for measurements: "n<TM>" (narrow, 16 TM pixels per wave, K <= 256),
+// wave; the rest the LDS-tiled one with the tile chosen below.  The pw_cfg override
+// selects a variant for measurements: "n<TM>" (narrow, 16 TM pixels per wave, K <= 256),
 // "w<BK>" (the earlier fixed tiles, k step 32 or 64) or "t<BM>x<BN>k<BK>o<OCC>".
 template <int EPI, bool PRO_ON>
 int launch_pw(const PwParams& p, hipStream_t s) {
@@ -532,7 +532,9 @@ int launch_pw(const PwParams& p, hipStream_t s) {
     int narrow_tm = 4, bk = 0;
     bool narrow = (p.N == 32 || p.N == 64) && (p.K == 32 || p.K == 64);
     const bool narrow_ok = (p.N == 32 || p.N == 64) && (p.K == 32 || p.K == 64 || p.K == 128 || p.K == 256);
-    if (const char* env = std::getenv("VH_PW_CFG")) {
+    const Override cfg("pw_cfg");
+    const char* const env = cfg.set() ? cfg.value : nullptr;
+    if (env) {
         if (env[0] == 'n' && narrow_ok) { narrow = true; narrow_tm = std::atoi(env + 1); }
         if (env[0] == 'w') { narrow = false; bk = std::atoi(env + 1); }
     }
@@ -559,7 +561,7 @@ int launch_pw(const PwParams& p, hipStream_t s) {
             default: return pick(std::integral_constant<int, 8>{});
         }
     }
-    if (const char* env = std::getenv("VH_PW_CFG")) {
+    if (env) {
         // d<BM>x<BN>o<OCC>: LDS-copy ring kernel (K % 64 == 0, N % BN == 0)
         int dm = 0, dn = 0, docc = 0;
         if (std::sscanf(env, "d%dx%do%d", &dm, &dn, &docc) == 3 && p.N % dn == 0 && p.K % 64 == 0) {
@@ -591,10 +593,11 @@ int launch_pw(const PwParams& p, hipStream_t s) {
     // 56x56 98 -> 86 us, 28x28 56 -> 49 us, 14x14 42 -> 35 us, proj_out 28x28 11.5 ->
     // 9.6 us, but slower where the pixel tiles x channel slices are fewer than 1024
     // (14x14 and 7x7 projections: the weights are loaded for one or two tiles).
-    // VH_PW_RESIDENT=0 turns it off, =2 takes it wherever the shape allows (tests).
+    // The pw_resident override "0" turns it off, "2" takes it wherever the shape allows
+    // (tests).
     if constexpr (!PRO_ON && EPI != PW_ADD) {
-        const char* res_env = std::getenv("VH_PW_RESIDENT");
-        const bool res_off = res_env && res_env[0] == '0', res_all = res_env && res_env[0] == '2';
+        const Override res("pw_resident");
+        const bool res_off = res.set() && res.value[0] == '0', res_all = res.set() && res.value[0] == '2';
         if (!res_off && bk == 0 && p.K % 64 == 0 && p.K <= 256 && p.N % 128 == 0) {
             const bool wide = p.N % 256 == 0 && p.K <= 128;
             const int64_t slices = p.N / (wide ? 256 : 128), mtiles = (p.M + 63) / 64;

@@ -155,8 +155,7 @@ __global__ __launch_bounds__(4 * D) void srnl_scan_kernel(const ScanParams p) {
     for (int64_t c = 0; c < nc; ++c) {
         __syncthreads();
         for (int idx = tid * 4; idx < D * D; idx += NT * 4)
-            *reinterpret_cast<float4*>(out_states + c * D * D + idx) =
-                *reinterpret_cast<const float4*>(S + idx);
+            store_state4(out_states + c * D * D + idx, *reinterpret_cast<const float4*>(S + idx), p.split_states);
         // The last chunk's gain only feeds a refresh that no output reads.
         if (c == nc - 1) break;
 
@@ -495,8 +494,8 @@ __global__ __launch_bounds__(64) void srnl_scan16_kernel(const ScanParams p) {
         __syncthreads();
 #pragma unroll
         for (int lam = 0; lam < NL; ++lam)
-            *reinterpret_cast<float4*>(p.states + ((line0 + lam) * p.max_chunks + c) * D * D + lane * 4) =
-                *reinterpret_cast<const float4*>(St + lam * SR + lane * 4);
+            store_state4(p.states + ((line0 + lam) * p.max_chunks + c) * D * D + lane * 4,
+                         *reinterpret_cast<const float4*>(St + lam * SR + lane * 4), p.split_states);
         if (c == nc - 1) break;
 
         float g[E];
@@ -1157,32 +1156,35 @@ constexpr int dtype_code_of() {
 }
 
 // Waves per line of the wide scan for this call: 0 = use the single-wave kernels.  Every
-// head_dim-32 scan and head_dim-16 scans with fewer lines than SIMDs use it.
-// VH_SCAN_WIDE = 0 | 1 | 2 | 4 forces the choice (1 only for head_dim 16); VH_SCAN_PACK
-// (a forced head_dim-16 packing) selects the single-wave kernels.
+// head_dim-32 scan and head_dim-16 scans with fewer lines than SIMDs use it.  The
+// scan_wide override (0 | 1 | 2 | 4) forces the choice (1 only for head_dim 16); a
+// scan_pack override (a forced head_dim-16 packing) selects the single-wave kernels.
 int wide_waves(int64_t lines, int d) {
-    if (const char* env = std::getenv("VH_SCAN_WIDE")) {
-        const int w = std::atoi(env);
+    const Override forced("scan_wide");
+    if (forced.set()) {
+        const int w = forced.as_int();
         if (w == 0) return 0;
         if (w == 2 || w == 4 || (w == 1 && d == 16)) return w;
     }
-    if (std::getenv("VH_SCAN_PACK")) return 0;   // a forced single-wave packing
+    if (Override("scan_pack").set()) return 0;   // a forced single-wave packing
     if (d == 32 || (d == 16 && lines < 1024)) return scan_wide_waves(lines, d);
     return 0;
 }
 
 void scan16_ut_packing(int64_t lines, int64_t heads, int* nl, int* tcw);
 
-// The block-form scan (bf16 activations, head_dim 16, at least 1024 lines; fewer take the
-// wide kernel) on channels-last maps stores its chunk-start states split into bf16 hi + lo
-// pairs for the readouts (split_state_at, readout_mfma).  The scan and the readout entry
-// points both decide the format here, from the same arguments.
+// Format of the chunk-start states in the workspace.  Spatial scans of bf16 maps with
+// head_dim 16 store them split into bf16 hi + lo pairs (split_state_at), the operands of
+// the matrix-core readout; every other scan stores FP32.  The format is a function of
+// these arguments alone: every scan kernel that can run for such a call (block form,
+// stepped, wide, under any dispatch override) stores it, so the readout, which decides
+// it from the same arguments, always decodes what the scan wrote.
 bool scan_ut_enabled() {
-    const char* ut = std::getenv("VH_SCAN_UT");
-    return !(ut && ut[0] == '0');
+    const Override ut("scan_ut");
+    return !(ut.set() && ut.value[0] == '0');
 }
-bool state_split_bf16(int io_dtype, int d, int64_t lines, bool spatial) {
-    return io_dtype == VH_DTYPE_BF16 && d == 16 && lines >= 1024 && spatial && scan_ut_enabled();
+bool state_split_bf16(int io_dtype, int d, bool spatial) {
+    return io_dtype == VH_DTYPE_BF16 && d == 16 && spatial;
 }
 
 template <int D, typename T>
@@ -1192,16 +1194,17 @@ void launch_scan(const ScanParams& sp, hipStream_t stream) {
         const int waves = wide_waves(lines, D);
         // Token blocks (head_dim 16, chunks of 64 tokens or more, several waves): measured
         // faster than the row split there, slower for shorter chunks and for head_dim 32.
-        // VH_SCAN_TB = 1 | 2 forces the row split or the blocks.
+        // The scan_tb override (1 | 2) forces the row split or the blocks.
         int max_chunk = 0;
         for (int r = 0; r < sp.R; ++r) max_chunk = std::max(max_chunk, sp.chunk[r]);
         int token_blocks = (D == 16 && max_chunk >= 64) ? 2 : 1;
-        if (const char* tbenv = std::getenv("VH_SCAN_TB")) token_blocks = std::atoi(tbenv) == 1 ? 1 : 2;
+        const Override tb("scan_tb");
+        if (tb.set()) token_blocks = tb.as_int() == 1 ? 1 : 2;
         if (waves > 0 && launch_scan_wide(sp, dtype_code_of<T>(), D, waves, token_blocks, stream)) return;
     }
     if constexpr (D == 16 && std::is_same<T, bf16_t>::value) {
-        // bf16 activations: the block form (srnl_ut.hip).  VH_SCAN_UT = 0 selects the
-        // stepped form below instead.
+        // bf16 activations: the block form (srnl_ut.hip).  The scan_ut override "0"
+        // selects the stepped form below instead.
         if (scan_ut_enabled()) {
             ScanParams up = sp;
             scan16_ut_packing(lines, sp.heads, &up.lines_per_wave, &up.tiles_per_wave);
@@ -1272,11 +1275,13 @@ int64_t max_chunk_count(int64_t length, const int64_t* chunks, int64_t R) {
 // one: measured on MI355X at the Tiny stages (B = 128), 2 lines x 2 tiles for 4096 and
 // 8192 lines (chunks 14 and 7) is 12-15 % faster than 4 x 4, and 1 line x 4 tiles for
 // 2048 lines (chunk 28) 13 % faster than 2 x 4.  The lines of a wave share (b, r), so NL
-// divides heads.  VH_SCAN_PACK = "<NL>x<TCW>" forces a packing (when heads allows it).
+// divides heads.  The scan_pack override "<NL>x<TCW>" forces a packing (when heads
+// allows it).
 void scan16_packing(int64_t lines, int64_t heads, int* nl, int* tcw) {
-    if (const char* env = std::getenv("VH_SCAN_PACK")) {
+    const Override forced("scan_pack");
+    if (forced.set()) {
         int fl = 0, ft = 0;
-        if (std::sscanf(env, "%dx%d", &fl, &ft) == 2 && (fl == 1 || fl == 2 || fl == 4) && (ft == 2 || ft == 4) &&
+        if (std::sscanf(forced.value, "%dx%d", &fl, &ft) == 2 && (fl == 1 || fl == 2 || fl == 4) && (ft == 2 || ft == 4) &&
             fl <= ft && heads % fl == 0) {
             *nl = fl;
             *tcw = ft;
@@ -1296,9 +1301,9 @@ void scan16_packing(int64_t lines, int64_t heads, int* nl, int* tcw) {
 // Measured on MI355X at the Tiny stages (B = 128, scan launches alone): 1 x 4 for 1024
 // lines (chunk 56: 270 us; 1 x 2 301 us), 1 x 2 for 2048 (chunk 28: 104 us; 1 x 4 217 us),
 // 2 x 2 for 4096 and 8192 (chunks 14 and 7: 56.5 and 53 us; 4 x 4 71 and 68 us).
-// VH_SCAN_PACK overrides it as for the stepped form.
+// The scan_pack override applies as for the stepped form.
 void scan16_ut_packing(int64_t lines, int64_t heads, int* nl, int* tcw) {
-    if (std::getenv("VH_SCAN_PACK")) {
+    if (Override("scan_pack").set()) {
         scan16_packing(lines, heads, nl, tcw);
         return;
     }
@@ -1363,7 +1368,7 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
     scan16_packing(lines, heads, &sp.lines_per_wave, &sp.tiles_per_wave);
     sp.aligned = x.spatial && R == 4 && chunks[0] == x.W && chunks[1] == x.W && chunks[2] == x.H &&
                  chunks[3] == x.H && x.H * x.W * x.st < (int64_t(1) << 31);
-    sp.split_states = state_split_bf16(io_dtype, d, lines, x.spatial != 0) ? 1 : 0;
+    sp.split_states = state_split_bf16(io_dtype, d, x.spatial != 0) ? 1 : 0;
     rc = dispatch_d(d, [&](auto dc) {
         constexpr int D = decltype(dc)::value;
         dispatch_t(io_dtype, [&](auto tv) { launch_scan<D, decltype(tv)>(sp, stream); });
@@ -1392,6 +1397,8 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
                             reinterpret_cast<uintptr_t>(aux) | reinterpret_cast<uintptr_t>(skip) |
                             reinterpret_cast<uintptr_t>(wgt);
     const bool out_f32 = out_dtype == VH_DTYPE_F32;
+    VH_REQUIRE(fp.split_states == ((io_dtype == VH_DTYPE_BF16 && d == 16 && !per_direction) ? 1 : 0), VH_ERR_ARG,
+               "SRNL readout: state format does not match the scan's");
     if ((d == 16 || (d == 32 && io_dtype != VH_DTYPE_F16)) && !per_direction && sp.chunk[0] == W &&
         sp.chunk[1] == W && sp.chunk[2] == H && sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0 &&
         H * W * C < (int64_t(1) << 31) && sp.max_chunks * d * d < (int64_t(1) << 31)) {
@@ -1401,22 +1408,13 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
         auto go = [&](auto tv, auto dc) {
             using T = decltype(tv);
             constexpr int DD = decltype(dc)::value;
-            if constexpr (std::is_same<T, bf16_t>::value && DD == 16) {
-                if (fp.split_states) {
-                    if (out_f32)
-                        hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD, true>),
-                                           dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0, stream, fp, tiles_h, tiles_w);
-                    else
-                        hipLaunchKernelGGL((srnl_readout_tile_kernel<T, T, DD, true>),
-                                           dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0, stream, fp, tiles_h, tiles_w);
-                    return;
-                }
-            }
+            // bf16 maps with head_dim 16 always carry split states (state_split_bf16)
+            constexpr bool SPLIT = std::is_same<T, bf16_t>::value && DD == 16;
             if (out_f32)
-                hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD>), dim3(static_cast<unsigned>(n_tiles)),
+                hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD, SPLIT>), dim3(static_cast<unsigned>(n_tiles)),
                                    dim3(256), 0, stream, fp, tiles_h, tiles_w);
             else
-                hipLaunchKernelGGL((srnl_readout_tile_kernel<T, T, DD>), dim3(static_cast<unsigned>(n_tiles)),
+                hipLaunchKernelGGL((srnl_readout_tile_kernel<T, T, DD, SPLIT>), dim3(static_cast<unsigned>(n_tiles)),
                                    dim3(256), 0, stream, fp, tiles_h, tiles_w);
         };
         int rc;
@@ -1561,7 +1559,7 @@ int vh_srnl_spatial_readout(const void* x, const void* q, int32_t io_dtype, cons
     VH_REQUIRE(workspace_bytes >= need, VH_ERR_WORKSPACE, "SRNL workspace needs %zu bytes, got %zu", need,
                workspace_bytes);
     sp.states = const_cast<float*>(static_cast<const float*>(workspace));
-    sp.split_states = state_split_bf16(io_dtype, head_dim, B * 4 * sp.heads, true) ? 1 : 0;
+    sp.split_states = state_split_bf16(io_dtype, head_dim, true) ? 1 : 0;
     return run_fuse(sp, x, q, 0, io_dtype, d_skip, skip_per_direction, dir_weight, out, H, W, C, head_dim,
                     static_cast<hipStream_t>(stream), aux, out_dtype);
 }

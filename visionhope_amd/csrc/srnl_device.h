@@ -314,6 +314,25 @@ __device__ __forceinline__ float split_state_at(const float* row, int col) {
     return __uint_as_float(static_cast<uint32_t>(u[j]) << 16) + __uint_as_float(static_cast<uint32_t>(u[4 + j]) << 16);
 }
 
+// Stores four consecutive entries M[i][4g..4g+3] of a chunk-start state at dst: FP32, or
+// when split, the same 16 bytes as bf16 hi[4] then bf16 lo[4] (round to nearest even,
+// |v - hi - lo| <= 2^-16 |v|), the format split_state_at reads.
+__device__ __forceinline__ void store_state4(float* dst, float4 v, bool split) {
+    if (!split) {
+        *reinterpret_cast<float4*>(dst) = v;
+        return;
+    }
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const uint32_t h01 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{v.x, v.y}, bf2));
+    const uint32_t h23 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{v.z, v.w}, bf2));
+    const f2 r01 = {v.x - __uint_as_float(h01 << 16), v.y - __uint_as_float(h01 & 0xffff0000u)};
+    const f2 r23 = {v.z - __uint_as_float(h23 << 16), v.w - __uint_as_float(h23 & 0xffff0000u)};
+    const uint32_t l01 = __builtin_bit_cast(uint32_t, __builtin_convertvector(r01, bf2));
+    const uint32_t l23 = __builtin_bit_cast(uint32_t, __builtin_convertvector(r23, bf2));
+    *reinterpret_cast<uint4*>(dst) = make_uint4(h01, h23, l01, l23);
+}
+
 // Scan with one line per workgroup of `waves` waves (srnl_wide.hip): head_dim 16 or 32,
 // fp32 or bf16 activations, vector-aligned rows.  Returns false (nothing launched) for
 // any other case.  scan_wide_waves picks the waves per line for a line count;

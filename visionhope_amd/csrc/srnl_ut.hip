@@ -186,16 +186,9 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
     for (int64_t c = 0; c < nc; ++c) {
 #pragma unroll
         for (int lam = 0; lam < NL; ++lam) {
-            float* const dst = p.states + ((line0 + lam) * p.max_chunks + c) * D * D + i16 * D + 4 * q;
-            if (p.split_states) {
-                // bf16 hi[4] then lo[4]: the readout's matrix-core operands, no split there
-                v4s h, l;
-                split4(sA[lam][0], h, l);
-                const uint2 hb = __builtin_bit_cast(uint2, h), lb = __builtin_bit_cast(uint2, l);
-                *reinterpret_cast<uint4*>(dst) = make_uint4(hb.x, hb.y, lb.x, lb.y);
-            } else {
-                *reinterpret_cast<float4*>(dst) = make_float4(sA[lam][0][0], sA[lam][0][1], sA[lam][0][2], sA[lam][0][3]);
-            }
+            // FP32, or bf16 hi[4] then lo[4]: the readout's matrix-core operands, no split there
+            store_state4(p.states + ((line0 + lam) * p.max_chunks + c) * D * D + i16 * D + 4 * q,
+                         make_float4(sA[lam][0][0], sA[lam][0][1], sA[lam][0][2], sA[lam][0][3]), p.split_states);
         }
         if (c == nc - 1) break;
 

@@ -359,7 +359,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scanw_kernel(const ScanParams p) 
         {   // chunk-start content memory -> workspace (read by the readout)
             float* dst = p.states + (line * p.max_chunks + c) * D * D;
             for (int idx = tid * 4; idx < D * D; idx += 64 * W * 4)
-                *reinterpret_cast<float4*>(dst + idx) = *reinterpret_cast<const float4*>(Sc + idx);
+                store_state4(dst + idx, *reinterpret_cast<const float4*>(Sc + idx), p.split_states);
         }
         // The last chunk's gain only feeds a refresh that no output reads.
         if (c == nc - 1) break;

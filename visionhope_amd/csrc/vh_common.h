@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdint>
 #include <cstdio>
 #include <type_traits>
@@ -20,6 +21,17 @@ namespace vh {
 // ---------------------------------------------------------------------------
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+
+// Dispatch overrides (vh_set_dispatch_override): the value forced for `name`, or an empty
+// string when none is set.  The kernel choice of every entry point is otherwise a function
+// of its arguments alone.
+struct Override {
+    char value[32];
+    explicit Override(const char* name);
+    bool set() const { return value[0] != 0; }
+    int as_int() const;
+    long long as_i64() const;
+};
 
 // Range checks of the recurrence's stability constants, shared by the forward and the
 // backward entry points (the reference validates the same ranges when it reads them from

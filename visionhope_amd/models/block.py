@@ -2,7 +2,6 @@
 ``models/block.py``), its reference-order forward, and the fused inference forward that
 prepared models run on the GPU."""
 
-import os
 import torch
 from torch import nn
 from torch.nn import functional as F
@@ -22,6 +21,11 @@ from ..utils.residual import can_fuse_residual_add, visionhope_residual_add
 
 
 _SIDE_STREAMS = {}
+
+# CPE and norm1 of the fused block path in one kernel where the map allows; False runs the
+# two kernels (for measurements).  A module attribute, not an environment variable, so the
+# path a forward takes does not depend on the caller's environment.
+FUSE_CPE_LAYERNORM = True
 
 
 def _side_stream(device):
@@ -180,12 +184,12 @@ class VisionHOPEBlock(nn.Module):
             return t_nhwc.permute(0, 3, 1, 2)
 
         # CPE and norm1: one pass (the sum and its LayerNorm) where the map allows
-        # (VH_CPE_LN=0 runs the two kernels, for measurements).
+        # (FUSE_CPE_LAYERNORM = False runs the two kernels, for measurements).
         h = None
         if self.cpe is not None:
             fused = (dwconv.depthwise_conv_add_layernorm(x, self.cpe, self.norm1.weight, self.norm1.bias,
                                                          self.norm1.eps)
-                     if x.dtype == act and os.environ.get("VH_CPE_LN", "1") != "0" else None)
+                     if x.dtype == act and FUSE_CPE_LAYERNORM else None)
             if fused is not None:
                 x, h = fused
             else:
@@ -275,6 +279,7 @@ class VisionHOPEBlock(nn.Module):
         lepe = None if self.local_position is None else torch.empty_like(x_local, memory_format=torch.channels_last)
         main = torch.cuda.current_stream(dev)
         side = _side_stream(dev)
+        op.announce_query_projection(x_nhwc)
         side.wait_stream(main)
         with torch.cuda.stream(side), torch.autocast("cuda", enabled=False):
             # Operands already in the compute dtype: the product autocast would run.

@@ -9,6 +9,7 @@ no CPU or PyTorch fallback for GPU tensors.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from pathlib import Path
 
@@ -24,7 +25,8 @@ _DTYPE_CODES = {torch.float32: VH_DTYPE_F32, torch.bfloat16: VH_DTYPE_BF16, torc
 
 # Symbols declared in include/visionhope_hip.h (tests check the library exports all of them).
 EXPORTED_SYMBOLS = (
-    "vh_abi_version", "vh_last_error", "vh_srnl_workspace_bytes", "vh_srnl_spatial_forward",
+    "vh_abi_version", "vh_last_error", "vh_set_dispatch_override", "vh_clear_dispatch_overrides",
+    "vh_grn_workspace_fallbacks", "vh_srnl_workspace_bytes", "vh_srnl_spatial_forward",
     "vh_srnl_spatial_forward_noalloc",
     "vh_srnl_spatial_scan", "vh_srnl_spatial_readout",
     "vh_srnl_line_forward_seq_noatomic", "vh_srnl_sequence_forward", "vh_srnl_forward",
@@ -64,6 +66,9 @@ _CP = ctypes.POINTER(SRNLConsts)
 _SIGNATURES = {
     "vh_abi_version": (ctypes.c_int, []),
     "vh_last_error": (ctypes.c_char_p, []),
+    "vh_set_dispatch_override": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p]),
+    "vh_clear_dispatch_overrides": (None, []),
+    "vh_grn_workspace_fallbacks": (ctypes.c_int, [_vp, _sz, _vp, ctypes.POINTER(ctypes.c_int64)]),
     "vh_srnl_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "vh_srnl_spatial_forward": (ctypes.c_int, [
         _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
@@ -194,3 +199,20 @@ def make_consts(step_scale, min_retention, retention_bias, injection_margin, spe
 def workspace(nbytes: int, device) -> torch.Tensor:
     """Workspace tensor of at least ``nbytes`` (fp32 elements, 256-byte granule)."""
     return torch.empty(max(1, (int(nbytes) + 255) // 256 * 64), dtype=torch.float32, device=device)
+
+
+@contextlib.contextmanager
+def dispatch_override(**values):
+    """Force kernel choices of the library for the calls inside the block, e.g.
+    ``with dispatch_override(scan_pack="2x2"): ...`` (names and values: the
+    ``vh_set_dispatch_override`` comment of ``include/visionhope_hip.h``).  For tests and
+    measurements: by default every entry point chooses from its arguments alone.  The
+    overrides are process-wide and are cleared on exit."""
+    lib = load_library()
+    try:
+        for name, value in values.items():
+            check(lib.vh_set_dispatch_override(name.encode(), str(value).encode()), "vh_set_dispatch_override")
+        yield
+    finally:
+        for name in values:
+            lib.vh_set_dispatch_override(name.encode(), None)
