@@ -187,6 +187,71 @@ def test_grn_one_pass_graph_replays(device):
         torch.cuda.synchronize()
 
 
+def test_grn_one_pass_two_graphs_replayed_in_reverse(device):
+    """Two graphs captured one after the other on the same capture stream share its GRN
+    workspace (created inside the first capture); replaying the second one first, before
+    the first graph ever ran, still gives the eager result (each captured call fills the
+    synchronisation header itself)."""
+    from visionhope_amd.utils.grn_cuda import visionhope_grn
+
+    gen = torch.Generator(device=device).manual_seed(79)
+    x1 = torch.randn(8, 56, 56, 96, device=device, generator=gen).bfloat16().permute(0, 3, 1, 2)
+    x2 = torch.randn(16, 28, 28, 192, device=device, generator=gen).bfloat16().permute(0, 3, 1, 2)
+    g1, b1 = torch.randn(96, device=device, generator=gen) * 0.1, torch.randn(96, device=device, generator=gen) * 0.1
+    g2, b2 = torch.randn(192, device=device, generator=gen) * 0.1, torch.randn(192, device=device, generator=gen) * 0.1
+    stream = torch.cuda.Stream(device=device)
+    graphs = [torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()]
+    with torch.cuda.graph(graphs[0], stream=stream):
+        out1 = visionhope_grn(x1, g1, b1, 1e-6)
+    with torch.cuda.graph(graphs[1], stream=stream):
+        out2 = visionhope_grn(x2, g2, b2, 1e-6)
+    eager1, eager2 = visionhope_grn(x1, g1, b1, 1e-6), visionhope_grn(x2, g2, b2, 1e-6)
+    for _ in range(2):
+        for out in (out1, out2):
+            out.zero_()
+        graphs[1].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out2, eager2)
+        graphs[0].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out1, eager1)
+
+
+def test_grn_one_pass_wait_give_up_is_correct_and_counted(oracle, device, dispatch):
+    """Forces every workgroup of the one-pass GRN to stop waiting, from the host and with
+    every kernel exiting normally: the image counters are preset so that they never reach
+    the piece count, and the wait is cut to 64 sleeps.  Each piece then computes its
+    image's statistics from x itself: the output still matches the oracle, the give-ups
+    are counted (vh_grn_workspace_fallbacks), and the counters are left zero, so the next
+    call, with the default limit, runs the ordinary exchange and gives up nowhere."""
+    from visionhope_amd.utils import hip
+    from visionhope_amd.utils.grn_cuda import _stream_workspace, grn_wait_fallbacks, visionhope_grn
+
+    batch, channels, height, width = 6, 96, 56, 56
+    x = randn(batch, channels, height, width, seed=91).bfloat16().contiguous(memory_format=torch.channels_last)
+    gamma, beta = randn(channels, seed=92, scale=0.1), randn(channels, seed=93, scale=0.1)
+    expected = oracle.grn(x.float().numpy(), gamma.numpy(), beta.numpy())
+    xd, gd, bd = x.to(device), gamma.to(device), beta.to(device)
+    lib = hip.load_library()
+    ws = _stream_workspace(lib.vh_grn_workspace_bytes(batch, channels, height, width), xd.device)
+    before = grn_wait_fallbacks(xd.device)
+    words = ws[:8192].view(torch.int32).view(256, 32)
+    words[:batch, 0] = -1          # 2^32 - 1: after every piece has counted, pieces - 1 < pieces
+    dispatch(grn_spin_limit=64)
+    y = visionhope_grn(xd, gd, bd, 1e-6)
+    torch.cuda.synchronize()
+    assert_close(y.cpu().numpy(), expected, 2e-5, "GRN after give-up")
+    gave_up = grn_wait_fallbacks(xd.device) - before
+    print(f"[grn] give-ups counted: {gave_up}", flush=True)
+    assert gave_up >= batch and gave_up % batch == 0, gave_up
+    assert int(words[:, 0].abs().sum()) == 0 and int(words[:, 16].abs().sum()) == 0
+    dispatch(grn_spin_limit=1 << 20)
+    y = visionhope_grn(xd, gd, bd, 1e-6)
+    torch.cuda.synchronize()
+    assert_close(y.cpu().numpy(), expected, 2e-5, "GRN after the counters were restored")
+    assert grn_wait_fallbacks(xd.device) - before == gave_up
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("channels", [3, 16, 64, 96, 128, 200, 512, 1024, 4096])
 @pytest.mark.parametrize("channels_last", [True, False])

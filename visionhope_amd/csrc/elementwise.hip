@@ -580,20 +580,27 @@ __global__ __launch_bounds__(256) void grn_stats_apply8_kernel(const T* __restri
 // whose pieces all lie below m complete; only the one image holding m can wait on a
 // workgroup that has not started, and it holds fewer than pieces <= kGrnMaxPieces slots of
 // an XCD (each holds hundreds of workgroups), so the others keep finishing and m is
-// dispatched.  The wait is also bounded (kGrnSpinLimit sleeps); a piece that gives up
-// stores NaN statistics instead of hanging.  No counter is shared by all workgroups (one
-// shared word costs a serialised atomic per workgroup).
+// dispatched.  That dispatch order is observed behaviour of the hardware, not a documented
+// guarantee, so nothing rests on it for correctness: the wait is bounded (spin_limit
+// sleeps, kGrnSpinLimit unless overridden), and a piece that gives up computes its image's
+// statistics itself from x (all S rows, read again) instead of from the other pieces'
+// partial sums.  Its output is then correct to FP32 rounding of a different summation
+// order, and it adds one to the fallback word of its image's line, which the host reads
+// with vh_grn_workspace_fallbacks.  No counter is shared by all workgroups (one shared word
+// costs a serialised atomic per workgroup).
 //
 // Synchronisation words: a fixed header of kGrnSyncImages 128-byte lines at the start of the
 // workspace (the partial sums of every GRN path start after it, so no path ever writes
 // into it), one line per image of a launch: word 0 counts the pieces that published, word
 // 16 the pieces done.  They must be zero when the launch starts; the last piece of each
-// image resets both, so the launch leaves them zero.  A launch covers at most
-// kGrnSyncImages images; larger batches take several launches.
+// image resets both, so the launch leaves them zero.  Word 8 counts fallbacks and is never
+// reset by a kernel.  A launch covers at most kGrnSyncImages images; larger batches take
+// several launches.
 constexpr int kGrnVec = 8;                  // rows per thread held in registers (or 2 kGrnVec)
 constexpr int kGrnMaxPieces = 64;
 constexpr uint32_t kGrnSpinLimit = 1u << 20;
 constexpr int kGrnSyncWords = 32;           // per image
+constexpr int kGrnFallbackWord = 8;         // within an image's line
 constexpr int kGrnSyncImages = 256;
 
 template <typename T, typename TO, int V>
@@ -601,7 +608,8 @@ __global__ __launch_bounds__(256) void grn_onepass8_kernel(const T* __restrict__
                                                           const float* __restrict__ beta, float* __restrict__ gx,
                                                           float* __restrict__ inv_den, TO* __restrict__ y,
                                                           uint32_t* __restrict__ sync, float* __restrict__ partial,
-                                                          int C, int S, int pieces, int b0, float eps, int piece_rows) {
+                                                          int C, int S, int pieces, int b0, float eps, int piece_rows,
+                                                          uint32_t spin_limit) {
     extern __shared__ __align__(16) float red[];   // [R][C] partial sums, then [C] gx; FP32 staging
     __shared__ uint32_t word;
     __shared__ float wsum[4];
@@ -659,29 +667,57 @@ __global__ __launch_bounds__(256) void grn_onepass8_kernel(const T* __restrict__
         uint32_t spins = 0;
         while (__hip_atomic_load(counted, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
                    static_cast<uint32_t>(pieces) &&
-               spins < kGrnSpinLimit) {
+               spins < spin_limit) {
             __builtin_amdgcn_s_sleep(2);
             ++spins;
         }
-        word = spins < kGrnSpinLimit;
+        word = spins < spin_limit;
+        if (spins >= spin_limit) atomicAdd(counted + kGrnFallbackWord, 1u);
     }
     __syncthreads();
-    const bool complete = word != 0;
-    float* const gsh = red;   // the [R][C] sums are no longer needed
+    const bool complete = word != 0;   // uniform over the workgroup
+    if (!complete) {
+        // Fallback: this piece's own sums of squares over every row of the image, into the
+        // [R][C] LDS rows (its own piece's sums there are superseded).
+        float a8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (lane_rows) {
+            for (int s = rr; s < S; s += R) {
+                float f[8];
+                pack8_to_f32<T>(load_pack8<T>(xb + static_cast<int64_t>(s) * C), f);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) a8[j] += f[j] * f[j];
+            }
+        }
+        __syncthreads();
+        if (lane_rows) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) red[rr * C + g * 8 + j] = a8[j];
+        }
+        __syncthreads();
+    }
+    float* const gsh = red;   // the [R][C] sums are no longer needed once read
     float local = 0.f;
     float* const img = partial + static_cast<int64_t>(b) * pieces * C;
     for (int c = t; c < C; c += nt) {
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-        int p = 0;
-        auto at = [&](int pc) { return __hip_atomic_load(&img[pc * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-        for (; p + 4 <= pieces; p += 4) {
-            a0 += at(p);
-            a1 += at(p + 1);
-            a2 += at(p + 2);
-            a3 += at(p + 3);
+        float gv;
+        if (complete) {
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+            int p = 0;
+            auto at = [&](int pc) { return __hip_atomic_load(&img[pc * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+            for (; p + 4 <= pieces; p += 4) {
+                a0 += at(p);
+                a1 += at(p + 1);
+                a2 += at(p + 2);
+                a3 += at(p + 3);
+            }
+            for (; p < pieces; ++p) a0 += at(p);
+            gv = sqrtf((a0 + a1) + (a2 + a3));
+        } else {
+            // column c of the [R][C] rows is read and written by this thread only
+            float sum = 0.f;
+            for (int q = 0; q < R; ++q) sum += red[q * C + c];
+            gv = sqrtf(sum);
         }
-        for (; p < pieces; ++p) a0 += at(p);
-        const float gv = sqrtf((a0 + a1) + (a2 + a3));
         gsh[c] = gv;
         local += gv;
     }
@@ -691,7 +727,7 @@ __global__ __launch_bounds__(256) void grn_onepass8_kernel(const T* __restrict__
     __syncthreads();
     float total_g = wsum[0];
     for (int w = 1; w < (nt + 63) / 64; ++w) total_g += wsum[w];
-    const float inv = complete ? 1.f / (total_g / static_cast<float>(C) + eps) : __builtin_nanf("");
+    const float inv = 1.f / (total_g / static_cast<float>(C) + eps);
     if (piece == 0) {
         for (int c = t; c < C; c += nt) gx[static_cast<int64_t>(b) * C + c] = gsh[c];
         if (t == 0) inv_den[b] = inv;
@@ -1035,8 +1071,8 @@ bool launch_ln_nhwc8(const void* x, const float* w, const float* b, void* yv, fl
     TO* y = static_cast<TO*>(yv);
     // Staged stores while the workgroup's rows fit in 32 KB of LDS (GP <= 4 for FP32 out).
     const size_t stage = static_cast<size_t>(256 >> lg) * C * sizeof(TO);
-    const char* env = std::getenv("VH_LN_STAGE");
-    if (stage <= 32768 && !(env && env[0] == '0')) {
+    const Override staged("ln_stage");
+    if (stage <= 32768 && !(staged.set() && staged.value[0] == '0')) {
         switch (gp) {
 #define VH_LN8S(G)                                                                                              \
     case G:                                                                                                     \
@@ -1277,6 +1313,22 @@ size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W) {
     return grn_sync_bytes() + static_cast<size_t>(B * nslab * C) * sizeof(float);
 }
 
+int vh_grn_workspace_fallbacks(const void* workspace, size_t workspace_bytes, void* stream, int64_t* count) {
+    VH_REQUIRE(workspace && count, VH_ERR_ARG, "GRN fallback query pointers must not be null");
+    VH_REQUIRE(workspace_bytes >= grn_sync_bytes(), VH_ERR_WORKSPACE, "GRN workspace needs at least %zu bytes, got %zu",
+               grn_sync_bytes(), workspace_bytes);
+    static_assert(kGrnSyncImages * kGrnSyncWords * 4 == 32768, "header size");
+    uint32_t words[kGrnSyncImages * kGrnSyncWords];
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (hipMemcpyAsync(words, workspace, sizeof(words), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return set_error(VH_ERR_LAUNCH, "GRN fallback query: copy of the synchronisation header failed");
+    int64_t n = 0;
+    for (int i = 0; i < kGrnSyncImages; ++i) n += words[i * kGrnSyncWords + kGrnFallbackWord];
+    *count = n;
+    return VH_OK;
+}
+
 int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const float* beta, void* y,
                    int32_t y_dtype, float* gx, float* inv_den, int64_t B, int64_t C, int64_t H,
                    int64_t W, float eps, void* workspace, size_t workspace_bytes, void* stream) {
@@ -1302,6 +1354,8 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
     int64_t piece_rows = 0;
     const int64_t pieces = grn_onepass_plan(C, S, dtype_bytes(io_dtype), &piece_rows, &vrows);
     if (pieces > 0 && grn_vectorised(C, x, y) && B * S * C < (int64_t(1) << 31)) {
+        const Override forced_spins("grn_spin_limit");
+        const uint32_t spin_limit = forced_spins.set() ? static_cast<uint32_t>(forced_spins.as_i64()) : kGrnSpinLimit;
         const int G = static_cast<int>(C / 8);
         const unsigned threads = static_cast<unsigned>((G * (256 / G) + 63) / 64 * 64);
         // [R][C] partial sums (rounded up to 16 bytes), then 2 KB of staging per wave for FP32 output
@@ -1317,17 +1371,20 @@ int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const fl
                         hipLaunchKernelGGL((grn_onepass8_kernel<T, TO, 4 * kGrnVec>), dim3(static_cast<unsigned>(nb * pieces)),
                                            dim3(threads), lds, s, static_cast<const T*>(x), gamma, beta, gx, inv_den,
                                            static_cast<TO*>(y), sync, partial, static_cast<int>(C), static_cast<int>(S),
-                                           static_cast<int>(pieces), static_cast<int>(b0), eps, static_cast<int>(piece_rows));
+                                           static_cast<int>(pieces), static_cast<int>(b0), eps, static_cast<int>(piece_rows),
+                                           spin_limit);
                     else if (vrows == 2 * kGrnVec)
                         hipLaunchKernelGGL((grn_onepass8_kernel<T, TO, 2 * kGrnVec>), dim3(static_cast<unsigned>(nb * pieces)),
                                            dim3(threads), lds, s, static_cast<const T*>(x), gamma, beta, gx, inv_den,
                                            static_cast<TO*>(y), sync, partial, static_cast<int>(C), static_cast<int>(S),
-                                           static_cast<int>(pieces), static_cast<int>(b0), eps, static_cast<int>(piece_rows));
+                                           static_cast<int>(pieces), static_cast<int>(b0), eps, static_cast<int>(piece_rows),
+                                           spin_limit);
                     else
                         hipLaunchKernelGGL((grn_onepass8_kernel<T, TO, kGrnVec>), dim3(static_cast<unsigned>(nb * pieces)),
                                            dim3(threads), lds, s, static_cast<const T*>(x), gamma, beta, gx, inv_den,
                                            static_cast<TO*>(y), sync, partial, static_cast<int>(C), static_cast<int>(S),
-                                           static_cast<int>(pieces), static_cast<int>(b0), eps, static_cast<int>(piece_rows));
+                                           static_cast<int>(pieces), static_cast<int>(b0), eps, static_cast<int>(piece_rows),
+                                           spin_limit);
                 }
             });
         });

@@ -5,6 +5,8 @@ launch on the current stream reads x once: each piece publishes its per-channel 
 x^2, waits for the other pieces of its image, then applies the FP32 affine output to the
 rows it holds.  Other maps take two or three launches (partial sums, statistics, apply).
 """
+import ctypes
+
 import torch
 from torch.autograd import Function
 
@@ -12,18 +14,50 @@ from . import hip
 from .cuda import on_tensor_device
 
 # One GRN workspace per (device, stream): its leading synchronisation words must be zero
-# when a workspace is first used, and every call leaves them zero, so a zero-filled
-# buffer is kept and reused; calls on one stream never overlap.
+# when a call starts, and every call leaves them zero, so a zero-filled buffer is kept and
+# reused; calls on one stream never overlap.  Inside a graph capture nothing that happens
+# outside the graph can be relied on (a workspace created during a capture gets its fill
+# only when that graph replays, and another graph may replay first), so a captured call
+# records a fill of the header right before its kernel; a workspace created during a
+# capture is zeroed once more before its first eager use.
 _STREAM_WORKSPACES = {}
+_HEADER_FLOATS = 32768 // 4   # the synchronisation header of vh_grn_workspace_bytes
 
 
 def _stream_workspace(nbytes, device):
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
-    ws = _STREAM_WORKSPACES.get(key)
-    if ws is None or ws.numel() * 4 < nbytes:
-        ws = torch.zeros(max(1, (int(nbytes) + 255) // 256 * 64), dtype=torch.float32, device=device)
-        _STREAM_WORKSPACES[key] = ws
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    capturing = torch.cuda.is_current_stream_capturing()
+    entry = _STREAM_WORKSPACES.get(key)
+    if entry is None or entry[0].numel() * 4 < nbytes:
+        ws = torch.zeros(max(_HEADER_FLOATS, (int(nbytes) + 255) // 256 * 64), dtype=torch.float32, device=device)
+        entry = _STREAM_WORKSPACES[key] = [ws, capturing]
+    ws, born_in_capture = entry
+    if capturing:
+        ws[:_HEADER_FLOATS].zero_()   # a kernel node of the graph, not a memset (replays stay correct)
+    elif born_in_capture:
+        ws[:_HEADER_FLOATS].zero_()
+        entry[1] = False
     return ws
+
+
+def grn_wait_fallbacks(device=None):
+    """How many times a workgroup of the one-pass GRN kernel, on any stream's workspace of
+    ``device``, stopped waiting for the rest of its image and computed the image's
+    statistics from its input itself (its output stays correct; a non-zero count shows
+    that workgroups of one launch did not all run together).  Synchronises those streams:
+    a diagnostic, not for use inside graph capture."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    lib = hip.load_library()
+    total = 0
+    for (index, handle), (ws, _) in list(_STREAM_WORKSPACES.items()):
+        if index != device.index:
+            continue
+        count = ctypes.c_int64(0)
+        hip.check(lib.vh_grn_workspace_fallbacks(hip.ptr(ws), ws.numel() * 4, ctypes.c_void_p(handle),
+                                                 ctypes.byref(count)), "vh_grn_workspace_fallbacks")
+        total += count.value
+    return total
 
 
 class _VisionHOPEGRNFunction(Function):
