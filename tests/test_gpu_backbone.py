@@ -149,3 +149,57 @@ def test_graph_replays_match_eager_forward(tiny_case, device):
             again = gpu(batch)
             torch.cuda.synchronize()
             assert torch.equal(again, eager), f"eager forward after replay {replay} differs"
+
+
+def test_graph_replay_on_changed_input_matches_independent_eager(tiny_case, device):
+    """The reference's graph validation (``analysis/benchmark.py:74-87``): the graph is
+    captured on one batch, new images are copied into its input buffer, and the replay is
+    compared with an independent eager forward of the new images (bf16: atol 1e-3, rtol
+    1e-2; the kernels are deterministic, so the logits are also equal bit for bit).  A
+    graph that had baked in a stale buffer or a value of the capture batch would fail."""
+    from visionhope_amd.inference.prepare import prepare_for_inference
+
+    model, images, _ = tiny_case
+    gpu = copy.deepcopy(model).to(device).to(memory_format=torch.channels_last)
+    prepare_for_inference(gpu)
+    static = images[:8].to(device).contiguous(memory_format=torch.channels_last)
+    fresh = images[8:16].flip(-1).to(device).contiguous(memory_format=torch.channels_last)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        gpu(static)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            captured = gpu(static)
+        outputs = []
+        for replay in range(2):
+            static.copy_(fresh if replay == 0 else images[:8].to(device))
+            graph.replay()
+            torch.cuda.synchronize()
+            expected = gpu(static.clone().contiguous(memory_format=torch.channels_last))
+            torch.cuda.synchronize()
+            torch.testing.assert_close(captured.float(), expected.float(), atol=1e-3, rtol=1e-2)
+            assert torch.equal(captured, expected), f"replay {replay} on changed input differs from eager"
+            outputs.append(captured.clone())
+    assert not torch.equal(outputs[0], outputs[1]), "the two input batches gave the same logits"
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_query_once_and_launch_audit(tiny_case, device, autocast):
+    """The reference's fast-path audit (``inference/audit.py:11-99``,
+    ``analysis/benchmark.py:48-71``) on the prepared Tiny forward: each of the 29 operators
+    projects B*H*W queries exactly once, and the profiler trace holds exactly one scan and
+    one readout launch per operator call."""
+    from visionhope_amd.inference.audit import audit_fast_path
+    from visionhope_amd.inference.prepare import prepare_for_inference
+
+    model, images, _ = tiny_case
+    gpu = copy.deepcopy(model).to(device).to(memory_format=torch.channels_last)
+    prepare_for_inference(gpu)
+    batch = images[:4].to(device).contiguous(memory_format=torch.channels_last)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        gpu(batch)
+        _, evidence = audit_fast_path(gpu, lambda: gpu(batch))
+    print(f"audit autocast={autocast}: {evidence}", flush=True)
+    assert evidence["fused_operators"] == 29 and evidence["fused_srnl_calls"] == 29
+    assert evidence["scan_kernels"] == 29 and evidence["readout_kernels"] == 29
+    assert evidence["query_once"] is True

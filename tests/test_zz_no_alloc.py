@@ -102,3 +102,56 @@ def test_noalloc_rejects_calls_beyond_its_scratch():
     rc = lib.vh_srnl_spatial_forward_noalloc(p, p, hip.VH_DTYPE_BF16, p, p, p, p, p, p, 0, p, p,
                                              2, 8, 8, 48, 12, chunks, _consts(), None)
     assert rc == hip.VH_ERR_HEAD_DIM
+
+
+_FOOTPRINT_PROBE = r"""
+import ctypes, json, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from visionhope_amd.utils import hip
+dev = torch.device("cuda:0")
+gen = torch.Generator().manual_seed(3)
+mems = [torch.randn(4, 2, 16, 16, generator=gen).mul(0.01).to(dev) for _ in range(3)]
+mems += [torch.zeros(4, 2, 16, device=dev) for _ in range(2)]
+x = torch.randn(1, 8, 8, 32, generator=gen).bfloat16().to(dev)
+q = torch.randn(1, 8, 8, 32, generator=gen).bfloat16().to(dev)
+skip, w = torch.zeros(32, device=dev), torch.ones(4, 32, device=dev)
+out, out2, ws = torch.empty(1, 8, 8, 32, device=dev), torch.empty(1, 8, 8, 32, device=dev), torch.empty(1 << 20, device=dev)
+lib = hip.load_library()
+chunks, keep = hip.int64_array([8] * 4)
+consts = hip.make_consts(0.025, 0.0, 2.197224577, 0.999, True, 0.999999)
+args = [hip.ptr(x), hip.ptr(q), 1, *[hip.ptr(m) for m in mems], hip.ptr(skip), 0, hip.ptr(w)]
+torch.cuda.synchronize()
+f0 = torch.cuda.mem_get_info()[0]
+hip.check(lib.vh_srnl_spatial_forward(*args, hip.ptr(out), 1, 8, 8, 32, 16, chunks, ctypes.byref(consts),
+                                      hip.ptr(ws), ws.numel() * 4, hip.stream_of(x)), "forward")
+torch.cuda.synchronize()
+f1 = torch.cuda.mem_get_info()[0]
+hip.check(lib.vh_srnl_spatial_forward_noalloc(*args, hip.ptr(out2), 1, 8, 8, 32, 16, chunks, ctypes.byref(consts),
+                                              hip.stream_of(x)), "noalloc")
+torch.cuda.synchronize()
+f2 = torch.cuda.mem_get_info()[0]
+print(json.dumps({"ordinary": f0 - f1, "noalloc": f1 - f2, "equal": bool(torch.equal(out, out2))}))
+"""
+
+
+@pytest.mark.gpu
+def test_scratch_array_is_held_only_by_processes_that_call_the_entry():
+    """The array lives in its own code object, which the HIP runtime loads at the first use
+    of that object's kernels or symbols: in a fresh process, an ordinary SRNL call adds a
+    few MiB of device memory (its own code object), and only the first no-alloc call adds
+    the array's 96 MiB."""
+    import json
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    proc = subprocess.run([sys.executable, "-c", _FOOTPRINT_PROBE, str(root)], capture_output=True, text=True,
+                          timeout=180)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    result = json.loads(proc.stdout.strip().splitlines()[-1])
+    print(f"[footprint] {result}", flush=True)
+    assert result["equal"]
+    assert result["ordinary"] < 32 << 20, result
+    assert result["noalloc"] >= SCRATCH_BYTES, result

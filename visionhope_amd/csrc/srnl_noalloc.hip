@@ -4,9 +4,11 @@
 // vh_srnl_spatial_forward takes a caller workspace for the scan's chunk-start content
 // memories ([lines, chunks, d, d] fp32, written by the scan and read by the readout).  This
 // variant keeps that buffer in a file-scope device array instead, so a call allocates
-// nothing.  The array lives in this file's code object: only a process that calls this
-// entry point loads it, and then holds kScratchBytes on every GPU it calls it on until the
-// process ends.
+// nothing.  The array lives in this file's code object, which the HIP runtime loads at the
+// first use of one of its kernels or symbols: only a process that calls this entry point
+// holds it, and then holds kScratchBytes on every GPU it calls it on until the process ends
+// (measured on MI355X in a fresh process: an ordinary SRNL call of the library adds 4 MiB of
+// device memory, the first call of this entry 98 MiB; tests/test_zz_no_alloc.py checks it).
 //
 // The device address of the array is looked up once per device (on the entry point's first
 // call with that device current) with hipGetSymbolAddress and kept; kernels receive that

@@ -100,6 +100,14 @@ class VisionHOPEOperator(nn.Module):
         ``[B, H*W, dim]``: ``W_q`` is applied once, then reordered."""
         return scan_orders(self.W_q(seq_hw), height, width)
 
+    def announce_query_projection(self, x_nhwc):
+        """Runs ``W_q``'s registered forward pre-hooks with the tensor about to be projected,
+        for inference paths that compute the projection without calling the module (a
+        native kernel, or a cached-weight product), so that hooks such as the query-once
+        audit see every projection exactly as a module call would show it."""
+        for hook in tuple(self.W_q._forward_pre_hooks.values()):
+            hook(self.W_q, (x_nhwc,))
+
     def direction_weights(self):
         """``[4, dim]`` merge weights of the four directions."""
         if self.direction_merge == "scale":
@@ -195,6 +203,7 @@ class VisionHOPEOperator(nn.Module):
         if torch.is_autocast_enabled("cuda"):
             # autocast's linear, with the weight cast once and cached instead of per call
             weight, bias = linear_weights(self.W_q, torch.get_autocast_dtype("cuda"))
+            self.announce_query_projection(x_nhwc)
             q_nhwc = F.linear(x_nhwc.to(weight.dtype), weight, bias)
         else:
             q_nhwc = self.W_q(x_nhwc)
