@@ -920,15 +920,13 @@ __device__ __forceinline__ v4f readout_mfma(const float (&m)[D / 4], const XRaw<
         const v4s hi = __builtin_bit_cast(v4s, make_uint2(__float_as_uint(m[0]), __float_as_uint(m[1])));
         const v4s lo = __builtin_bit_cast(v4s, make_uint2(__float_as_uint(m[2]), __float_as_uint(m[3])));
         const v4s qs = bf16x4_bits(qr.v);
-        y = mfma_bf16(hi, qs, y);
-        y = mfma_bf16(lo, qs, y);
+        y = mfma_bf16x2(hi, lo, qs, qs, y);   // (hi + lo) q in one 16x16x32 product
     } else if constexpr (std::is_same<T, bf16_t>::value) {
         using Bf = BfOp<D>;
         typename Bf::type hi, lo;
         Bf::split(m, hi, lo);
         const auto qs = Bf::exact(qr);
-        y = Bf::mma(hi, qs, y);
-        y = Bf::mma(lo, qs, y);
+        y = Bf::mma_pair(hi, lo, qs, qs, y);
     } else {
         float qv[D / 4];
         decode_x<T, D>(qr, qv);

@@ -84,6 +84,19 @@ __device__ __forceinline__ v4f mfma_bf16(v4s a, v4s b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
+// a0 b0 + a1 b1 (+ c) in ONE v_mfma_f32_16x16x32_bf16: that instruction takes 8 consecutive
+// k from each lane instead of 4, so lane l's 8 values [a0, a1] of A row l%16 meet [b0, b1] of
+// B column l%16: the same products as mfma_bf16(a0, b0) + mfma_bf16(a1, b1), one issue.
+// Never chain its result as the accumulator of a 16x16x16 product (or the reverse): the
+// compiler issues such a pair back to back, and on MI355X the second product then read a
+// stale accumulator.  Chains of one product size are safe.
+typedef __bf16 v8bf16_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ v4f mfma_bf16x2(v4s a0, v4s a1, v4s b0, v4s b1, v4f c) {
+    const v8bf16_t a = __builtin_bit_cast(v8bf16_t, __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7));
+    const v8bf16_t b = __builtin_bit_cast(v8bf16_t, __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7));
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 typedef float v4fl __attribute__((ext_vector_type(4)));
 
@@ -239,6 +252,10 @@ template <>
 struct BfOp<16> {
     using type = v4s;
     static __device__ __forceinline__ v4f mma(v4s a, v4s b, v4f c) { return mfma_bf16(a, b, c); }
+    // a0 b0 + a1 b1 + c: one 16x16x32 product
+    static __device__ __forceinline__ v4f mma_pair(v4s a0, v4s a1, v4s b0, v4s b1, v4f c) {
+        return mfma_bf16x2(a0, a1, b0, b1, c);
+    }
     static __device__ __forceinline__ void split(const float (&v)[4], v4s& hi, v4s& lo) { split_bf16(v, hi, lo); }
     static __device__ __forceinline__ v4s exact(const XRaw<bf16_t, 16>& r) { return bf16x4_bits(r.v); }
 };
@@ -247,6 +264,10 @@ struct BfOp<32> {
     using type = v8bf;
     static __device__ __forceinline__ v4f mma(v8bf a, v8bf b, v4f c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    // a0 b0 + a1 b1 + c: two 16x16x32 products (K = 32 fills one instruction already)
+    static __device__ __forceinline__ v4f mma_pair(v8bf a0, v8bf a1, v8bf b0, v8bf b1, v4f c) {
+        return mma(a1, b1, mma(a0, b0, c));
     }
     static __device__ __forceinline__ void split(const float (&v)[8], v8bf& hi, v8bf& lo) {
         v8fl f;

@@ -65,7 +65,9 @@ __device__ __forceinline__ void split4(const v4f& v, v4s& hi, v4s& lo) {
     split4(a, hi, lo);
 }
 
-// A B + C for FP32 A, B given as bf16 hi + lo (the lo x lo term dropped).
+// A B + C for FP32 A, B given as bf16 hi + lo (the lo x lo term dropped).  Three products of
+// one size: an accumulation chain that mixes 16x16x32 and 16x16x16 products on one
+// accumulator was issued back to back by the compiler and gave wrong results on MI355X.
 __device__ __forceinline__ v4f mma3(v4s ah, v4s al, v4s bh, v4s bl, v4f c) {
     c = mfma_bf16(ah, bh, c);
     c = mfma_bf16(ah, bl, c);
