@@ -76,6 +76,9 @@ const char* vh_last_error(void);
  *   conv_band        "0" | "1"        3x3 convolution band kernel
  *   grn_spin_limit   1 .. 2^20        one-pass GRN: sleeps before a piece stops waiting
  *                                     for the other pieces of its image
+ *   fusion_tile      "<a>x<b>x<h>"    direction fusion: 2^a x 2^b pixel tiles, h heads per
+ *                                     workgroup
+ *   grn_pieces       2 .. 64          one-pass GRN: pieces per image
  * Results stay within each kernel's stated tolerance under every override: an
  * override changes which kernel runs, never what it computes. */
 int vh_set_dispatch_override(const char* name, const char* value);

@@ -1205,8 +1205,19 @@ int vh_postprocess_scale_forward(const void* Y, const void* X, int32_t io_dtype,
                             reinterpret_cast<uintptr_t>(scale);
     const int64_t groups = H * W * heads * (head_dim / 8);
     if (channels_last && head_dim >= 8 && align % 16 == 0) {
-        const int th_log2 = 2, tw_log2 = 2;
-        const int hpb = static_cast<int>(std::min<int64_t>(heads, std::max(1, 96 / head_dim)));
+        int th_log2 = 2, tw_log2 = 2;
+        int hpb = static_cast<int>(std::min<int64_t>(heads, std::max(1, 96 / head_dim)));
+        // fusion_tile override "<log2 TH>x<log2 TW>x<heads per workgroup>" (measurements)
+        const Override tile("fusion_tile");
+        int ft = 0, fw = 0, fh = 0;
+        if (tile.set() && std::sscanf(tile.value, "%dx%dx%d", &ft, &fw, &fh) == 3) {
+            // the kernel is built for at most 256 threads (its launch bounds)
+            VH_REQUIRE((1 << (ft + fw)) * std::min<int64_t>(fh, heads) * (head_dim / 8) <= 256, VH_ERR_ARG,
+                       "fusion_tile override %s needs more than 256 threads per workgroup", tile.value);
+            th_log2 = ft;
+            tw_log2 = fw;
+            hpb = static_cast<int>(std::min<int64_t>(heads, fh));
+        }
         const int64_t tiles_w = (W + (1 << tw_log2) - 1) >> tw_log2, tiles_h = (H + (1 << th_log2) - 1) >> th_log2;
         const int64_t chunks = (heads + hpb - 1) / hpb;
         const size_t lds = static_cast<size_t>((1 << (th_log2 + tw_log2)) * hpb * head_dim) * sizeof(float);
@@ -1291,8 +1302,10 @@ static size_t grn_sync_bytes() {
 static int64_t grn_onepass_plan(int64_t C, int64_t S, int elem_bytes, int64_t* piece_rows, int* vrows) {
     if (C % 8 != 0 || C / 8 > 256) return 0;
     const int64_t R = 256 / (C / 8);
-    const int64_t want = std::min<int64_t>(std::max<int64_t>(5, (S + 4 * kGrnVec * R - 1) / (4 * kGrnVec * R)),
-                                           (S + R - 1) / R);
+    int64_t want = std::min<int64_t>(std::max<int64_t>(5, (S + 4 * kGrnVec * R - 1) / (4 * kGrnVec * R)),
+                                     (S + R - 1) / R);
+    const Override forced("grn_pieces");   // measurements: pieces per image
+    if (forced.set()) want = std::min<int64_t>(forced.as_int(), (S + R - 1) / R);
     const int64_t rows = (S + want - 1) / want;
     const int64_t pieces = (S + rows - 1) / rows;
     const int64_t v = (rows + R - 1) / R;

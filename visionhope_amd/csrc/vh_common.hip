@@ -77,6 +77,13 @@ bool pw_cfg_ok(const char* v) {
     return false;
 }
 
+bool fusion_tile_ok(const char* v) {
+    int th = 0, tw = 0, hpb = 0;
+    char tail = 0;
+    return std::sscanf(v, "%dx%dx%d%c", &th, &tw, &hpb, &tail) == 3 && th >= 0 && th <= 4 && tw >= 0 && tw <= 4 &&
+           hpb >= 1 && hpb <= 64;
+}
+
 struct OverrideSlot {
     const char* name;
     bool (*valid)(const char*);
@@ -97,6 +104,8 @@ OverrideSlot g_overrides[] = {
     {"ln_stage", [](const char* v) { return one_of(v, {"0", "1"}); }, ""},
     {"conv_band", [](const char* v) { return one_of(v, {"0", "1"}); }, ""},
     {"grn_spin_limit", [](const char* v) { return is_uint(v, 1, 1 << 20); }, ""},
+    {"fusion_tile", fusion_tile_ok, ""},
+    {"grn_pieces", [](const char* v) { return is_uint(v, 2, 64); }, ""},
 };
 std::mutex g_override_mutex;
 
