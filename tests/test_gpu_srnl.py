@@ -388,3 +388,41 @@ def test_sequence_scan_wide(oracle, device, dispatch, head_dim, waves, mode, chu
                             q.to(device), list(chunks), q_raw=True)
     expected = oracle.sequence_forward(x.float().numpy(), q.float().numpy(), mems, list(chunks))
     assert_close(y.float().cpu().numpy(), expected, tol, f"wide sequence d={head_dim} W={waves} {mode} {chunks}")
+
+
+# bf16 head_dim-16 scans with fewer lines than SIMDs take the block form with one workgroup
+# per line and the chunk's 16-token blocks spread over 1, 2, 4 or 8 waves (chunks of at most
+# 128 tokens; longer chunks keep the wide scan).  FP32 output of a bf16 scan: the block form's
+# hi + lo products put it within about 2^-16 of the oracle.
+FEW_LINES_TOL = 2e-5
+
+
+@pytest.mark.parametrize("height,width,heads", [(56, 56, 2), (28, 28, 4), (9, 6, 3), (16, 128, 1), (32, 100, 1),
+                                                (7, 7, 2), (128, 128, 1)])
+@pytest.mark.parametrize("kind", ["perturbed", "strong"])
+def test_spatial_few_lines_block_form(oracle, device, height, width, heads, kind):
+    channels = heads * 16
+    mems = memories(4, heads, 16, kind=kind, seed=height * 3 + width)
+    x = randn(2, height, width, channels, seed=height + 101).bfloat16()
+    q = randn(2, height, width, channels, seed=width + 102).bfloat16()
+    skip = randn(channels, seed=103, scale=0.1)
+    wts = 1 + randn(4, channels, seed=104, scale=0.1)
+    got = _spatial(device, x, q, mems, skip, wts, (width, width, height, height))
+    expected = oracle.operator_forward(x.float().numpy(), q.float().numpy(), mems, skip.numpy(), wts.numpy(), 16)
+    assert_close(got, expected, FEW_LINES_TOL, f"few-line block form {height}x{width} heads={heads} {kind}")
+
+
+@pytest.mark.parametrize("chunks", [(5, 16, 64, 3), (65, 128, 100, 17), (128, 128, 128, 128), (200, 40, 7, 33)])
+def test_sequence_few_lines_block_form(oracle, device, chunks):
+    """Packed bf16 sequences (263 tokens, ragged last chunks) through the few-line block form;
+    a chunk of 200 tokens (more than 8 blocks) sends the launch to the wide scan."""
+    from visionhope_amd.models.srnl_core.chunk import srnl_packed_forward
+
+    batch, directions, heads, length = 1, 4, 2, 263
+    mems = memories(directions, heads, 16, kind="strong", seed=sum(chunks))
+    x, q = _packed_case(batch, directions, heads, length, 16, torch.bfloat16, seed=107)
+    y = srnl_packed_forward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device),
+                            q.to(device), list(chunks), q_raw=True)
+    expected = oracle.sequence_forward(x.float().numpy(), q.float().numpy(), mems, list(chunks))
+    # bf16 output: one rounding of the result on top of the scan's error
+    assert_close(y.float().cpu().numpy(), expected, 5e-3, f"few-line sequence {chunks}")

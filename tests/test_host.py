@@ -395,3 +395,22 @@ def test_gelu_fit_accuracy():
         h = (t * np.exp2((p - (f32(0.72134752044448170) * x) * x).astype(f32))).astype(f32)
         gb = (np.maximum(x, f32(0)) - np.abs(x) * h).astype(f32).astype(np.float64)
         assert np.abs(gb - exact).max() > 1e-3
+
+
+def test_audit_kernel_families_cover_every_scan_and_readout_kernel():
+    """The launch audit counts kernels by name: every scan and readout kernel the library
+    defines must belong to exactly one of its families."""
+    import re
+    from pathlib import Path
+
+    from visionhope_amd.inference.audit import READOUT_KERNELS, SCAN_KERNELS
+
+    csrc = Path(__file__).resolve().parents[1] / "visionhope_amd" / "csrc"
+    names = set()
+    for path in csrc.glob("*.hip"):
+        names.update(re.findall(r"\bvoid\s+(srnl_\w+_kernel)\s*\(", path.read_text()))
+    forward = {n for n in names if "backward" not in n}
+    assert forward, "no kernels found"
+    for name in forward:
+        hits = [f for f in SCAN_KERNELS + READOUT_KERNELS if re.fullmatch(re.escape(f), name)]
+        assert len(hits) == 1, (name, hits)

@@ -1198,6 +1198,13 @@ void launch_scan(const ScanParams& sp, hipStream_t stream) {
         int token_blocks = (D == 16 && max_chunk >= 64) ? 2 : 1;
         const Override tb("scan_tb");
         if (tb.set()) token_blocks = tb.as_int() == 1 ? 1 : 2;
+        if constexpr (D == 16 && std::is_same<T, bf16_t>::value) {
+            // Few lines, bf16: the block form with a chunk's blocks spread over the waves of
+            // one workgroup per line (srnl_utw.hip), unless a dispatch override forces the
+            // wide scan or the stepped form.
+            if (waves > 0 && scan_ut_enabled() && !Override("scan_wide").set() && launch_scan16_utw(sp, stream))
+                return;
+        }
         if (waves > 0 && launch_scan_wide(sp, dtype_code_of<T>(), D, waves, token_blocks, stream)) return;
     }
     if constexpr (D == 16 && std::is_same<T, bf16_t>::value) {

@@ -362,6 +362,10 @@ int scan_wide_waves(int64_t lines, int head_dim);
 // Scan for head_dim 16 with bf16 activations in the block form (srnl_ut.hip), packed as
 // sp.lines_per_wave x sp.tiles_per_wave like srnl_scan16_kernel.
 bool launch_scan16_ut(const ScanParams& sp, hipStream_t stream);
+// The block form with the blocks of a chunk spread over the waves of one workgroup per line
+// (srnl_utw.hip): head_dim 16, bf16 activations, chunks of at most 128 tokens.  Returns
+// false (nothing launched) when the chunks or the input alignment do not allow it.
+bool launch_scan16_utw(const ScanParams& sp, hipStream_t stream);
 bool launch_scan_wide(const ScanParams& sp, int io_dtype, int head_dim, int waves, int token_blocks,
                       hipStream_t stream);
 
