@@ -1202,7 +1202,9 @@ void launch_scan(const ScanParams& sp, hipStream_t stream) {
             // Few lines, bf16: the block form with a chunk's blocks spread over the waves of
             // one workgroup per line (srnl_utw.hip), unless a dispatch override forces the
             // wide scan or the stepped form.
-            if (waves > 0 && scan_ut_enabled() && !Override("scan_wide").set() && launch_scan16_utw(sp, stream))
+            const Override utw("scan_utw");   // "1": whenever the chunks allow, "0": never
+            const bool utw_on = utw.set() ? utw.value[0] == '1' : waves > 0;
+            if (utw_on && scan_ut_enabled() && !Override("scan_wide").set() && launch_scan16_utw(sp, stream))
                 return;
         }
         if (waves > 0 && launch_scan_wide(sp, dtype_code_of<T>(), D, waves, token_blocks, stream)) return;

@@ -9,16 +9,18 @@
 //     substitution, X_w = a_15 I - (K D_a) Z, Y_w = -Delta Z -- exactly as srnl_ut.hip forms
 //     one tile's map (reference recurrence: inference_recurrence.cuh:32-135, memory.cuh:
 //     219-233);
-//   * the maps compose in a tree of log2 W levels through LDS, (X_a, Y_a) then (X_b, Y_b)
-//     giving (X_a X_b, Y_a X_b + Y_b), and the chunk gain from G = I is X + Y;
+//   * the maps compose in order on wave 0 (srnl_ut.hip's chain): wave 0 forms G^T =
+//     (X_0 + Y_0)^T in registers, the other waves hand X_w and Y_w^T over through LDS, and
+//     G^T <- X_w^T G^T + Y_w^T follows block by block -- one barrier, no transposes (a tree
+//     of log2 W levels measured 3,800 of 8,600 cycles per chunk at W = 8, against about
+//     1,200 for the chain);
 //   * the state S = [M_m; M_v; M_k; e; a; 0] (64 x 16 FP32) lives in LDS; the refresh
 //     S <- S G (the reference's M <- M G and e <- G^T e, a <- G^T a, :119-133) is split over
 //     the waves by 16-row blocks.
 //
-// Matrices pass between waves in LDS column by column: a map M in the accumulator layout of
-// lane 16 q + j (rows 4q..4q+3 of column j) is stored as Mt[16 j + 4 q ...], so the B
-// operand of the next product (the same layout) is one 16-byte load, and the A operand
-// (row i, columns 4q..4q+3) four scalar loads.  Slots past the chunk act as the identity.
+// Matrices pass between waves in LDS in the accumulator layout of lane 16 q + j (rows
+// 4q..4q+3 of column j at [16 j + 4 q ...]): X_w is then the A operand of X_w^T and Y_w^T
+// the addend, one 16-byte load each.  Slots past the chunk act as the identity.
 #include "srnl_block_form.h"
 
 namespace vh {
@@ -47,10 +49,10 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
     __shared__ __align__(16) float tk[W][64];         // per slot: rho, kappa, -a_{t-1}, w
     __shared__ __align__(16) float Lc[W][256];        // L[s][t] at [t][s]
     __shared__ __align__(16) float Zs[W][256];        // Z[s][f] at [f][s]
-    __shared__ __align__(16) float Xt[W][256];        // block maps, column-major
-    __shared__ __align__(16) float Yt[W][256];
+    __shared__ __align__(16) float Xt[W][256];        // X_w, accumulator layout
+    __shared__ __align__(16) float Yt[W][256];        // Y_w^T, accumulator layout
     __shared__ __align__(16) float St[64 * D];        // state rows, row-major
-    __shared__ __align__(16) float Gt[256];           // chunk gain, column-major
+    __shared__ __align__(16) float Gr[256];           // chunk gain G, row-major
 
     const int tid = static_cast<int>(threadIdx.x);
     const int wv = tid >> 6, lane = tid & 63, i16 = lane & 15, q = lane >> 4;
@@ -113,6 +115,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
                          ld4(St + i16 * D + 4 * q), p.split_states);
         if (c == nc - 1) break;
 
+        v4f gT = {0.f, 0.f, 0.f, 0.f};   // wave 0: G^T of the blocks composed so far
         if (wv < nblk) {
             if (!have) load_x(c, xr, xok);
             const bool valid = 16 * wv + i16 < C;   // slot inside the chunk (every such token is < L here)
@@ -236,7 +239,9 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
                     *reinterpret_cast<float4*>(Zsw + i16 * 16 + s) = make_float4(zc[s], zc[s + 1], zc[s + 2], zc[s + 3]);
             }
             wave_sync();
-            // ---- the block's map: X = a_15 I - (K D_a) Z, Y = -Delta Z (accumulator layout) ----
+            // ---- the block's map: X = a_15 I - (K D_a) Z, Y = -Delta Z; wave 0 (the first
+            //      block, entered with G = I) keeps (X_0 + Y_0)^T, the others hand over X_w
+            //      and Y_w^T (accumulator layouts) ----
             {
                 const float4 z4f = ld4(Zsw + i16 * 16 + 4 * q);
                 const float4 k4 = ld4(kTw + i16 * DKS + 4 * q);
@@ -247,59 +252,41 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
                 const float ndl[4] = {d4.x, d4.y, d4.z, d4.w};
                 v4s zh, zl, kah, kal, dlh, dll;
                 split4(zv, zh, zl);
-                split4(nka, kah, kal);
-                split4(ndl, dlh, dll);
-                st4(Xt[wv] + i16 * 16 + 4 * q, mma3(kah, kal, zh, zl, diag4(decay, q, i16)));
-                st4(Yt[wv] + i16 * 16 + 4 * q, mma3(dlh, dll, zh, zl, v4f{0.f, 0.f, 0.f, 0.f}));
-            }
-        } else {
-            // a block past the chunk: the identity map
-            st4(Xt[wv] + i16 * 16 + 4 * q, diag4(1.f, q, i16));
-            st4(Yt[wv] + i16 * 16 + 4 * q, v4f{0.f, 0.f, 0.f, 0.f});
-        }
-
-        // ---- composition tree: (X_a, Y_a) then (X_b, Y_b) = (X_a X_b, Y_a X_b + Y_b) ----
-#pragma unroll
-        for (int step = 1; step < W; step *= 2) {
-            __syncthreads();
-            if ((wv & (2 * step - 1)) == 0) {
-                const float* xa = Xt[wv];
-                const float* ya = Yt[wv];
-                float xav[4], yav[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {   // A operand: row i16, columns 4q..4q+3
-                    xav[k] = xa[(4 * q + k) * 16 + i16];
-                    yav[k] = ya[(4 * q + k) * 16 + i16];
-                }
-                const float4 xb4 = ld4(Xt[wv + step] + i16 * 16 + 4 * q);   // B operand of X_b
-                const float4 yb4 = ld4(Yt[wv + step] + i16 * 16 + 4 * q);   // Y_b, accumulator layout
-                const float xbv[4] = {xb4.x, xb4.y, xb4.z, xb4.w};
-                v4s xah, xal, yah, yal, xbh, xbl;
-                split4(xav, xah, xal);
-                split4(yav, yah, yal);
-                split4(xbv, xbh, xbl);
-                const v4f xn = mma3(xah, xal, xbh, xbl, v4f{0.f, 0.f, 0.f, 0.f});
-                const v4f yn = mma3(yah, yal, xbh, xbl, v4f{yb4.x, yb4.y, yb4.z, yb4.w});
-                if (2 * step == W) {
-                    st4(Gt + i16 * 16 + 4 * q, xn + yn);   // the chunk gain from G = I
+                if (wv == 0) {
+                    const float nb[4] = {nka[0] + ndl[0], nka[1] + ndl[1], nka[2] + ndl[2], nka[3] + ndl[3]};
+                    v4s nbh, nbl;
+                    split4(nb, nbh, nbl);
+                    gT = mma3(zh, zl, nbh, nbl, diag4(decay, q, i16));   // (X_0 + Y_0)^T
                 } else {
-                    st4(Xt[wv] + i16 * 16 + 4 * q, xn);
-                    st4(Yt[wv] + i16 * 16 + 4 * q, yn);
+                    split4(nka, kah, kal);
+                    split4(ndl, dlh, dll);
+                    st4(Xt[wv] + i16 * 16 + 4 * q, mma3(kah, kal, zh, zl, diag4(decay, q, i16)));   // X_w
+                    st4(Yt[wv] + i16 * 16 + 4 * q, mma3(zh, zl, dlh, dll, v4f{0.f, 0.f, 0.f, 0.f}));  // Y_w^T
                 }
             }
         }
-        if constexpr (W == 1) {
-            const float4 x4 = ld4(Xt[0] + i16 * 16 + 4 * q), y4 = ld4(Yt[0] + i16 * 16 + 4 * q);
-            *reinterpret_cast<float4*>(Gt + i16 * 16 + 4 * q) =
-                make_float4(x4.x + y4.x, x4.y + y4.y, x4.z + y4.z, x4.w + y4.w);
+        __syncthreads();
+        // ---- composition on wave 0: G^T <- X_w^T G^T + Y_w^T, then G row-major ----
+        if (wv == 0) {
+            for (int w = 1; w < nblk; ++w) {
+                const float4 x4 = ld4(Xt[w] + i16 * 16 + 4 * q);   // A operand of X_w^T
+                const float4 y4 = ld4(Yt[w] + i16 * 16 + 4 * q);   // Y_w^T
+                const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+                v4s xh, xl, gh, gl;
+                split4(xv, xh, xl);
+                split4(gT, gh, gl);
+                gT = mma3(xh, xl, gh, gl, v4f{y4.x, y4.y, y4.z, y4.w});
+            }
+            st4(Gr + i16 * 16 + 4 * q, gT);   // lane (j, q) holds G[j][4q..4q+3]
         }
         __syncthreads();
         // ---- refresh: S <- S G, one 16-row block per wave ----
         for (int R = wv; R < 4; R += W) {
             const float4 s4 = ld4(St + (16 * R + i16) * D + 4 * q);   // A operand: row 16R + i16
-            const float4 g4 = ld4(Gt + i16 * 16 + 4 * q);             // B operand: column i16 of G
             const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
-            const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
+            float gv[4];                                              // B operand: column i16 of G
+#pragma unroll
+            for (int k = 0; k < 4; ++k) gv[k] = Gr[(4 * q + k) * 16 + i16];
             v4s sh, sl, gh, gl;
             split4(sv, sh, sl);
             split4(gv, gh, gl);

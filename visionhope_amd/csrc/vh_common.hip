@@ -95,6 +95,7 @@ OverrideSlot g_overrides[] = {
     {"scan_wide", [](const char* v) { return one_of(v, {"0", "1", "2", "4"}); }, ""},
     {"scan_tb", [](const char* v) { return one_of(v, {"1", "2"}); }, ""},
     {"scan_pack", scan_pack_ok, ""},
+    {"scan_utw", [](const char* v) { return one_of(v, {"0", "1"}); }, ""},
     {"pw_cfg", pw_cfg_ok, ""},
     {"pw_resident", [](const char* v) { return one_of(v, {"0", "2"}); }, ""},
     {"dw_tile", [](const char* v) { return one_of(v, {"0", "1", "2"}); }, ""},   // off / by shape / everywhere
