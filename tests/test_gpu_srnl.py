@@ -412,6 +412,40 @@ def test_spatial_few_lines_block_form(oracle, device, height, width, heads, kind
     assert_close(got, expected, FEW_LINES_TOL, f"few-line block form {height}x{width} heads={heads} {kind}")
 
 
+@pytest.mark.parametrize("height,width,heads", [(56, 56, 3), (28, 28, 2), (14, 14, 2), (9, 6, 3), (7, 40, 1),
+                                                (64, 64, 1), (65, 20, 1)])
+@pytest.mark.parametrize("kind", ["perturbed", "strong"])
+def test_spatial_head_dim32_block_form(oracle, device, height, width, heads, kind):
+    """head_dim 32, bf16: the block form with one workgroup per line and the chunk's blocks
+    over 1, 2 or 4 waves (chunks of up to 64 tokens; the 65-row map sends its column scans'
+    launch to the wide scan)."""
+    channels = heads * 32
+    mems = memories(4, heads, 32, kind=kind, seed=height * 5 + width)
+    x = randn(2, height, width, channels, seed=height + 111).bfloat16()
+    q = randn(2, height, width, channels, seed=width + 112).bfloat16()
+    skip = randn(channels, seed=113, scale=0.1)
+    wts = 1 + randn(4, channels, seed=114, scale=0.1)
+    got = _spatial(device, x, q, mems, skip, wts, (width, width, height, height))
+    expected = oracle.operator_forward(x.float().numpy(), q.float().numpy(), mems, skip.numpy(), wts.numpy(), 32)
+    assert_close(got, expected, FEW_LINES_TOL, f"d=32 block form {height}x{width} heads={heads} {kind}")
+
+
+@pytest.mark.parametrize("chunks", [(5, 16, 64, 3), (64, 33, 17, 48), (65, 7, 30, 12)])
+def test_sequence_head_dim32_block_form(oracle, device, chunks):
+    """Packed bf16 sequences with head_dim 32 (157 tokens, ragged last chunks) through the
+    block form; a chunk of 65 tokens sends the launch to the wide scan."""
+    from visionhope_amd.models.srnl_core.chunk import srnl_packed_forward
+
+    batch, directions, heads, length = 2, 4, 2, 157
+    mems = memories(directions, heads, 32, kind="strong", seed=sum(chunks) + 1)
+    x, q = _packed_case(batch, directions, heads, length, 32, torch.bfloat16, seed=117)
+    y = srnl_packed_forward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device),
+                            q.to(device), list(chunks), q_raw=True)
+    expected = oracle.sequence_forward(x.float().numpy(), q.float().numpy(), mems, list(chunks))
+    # bf16 output: one rounding of the result on top of the scan's error
+    assert_close(y.float().cpu().numpy(), expected, 5e-3, f"d=32 sequence {chunks}")
+
+
 @pytest.mark.parametrize("chunks", [(5, 16, 64, 3), (65, 128, 100, 17), (128, 128, 128, 128), (200, 40, 7, 33)])
 def test_sequence_few_lines_block_form(oracle, device, chunks):
     """Packed bf16 sequences (263 tokens, ragged last chunks) through the few-line block form;

@@ -19,7 +19,8 @@ PKG = CSRC.parent
 LIB_DIR = PKG / "_lib"
 LIB_NAME = "libvisionhope_hip.so"
 SOURCES = ("vh_common.hip", "srnl.hip", "elementwise.hip", "dwconv.hip", "pointwise.hip", "conv3x3.hip", "srnl_backward.hip",
-           "tail_backward.hip", "srnl_noalloc.hip", "srnl_wide.hip", "srnl_ut.hip", "srnl_utw.hip")
+           "tail_backward.hip", "srnl_noalloc.hip", "srnl_wide.hip", "srnl_ut.hip", "srnl_utw.hip",
+           "srnl_utw32.hip")
 ARCH = os.environ.get("VISIONHOPE_OFFLOAD_ARCH", "gfx950")
 
 # Packed-fp32 VALU ops are disabled for all device code (hipcc's host pass

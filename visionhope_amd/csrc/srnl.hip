@@ -1207,6 +1207,15 @@ void launch_scan(const ScanParams& sp, hipStream_t stream) {
             if (utw_on && scan_ut_enabled() && !Override("scan_wide").set() && launch_scan16_utw(sp, stream))
                 return;
         }
+        if constexpr (D == 32 && std::is_same<T, bf16_t>::value) {
+            // head_dim 32, bf16: the block form with one workgroup per line (srnl_utw32.hip)
+            // for chunks of up to 64 tokens, unless an override forces the wide scan
+            // (scan_wide), the stepped forms (scan_ut "0") or turns it off (scan_utw "0").
+            const Override utw("scan_utw");
+            const bool utw_on = !(utw.set() && utw.value[0] == '0');
+            if (utw_on && scan_ut_enabled() && !Override("scan_wide").set() && launch_scan32_utw(sp, stream))
+                return;
+        }
         if (waves > 0 && launch_scan_wide(sp, dtype_code_of<T>(), D, waves, token_blocks, stream)) return;
     }
     if constexpr (D == 16 && std::is_same<T, bf16_t>::value) {

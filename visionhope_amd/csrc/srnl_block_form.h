@@ -36,6 +36,17 @@ __device__ __forceinline__ v4f mma3(v4s ah, v4s al, v4s bh, v4s bl, v4f c) {
     return mfma_bf16(al, bh, c);
 }
 
+// The same over K = 32 held as two 16-wide K tiles (each operand: the lane's quads of tile 0
+// and tile 1): three 16x16x32 products, which take tile 0's quad and tile 1's quad of a lane
+// as eight consecutive k (the sum over k does not depend on their order).  One product size
+// per chain, as for mma3.
+__device__ __forceinline__ v4f mma3k2(const v4s (&ah)[2], const v4s (&al)[2], const v4s (&bh)[2], const v4s (&bl)[2],
+                                      v4f c) {
+    c = mfma_bf16x2(ah[0], ah[1], bh[0], bh[1], c);
+    c = mfma_bf16x2(ah[0], ah[1], bl[0], bl[1], c);
+    return mfma_bf16x2(al[0], al[1], bh[0], bh[1], c);
+}
+
 // d I in the accumulator layout of lane 16 q + i (entries: rows 4q..4q+3 of column i).
 __device__ __forceinline__ v4f diag4(float d, int q, int i) {
     v4f o;

@@ -366,6 +366,9 @@ bool launch_scan16_ut(const ScanParams& sp, hipStream_t stream);
 // (srnl_utw.hip): head_dim 16, bf16 activations, chunks of at most 128 tokens.  Returns
 // false (nothing launched) when the chunks or the input alignment do not allow it.
 bool launch_scan16_utw(const ScanParams& sp, hipStream_t stream);
+// head_dim 32, bf16 activations, chunks of at most 64 tokens (srnl_utw32.hip); false when
+// the call does not qualify.
+bool launch_scan32_utw(const ScanParams& sp, hipStream_t stream);
 bool launch_scan_wide(const ScanParams& sp, int io_dtype, int head_dim, int waves, int token_blocks,
                       hipStream_t stream);
 

@@ -23,8 +23,8 @@ from ..models.srnl import SRNL
 from ..utils.grn import GlobalResponseNorm
 
 # Kernel families of libvisionhope_hip.so: one scan and one readout per SRNL call.
-SCAN_KERNELS = ("srnl_scan16_ut_kernel", "srnl_scan16_utw_kernel", "srnl_scan16_kernel", "srnl_scanw_kernel",
-                "srnl_scan_kernel")
+SCAN_KERNELS = ("srnl_scan16_ut_kernel", "srnl_scan16_utw_kernel", "srnl_scan32_utw_kernel", "srnl_scan16_kernel",
+                "srnl_scanw_kernel", "srnl_scan_kernel")
 READOUT_KERNELS = ("srnl_readout_tile_kernel", "srnl_fuse_readout_kernel", "srnl_packed_readout_kernel")
 
 
