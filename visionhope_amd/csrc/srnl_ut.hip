@@ -55,8 +55,11 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
     __shared__ __align__(16) float kT[D * DKS];     // normalised keys [feature][slot]
     __shared__ __align__(16) float ndT[D * DKS];    // v - k [feature][slot]
     __shared__ __align__(16) float tk[4 * TT];      // per slot: rho, kappa, -a_{t-1}, w
-    __shared__ __align__(16) float Lc[TCW * 256];   // per tile: L[s][t] at [t][s]
-    __shared__ __align__(16) float Zs[TCW * 256];   // per tile: Z[s][f] at [f][s]
+    // L and Z rows are padded to LS = 20 floats, so that 16-byte accesses of 16 lanes down a
+    // column of rows fall in different LDS banks.
+    constexpr int LS = 20;
+    __shared__ __align__(16) float Lc[TCW * 16 * LS];   // per tile: L[s][t] at [t][s]
+    __shared__ __align__(16) float Zs[TCW * 16 * LS];   // per tile: Z[s][f] at [f][s]
     __shared__ __align__(16) float gr[NL * 2 * D];  // per line: e, a (gate operand rows)
 
     const int64_t groups = p.B * p.R * p.heads / NL;
@@ -274,7 +277,7 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
                 float lv[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) lv[j] = (4 * q + j < i16) ? P[j] : 0.f;
-                *reinterpret_cast<float4*>(Lc + (16 * tc + i16) * 16 + 4 * q) = make_float4(lv[0], lv[1], lv[2], lv[3]);
+                *reinterpret_cast<float4*>(Lc + (16 * tc + i16) * LS + 4 * q) = make_float4(lv[0], lv[1], lv[2], lv[3]);
             }
             __syncthreads();
             // ---- Z = (I + L)^-1 W K^T: lane 16 b + f solves column f of tile b from the last
@@ -296,7 +299,7 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
                     for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
                         for (int s0 = 0; s0 < v0 + dv; s0 += 4) {
-                            const float4 l4 = ld4(Lc + (16 * q + v0 + dv) * 16 + s0);
+                            const float4 l4 = ld4(Lc + (16 * q + v0 + dv) * LS + s0);
                             buf[dv][s0] = l4.x; buf[dv][s0 + 1] = l4.y; buf[dv][s0 + 2] = l4.z; buf[dv][s0 + 3] = l4.w;
                         }
                 };
@@ -322,7 +325,7 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
                 __builtin_amdgcn_sched_barrier(0);
                 solve_group(4, lA);
                 solve_group(0, lB);
-                float* dst = Zs + (16 * q + i16) * 16;
+                float* dst = Zs + (16 * q + i16) * LS;
 #pragma unroll
                 for (int s = 0; s < 16; s += 4)
                     *reinterpret_cast<float4*>(dst + s) = make_float4(zc[s], zc[s + 1], zc[s + 2], zc[s + 3]);
@@ -349,7 +352,7 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
                     const int tc = lam * TPL + bt;
                     // D(Z): lane 16 q + f holds Z[4q + j][f]; feature-major operands of the
                     // block (slot 4q + j, feature f): -(k a_{t-1}) and -delta
-                    const float4 z4 = ld4(Zs + (16 * tc + i16) * 16 + 4 * q);
+                    const float4 z4 = ld4(Zs + (16 * tc + i16) * LS + 4 * q);
                     const float4 k4 = ld4(kT + i16 * DKS + 16 * tc + 4 * q);
                     const float4 d4 = ld4(ndT + i16 * DKS + 16 * tc + 4 * q);
                     const float4 a4 = ld4(tk + 2 * TT + 16 * tc + 4 * q);

@@ -19,8 +19,8 @@
 //     the waves by 16-row blocks.
 //
 // Matrices pass between waves in LDS in the accumulator layout of lane 16 q + j (rows
-// 4q..4q+3 of column j at [16 j + 4 q ...]): X_w is then the A operand of X_w^T and Y_w^T
-// the addend, one 16-byte load each.  Slots past the chunk act as the identity.
+// 4q..4q+3 of column j), read back by the lane that wrote them: X_w is then the A operand of
+// X_w^T and Y_w^T the addend, one 16-byte load each.  Slots past the chunk act as the identity.
 #include "srnl_block_form.h"
 
 namespace vh {
@@ -43,16 +43,19 @@ __device__ __forceinline__ void st4(float* p, const v4f& v) {
 
 template <int W, bool SPATIAL>
 __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParams p) {
-    constexpr int D = 16, DKS = 20;   // padded slot stride of the key tables
+    // Row strides are padded to 20 floats (keys, L, Z, state, G) so that the 16-byte loads of
+    // 16 lanes down a column of rows fall in different LDS banks; the hand-over maps are read
+    // back by the lane that wrote them, so they are stored lane-major.
+    constexpr int D = 16, DKS = 20, TS = 20, SD = 20;
     __shared__ __align__(16) float kT[W][D * DKS];    // normalised keys [feature][slot]
     __shared__ __align__(16) float ndT[W][D * DKS];   // v - k [feature][slot]
     __shared__ __align__(16) float tk[W][64];         // per slot: rho, kappa, -a_{t-1}, w
-    __shared__ __align__(16) float Lc[W][256];        // L[s][t] at [t][s]
-    __shared__ __align__(16) float Zs[W][256];        // Z[s][f] at [f][s]
-    __shared__ __align__(16) float Xt[W][256];        // X_w, accumulator layout
-    __shared__ __align__(16) float Yt[W][256];        // Y_w^T, accumulator layout
-    __shared__ __align__(16) float St[64 * D];        // state rows, row-major
-    __shared__ __align__(16) float Gr[256];           // chunk gain G, row-major
+    __shared__ __align__(16) float Lc[W][16 * TS];    // L[s][t] at [t][s]
+    __shared__ __align__(16) float Zs[W][16 * TS];    // Z[s][f] at [f][s]
+    __shared__ __align__(16) float Xt[W][256];        // X_w, accumulator layout, lane-major
+    __shared__ __align__(16) float Yt[W][256];        // Y_w^T, accumulator layout, lane-major
+    __shared__ __align__(16) float St[64 * SD];       // state rows
+    __shared__ __align__(16) float Gr[16 * SD];       // chunk gain G, by rows
 
     const int tid = static_cast<int>(threadIdx.x);
     const int wv = tid >> 6, lane = tid & 63, i16 = lane & 15, q = lane >> 4;
@@ -72,7 +75,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
         else if (row < 48) v = ld4(p.Mk + sidx * D * D + (row - 32) * D + c4);
         else if (row == 48) v = ld4(p.Me + sidx * D + c4);
         else if (row == 49) v = ld4(p.Ma + sidx * D + c4);
-        *reinterpret_cast<float4*>(St + row * D + c4) = v;
+        *reinterpret_cast<float4*>(St + row * SD + c4) = v;
     }
 
     const int C = chunk_of(p.chunk, r);
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
     for (int64_t c = 0; c < nc; ++c) {
         if (wv == 0)   // chunk-start M_m for the readout
             store_state4(p.states + (line * p.max_chunks + c) * D * D + i16 * D + 4 * q,
-                         ld4(St + i16 * D + 4 * q), p.split_states);
+                         ld4(St + i16 * SD + 4 * q), p.split_states);
         if (c == nc - 1) break;
 
         v4f gT = {0.f, 0.f, 0.f, 0.f};   // wave 0: G^T of the blocks composed so far
@@ -122,9 +125,9 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
             // ---- token phase: [M_k; M_v] x and (x.e, x.a) on the matrix cores ----
             v4s akh, akl, avh, avl, gah, gal;
             {
-                const float4 mk = ld4(St + (32 + i16) * D + 4 * q);
-                const float4 mv = ld4(St + (16 + i16) * D + 4 * q);
-                const float4 g4 = ld4(St + (48 + (i16 & 1)) * D + 4 * q);
+                const float4 mk = ld4(St + (32 + i16) * SD + 4 * q);
+                const float4 mv = ld4(St + (16 + i16) * SD + 4 * q);
+                const float4 g4 = ld4(St + (48 + (i16 & 1)) * SD + 4 * q);
                 const bool on = (i16 & 3) < 2;   // operand rows 4q' + 0 / 4q' + 1: e / a, others zero
                 const float ak[4] = {mk.x, mk.y, mk.z, mk.w};
                 const float av[4] = {mv.x, mv.y, mv.z, mv.w};
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
                 float lv[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) lv[j] = (4 * q + j < i16) ? P[j] : 0.f;
-                *reinterpret_cast<float4*>(Lcw + i16 * 16 + 4 * q) = make_float4(lv[0], lv[1], lv[2], lv[3]);
+                *reinterpret_cast<float4*>(Lcw + i16 * TS + 4 * q) = make_float4(lv[0], lv[1], lv[2], lv[3]);
             }
             wave_sync();
             // ---- Z = (I + L)^-1 W K^T: lane f (of the first 16) solves column f from the last
@@ -213,7 +216,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
                     for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
                         for (int s0 = 0; s0 < v0 + dv; s0 += 4) {
-                            const float4 l4 = ld4(Lcw + (v0 + dv) * 16 + s0);
+                            const float4 l4 = ld4(Lcw + (v0 + dv) * TS + s0);
                             buf[dv][s0] = l4.x; buf[dv][s0 + 1] = l4.y; buf[dv][s0 + 2] = l4.z; buf[dv][s0 + 3] = l4.w;
                         }
                 };
@@ -236,14 +239,14 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
                 solve_group(0, lB);
 #pragma unroll
                 for (int s = 0; s < 16; s += 4)
-                    *reinterpret_cast<float4*>(Zsw + i16 * 16 + s) = make_float4(zc[s], zc[s + 1], zc[s + 2], zc[s + 3]);
+                    *reinterpret_cast<float4*>(Zsw + i16 * TS + s) = make_float4(zc[s], zc[s + 1], zc[s + 2], zc[s + 3]);
             }
             wave_sync();
             // ---- the block's map: X = a_15 I - (K D_a) Z, Y = -Delta Z; wave 0 (the first
             //      block, entered with G = I) keeps (X_0 + Y_0)^T, the others hand over X_w
             //      and Y_w^T (accumulator layouts) ----
             {
-                const float4 z4f = ld4(Zsw + i16 * 16 + 4 * q);
+                const float4 z4f = ld4(Zsw + i16 * TS + 4 * q);
                 const float4 k4 = ld4(kTw + i16 * DKS + 4 * q);
                 const float4 d4 = ld4(ndTw + i16 * DKS + 4 * q);
                 const float4 a4 = ld4(tkw + 32 + 4 * q);
@@ -260,8 +263,8 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
                 } else {
                     split4(nka, kah, kal);
                     split4(ndl, dlh, dll);
-                    st4(Xt[wv] + i16 * 16 + 4 * q, mma3(kah, kal, zh, zl, diag4(decay, q, i16)));   // X_w
-                    st4(Yt[wv] + i16 * 16 + 4 * q, mma3(zh, zl, dlh, dll, v4f{0.f, 0.f, 0.f, 0.f}));  // Y_w^T
+                    st4(Xt[wv] + 4 * lane, mma3(kah, kal, zh, zl, diag4(decay, q, i16)));   // X_w
+                    st4(Yt[wv] + 4 * lane, mma3(zh, zl, dlh, dll, v4f{0.f, 0.f, 0.f, 0.f}));  // Y_w^T
                 }
             }
         }
@@ -269,30 +272,30 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
         // ---- composition on wave 0: G^T <- X_w^T G^T + Y_w^T, then G row-major ----
         if (wv == 0) {
             for (int w = 1; w < nblk; ++w) {
-                const float4 x4 = ld4(Xt[w] + i16 * 16 + 4 * q);   // A operand of X_w^T
-                const float4 y4 = ld4(Yt[w] + i16 * 16 + 4 * q);   // Y_w^T
+                const float4 x4 = ld4(Xt[w] + 4 * lane);   // A operand of X_w^T
+                const float4 y4 = ld4(Yt[w] + 4 * lane);   // Y_w^T
                 const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
                 v4s xh, xl, gh, gl;
                 split4(xv, xh, xl);
                 split4(gT, gh, gl);
                 gT = mma3(xh, xl, gh, gl, v4f{y4.x, y4.y, y4.z, y4.w});
             }
-            st4(Gr + i16 * 16 + 4 * q, gT);   // lane (j, q) holds G[j][4q..4q+3]
+            st4(Gr + i16 * SD + 4 * q, gT);   // lane (j, q) holds G[j][4q..4q+3]
         }
         __syncthreads();
         // ---- refresh: S <- S G, one 16-row block per wave ----
         for (int R = wv; R < 4; R += W) {
-            const float4 s4 = ld4(St + (16 * R + i16) * D + 4 * q);   // A operand: row 16R + i16
+            const float4 s4 = ld4(St + (16 * R + i16) * SD + 4 * q);   // A operand: row 16R + i16
             const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
             float gv[4];                                              // B operand: column i16 of G
 #pragma unroll
-            for (int k = 0; k < 4; ++k) gv[k] = Gr[(4 * q + k) * 16 + i16];
+            for (int k = 0; k < 4; ++k) gv[k] = Gr[(4 * q + k) * SD + i16];
             v4s sh, sl, gh, gl;
             split4(sv, sh, sl);
             split4(gv, gh, gl);
             const v4f sn = mma3(sh, sl, gh, gl, v4f{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int k = 0; k < 4; ++k) St[(16 * R + 4 * q + k) * D + i16] = sn[k];
+            for (int k = 0; k < 4; ++k) St[(16 * R + 4 * q + k) * SD + i16] = sn[k];
         }
         __syncthreads();
     }
