@@ -911,16 +911,26 @@ __device__ __forceinline__ float xraw_sumsq(const XRaw<T, D>& r) {
 // y = M q~ for 16 pixels on the matrix cores: lane l = 16 g + n gives M row n (of the
 // 16-channel half) and pixel n's query over the K-range [g D/4, (g+1) D/4), and receives
 // channels 4g..4g+3 of the half for pixel n.  bf16: M as hi + lo, q exact.
-// SPLIT (bf16, D = 16): m holds the bits of the stored bf16 hi[4], lo[4] pair.
+// SPLIT (bf16, D = 16 or 32): m holds the bits of the stored bf16 hi[4], lo[4] pairs (one
+// pair per 4 entries).
 template <typename T, int D, bool SPLIT = false>
 __device__ __forceinline__ v4f readout_mfma(const float (&m)[D / 4], const XRaw<T, D>& qr) {
     v4f y = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (SPLIT) {
-        static_assert(std::is_same<T, bf16_t>::value && D == 16, "split states: bf16, head_dim 16");
+    if constexpr (SPLIT && D == 16) {
+        static_assert(std::is_same<T, bf16_t>::value, "split states: bf16");
         const v4s hi = __builtin_bit_cast(v4s, make_uint2(__float_as_uint(m[0]), __float_as_uint(m[1])));
         const v4s lo = __builtin_bit_cast(v4s, make_uint2(__float_as_uint(m[2]), __float_as_uint(m[3])));
         const v4s qs = bf16x4_bits(qr.v);
         y = mfma_bf16x2(hi, lo, qs, qs, y);   // (hi + lo) q in one 16x16x32 product
+    } else if constexpr (SPLIT) {
+        static_assert(std::is_same<T, bf16_t>::value && D == 32, "split states: bf16, head_dim 16 or 32");
+        // entries 8g..8g+3 then 8g+4..8g+7: hi of both groups, then lo of both
+        const v8bf hi = __builtin_bit_cast(v8bf, make_uint4(__float_as_uint(m[0]), __float_as_uint(m[1]),
+                                                            __float_as_uint(m[4]), __float_as_uint(m[5])));
+        const v8bf lo = __builtin_bit_cast(v8bf, make_uint4(__float_as_uint(m[2]), __float_as_uint(m[3]),
+                                                            __float_as_uint(m[6]), __float_as_uint(m[7])));
+        const auto qs = BfOp<32>::exact(qr);
+        y = BfOp<32>::mma(lo, qs, BfOp<32>::mma(hi, qs, y));   // two 16x16x32 products
     } else if constexpr (std::is_same<T, bf16_t>::value) {
         using Bf = BfOp<D>;
         typename Bf::type hi, lo;
@@ -1172,8 +1182,8 @@ int wide_waves(int64_t lines, int d) {
 void scan16_ut_packing(int64_t lines, int64_t heads, int* nl, int* tcw);
 
 // Format of the chunk-start states in the workspace.  Spatial scans of bf16 maps with
-// head_dim 16 store them split into bf16 hi + lo pairs (split_state_at), the operands of
-// the matrix-core readout; every other scan stores FP32.  The format is a function of
+// head_dim 16 or 32 store them split into bf16 hi + lo pairs (split_state_at), the operands
+// of the matrix-core readout; every other scan stores FP32.  The format is a function of
 // these arguments alone: every scan kernel that can run for such a call (block form,
 // stepped, wide, under any dispatch override) stores it, so the readout, which decides
 // it from the same arguments, always decodes what the scan wrote.
@@ -1182,7 +1192,7 @@ bool scan_ut_enabled() {
     return !(ut.set() && ut.value[0] == '0');
 }
 bool state_split_bf16(int io_dtype, int d, bool spatial) {
-    return io_dtype == VH_DTYPE_BF16 && d == 16 && spatial;
+    return io_dtype == VH_DTYPE_BF16 && (d == 16 || d == 32) && spatial;
 }
 
 template <int D, typename T>
@@ -1413,7 +1423,7 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
                             reinterpret_cast<uintptr_t>(aux) | reinterpret_cast<uintptr_t>(skip) |
                             reinterpret_cast<uintptr_t>(wgt);
     const bool out_f32 = out_dtype == VH_DTYPE_F32;
-    VH_REQUIRE(fp.split_states == ((io_dtype == VH_DTYPE_BF16 && d == 16 && !per_direction) ? 1 : 0), VH_ERR_ARG,
+    VH_REQUIRE(fp.split_states == ((io_dtype == VH_DTYPE_BF16 && (d == 16 || d == 32) && !per_direction) ? 1 : 0), VH_ERR_ARG,
                "SRNL readout: state format does not match the scan's");
     if ((d == 16 || (d == 32 && io_dtype != VH_DTYPE_F16)) && !per_direction && sp.chunk[0] == W &&
         sp.chunk[1] == W && sp.chunk[2] == H && sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0 &&
@@ -1424,8 +1434,8 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
         auto go = [&](auto tv, auto dc) {
             using T = decltype(tv);
             constexpr int DD = decltype(dc)::value;
-            // bf16 maps with head_dim 16 always carry split states (state_split_bf16)
-            constexpr bool SPLIT = std::is_same<T, bf16_t>::value && DD == 16;
+            // bf16 maps always carry split states here (state_split_bf16)
+            constexpr bool SPLIT = std::is_same<T, bf16_t>::value;
             if (out_f32)
                 hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD, SPLIT>), dim3(static_cast<unsigned>(n_tiles)),
                                    dim3(256), 0, stream, fp, tiles_h, tiles_w);

@@ -19,7 +19,8 @@
 // j), which the receiving lane reads back as it was written.  The accumulator layout of a
 // tile C is the A-operand layout of C^T and the B-operand layout of C, so X_w's tile (K, I)
 // is the A operand of (X_w^T)[I][K].  Slots past the chunk act as the identity.  The
-// chunk-start M_m goes to the workspace in FP32 for the readout.
+// chunk-start M_m goes to the workspace for the readout, split into bf16 hi + lo pairs for
+// spatial maps (p.split_states).
 #include "srnl_block_form.h"
 
 namespace vh {
@@ -122,12 +123,13 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
     if (wv < nblk && nc > 1) load_x(0, xr, xok);
     __syncthreads();
     for (int64_t c = 0; c < nc; ++c) {
-        // chunk-start M_m for the readout (FP32), a fixed number of stores per thread
+        // chunk-start M_m for the readout (FP32 or split, p.split_states), a fixed number of
+        // stores per thread
 #pragma unroll
         for (int k = 0; k < D * D / 4 / (64 * W); ++k) {
             const int idx = tid + 64 * W * k;
-            *reinterpret_cast<float4*>(p.states + (line * p.max_chunks + c) * D * D + idx * 4) =
-                ld4(St + (idx >> 3) * SD + (idx & 7) * 4);
+            store_state4(p.states + (line * p.max_chunks + c) * D * D + idx * 4, ld4(St + (idx >> 3) * SD + (idx & 7) * 4),
+                         p.split_states);
         }
         if (c == nc - 1) break;
 
