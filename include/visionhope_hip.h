@@ -70,9 +70,10 @@ const char* vh_last_error(void);
  *   scan_wide        "0"|"1"|"2"|"4"  SRNL: waves per line of the wide scan (0: none)
  *   scan_tb          "1" | "2"        wide scan: row split / token blocks
  *   scan_pack        "<L>x<T>"        head_dim-16 scans: lines and 16-slot tiles per wave
- *   scan_utw         "0" | "1"        bf16 head_dim 16: the block form with a chunk's blocks
- *                                     over the waves of one workgroup per line, never /
- *                                     whenever the chunks allow (default: below 1024 lines)
+ *   scan_utw         "0" | "1"        bf16 head_dim 16 and 32: the block form with a chunk's
+ *                                     blocks over the waves of one workgroup per line, never /
+ *                                     whenever the chunks allow (default: head_dim 16 below
+ *                                     1024 lines; head_dim 32 always, chunks up to 64)
  *   pw_cfg, pw_resident               1x1 convolution kernel variants
  *   dw_tile, dw_tile_cs, dw_tile_p, dw_launch_bytes   depthwise kernel variants
  *   ln_stage         "0" | "1"        LayerNorm staged stores
