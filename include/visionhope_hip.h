@@ -352,7 +352,7 @@ int vh_dwconv2d_gelu_grn_forward(
 /* 1x1 convolution on channels-last bf16 maps as a GEMM on the matrix cores:
  * out [M, N] = epi(x' [M, K] . weight^T + bias) with weight [N, K] bf16 (the 1x1
  * kernel as stored, cast to bf16 as autocast casts it), bias [N] fp32 (or NULL),
- * M = B*H*W pixels, K % 32 == 0, N = 32, 64 or a multiple of 128,
+ * M = B*H*W pixels, K % 32 == 0, N % 32 == 0,
  * 16-byte aligned tensors.  The linear result is rounded to bf16 first, as the
  * reference's autocast linear output is; then
  *   epilogue 0: out = that value                              (proj_in, local_gate, W_q, proj_out)

@@ -151,7 +151,7 @@ def test_pointwise_conv_rejects_bad_arguments(lib):
 
     assert call(dtype=hip.VH_DTYPE_F32) == hip.VH_ERR_DTYPE
     assert call(k=48) == hip.VH_ERR_SHAPE                # K % 32 != 0
-    assert call(n=96) == hip.VH_ERR_SHAPE                # not 32, 64 or a multiple of 128
+    assert call(n=48) == hip.VH_ERR_SHAPE                # N % 32 != 0
     assert call(n=48) == hip.VH_ERR_SHAPE
     assert call(m=0) == hip.VH_ERR_SHAPE
     assert call(epilogue=4) == hip.VH_ERR_ARG

@@ -31,7 +31,11 @@ def _linear_ref(x, module):
 
 @pytest.mark.parametrize("m", [1, 37, 256, 1000])
 @pytest.mark.parametrize("k,n", [(64, 32), (32, 32), (128, 64), (96, 128), (256, 128), (64, 256),
-                                 (1024, 256), (256, 1024), (512, 384), (2048, 512)])
+                                 (1024, 256), (256, 1024), (512, 384), (2048, 512),
+                                 # widths that are multiples of 32 or 64 but not of 128 (Base: 96, 192,
+                                 # 224, 320, 448), shallow and deep
+                                 (192, 96), (384, 96), (96, 96), (96, 192), (768, 192), (448, 224),
+                                 (224, 224), (224, 448), (1792, 448), (640, 320), (320, 320)])
 def test_pointwise_bias(device, m, k, n):
     from visionhope_amd.utils import pointwise
 
@@ -88,7 +92,8 @@ def test_pointwise_resident_weights_match_tiled_kernel(device, dispatch, k, n, m
     assert_close(got[rows].double().cpu().numpy(), ref.double().numpy(), 5e-3, f"resident K={k} N={n} M={m}")
 
 
-@pytest.mark.parametrize("k,n", [(256, 64), (1024, 256), (64, 32), (512, 128), (128, 512)])
+@pytest.mark.parametrize("k,n", [(256, 64), (1024, 256), (64, 32), (512, 128), (128, 512), (384, 96), (768, 192),
+                                 (1792, 448)])
 @pytest.mark.parametrize("with_grn", [False, True])
 @pytest.mark.parametrize("hw", [(5, 7), (16, 20)])
 def test_pointwise_residual_and_grn(device, k, n, with_grn, hw):
@@ -107,9 +112,11 @@ def test_pointwise_residual_and_grn(device, k, n, with_grn, hw):
         scale = 1 + randn(images, k, seed=7, scale=0.3)
         beta = randn(k, seed=8, scale=0.2)
         grn = (scale.to(device), beta.to(device))
-        # The kernel computes x * scale + beta in fp32 (one fused multiply-add); compare
-        # against that rounding, not the fp64 one, so the operands agree exactly.
-        operand = _bf16(torch.addcmul(beta.float(), x.float(), scale.float()[:, None, None, :]))
+        # The kernel computes x * scale + beta in fp32 with one fused multiply-add; compare
+        # against that single rounding (the product is exact in float64), not against
+        # torch.addcmul on the CPU, which fuses or not depending on the host's vector path.
+        fused = x.double() * scale.double()[:, None, None, :] + beta.double()
+        operand = _bf16(fused.float())
     got = pointwise.pointwise_conv(x.to(device), lin.to(device), pointwise.EPI_ADD, residual=r.to(device), grn=grn)
     expected = _bf16(r.double() + _linear_ref(operand, lin.cpu()).double())
     assert_close(got.double().cpu().numpy(), expected.double().numpy(), 5e-3, f"pw add grn={with_grn}")
@@ -134,7 +141,7 @@ def test_pointwise_rejects_unsupported(device):
     with pytest.raises(ValueError):
         pointwise.pointwise_conv(_bf16(randn(4, 48)).to(device), nn.Linear(48, 64).to(device))
     with pytest.raises(ValueError):
-        pointwise.pointwise_conv(_bf16(randn(4, 64)).to(device), nn.Linear(64, 96).to(device))
+        pointwise.pointwise_conv(_bf16(randn(4, 64)).to(device), nn.Linear(64, 48).to(device))
     with pytest.raises(ValueError):
         pointwise.pointwise_conv(randn(4, 64).to(device), nn.Linear(64, 64).to(device))   # fp32 x
 
@@ -152,3 +159,18 @@ def test_grn_scale_matches_grn(oracle, device, dtype):
     y = x.float() * scale.cpu()[:, :, None, None] + beta[None, :, None, None]
     expected = oracle.grn(x.float().numpy(), gamma.numpy(), beta.numpy())
     assert_close(y.numpy(), expected, 2e-5, "GRN scale")
+
+
+@pytest.mark.parametrize("batch,channels,hw", [(8, 384, 64), (2, 1792, 32), (63, 64, 12), (64, 64, 12), (1, 2048, 9)])
+def test_grn_scale_few_and_many_images(oracle, device, batch, channels, hw):
+    """The statistics of few images (fewer than 64: slab sums spread over channel blocks,
+    up to 256 slabs per image) and of many (one workgroup per image) against the oracle."""
+    from visionhope_amd.utils.grn_cuda import grn_scale
+
+    x = randn(batch, channels, hw, hw, seed=13).bfloat16().contiguous(memory_format=torch.channels_last)
+    gamma = randn(channels, seed=14, scale=0.2)
+    beta = randn(channels, seed=15, scale=0.2)
+    scale = grn_scale(x.to(device), gamma.to(device), 1e-6)
+    y = x.float() * scale.cpu()[:, :, None, None] + beta[None, :, None, None]
+    expected = oracle.grn(x.float().numpy(), gamma.numpy(), beta.numpy())
+    assert_close(y.numpy(), expected, 2e-5, f"GRN scale B={batch} C={channels} {hw}x{hw}")

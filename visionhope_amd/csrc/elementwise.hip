@@ -456,6 +456,66 @@ __global__ __launch_bounds__(256) void grn_gx_kernel(const float* __restrict__ p
         gx[static_cast<int64_t>(b) * C + c] = sqrtf((part[0][cl] + part[1][cl]) + (part[2][cl] + part[3][cl]));
 }
 
+// The statistics of grn_finalize_kernel for few images with many slabs (B = 8 at 512^2:
+// 256 slabs per image), where one workgroup per image leaves most CUs idle and waits on
+// its loads.  Step 1, gx: a workgroup takes 64 channels of one image, thread j of a channel
+// sums slabs j, j + 4, ... into eight accumulators (eight loads in flight), and the four
+// sums meet in LDS in a fixed order.  Grid: channel blocks x images.
+__global__ __launch_bounds__(256) void grn_gx8_kernel(const float* __restrict__ partial, float* __restrict__ gx, int C,
+                                                     int nslab) {
+    __shared__ float part[4][64];
+    const int cl = threadIdx.x & 63, j = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl, b = blockIdx.y;
+    float a = 0.f;
+    if (c < C) {
+        const float* pc = partial + static_cast<int64_t>(b) * nslab * C + c;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        int s = j;
+        for (; s + 28 < nslab; s += 32) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = pc[static_cast<int64_t>(s + 4 * u) * C];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc[u] += v[u];
+        }
+        for (; s < nslab; s += 4) acc[0] += pc[static_cast<int64_t>(s) * C];
+        a = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    }
+    part[j][cl] = a;
+    __syncthreads();
+    if (j == 0 && c < C)
+        gx[static_cast<int64_t>(b) * C + c] = sqrtf((part[0][cl] + part[1][cl]) + (part[2][cl] + part[3][cl]));
+}
+
+// Step 2: inv_den[b] = 1 / (mean_c gx[b, c] + eps) and, when asked, the apply factor
+// scale[b, c] = 1 + gamma[c] gx[b, c] inv_den[b] (the fp32 operations of grn_finalize_kernel).
+// One workgroup per image.
+__global__ __launch_bounds__(256) void grn_image_scale_kernel(const float* __restrict__ gx, float* __restrict__ inv_den,
+                                                             int64_t C, float eps, const float* __restrict__ gamma,
+                                                             float* __restrict__ scale) {
+    __shared__ float wsum[4];
+    __shared__ float inv_sh;
+    const int64_t b = blockIdx.x;
+    const int t = threadIdx.x;
+    float local = 0.f;
+    for (int64_t c = t; c < C; c += 256) local += gx[b * C + c];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off);
+    if ((t & 63) == 0) wsum[t >> 6] = local;
+    __syncthreads();
+    if (t == 0) {
+        const float total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+        const float inv = 1.f / (total / static_cast<float>(C) + eps);
+        inv_den[b] = inv;
+        inv_sh = inv;
+    }
+    if (scale) {
+        __syncthreads();
+        const float inv = inv_sh;
+        for (int64_t c = t; c < C; c += 256) scale[b * C + c] = 1.f + gamma[c] * (gx[b * C + c] * inv);
+    }
+}
+
 // Apply for wide maps: every workgroup of image b forms inv_den from gx (fixed order, so all
 // workgroups agree bit for bit) and workgroup 0 stores it.
 template <typename T, typename TO>
@@ -1505,8 +1565,16 @@ int vh_grn_scale_forward(const void* x, int32_t io_dtype, const float* gamma, fl
         hipLaunchKernelGGL((grn_partial8_kernel<T>), dim3(static_cast<unsigned>(vslab), static_cast<unsigned>(B)),
                            dim3(G * R), red, s, static_cast<const T*>(x), partial, static_cast<int>(C),
                            static_cast<int>(S), rows, vslab);
-        hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s, partial, gx,
-                           inv_den, C, static_cast<int64_t>(vslab), eps, gamma, scale);
+        if (B >= 64) {
+            hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s, partial,
+                               gx, inv_den, C, static_cast<int64_t>(vslab), eps, gamma, scale);
+        } else {
+            // few images: the slab sums spread over channel blocks x images (grn_gx8_kernel)
+            hipLaunchKernelGGL(grn_gx8_kernel, dim3(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>(B)),
+                               dim3(256), 0, s, partial, gx, static_cast<int>(C), vslab);
+            hipLaunchKernelGGL(grn_image_scale_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, gx, inv_den, C,
+                               eps, gamma, scale);
+        }
     });
     if (rc) return rc;
     return check_launch("grn statistics kernels");

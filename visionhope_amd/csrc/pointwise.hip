@@ -628,25 +628,29 @@ int launch_pw(const PwParams& p, hipStream_t s) {
             return go(pointwise_gemm_kernel<BM_, BN_, WGM_, BK_, EPI, 2, OCC_>, BM_, BN_);
         return go(pointwise_gemm_kernel<BM_, BN_, WGM_, BK_, EPI, PRO, OCC_>, BM_, BN_);
     };
-    if (bk == 0 && p.K % 64 == 0 && p.K >= 128 && (p.N == 64 || (p.N % 128 == 0 && (p.K >= 256 || p.N <= 256)))) {
+    if (bk == 0 && p.K % 64 == 0 && p.K >= 128 &&
+        ((p.N % 128 != 0 && p.N % 64 == 0) || (p.N % 128 == 0 && (p.K >= 256 || p.N <= 256)))) {
         // Deep products: the LDS-copy ring (measured on MI355X at the Tiny shapes,
         // B = 128: 5-40 % faster than the register-staged tiles from K = 128 up, except
         // K = 128 with N = 512, where the wide output favours the 4-resident tiles).
-        const bool stage_grn = PRO_ON && p.rows_per_image.d >= (p.N == 64 ? 128u : 64u);
+        // Widths that are multiples of 64 but not of 128 take 64-channel tiles.
+        const bool n64 = p.N % 128 != 0;
+        const bool stage_grn = PRO_ON && p.rows_per_image.d >= (n64 ? 128u : 64u);
         if (!PRO_ON || stage_grn) {
-            if (p.N == 64) return go(pointwise_dma_kernel<128, 64, 2, EPI, PRO_ON, 3>, 128, 64);
+            if (n64) return go(pointwise_dma_kernel<128, 64, 2, EPI, PRO_ON, 3>, 128, 64);
             if (p.K >= 1024) return go(pointwise_dma_kernel<64, 128, 2, EPI, PRO_ON, 2>, 64, 128);
             return go(pointwise_dma_kernel<64, 128, 2, EPI, PRO_ON, 3>, 64, 128);
         }
     }
     if (bk == 0) {
         // Shorter products: register-staged tiles.  They want small tiles and many
-        // resident blocks (more k tiles in flight per CU).
+        // resident blocks (more k tiles in flight per CU).  Widths that are not multiples
+        // of 128 take 32- or 64-channel tiles.
         using std::integral_constant;
-        if (p.N == 32)
+        if (p.N % 64 != 0)
             return tiled(integral_constant<int, 256>{}, integral_constant<int, 32>{}, integral_constant<int, 4>{},
                          integral_constant<int, 32>{}, integral_constant<int, 1>{});
-        if (p.N == 64)
+        if (p.N % 128 != 0)
             return tiled(integral_constant<int, 128>{}, integral_constant<int, 64>{}, integral_constant<int, 2>{},
                          integral_constant<int, 32>{}, integral_constant<int, 4>{});
         if (p.K <= 128 || (p.K == 256 && p.N >= 512))
@@ -659,12 +663,12 @@ int launch_pw(const PwParams& p, hipStream_t s) {
                      integral_constant<int, 64>{}, integral_constant<int, 2>{});
     }
     if (bk == 32) {
-        if (p.N == 32) return go(pointwise_gemm_kernel<256, 32, 4, 32, EPI, PRO>, 256, 32);
-        if (p.N == 64) return go(pointwise_gemm_kernel<256, 64, 4, 32, EPI, PRO>, 256, 64);
+        if (p.N % 64 != 0) return go(pointwise_gemm_kernel<256, 32, 4, 32, EPI, PRO>, 256, 32);
+        if (p.N % 128 != 0) return go(pointwise_gemm_kernel<256, 64, 4, 32, EPI, PRO>, 256, 64);
         return go(pointwise_gemm_kernel<128, 128, 2, 32, EPI, PRO>, 128, 128);
     }
-    if (p.N == 32) return go(pointwise_gemm_kernel<256, 32, 4, 64, EPI, PRO>, 256, 32);
-    if (p.N == 64) return go(pointwise_gemm_kernel<256, 64, 4, 64, EPI, PRO>, 256, 64);
+    if (p.N % 64 != 0) return go(pointwise_gemm_kernel<256, 32, 4, 64, EPI, PRO>, 256, 32);
+    if (p.N % 128 != 0) return go(pointwise_gemm_kernel<256, 64, 4, 64, EPI, PRO>, 256, 64);
     return go(pointwise_gemm_kernel<128, 128, 2, 64, EPI, PRO>, 128, 128);
 }
 
@@ -683,8 +687,7 @@ extern "C" int vh_pointwise_conv_nhwc_forward(const void* x, int32_t io_dtype, c
                io_dtype);
     VH_REQUIRE(M > 0 && N > 0 && K > 0, VH_ERR_SHAPE, "pointwise conv expects nonempty operands");
     VH_REQUIRE(K % 32 == 0 && K <= 65536, VH_ERR_SHAPE, "pointwise conv needs K %% 32 == 0, got %lld", (long long)K);
-    VH_REQUIRE(N == 32 || N == 64 || N % 128 == 0, VH_ERR_SHAPE,
-               "pointwise conv needs N = 32, 64 or a multiple of 128, got %lld", (long long)N);
+    VH_REQUIRE(N % 32 == 0, VH_ERR_SHAPE, "pointwise conv needs N %% 32 == 0, got %lld", (long long)N);
     VH_REQUIRE(M * std::max(N, K) < (int64_t(1) << 40), VH_ERR_SHAPE, "pointwise conv operands too large");
     VH_REQUIRE(epilogue >= PW_BIAS && epilogue <= PW_SILU, VH_ERR_ARG, "unknown epilogue %d", epilogue);
     VH_REQUIRE(epilogue != PW_ADD || residual != nullptr, VH_ERR_ARG, "epilogue 2 needs the residual");

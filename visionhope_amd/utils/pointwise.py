@@ -39,9 +39,9 @@ def is_pointwise(module):
 
 
 def supported(in_features, out_features):
-    """Shapes the matrix-core kernel covers (K % 32 == 0; N = 32, 64 or a multiple of 128)."""
+    """Shapes the matrix-core kernel covers (K and N multiples of 32)."""
     n, k = out_features, in_features
-    return k % 32 == 0 and (n in (32, 64) or n % 128 == 0)
+    return k % 32 == 0 and n % 32 == 0
 
 
 def pointwise_operands(module):
