@@ -959,7 +959,7 @@ __device__ __forceinline__ v4f readout_mfma(const float (&m)[D / 4], const XRaw<
 // once.  Loads are branch-free (positions past the image edge read the edge pixel and
 // are never stored), so every load of a wave's four columns or rows is in flight at
 // once, and the row loads are issued before the column work.  head_dim 32 runs the two
-// halves one after the other.
+// 16-channel halves in two workgroups.
 // ---------------------------------------------------------------------------
 template <typename T, typename TO, int D, bool SPLIT = false>
 __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams p, const int64_t tiles_h,
@@ -967,9 +967,14 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
     constexpr int REC = 20, PER = 4, KQ = D / 4;   // 16 channels + 4 padding floats per pixel record
     using Raw = typename Pix4<T>::Raw;
     __shared__ __align__(16) float col[256 * REC];
-    // Tile indices fit 32 bits (the host checks the grid size).
+    // Tile indices fit 32 bits (the host checks the grid size).  head_dim 32: two
+    // workgroups per tile, one per 16-channel half (the halves' registers do not share a
+    // wave, so more waves stay resident).
+    constexpr int NH = D / 16;
     const uint32_t thw = static_cast<uint32_t>(tiles_h * tiles_w), ntw = static_cast<uint32_t>(tiles_w);
-    const uint32_t tile = xcd_remap_any(blockIdx.x, gridDim.x);
+    const uint32_t wg = xcd_remap_any(blockIdx.x, gridDim.x);
+    const uint32_t tile = wg / NH;
+    const int my_half = static_cast<int>(wg % NH);
     const uint32_t bh = tile / thw, in_img = tile - bh * thw;
     const uint32_t th = in_img / ntw, tw = in_img - th * ntw;
     const uint32_t heads = static_cast<uint32_t>(p.heads);
@@ -997,8 +1002,8 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
         }
     };
     const int wr = min(w0 + n, W - 1), hc = min(h0 + n, H - 1);
-#pragma unroll
-    for (int half = 0; half < D / 16; ++half) {
+    {
+        const int half = my_half;
         const int64_t cbase = head * D + 16 * half + 4 * g;   // this lane's 4 output channels
         const int cl = 16 * half + 4 * g;                      // ... relative to the head
         const T* xb = static_cast<const T*>(p.x) + img;
@@ -1098,7 +1103,6 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
                 }
             }
         }
-        if (half + 1 < D / 16) __syncthreads();   // the next half rewrites the column buffer
     }
 }
 
@@ -1429,7 +1433,8 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
         sp.chunk[1] == W && sp.chunk[2] == H && sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0 &&
         H * W * C < (int64_t(1) << 31) && sp.max_chunks * d * d < (int64_t(1) << 31)) {
         const int64_t tiles_h = (H + 15) / 16, tiles_w = (W + 15) / 16;
-        const int64_t n_tiles = sp.B * sp.heads * tiles_h * tiles_w;
+        // one workgroup per tile and 16-channel half
+        const int64_t n_tiles = sp.B * sp.heads * tiles_h * tiles_w * (d / 16);
         VH_REQUIRE(n_tiles <= 0x7fffffff, VH_ERR_SHAPE, "SRNL readout grid too large");
         auto go = [&](auto tv, auto dc) {
             using T = decltype(tv);
