@@ -10,8 +10,9 @@
 //     16-feature steps of bf16 products, the triangle L = diag(rho) K^T K diag(kappa) over
 //     the 32 features, Z = (I + L)^-1 W K^T by back substitution (32 columns, one lane
 //     each), then the four 16 x 16 tiles of X_w = a_15 I - (K D_a) Z and of Y_w^T = -(Delta Z)^T;
-//   * wave 0 composes the maps in order on its tiles of G^T: G^T <- X_w^T G^T + Y_w^T,
-//     tile (I, J) = sum_K (X_w^T)[I][K] (G^T)[K][J] + (Y_w^T)[I][J];
+//   * the maps compose in order, G^T <- X_w^T G^T + Y_w^T, with tile (I, J) =
+//     sum_K (X_w^T)[I][K] (G^T)[K][J] + (Y_w^T)[I][J] on wave 2I + J (mod W), one barrier per
+//     block;
 //   * the state S = [M_m; M_v; M_k; e; a; 0] (98 rows padded to 112, 32 columns, FP32) lives
 //     in LDS; the refresh S <- S G (reference :119-133) runs by 16-row blocks over the waves.
 //
@@ -62,6 +63,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
     __shared__ __align__(16) float Yt[XW][4 * 256];   // waves 1..: Y_w^T tile (I, J) at [2I + J], lane-major
     __shared__ __align__(16) float St[SR * SD];       // state rows
     __shared__ __align__(16) float Gr[D * SD];        // chunk gain G, by rows
+    __shared__ __align__(16) float G0[4 * 256];       // wave 0: (X_0 + Y_0)^T tile (I, J) at [2I + J], lane-major
 
     const int tid = static_cast<int>(threadIdx.x);
     const int wv = tid >> 6, lane = tid & 63, i16 = lane & 15, q = lane >> 4;
@@ -115,9 +117,8 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
     float* const LZw = LZ[wv];
 
     // x is always loaded one computing chunk ahead, so the only loads in flight when a chunk
-    // starts are its own x, issued before the previous chunk-start store: the wait for them
-    // leaves that store outstanding (a load path after the store would make the compiler
-    // wait for the store's completion too, about 2,000 cycles per chunk).
+    // starts are its own x, issued before the chunk-start store: the wait for them leaves
+    // that store outstanding.
     uint2 xr[2] = {make_uint2(0u, 0u), make_uint2(0u, 0u)};
     bool xok = false;
     if (wv < nblk && nc > 1) load_x(0, xr, xok);
@@ -133,7 +134,6 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
         }
         if (c == nc - 1) break;
 
-        v4f gT[2][2];   // wave 0: tiles of G^T of the blocks composed so far
         if (wv < nblk) {
             const bool valid = 16 * wv + i16 < C;   // slot inside the chunk (every such token is < L here)
             // ---- token phase: [M_k; M_v] x and (x.e, x.a), two 16-feature steps each ----
@@ -301,8 +301,13 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
 #pragma unroll
                     for (int I = 0; I < 2; ++I)
 #pragma unroll
-                        for (int J = 0; J < 2; ++J)
-                            gT[I][J] = mma3(zh[I], zl[I], nbh[J], nbl[J], I == J ? dI : z0);   // (X_0 + Y_0)^T
+                        for (int J = 0; J < 2; ++J) {
+                            const v4f gT = mma3(zh[I], zl[I], nbh[J], nbl[J], I == J ? dI : z0);   // (X_0 + Y_0)^T
+                            // one block: G itself (lane (j, q) of tile (I, J) holds
+                            // G[16J + j][16I + 4q..16I + 4q + 3]); else the composition's start
+                            if (nblk == 1) st4(Gr + (16 * J + i16) * SD + 16 * I + 4 * q, gT);
+                            else st4(G0 + (2 * I + J) * 256 + 4 * lane, gT);
+                        }
                 } else {
                     v4s kah[2], kal[2], dlh[2], dll[2];
 #pragma unroll
@@ -324,34 +329,31 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
             }
         }
         __syncthreads();
-        // ---- composition on wave 0: (G^T)[I][J] <- sum_K (X_w^T)[I][K] (G^T)[K][J] + (Y_w^T)[I][J],
-        //      then G row-major ----
-        if (wv == 0) {
+        // ---- composition, tile (I, J) of G^T on wave 2I + J (mod W):
+        //      (G^T)[I][J] <- sum_K (X_w^T)[I][K] (G^T)[K][J] + (Y_w^T)[I][J], one barrier per
+        //      block.  Step w writes its tiles over Y_w's (each read only by the wave that
+        //      owns the tile); the last step writes G by rows. ----
+        {
+            const float* gprev = G0;
             for (int w = 1; w < nblk; ++w) {
-                v4s gh[2][2], gl[2][2], xh[2][2], xl[2][2];
+                if (w > 1) __syncthreads();   // step w - 1's tiles written
+                float* const ynext = Yt[w - 1];
+                for (int t = wv; t < 4; t += W) {
+                    const int I = t >> 1, J = t & 1;
+                    v4s gh[2], gl[2], xh[2], xl[2];
 #pragma unroll
-                for (int K = 0; K < 2; ++K)
-#pragma unroll
-                    for (int J = 0; J < 2; ++J) {
-                        blockform::split4(gT[K][J], gh[K][J], gl[K][J]);
-                        split4(ld4(Xt[w - 1] + (2 * K + J) * 256 + 4 * lane), xh[K][J], xl[K][J]);
-                    }
-#pragma unroll
-                for (int I = 0; I < 2; ++I)
-#pragma unroll
-                    for (int J = 0; J < 2; ++J) {
-                        const float4 y4 = ld4(Yt[w - 1] + (2 * I + J) * 256 + 4 * lane);
+                    for (int K = 0; K < 2; ++K) {
+                        split4(ld4(gprev + (2 * K + J) * 256 + 4 * lane), gh[K], gl[K]);
                         // (X_w^T)[I][K] is the transpose of X_w's tile (K, I)
-                        const v4s ah[2] = {xh[0][I], xh[1][I]}, al[2] = {xl[0][I], xl[1][I]};
-                        const v4s bh[2] = {gh[0][J], gh[1][J]}, bl[2] = {gl[0][J], gl[1][J]};
-                        gT[I][J] = mma3k2(ah, al, bh, bl, v4f{y4.x, y4.y, y4.z, y4.w});
+                        split4(ld4(Xt[w - 1] + (2 * K + I) * 256 + 4 * lane), xh[K], xl[K]);
                     }
+                    const float4 y4 = ld4(ynext + t * 256 + 4 * lane);
+                    const v4f gT = mma3k2(xh, xl, gh, gl, v4f{y4.x, y4.y, y4.z, y4.w});
+                    if (w == nblk - 1) st4(Gr + (16 * J + i16) * SD + 16 * I + 4 * q, gT);
+                    else st4(ynext + t * 256 + 4 * lane, gT);
+                }
+                gprev = ynext;
             }
-            // lane (j, q) of tile (I, J) holds G[16J + j][16I + 4q..16I + 4q + 3]
-#pragma unroll
-            for (int I = 0; I < 2; ++I)
-#pragma unroll
-                for (int J = 0; J < 2; ++J) st4(Gr + (16 * J + i16) * SD + 16 * I + 4 * q, gT[I][J]);
         }
         __syncthreads();
         // ---- refresh: S <- S G, 16-row blocks over the waves (A: S rows; B: G columns) ----
