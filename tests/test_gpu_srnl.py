@@ -460,3 +460,33 @@ def test_sequence_few_lines_block_form(oracle, device, chunks):
     expected = oracle.sequence_forward(x.float().numpy(), q.float().numpy(), mems, list(chunks))
     # bf16 output: one rounding of the result on top of the scan's error
     assert_close(y.float().cpu().numpy(), expected, 5e-3, f"few-line sequence {chunks}")
+
+
+@pytest.mark.parametrize("head_dim,batch,heads,length,chunks", [
+    (16, 2, 2, 70, (16, 33, 64, 7)),      # few lines: one workgroup per line
+    (16, 64, 4, 24, (8, 16, 12, 24)),     # 1024 lines: lines packed per wave
+    (32, 2, 2, 70, (16, 33, 64, 7)),      # head_dim 32 block form
+])
+def test_sequence_per_line_memories_block_form(oracle, device, head_dim, batch, heads, length, chunks):
+    """5-D memories (one state per line, chunk.cu:287) through the bf16 block-form scans;
+    the oracle runs each line as a problem of its own with that line's memories."""
+    from visionhope_amd.models.srnl_core.chunk import srnl_packed_forward
+
+    directions = 4
+    shared = memories(directions, heads, head_dim, kind="perturbed", seed=head_dim + batch)
+    gen = np.random.default_rng(head_dim * 7 + batch)
+    mems = tuple(np.ascontiguousarray(np.stack([m + 0.05 * gen.standard_normal(m.shape).astype(np.float32)
+                                                for _ in range(batch)]), dtype=np.float32) for m in shared)
+    x, q = _packed_case(batch, directions, heads, length, head_dim, torch.bfloat16, seed=127 + head_dim)
+    y = srnl_packed_forward(tuple(torch.from_numpy(m).to(device) for m in mems), x.to(device), q.to(device),
+                            list(chunks), q_raw=True)
+    xf, qf = x.float().numpy(), q.float().numpy()
+    expected = np.empty((batch, directions, heads, length, head_dim), np.float32)
+    for b in range(batch):
+        for r in range(directions):
+            for h in range(heads):
+                line_mems = [m[b, r, h][None, None] for m in mems]
+                expected[b, r, h] = oracle.sequence_forward(
+                    xf[b:b + 1, r:r + 1, h:h + 1], qf[b:b + 1, r:r + 1, :, h * head_dim:(h + 1) * head_dim],
+                    line_mems, [chunks[r]])[0, 0, 0]
+    assert_close(y.float().cpu().numpy(), expected, 5e-3, f"per-line memories d={head_dim} lines={batch * directions * heads}")
