@@ -66,11 +66,11 @@ const char* vh_last_error(void);
  * vh_set_dispatch_override(name, value) forces one choice for every later call
  * in this process until it is cleared (value NULL or ""); an unknown name or a
  * malformed value returns VH_ERR_ARG and changes nothing.  Names and values:
- *   scan_ut          "0" | "1"        SRNL head_dim-16 bf16: stepped form / block form
+ *   scan_ut          "0" | "1"        SRNL head_dim 16 and 32: stepped form / block form
  *   scan_wide        "0"|"1"|"2"|"4"  SRNL: waves per line of the wide scan (0: none)
  *   scan_tb          "1" | "2"        wide scan: row split / token blocks
  *   scan_pack        "<L>x<T>"        head_dim-16 scans: lines and 16-slot tiles per wave
- *   scan_utw         "0" | "1"        bf16 head_dim 16 and 32: the block form with a chunk's
+ *   scan_utw         "0" | "1"        head_dim 16 and 32: the block form with a chunk's
  *                                     blocks over the waves of one workgroup per line, never /
  *                                     whenever the chunks allow (default: head_dim 16 below
  *                                     1024 lines; head_dim 32 always, chunks up to 64)

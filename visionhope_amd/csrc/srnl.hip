@@ -1212,33 +1212,33 @@ void launch_scan(const ScanParams& sp, hipStream_t stream) {
         int token_blocks = (D == 16 && max_chunk >= 64) ? 2 : 1;
         const Override tb("scan_tb");
         if (tb.set()) token_blocks = tb.as_int() == 1 ? 1 : 2;
-        if constexpr (D == 16 && std::is_same<T, bf16_t>::value) {
-            // Few lines, bf16: the block form with a chunk's blocks spread over the waves of
-            // one workgroup per line (srnl_utw.hip), unless a dispatch override forces the
-            // wide scan or the stepped form.
+        if constexpr (D == 16) {
+            // Few lines: the block form with a chunk's blocks spread over the waves of one
+            // workgroup per line (srnl_utw.hip), unless a dispatch override forces the wide
+            // scan or the stepped form.
             const Override utw("scan_utw");   // "1": whenever the chunks allow, "0": never
             const bool utw_on = utw.set() ? utw.value[0] == '1' : waves > 0;
-            if (utw_on && scan_ut_enabled() && !Override("scan_wide").set() && launch_scan16_utw(sp, stream))
+            if (utw_on && scan_ut_enabled() && !Override("scan_wide").set() && launch_scan16_utw<T>(sp, stream))
                 return;
         }
-        if constexpr (D == 32 && std::is_same<T, bf16_t>::value) {
-            // head_dim 32, bf16: the block form with one workgroup per line (srnl_utw32.hip)
-            // for chunks of up to 64 tokens, unless an override forces the wide scan
-            // (scan_wide), the stepped forms (scan_ut "0") or turns it off (scan_utw "0").
+        if constexpr (D == 32) {
+            // head_dim 32: the block form with one workgroup per line (srnl_utw32.hip) for
+            // chunks of up to 64 tokens, unless an override forces the wide scan (scan_wide),
+            // the stepped forms (scan_ut "0") or turns it off (scan_utw "0").
             const Override utw("scan_utw");
             const bool utw_on = !(utw.set() && utw.value[0] == '0');
-            if (utw_on && scan_ut_enabled() && !Override("scan_wide").set() && launch_scan32_utw(sp, stream))
+            if (utw_on && scan_ut_enabled() && !Override("scan_wide").set() && launch_scan32_utw<T>(sp, stream))
                 return;
         }
         if (waves > 0 && launch_scan_wide(sp, dtype_code_of<T>(), D, waves, token_blocks, stream)) return;
     }
-    if constexpr (D == 16 && std::is_same<T, bf16_t>::value) {
-        // bf16 activations: the block form (srnl_ut.hip).  The scan_ut override "0"
-        // selects the stepped form below instead.
+    if constexpr (D == 16) {
+        // The block form (srnl_ut.hip).  The scan_ut override "0" selects the stepped form
+        // below instead.
         if (scan_ut_enabled()) {
             ScanParams up = sp;
             scan16_ut_packing(lines, sp.heads, &up.lines_per_wave, &up.tiles_per_wave);
-            if (launch_scan16_ut(up, stream)) return;
+            if (launch_scan16_ut<T>(up, stream)) return;
         }
     }
     if constexpr (D == 16) {

@@ -1,5 +1,6 @@
-// Helpers of the block-form (UT) SRNL scans (srnl_ut.hip, srnl_utw.hip): FP32 values as
-// bf16 hi + lo matrix-core operands and the 16x16 products built from them.
+// Helpers of the block-form (UT) SRNL scans (srnl_ut.hip, srnl_utw.hip, srnl_utw32.hip):
+// FP32 values as bf16 hi + lo matrix-core operands, the 16x16 products built from them and
+// the token operands of bf16, fp16 and FP32 maps.
 #pragma once
 
 #include "srnl_device.h"
@@ -46,6 +47,55 @@ __device__ __forceinline__ v4f mma3k2(const v4s (&ah)[2], const v4s (&al)[2], co
     c = mfma_bf16x2(ah[0], ah[1], bl[0], bl[1], c);
     return mfma_bf16x2(al[0], al[1], bh[0], bh[1], c);
 }
+
+// x of one lane's four features of a token as bf16 matrix-core operands.  bf16 maps enter
+// exactly (hi = the bits, no lo); fp16 and FP32 maps are decoded and split into hi + lo,
+// exact for every fp16 value (11 significant bits, exponents inside bf16's range) and within
+// 2^-16 |x| for FP32.  Products against x keep the state's hi + lo: two products for exact
+// x, three (lo x lo dropped, as in mma3) otherwise.
+template <typename T>
+struct XQuad {
+    static constexpr bool EXACT = std::is_same<T, bf16_t>::value;
+    using Raw = XRaw<T, 16>;   // 8 bytes (16-bit types) or 16 bytes (FP32)
+    // one vector load; `p` aligned to the raw size
+    static __device__ __forceinline__ Raw load(const T* p) { return load_xraw<T, 16>(p); }
+    // element by element, for rows that are not aligned
+    static __device__ __forceinline__ Raw load_scalar(const T* p) {
+        Raw r;
+        if constexpr (sizeof(T) == 4)
+            r.v = make_uint4(__float_as_uint(p[0]), __float_as_uint(p[1]), __float_as_uint(p[2]), __float_as_uint(p[3]));
+        else
+            r.v = make_uint2(static_cast<uint32_t>(p[0].bits) | (static_cast<uint32_t>(p[1].bits) << 16),
+                             static_cast<uint32_t>(p[2].bits) | (static_cast<uint32_t>(p[3].bits) << 16));
+        return r;
+    }
+    // operands of a token; zero for a slot past the chunk
+    static __device__ __forceinline__ void operands(const Raw& r, bool ok, v4s& hi, v4s& lo) {
+        if constexpr (EXACT) {
+            hi = ok ? bf16x4_bits(r.v) : v4s{0, 0, 0, 0};
+            lo = v4s{0, 0, 0, 0};
+        } else {
+            float x[4];
+            decode_x<T, 16>(r, x);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) x[j] = ok ? x[j] : 0.f;
+            split4(x, hi, lo);
+        }
+    }
+    // A X + c, A (state rows) as hi + lo, X the token columns
+    static __device__ __forceinline__ v4f mma(v4s ah, v4s al, v4s xh, v4s xl, v4f c) {
+        if constexpr (EXACT) return mfma_bf16(al, xh, mfma_bf16(ah, xh, c));
+        else return mma3(ah, al, xh, xl, c);
+    }
+    // the same over K = 32: a lane's quads of the two 16-feature halves
+    static __device__ __forceinline__ v4f mma_k2(const v4s (&ah)[2], const v4s (&al)[2], const v4s (&xh)[2],
+                                                 const v4s (&xl)[2], v4f c) {
+        if constexpr (EXACT)
+            return mfma_bf16x2(al[0], al[1], xh[0], xh[1], mfma_bf16x2(ah[0], ah[1], xh[0], xh[1], c));
+        else
+            return mma3k2(ah, al, xh, xl, c);
+    }
+};
 
 // d I in the accumulator layout of lane 16 q + i (entries: rows 4q..4q+3 of column i).
 __device__ __forceinline__ v4f diag4(float d, int q, int i) {

@@ -359,15 +359,18 @@ __device__ __forceinline__ void store_state4(float* dst, float4 v, bool split) {
 // any other case.  scan_wide_waves picks the waves per line for a line count;
 // token_blocks > 1 selects the token-block mode (blocks of the chunk composed).
 int scan_wide_waves(int64_t lines, int head_dim);
-// Scan for head_dim 16 with bf16 activations in the block form (srnl_ut.hip), packed as
-// sp.lines_per_wave x sp.tiles_per_wave like srnl_scan16_kernel.
+// Scan for head_dim 16 in the block form (srnl_ut.hip), packed as sp.lines_per_wave x
+// sp.tiles_per_wave like srnl_scan16_kernel.  T: the activation type (bf16_t, f16_t, float).
+template <typename T>
 bool launch_scan16_ut(const ScanParams& sp, hipStream_t stream);
 // The block form with the blocks of a chunk spread over the waves of one workgroup per line
-// (srnl_utw.hip): head_dim 16, bf16 activations, chunks of at most 128 tokens.  Returns
-// false (nothing launched) when the chunks or the input alignment do not allow it.
+// (srnl_utw.hip): head_dim 16, chunks of at most 128 tokens.  Returns false (nothing
+// launched) when the chunks or the input alignment do not allow it.
+template <typename T>
 bool launch_scan16_utw(const ScanParams& sp, hipStream_t stream);
-// head_dim 32, bf16 activations, chunks of at most 64 tokens (srnl_utw32.hip); false when
-// the call does not qualify.
+// head_dim 32, chunks of at most 64 tokens (srnl_utw32.hip); false when the call does not
+// qualify.
+template <typename T>
 bool launch_scan32_utw(const ScanParams& sp, hipStream_t stream);
 bool launch_scan_wide(const ScanParams& sp, int io_dtype, int head_dim, int waves, int token_blocks,
                       hipStream_t stream);

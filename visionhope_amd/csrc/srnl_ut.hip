@@ -1,5 +1,5 @@
-// SRNL chunk scan for head_dim 16 with bf16 activations: the block form of the gain
-// recurrence, with the serial part reduced to one matrix-core product per 16 tokens.
+// SRNL chunk scan for head_dim 16 (bf16, fp16 or FP32 activations): the block form of the
+// gain recurrence, with the serial part reduced to one matrix-core product per 16 tokens.
 //
 // Reference recurrence (models/srnl_core/csrc/inference_recurrence.cuh:32-135, memory.cuh:
 // 219-233), per line and chunk, from the chunk-start state M_m, M_v, M_k, e, a:
@@ -25,8 +25,9 @@
 // of line tc / TPL):
 //   * state S = [M_m; M_v; M_k; e; a; 0] (64 x 16 FP32) stays in registers in the MFMA
 //     A-operand layout (lane 16 q + i: row 16 R + i, columns 4q..4q+3);
-//   * projections [M_k; M_v] X and the gate pre-activations on bf16 MFMAs (x exact, the
-//     FP32 state as bf16 hi + lo), norms by row-swap permutes, gates per token lane;
+//   * projections [M_k; M_v] X and the gate pre-activations on bf16 MFMAs (bf16 x exact,
+//     fp16 / FP32 x and the FP32 state as bf16 hi + lo), norms by row-swap permutes, gates
+//     per token lane;
 //   * per-slot scalars through one DPP prefix sum per tile: cl_t = sum log2 alpha, so
 //     a_t / a_s = 2^(cl_t - cl_s) (every ratio used is <= 1; no overflow for any alpha);
 //   * Gram tiles K^T K and the triangle L on the matrix cores (bf16 hi + lo operands,
@@ -47,9 +48,10 @@ using namespace blockform;
 
 // Two-tile packings run two waves per SIMD (their line counts give 2048 or more waves), so
 // they are held to 256 VGPRs; four-tile packings run one wave per SIMD.
-template <int NL, int TCW, bool SPATIAL>
+template <typename T, int NL, int TCW, bool SPATIAL>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(TCW == 2 ? 2 : 1)))
 void srnl_scan16_ut_kernel(const ScanParams p) {
+    using XQ = XQuad<T>;
     static_assert((TCW == 2 || TCW == 4) && NL <= TCW, "tile packing");
     constexpr int D = 16, TT = 16 * TCW, S = TT / NL, TPL = TCW / NL, DKS = TT + 4;
     __shared__ __align__(16) float kT[D * DKS];     // normalised keys [feature][slot]
@@ -100,10 +102,10 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
     const int64_t nc = (p.L + C - 1) / C;
     const int my_slot = lane % S;
     const bool slot_lane = lane < TT;
-    const bf16_t* xcol[TCW];
+    const T* xcol[TCW];
 #pragma unroll
     for (int tc = 0; tc < TCW; ++tc)
-        xcol[tc] = static_cast<const bf16_t*>(p.x.ptr) + b * p.x.sb + r * p.x.sr + (head0 + tc / TPL) * p.x.sh + 4 * q;
+        xcol[tc] = static_cast<const T*>(p.x.ptr) + b * p.x.sb + r * p.x.sr + (head0 + tc / TPL) * p.x.sh + 4 * q;
     // Row/column chunks of the spatial operator: token i of chunk cc of scan r is pixel
     // pa*cc + pb*i + pc (32-bit; the host enables this only when H*W*pixel_stride < 2^31).
     int pa = 0, pb = 0, pc = 0, pst = 0;
@@ -116,7 +118,7 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
     }
     // x operands move as raw bits, loaded without a branch (invalid slots read their
     // line's first token and are zeroed when decoded).
-    auto issue_tile = [&](int64_t cc, int base, int cnt, uint2 (&raw)[TCW], unsigned& valid) {
+    auto issue_tile = [&](int64_t cc, int base, int cnt, typename XQ::Raw (&raw)[TCW], unsigned& valid) {
         valid = 0;
         int64_t offs[TCW];
 #pragma unroll
@@ -132,18 +134,14 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
         }
         if (p.x_vec) {
 #pragma unroll
-            for (int tc = 0; tc < TCW; ++tc) raw[tc] = *reinterpret_cast<const uint2*>(xcol[tc] + offs[tc]);
+            for (int tc = 0; tc < TCW; ++tc) raw[tc] = XQ::load(xcol[tc] + offs[tc]);
         } else {
 #pragma unroll
-            for (int tc = 0; tc < TCW; ++tc) {
-                const bf16_t* src = xcol[tc] + offs[tc];
-                raw[tc] = make_uint2(static_cast<uint32_t>(src[0].bits) | (static_cast<uint32_t>(src[1].bits) << 16),
-                                     static_cast<uint32_t>(src[2].bits) | (static_cast<uint32_t>(src[3].bits) << 16));
-            }
+            for (int tc = 0; tc < TCW; ++tc) raw[tc] = XQ::load_scalar(xcol[tc] + offs[tc]);
         }
     };
 
-    uint2 xr[TCW];
+    typename XQ::Raw xr[TCW];
     unsigned xvalid = 0;
     bool have_next = false;
 
@@ -183,11 +181,12 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
 #pragma unroll
             for (int tc = 0; tc < TCW; ++tc) {
                 const int lam = tc / TPL;
-                const v4s xs = ((xvalid >> tc) & 1u) ? bf16x4_bits(xr[tc]) : v4s{0, 0, 0, 0};
+                v4s xh, xl;
+                XQ::operands(xr[tc], (xvalid >> tc) & 1u, xh, xl);
                 const v4f z4 = {0.f, 0.f, 0.f, 0.f};
-                kacc[tc] = mfma_bf16(akl[lam], xs, mfma_bf16(akh[lam], xs, z4));
-                vacc[tc] = mfma_bf16(avl[lam], xs, mfma_bf16(avh[lam], xs, z4));
-                const v4f gacc = mfma_bf16(gal[lam], xs, mfma_bf16(gah[lam], xs, z4));
+                kacc[tc] = XQ::mma(akh[lam], akl[lam], xh, xl, z4);
+                vacc[tc] = XQ::mma(avh[lam], avl[lam], xh, xl, z4);
+                const v4f gacc = XQ::mma(gah[lam], gal[lam], xh, xl, z4);
                 pe[tc] = gacc[0];
                 pq[tc] = gacc[1];
             }
@@ -414,12 +413,13 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
     }
 }
 
+template <typename T>
 bool launch_scan16_ut(const ScanParams& sp, hipStream_t stream) {
     const int64_t lines = sp.B * sp.R * sp.heads;
     const int nl = sp.lines_per_wave, tcw = sp.tiles_per_wave;
     const unsigned grid = static_cast<unsigned>(lines / nl);
     auto go = [&](auto nlc, auto tcc, auto spc) {
-        hipLaunchKernelGGL((srnl_scan16_ut_kernel<decltype(nlc)::value, decltype(tcc)::value, decltype(spc)::value>),
+        hipLaunchKernelGGL((srnl_scan16_ut_kernel<T, decltype(nlc)::value, decltype(tcc)::value, decltype(spc)::value>),
                            dim3(grid), dim3(64), 0, stream, sp);
     };
     using S1 = std::integral_constant<int, 1>;
@@ -439,5 +439,8 @@ bool launch_scan16_ut(const ScanParams& sp, hipStream_t stream) {
     else pack(std::false_type{});
     return true;
 }
+template bool launch_scan16_ut<bf16_t>(const ScanParams&, hipStream_t);
+template bool launch_scan16_ut<f16_t>(const ScanParams&, hipStream_t);
+template bool launch_scan16_ut<float>(const ScanParams&, hipStream_t);
 
 }  // namespace vh

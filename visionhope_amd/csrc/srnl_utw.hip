@@ -1,4 +1,4 @@
-// SRNL chunk scan for head_dim 16 with bf16 activations when the lines are few (fewer than
+// SRNL chunk scan for head_dim 16 (bf16, fp16 or FP32 activations) when the lines are few (fewer than
 // the GPU's 1024 SIMDs: VisionHOPE-Base at 512^2 has 96 to 640 lines per launch, with chunks
 // of 128 down to 16 tokens).  It is the block form of srnl_ut.hip (same algebra, same
 // operand arithmetic) with the blocks of a chunk spread over the waves of a workgroup:
@@ -41,8 +41,9 @@ __device__ __forceinline__ void st4(float* p, const v4f& v) {
 
 }  // namespace
 
-template <int W, bool SPATIAL>
+template <typename T, int W, bool SPATIAL>
 __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParams p) {
+    using XQ = XQuad<T>;
     // Row strides are padded to 20 floats (keys, L, Z, state, G) so that the 16-byte loads of
     // 16 lanes down a column of rows fall in different LDS banks; the hand-over maps are read
     // back by the lane that wrote them, so they are stored lane-major.
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
     const int C = chunk_of(p.chunk, r);
     const int64_t nc = (p.L + C - 1) / C;
     const int nblk = (C + 15) / 16;
-    const bf16_t* xcol = static_cast<const bf16_t*>(p.x.ptr) + b * p.x.sb + r * p.x.sr + head * p.x.sh + 4 * q;
+    const T* xcol = static_cast<const T*>(p.x.ptr) + b * p.x.sb + r * p.x.sr + head * p.x.sh + 4 * q;
     int pa = 0, pb = 0, pc = 0, pst = 0;
     if constexpr (SPATIAL) {
         const int Wd = static_cast<int>(p.x.W), L = static_cast<int>(p.x.H * p.x.W);
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
     }
     // x of token (chunk cc, slot 16 wv + i16), features 4q..4q+3, as raw bits; slots past the
     // chunk read the line's first token and are zeroed when decoded
-    auto load_x = [&](int64_t cc, uint2& raw, bool& ok) {
+    auto load_x = [&](int64_t cc, typename XQ::Raw& raw, bool& ok) {
         const int slot = 16 * wv + i16;
         const int64_t tok = cc * C + slot;
         ok = slot < C && tok < p.L;
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
             if (SPATIAL && p.aligned) off = static_cast<int64_t>(pa * static_cast<int>(cc) + pb * slot + pc) * pst;
             else off = token_offset<SPATIAL>(p.x, r, tok);
         }
-        raw = *reinterpret_cast<const uint2*>(xcol + off);
+        raw = XQ::load(xcol + off);
     };
     float* const kTw = kT[wv];
     float* const ndTw = ndT[wv];
@@ -109,7 +110,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
     float* const Lcw = Lc[wv];
     float* const Zsw = Zs[wv];
 
-    uint2 xr = make_uint2(0u, 0u);
+    typename XQ::Raw xr{};
     bool xok = false, have = false;
     __syncthreads();
     for (int64_t c = 0; c < nc; ++c) {
@@ -136,11 +137,12 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
                 split4(av, avh, avl);
                 split4(ga, gah, gal);
             }
-            const v4s xs = xok ? bf16x4_bits(xr) : v4s{0, 0, 0, 0};
+            v4s xh, xl;
+            XQ::operands(xr, xok, xh, xl);
             const v4f z4 = {0.f, 0.f, 0.f, 0.f};
-            const v4f kacc = mfma_bf16(akl, xs, mfma_bf16(akh, xs, z4));
-            const v4f vacc = mfma_bf16(avl, xs, mfma_bf16(avh, xs, z4));
-            const v4f gacc = mfma_bf16(gal, xs, mfma_bf16(gah, xs, z4));
+            const v4f kacc = XQ::mma(akh, akl, xh, xl, z4);
+            const v4f vacc = XQ::mma(avh, avl, xh, xl, z4);
+            const v4f gacc = XQ::mma(gah, gal, xh, xl, z4);
             // the next computing chunk's x, in flight during the rest of this chunk
             have = c + 1 < nc - 1;
             if (have) load_x(c + 1, xr, xok);
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
 
 // Waves per line of the few-line block-form scan: the chunk's 16-slot blocks rounded up to
 // a power of two; 0 when a chunk exceeds 8 blocks (128 tokens) or the input rows are not
-// aligned for 8-byte loads.
+// aligned for vector loads.
 int scan16_utw_waves(const ScanParams& sp) {
     int max_chunk = 0;
     for (int r = 0; r < sp.R; ++r) max_chunk = std::max(max_chunk, sp.chunk[r]);
@@ -314,13 +316,14 @@ int scan16_utw_waves(const ScanParams& sp) {
     return w;
 }
 
+template <typename T>
 bool launch_scan16_utw(const ScanParams& sp, hipStream_t stream) {
     const int waves = scan16_utw_waves(sp);
     if (waves == 0) return false;
     const unsigned grid = static_cast<unsigned>(sp.B * sp.R * sp.heads);
     auto go = [&](auto wc, auto spc) {
         constexpr int WV = decltype(wc)::value;
-        hipLaunchKernelGGL((srnl_scan16_utw_kernel<WV, decltype(spc)::value>), dim3(grid), dim3(64 * WV), 0, stream,
+        hipLaunchKernelGGL((srnl_scan16_utw_kernel<T, WV, decltype(spc)::value>), dim3(grid), dim3(64 * WV), 0, stream,
                            sp);
     };
     auto pick = [&](auto spc) {
@@ -335,5 +338,9 @@ bool launch_scan16_utw(const ScanParams& sp, hipStream_t stream) {
     else pick(std::false_type{});
     return true;
 }
+
+template bool launch_scan16_utw<bf16_t>(const ScanParams&, hipStream_t);
+template bool launch_scan16_utw<f16_t>(const ScanParams&, hipStream_t);
+template bool launch_scan16_utw<float>(const ScanParams&, hipStream_t);
 
 }  // namespace vh

@@ -1,4 +1,4 @@
-// SRNL chunk scan for head_dim 32 with bf16 activations in the block form: the algebra of
+// SRNL chunk scan for head_dim 32 (bf16, fp16 or FP32 activations) in the block form: the algebra of
 // srnl_ut.hip (same operand arithmetic) with the 32-wide matrices cut into 2 x 2 tiles of
 // 16 x 16 matrix-core products, and the layout of srnl_utw.hip (one workgroup per line, the
 // chunk's 16-token blocks spread over its waves).  Reference recurrence:
@@ -47,8 +47,9 @@ __device__ __forceinline__ void split4(const float4& v, v4s& hi, v4s& lo) {
 
 }  // namespace
 
-template <int W, bool SPATIAL>
+template <typename T, int W, bool SPATIAL>
 __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParams p) {
+    using XQ = XQuad<T>;
     // Row strides are padded (keys 20, L and Z 20, state and G 36 floats) so that the 16-byte
     // loads of 16 lanes down a column of rows fall in different LDS banks; the hand-over
     // tiles are read back by the lane that wrote them, so they are stored lane-major.
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
     const int C = chunk_of(p.chunk, r);
     const int64_t nc = (p.L + C - 1) / C;
     const int nblk = (C + 15) / 16;
-    const bf16_t* xcol = static_cast<const bf16_t*>(p.x.ptr) + b * p.x.sb + r * p.x.sr + head * p.x.sh + 4 * q;
+    const T* xcol = static_cast<const T*>(p.x.ptr) + b * p.x.sb + r * p.x.sr + head * p.x.sh + 4 * q;
     int pa = 0, pb = 0, pc = 0, pst = 0;
     if constexpr (SPATIAL) {
         const int Wd = static_cast<int>(p.x.W), L = static_cast<int>(p.x.H * p.x.W);
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
     }
     // x of token (chunk cc, slot 16 wv + i16), features 4q..4q+3 and 16+4q..16+4q+3, as raw
     // bits; slots past the chunk read the line's first token and are zeroed when decoded
-    auto load_x = [&](int64_t cc, uint2 (&raw)[2], bool& ok) {
+    auto load_x = [&](int64_t cc, typename XQ::Raw (&raw)[2], bool& ok) {
         const int slot = 16 * wv + i16;
         const int64_t tok = cc * C + slot;
         ok = slot < C && tok < p.L;
@@ -108,8 +109,8 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
             if (SPATIAL && p.aligned) off = static_cast<int64_t>(pa * static_cast<int>(cc) + pb * slot + pc) * pst;
             else off = token_offset<SPATIAL>(p.x, r, tok);
         }
-        raw[0] = *reinterpret_cast<const uint2*>(xcol + off);
-        raw[1] = *reinterpret_cast<const uint2*>(xcol + off + 16);
+        raw[0] = XQ::load(xcol + off);
+        raw[1] = XQ::load(xcol + off + 16);
     };
     float* const kTw = kT[wv];
     float* const ndTw = ndT[wv];
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
     // x is always loaded one computing chunk ahead, so the only loads in flight when a chunk
     // starts are its own x, issued before the chunk-start store: the wait for them leaves
     // that store outstanding.
-    uint2 xr[2] = {make_uint2(0u, 0u), make_uint2(0u, 0u)};
+    typename XQ::Raw xr[2] = {};
     bool xok = false;
     if (wv < nblk && nc > 1) load_x(0, xr, xok);
     __syncthreads();
@@ -137,7 +138,9 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
         if (wv < nblk) {
             const bool valid = 16 * wv + i16 < C;   // slot inside the chunk (every such token is < L here)
             // ---- token phase: [M_k; M_v] x and (x.e, x.a), two 16-feature steps each ----
-            const v4s xs[2] = {xok ? bf16x4_bits(xr[0]) : v4s{0, 0, 0, 0}, xok ? bf16x4_bits(xr[1]) : v4s{0, 0, 0, 0}};
+            v4s xh[2], xl[2];
+            XQ::operands(xr[0], xok, xh[0], xl[0]);
+            XQ::operands(xr[1], xok, xh[1], xl[1]);
             // (both 16-feature steps in one 16x16x32 product: the lane's two quads as 8 k)
             v4f kacc[2], vacc[2], gacc;
             const bool on = (i16 & 3) < 2;   // operand rows 4q' + 0 / 4q' + 1: e / a, others zero
@@ -147,10 +150,10 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
                 v4s h[2], l[2];
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) split4(ld4(St + (64 + 16 * RB + i16) * SD + 16 * kk + 4 * q), h[kk], l[kk]);
-                kacc[RB] = mfma_bf16x2(l[0], l[1], xs[0], xs[1], mfma_bf16x2(h[0], h[1], xs[0], xs[1], z4));
+                kacc[RB] = XQ::mma_k2(h, l, xh, xl, z4);
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) split4(ld4(St + (32 + 16 * RB + i16) * SD + 16 * kk + 4 * q), h[kk], l[kk]);
-                vacc[RB] = mfma_bf16x2(l[0], l[1], xs[0], xs[1], mfma_bf16x2(h[0], h[1], xs[0], xs[1], z4));
+                vacc[RB] = XQ::mma_k2(h, l, xh, xl, z4);
             }
             {
                 v4s h[2], l[2];
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
                     if (!on) g4 = make_float4(0.f, 0.f, 0.f, 0.f);
                     split4(g4, h[kk], l[kk]);
                 }
-                gacc = mfma_bf16x2(l[0], l[1], xs[0], xs[1], mfma_bf16x2(h[0], h[1], xs[0], xs[1], z4));
+                gacc = XQ::mma_k2(h, l, xh, xl, z4);
             }
             // the next computing chunk's x, in flight during the rest of this chunk
             if (c + 1 < nc - 1) load_x(c + 1, xr, xok);
@@ -390,7 +393,7 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
 
 // Waves per line of the head_dim-32 block-form scan: the chunk's 16-slot blocks rounded up to
 // a power of two; 0 when a chunk exceeds 4 blocks (64 tokens) or the input rows are not
-// aligned for 8-byte loads.
+// aligned for vector loads.
 int scan32_utw_waves(const ScanParams& sp) {
     int max_chunk = 0;
     for (int r = 0; r < sp.R; ++r) max_chunk = std::max(max_chunk, sp.chunk[r]);
@@ -401,13 +404,14 @@ int scan32_utw_waves(const ScanParams& sp) {
     return w;
 }
 
+template <typename T>
 bool launch_scan32_utw(const ScanParams& sp, hipStream_t stream) {
     const int waves = scan32_utw_waves(sp);
     if (waves == 0) return false;
     const unsigned grid = static_cast<unsigned>(sp.B * sp.R * sp.heads);
     auto go = [&](auto wc, auto spc) {
         constexpr int WV = decltype(wc)::value;
-        hipLaunchKernelGGL((srnl_scan32_utw_kernel<WV, decltype(spc)::value>), dim3(grid), dim3(64 * WV), 0, stream,
+        hipLaunchKernelGGL((srnl_scan32_utw_kernel<T, WV, decltype(spc)::value>), dim3(grid), dim3(64 * WV), 0, stream,
                            sp);
     };
     auto pick = [&](auto spc) {
@@ -421,5 +425,9 @@ bool launch_scan32_utw(const ScanParams& sp, hipStream_t stream) {
     else pick(std::false_type{});
     return true;
 }
+
+template bool launch_scan32_utw<bf16_t>(const ScanParams&, hipStream_t);
+template bool launch_scan32_utw<f16_t>(const ScanParams&, hipStream_t);
+template bool launch_scan32_utw<float>(const ScanParams&, hipStream_t);
 
 }  // namespace vh
