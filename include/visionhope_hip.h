@@ -246,6 +246,13 @@ size_t vh_grn_workspace_bytes(int64_t B, int64_t C, int64_t H, int64_t W);
  * the reference, whose GRN has no cross-workgroup wait (grn_cuda.cu:290-320). */
 int vh_grn_workspace_fallbacks(const void* workspace, size_t workspace_bytes, void* stream, int64_t* count);
 
+/* Whether `stream` is capturing a HIP graph and, if so, the capture's identifier (unique
+ * per capture; *id = 0 otherwise).  A query that records nothing, valid during capture.
+ * No counterpart in the reference: the GRN wrapper keeps one workspace per captured graph
+ * (its zero fill a node of that graph) so that graphs replayed in any order never share
+ * synchronisation words. */
+int vh_stream_capture_id(void* stream, int32_t* capturing, uint64_t* id);
+
 /* GRN on channels-last x [B, H, W, C] (io_dtype): gx = ||x||_2 over H*W,
  * nx = gx / (mean_c gx + eps), y = x (1 + gamma nx) + beta, y [B, H, W, C] computed
  * in fp32 and stored as y_dtype (VH_DTYPE_F32 reproduces the reference's output;

@@ -188,10 +188,10 @@ def test_grn_one_pass_graph_replays(device):
 
 
 def test_grn_one_pass_two_graphs_replayed_in_reverse(device):
-    """Two graphs captured one after the other on the same capture stream share its GRN
-    workspace (created inside the first capture); replaying the second one first, before
-    the first graph ever ran, still gives the eager result (each captured call fills the
-    synchronisation header itself)."""
+    """Two graphs captured one after the other on the same capture stream: replaying the
+    second one first, before the first graph ever ran, still gives the eager result (each
+    capture creates its own GRN workspace, zeroed by a node of that graph), and so does a
+    graph of three calls that share one workspace (each call leaves its words zero)."""
     from visionhope_amd.utils.grn_cuda import visionhope_grn
 
     gen = torch.Generator(device=device).manual_seed(79)
@@ -204,14 +204,15 @@ def test_grn_one_pass_two_graphs_replayed_in_reverse(device):
     with torch.cuda.graph(graphs[0], stream=stream):
         out1 = visionhope_grn(x1, g1, b1, 1e-6)
     with torch.cuda.graph(graphs[1], stream=stream):
-        out2 = visionhope_grn(x2, g2, b2, 1e-6)
+        out2 = [visionhope_grn(x2, g2, b2, 1e-6) for _ in range(3)]
     eager1, eager2 = visionhope_grn(x1, g1, b1, 1e-6), visionhope_grn(x2, g2, b2, 1e-6)
     for _ in range(2):
-        for out in (out1, out2):
+        for out in (out1, *out2):
             out.zero_()
         graphs[1].replay()
         torch.cuda.synchronize()
-        assert torch.equal(out2, eager2)
+        for out in out2:
+            assert torch.equal(out, eager2)
         graphs[0].replay()
         torch.cuda.synchronize()
         assert torch.equal(out1, eager1)

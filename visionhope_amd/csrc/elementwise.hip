@@ -1402,6 +1402,17 @@ int vh_grn_workspace_fallbacks(const void* workspace, size_t workspace_bytes, vo
     return VH_OK;
 }
 
+int vh_stream_capture_id(void* stream, int32_t* capturing, uint64_t* id) {
+    VH_REQUIRE(capturing && id, VH_ERR_ARG, "capture query pointers must not be null");
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &status, &cid) != hipSuccess)
+        return set_error(VH_ERR_LAUNCH, "hipStreamGetCaptureInfo failed");
+    *capturing = status == hipStreamCaptureStatusActive ? 1 : 0;
+    *id = *capturing ? static_cast<uint64_t>(cid) : 0;
+    return VH_OK;
+}
+
 int vh_grn_forward(const void* x, int32_t io_dtype, const float* gamma, const float* beta, void* y,
                    int32_t y_dtype, float* gx, float* inv_den, int64_t B, int64_t C, int64_t H,
                    int64_t W, float eps, void* workspace, size_t workspace_bytes, void* stream) {

@@ -13,31 +13,34 @@ from torch.autograd import Function
 from . import hip
 from .cuda import on_tensor_device
 
-# One GRN workspace per (device, stream): its leading synchronisation words must be zero
-# when a call starts, and every call leaves them zero, so a zero-filled buffer is kept and
-# reused; calls on one stream never overlap.  Inside a graph capture nothing that happens
-# outside the graph can be relied on (a workspace created during a capture gets its fill
-# only when that graph replays, and another graph may replay first), so a captured call
-# records a fill of the header right before its kernel; a workspace created during a
-# capture is zeroed once more before its first eager use.
+# One GRN workspace per (device, stream) outside graph capture, and one per captured graph.
+# Its leading synchronisation words must be zero when a call starts and every call leaves
+# them zero, so a buffer zeroed when it is created is reused as is; calls on one stream
+# never overlap.  Inside a capture nothing done outside the graph can be relied on (graphs
+# replay in any order, long after they were captured), so the first call of a capture
+# creates the graph's own workspace, whose zero fill is a node of that graph ahead of the
+# call, and the capture's later calls reuse it.  Captured workspaces are kept for the life
+# of the process: a graph may be replayed at any time.
 _STREAM_WORKSPACES = {}
 _HEADER_FLOATS = 32768 // 4   # the synchronisation header of vh_grn_workspace_bytes
 
 
+def _capture_id(lib, stream):
+    """0 outside graph capture, else 1 + the capture's identifier (vh_stream_capture_id)."""
+    capturing, ident = ctypes.c_int32(0), ctypes.c_uint64(0)
+    hip.check(lib.vh_stream_capture_id(ctypes.c_void_p(stream.cuda_stream), ctypes.byref(capturing),
+                                       ctypes.byref(ident)), "vh_stream_capture_id")
+    return ident.value + 1 if capturing.value else 0
+
+
 def _stream_workspace(nbytes, device):
     stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
-    capturing = torch.cuda.is_current_stream_capturing()
-    entry = _STREAM_WORKSPACES.get(key)
-    if entry is None or entry[0].numel() * 4 < nbytes:
-        ws = torch.zeros(max(_HEADER_FLOATS, (int(nbytes) + 255) // 256 * 64), dtype=torch.float32, device=device)
-        entry = _STREAM_WORKSPACES[key] = [ws, capturing]
-    ws, born_in_capture = entry
-    if capturing:
-        ws[:_HEADER_FLOATS].zero_()   # a kernel node of the graph, not a memset (replays stay correct)
-    elif born_in_capture:
-        ws[:_HEADER_FLOATS].zero_()
-        entry[1] = False
+    key = (device.index, stream.cuda_stream, _capture_id(hip.load_library(), stream))
+    ws = _STREAM_WORKSPACES.get(key)
+    if ws is None or ws.numel() * 4 < nbytes:
+        # zeroed on creation: in a capture, by a fill node of this graph
+        ws = _STREAM_WORKSPACES[key] = torch.zeros(max(_HEADER_FLOATS, (int(nbytes) + 255) // 256 * 64),
+                                                   dtype=torch.float32, device=device)
     return ws
 
 
@@ -50,7 +53,7 @@ def grn_wait_fallbacks(device=None):
     device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
     lib = hip.load_library()
     total = 0
-    for (index, handle), (ws, _) in list(_STREAM_WORKSPACES.items()):
+    for (index, handle, _), ws in list(_STREAM_WORKSPACES.items()):
         if index != device.index:
             continue
         count = ctypes.c_int64(0)

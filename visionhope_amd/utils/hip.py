@@ -26,7 +26,7 @@ _DTYPE_CODES = {torch.float32: VH_DTYPE_F32, torch.bfloat16: VH_DTYPE_BF16, torc
 # Symbols declared in include/visionhope_hip.h (tests check the library exports all of them).
 EXPORTED_SYMBOLS = (
     "vh_abi_version", "vh_last_error", "vh_set_dispatch_override", "vh_clear_dispatch_overrides",
-    "vh_grn_workspace_fallbacks", "vh_srnl_workspace_bytes", "vh_srnl_spatial_forward",
+    "vh_grn_workspace_fallbacks", "vh_stream_capture_id", "vh_srnl_workspace_bytes", "vh_srnl_spatial_forward",
     "vh_srnl_spatial_forward_noalloc",
     "vh_srnl_spatial_scan", "vh_srnl_spatial_readout",
     "vh_srnl_line_forward_seq_noatomic", "vh_srnl_sequence_forward", "vh_srnl_forward",
@@ -69,6 +69,7 @@ _SIGNATURES = {
     "vh_set_dispatch_override": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p]),
     "vh_clear_dispatch_overrides": (None, []),
     "vh_grn_workspace_fallbacks": (ctypes.c_int, [_vp, _sz, _vp, ctypes.POINTER(ctypes.c_int64)]),
+    "vh_stream_capture_id": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_uint64)]),
     "vh_srnl_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "vh_srnl_spatial_forward": (ctypes.c_int, [
         _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
