@@ -199,7 +199,7 @@ def test_fused_block_bf16_gemm_paths(oracle, device, monkeypatch, dim, native_ge
     from visionhope_amd.models.block import VisionHOPEBlock
 
     if not native_gemm:
-        monkeypatch.setattr(block_mod, "_matrix_core_ok", lambda t, module: False)
+        monkeypatch.setattr(block_mod, "_matrix_core_ok", lambda t, module, grn_prologue=False: False)
     torch.manual_seed(17)
     block = VisionHOPEBlock(dim, head_dim=16)
     perturb_block(block, seed=18)

@@ -95,11 +95,12 @@ def test_pointwise_resident_weights_match_tiled_kernel(device, dispatch, k, n, m
 @pytest.mark.parametrize("k,n", [(256, 64), (1024, 256), (64, 32), (512, 128), (128, 512), (384, 96), (768, 192),
                                  (1792, 448)])
 @pytest.mark.parametrize("with_grn", [False, True])
-@pytest.mark.parametrize("hw", [(5, 7), (16, 20)])
+@pytest.mark.parametrize("hw", [(5, 7), (7, 7), (8, 10), (16, 20)])
 def test_pointwise_residual_and_grn(device, k, n, with_grn, hw):
     """fc2 of the FFN: r + fc2(GRN(h)), the GRN applied to the operand as it is loaded:
-    per chunk from global memory when images are smaller than a tile (35 pixels: images
-    split inside 16-row tiles), staged in LDS per k tile otherwise (320 pixels)."""
+    staged in LDS per k tile with the scale rows of the two images a block can span (320
+    pixels; 80 with 64-row blocks) or of three (35, 49 and 80 pixels per image with blocks
+    of up to 2x the image), per chunk from global memory when images are smaller still."""
     from visionhope_amd.utils import pointwise
 
     images, (h, w) = 3, hw

@@ -210,13 +210,17 @@ __device__ __forceinline__ void wait_vmem() {
 }
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <int BM, int BN, int WGM, int EPI, bool PRO, int OCC>
+// NI > 0: GRN prologue, the k tile's scale rows of the NI images a block can span (at least
+// BM / (NI - 1) pixels per image) and beta staged in LDS with the operand tiles.
+template <int BM, int BN, int WGM, int EPI, int NI, int OCC>
 __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams p) {
     constexpr int BK = 64, WGN = 4 / WGM, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
-    static_assert(TN % 2 == 0 && BM % 32 == 0 && BN % 32 == 0, "tile shape");
+    constexpr bool PRO = NI > 0;
+    static_assert(TN % 2 == 0 && BM % 32 == 0 && BN % 32 == 0 && NI >= 0 && NI <= 3, "tile shape");
     constexpr int A_INS = BM / 32, B_INS = BN / 32;             // wave instructions per operand and stage
     constexpr int D = A_INS + B_INS + (PRO ? 1 : 0);            // copies per wave and stage
-    constexpr int GRN_BYTES = PRO ? 3 * BK * 4 : 0;
+    constexpr int GRN_CPW = (NI + 1) * BK / 16;                 // 16-byte GRN chunks per wave and stage
+    constexpr int GRN_BYTES = PRO ? (NI + 1) * BK * 4 : 0;
     constexpr int STAGE = (BM + BN) * BK * 2 + GRN_BYTES;
     __shared__ __align__(16) unsigned char lds[3 * STAGE];
     __shared__ float gtab[EPI == PW_GELU ? GELU_TAB_N : 1];
@@ -256,8 +260,8 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
     if constexpr (PRO) {
         img0 = fast_div(static_cast<uint32_t>(m0), p.rows_per_image);
         const int64_t last_img = fast_div(static_cast<uint32_t>(p.M - 1), p.rows_per_image);
-        const int j = 12 * wv + std::min(lane, 11), which = j / 16, off = 4 * (j % 16);
-        gsrc = which < 2 ? p.pro_scale + std::min<int64_t>(img0 + which, last_img) * K + off : p.pro_shift + off;
+        const int j = GRN_CPW * wv + std::min(lane, GRN_CPW - 1), which = j / 16, off = 4 * (j % 16);
+        gsrc = which < NI ? p.pro_scale + std::min<int64_t>(img0 + which, last_img) * K + off : p.pro_shift + off;
     }
     auto issue = [&](int t) {
         const uint32_t sb = lds0 + (t % 3) * STAGE;
@@ -269,8 +273,9 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
         for (int i = 0; i < B_INS; ++i)
             lds_dma16(bsrc[i] + kt, __builtin_amdgcn_readfirstlane(sb + BM * BK * 2 + (wv * B_INS + i) * 1024));
         if constexpr (PRO) {
-            // 48 chunks of scale (two image rows) and beta: 12 per wave.
-            if (lane < 12) lds_dma16(gsrc + kt, __builtin_amdgcn_readfirstlane(sb + (BM + BN) * BK * 2 + wv * 12 * 16));
+            // 16 (NI + 1) chunks of scale (NI image rows) and beta: 4 (NI + 1) per wave.
+            if (lane < GRN_CPW)
+                lds_dma16(gsrc + kt, __builtin_amdgcn_readfirstlane(sb + (BM + BN) * BK * 2 + wv * GRN_CPW * 16));
         }
     };
     auto slot = [](int r, int c) { return (r * 8 + (c ^ (r & 7))) * 16; };
@@ -311,7 +316,7 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm) {
                 bfr[tm] = *reinterpret_cast<const uint4*>(sa + slot(wm * WM + 16 * tm + i16, c));
-                if constexpr (PRO) bfr[tm] = grn_apply8(bfr[tm], sg + rel[tm] * BK + 8 * c, sg + 2 * BK + 8 * c);
+                if constexpr (PRO) bfr[tm] = grn_apply8(bfr[tm], sg + rel[tm] * BK + 8 * c, sg + NI * BK + 8 * c);
             }
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
@@ -562,15 +567,19 @@ int launch_pw(const PwParams& p, hipStream_t s) {
         }
     }
     if (env) {
-        // d<BM>x<BN>o<OCC>: LDS-copy ring kernel (K % 64 == 0, N % BN == 0)
-        int dm = 0, dn = 0, docc = 0;
-        if (std::sscanf(env, "d%dx%do%d", &dm, &dn, &docc) == 3 && p.N % dn == 0 && p.K % 64 == 0) {
+        // d<BM>x<BN>o<OCC>[w<WGM>]: LDS-copy ring kernel (K % 64 == 0, N % BN == 0), the
+        // four waves as WGM x (4 / WGM) (default 2, 4 for BM = 256)
+        int dm = 0, dn = 0, docc = 0, dw = 0;
+        const int dfields = std::sscanf(env, "d%dx%do%dw%d", &dm, &dn, &docc, &dw);
+        if (dfields >= 3 && p.N % dn == 0 && p.K % 64 == 0) {
+            if (dfields == 3) dw = dm == 256 ? 4 : 2;
             const bool stage_grn = PRO_ON && p.rows_per_image.d >= static_cast<uint32_t>(dm);
 #define VH_PWD(BM_, BN_, WGM_, OCC_)                                                                     \
-    if (dm == BM_ && dn == BN_ && docc == OCC_ && (stage_grn || !PRO_ON))                                \
-        return go(pointwise_dma_kernel<BM_, BN_, WGM_, EPI, PRO_ON, OCC_>, BM_, BN_);
+    if (dm == BM_ && dn == BN_ && docc == OCC_ && dw == WGM_ && (stage_grn || !PRO_ON))                  \
+        return go(pointwise_dma_kernel<BM_, BN_, WGM_, EPI, PRO_ON ? 2 : 0, OCC_>, BM_, BN_);
             VH_PWD(128, 128, 2, 1) VH_PWD(128, 128, 2, 2) VH_PWD(64, 128, 2, 2) VH_PWD(64, 128, 2, 3)
             VH_PWD(128, 64, 2, 2) VH_PWD(128, 64, 2, 3) VH_PWD(256, 128, 4, 1)
+            VH_PWD(64, 128, 4, 2) VH_PWD(64, 128, 4, 3) VH_PWD(128, 128, 4, 2) VH_PWD(128, 64, 4, 3)
 #undef VH_PWD
         }
         // t<BM>x<BN>k<BK>o<OCC> (tiled variants for measurements, N % BN == 0)
@@ -634,12 +643,26 @@ int launch_pw(const PwParams& p, hipStream_t s) {
         // B = 128: 5-40 % faster than the register-staged tiles from K = 128 up, except
         // K = 128 with N = 512, where the wide output favours the 4-resident tiles).
         // Widths that are multiples of 64 but not of 128 take 64-channel tiles.
+        // With the GRN prologue the four waves split the tile 4 x 1 (each wave owns whole
+        // pixel rows, so each x fragment is transformed once per block instead of twice),
+        // and the block stages the scale rows of the two or three images it can span
+        // (measured on MI355X: Tiny 14x14 fc2 34.2 -> 32.0 us, Base 512^2 fc2 at 64x64x768 ->
+        // 192 29.9 -> 25.1 us and 32x32x1792 -> 448 36.7 -> 29.1 us; Tiny 7x7 fc2, 49
+        // pixels per image, 76 us on the register-staged kernel).
         const bool n64 = p.N % 128 != 0;
-        const bool stage_grn = PRO_ON && p.rows_per_image.d >= (n64 ? 128u : 64u);
-        if (!PRO_ON || stage_grn) {
-            if (n64) return go(pointwise_dma_kernel<128, 64, 2, EPI, PRO_ON, 3>, 128, 64);
-            if (p.K >= 1024) return go(pointwise_dma_kernel<64, 128, 2, EPI, PRO_ON, 2>, 64, 128);
-            return go(pointwise_dma_kernel<64, 128, 2, EPI, PRO_ON, 3>, 64, 128);
+        const uint32_t bm = n64 ? 128u : 64u, rpi = p.rows_per_image.d;
+        if (!PRO_ON) {
+            if (n64) return go(pointwise_dma_kernel<128, 64, 2, EPI, 0, 3>, 128, 64);
+            if (p.K >= 1024) return go(pointwise_dma_kernel<64, 128, 2, EPI, 0, 2>, 64, 128);
+            return go(pointwise_dma_kernel<64, 128, 2, EPI, 0, 3>, 64, 128);
+        }
+        if (rpi >= bm) {
+            if (n64) return go(pointwise_dma_kernel<128, 64, 4, EPI, 2, 3>, 128, 64);
+            return go(pointwise_dma_kernel<64, 128, 4, EPI, 2, 3>, 64, 128);
+        }
+        if (2 * rpi >= bm) {
+            if (n64) return go(pointwise_dma_kernel<128, 64, 4, EPI, 3, 3>, 128, 64);
+            return go(pointwise_dma_kernel<64, 128, 4, EPI, 3, 3>, 64, 128);
         }
     }
     if (bk == 0) {

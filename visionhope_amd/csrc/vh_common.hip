@@ -73,6 +73,7 @@ bool pw_cfg_ok(const char* v) {
     if (v[0] == 'n') return one_of(v + 1, {"1", "2", "4"});
     if (v[0] == 'w') return one_of(v + 1, {"32", "64"});
     if (std::sscanf(v, "d%dx%do%d%c", &a, &b, &c, &tail) == 3) return a > 0 && b > 0 && c > 0;
+    if (std::sscanf(v, "d%dx%do%dw%d%c", &a, &b, &c, &d, &tail) == 4) return a > 0 && b > 0 && c > 0 && (d == 2 || d == 4);
     if (std::sscanf(v, "t%dx%dk%do%d%c", &a, &b, &c, &d, &tail) == 4) return a > 0 && b > 0 && c > 0 && d > 0;
     return false;
 }

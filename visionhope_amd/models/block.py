@@ -14,7 +14,7 @@ from .srnl_core.fused import srnl_spatial_readout, srnl_spatial_scan
 from ..utils import dwconv, pointwise
 from ..utils.cached_params import contiguous_fp32, linear_weights
 from ..utils.grn import GlobalResponseNorm
-from ..utils.grn_cuda import grn_scale, visionhope_grn
+from ..utils.grn_cuda import grn_scale, grn_statistics_supported, visionhope_grn
 from ..utils.layer_norm_cuda import (can_fuse_add_layernorm2d, can_fuse_layernorm2d, visionhope_add_layernorm2d,
                                      visionhope_layernorm2d)
 from ..utils.residual import can_fuse_residual_add, visionhope_residual_add
@@ -42,22 +42,25 @@ def _is_pointwise(conv):
 
 
 # Short (few-pixel) products with K x N at or above this go to the library GEMM: on the
-# Tiny stage-4 FFN (6272 pixels, 512 <-> 2048 channels) its tiles keep the matrix cores
+# Tiny stage-4 fc1 (6272 pixels, 512 -> 2048 channels) its tiles keep the matrix cores
 # busier than the native kernel's, more than the fused epilogue saves (measured on
-# MI355X, whole forward).  Every other projection takes the native kernel.
+# MI355X, whole forward).  Every other projection takes the native kernel, and so does an
+# fc2 that takes the GRN on its operand (the library path needs a separate GRN pass:
+# Tiny forward 9.57 -> 9.50 ms with the stage-4 fc2 native).
 _LIBRARY_MIN_KN = 1 << 20
 _LIBRARY_MAX_PIXELS = 16384
 
 
-def _matrix_core_ok(t_nhwc, module):
+def _matrix_core_ok(t_nhwc, module, grn_prologue=False):
     """Whether the bf16 matrix-core 1x1 kernel takes ``module`` on the NHWC view ``t``
-    (otherwise the library GEMM runs on the autocast-cast operands)."""
+    (otherwise the library GEMM runs on the autocast-cast operands); ``grn_prologue``: the
+    product would take the GRN on its operand."""
     weight = module.weight
     n, k = weight.shape[0], weight.shape[1]
     pixels = t_nhwc.numel() // max(t_nhwc.shape[-1], 1)
     return (t_nhwc.is_contiguous() and t_nhwc.data_ptr() % 16 == 0 and module.bias is not None
             and pointwise.supported(k, n) and t_nhwc.shape[-1] == k
-            and (pixels >= _LIBRARY_MAX_PIXELS or k * n < _LIBRARY_MIN_KN))
+            and (grn_prologue or pixels >= _LIBRARY_MAX_PIXELS or k * n < _LIBRARY_MIN_KN))
 
 
 def _grn_beta(grn):
@@ -231,8 +234,10 @@ class VisionHOPEBlock(nn.Module):
         f = project(h.permute(0, 2, 3, 1), ffn.fc1, pointwise.EPI_GELU)
         use_grn = isinstance(ffn.grn, GlobalResponseNorm)
         x_nhwc = x.permute(0, 2, 3, 1)
+        # the GRN statistics of fc2's operand must be computable natively for the fused fc2
+        grn_stats_ok = not use_grn or grn_statistics_supported(f.shape[-1], f.numel())
         fc2_fused = (act == torch.bfloat16 and self.gamma2 is None and x.dtype == act and x_nhwc.is_contiguous()
-                     and _matrix_core_ok(f, ffn.fc2))
+                     and grn_stats_ok and _matrix_core_ok(f, ffn.fc2, grn_prologue=use_grn))
         scale = None
         if ffn.use_dwconv:
             fused = None

@@ -134,6 +134,13 @@ def visionhope_grn(x, gamma, beta, eps, out_dtype=torch.float32):
     return _VisionHOPEGRNFunction.apply(x, gamma, beta, eps, out_dtype)
 
 
+def grn_statistics_supported(channels, numel):
+    """Whether ``grn_scale`` takes a map of ``channels`` channels and ``numel`` elements
+    (the limits of ``vh_grn_scale_forward``: C % 8 == 0, C <= 2048, fewer than 2^31
+    elements; channels-last and 16-byte aligned as torch allocates them)."""
+    return channels % 8 == 0 and 0 < channels <= 2048 and numel < (1 << 31)
+
+
 @on_tensor_device
 def grn_scale(x, gamma, eps):
     """GRN statistics of the channels-last map ``x [B, C, H, W]``: the FP32 factor
