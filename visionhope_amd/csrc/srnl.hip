@@ -959,12 +959,15 @@ __device__ __forceinline__ v4f readout_mfma(const float (&m)[D / 4], const XRaw<
 // once.  Loads are branch-free (positions past the image edge read the edge pixel and
 // are never stored), so every load of a wave's four columns or rows is in flight at
 // once, and the row loads are issued before the column work.  head_dim 32 runs the two
-// 16-channel halves in two workgroups.
+// 16-channel halves in two workgroups.  TP = 8 (maps of at most 8 x 8): 8 x 8-pixel tiles,
+// two rows and two columns per wave, so a 7 x 7 map issues half the loads of a 16 x 16
+// tile (the 16-pixel product still runs; the lanes past the tile store nothing).
 // ---------------------------------------------------------------------------
-template <typename T, typename TO, int D, bool SPLIT = false>
+template <typename T, typename TO, int D, bool SPLIT = false, int TP = 16>
 __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams p, const int64_t tiles_h,
                                                                 const int64_t tiles_w) {
-    constexpr int REC = 20, PER = 4, KQ = D / 4;   // 16 channels + 4 padding floats per pixel record
+    static_assert(TP == 16 || TP == 8, "tile size");
+    constexpr int REC = 20, PER = TP / 4, KQ = D / 4;   // 16 channels + 4 padding floats per pixel record
     using Raw = typename Pix4<T>::Raw;
     __shared__ __align__(16) float col[256 * REC];
     // Tile indices fit 32 bits (the host checks the grid size).  head_dim 32: two
@@ -983,7 +986,7 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
     const int H = static_cast<int>(p.H), W = static_cast<int>(p.W);
     const int64_t C = p.C, L = p.H * p.W;
     const int Ci = static_cast<int>(C);
-    const int h0 = static_cast<int>(th) * 16, w0 = static_cast<int>(tw) * 16;
+    const int h0 = static_cast<int>(th) * TP, w0 = static_cast<int>(tw) * TP;
     // Workgroup-uniform bases and 32-bit lane offsets (the host requires H * W * C < 2^31
     // and per-line state blocks below 2^31 floats), so loads take a scalar base.
     const int64_t img = b * L * C + head * D;
@@ -1017,7 +1020,7 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
         [[maybe_unused]] Raw ra[PER];
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int h = min(h0 + 4 * wv + k, H - 1);
+            const int h = min(h0 + PER * wv + k, H - 1);
             rq[k] = load_q(h, wr);
             rx[k] = *reinterpret_cast<const Raw*>(xb + (pix(h, wr) + cl));
             load_m(st[0], h, mrow, m0[k]);
@@ -1041,7 +1044,7 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
             float m2[PER][KQ], m3[PER][KQ];
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
-                const int w = min(w0 + 4 * wv + k, W - 1);
+                const int w = min(w0 + PER * wv + k, W - 1);
                 cq[k] = load_q(hc, w);
                 cx[k] = *reinterpret_cast<const Raw*>(xb + (pix(hc, w) + cl));
                 load_m(st[2], w, mrow, m2[k]);
@@ -1059,7 +1062,7 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     c23[j] = wt[2][j] * (y2[j] * inv + sk[2][j] * xv[j]) + wt[3][j] * (y3[j] * inv + sk[3][j] * xv[j]);
-                *reinterpret_cast<float4*>(col + ((4 * wv + k) * 16 + n) * REC + 4 * g) =
+                *reinterpret_cast<float4*>(col + ((PER * wv + k) * 16 + n) * REC + 4 * g) =
                     make_float4(c23[0], c23[1], c23[2], c23[3]);
             }
         }
@@ -1068,7 +1071,7 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
         const int w = w0 + n;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            const int hh = 4 * wv + k, h = h0 + hh;
+            const int hh = PER * wv + k, h = h0 + hh;
             float xv[4];
             raw4_to_f32<T>(rx[k], xv);
             const float inv = __builtin_amdgcn_rsqf(fmaxf(xor16_32_sum(xraw_sumsq<T, D>(rq[k])), 1e-24f));
@@ -1087,7 +1090,7 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
 #pragma unroll
                 for (int j = 0; j < 4; ++j) o[j] += a[j];
             }
-            if (h < H && w < W) {
+            if (h < H && w < W && n < TP) {
                 const int64_t at = img + (pix(h, w) + cl);
                 if constexpr (sizeof(TO) == 4) {
                     *reinterpret_cast<float4*>(static_cast<float*>(p.out) + at) = make_float4(o[0], o[1], o[2], o[3]);
@@ -1432,7 +1435,10 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
     if ((d == 16 || (d == 32 && io_dtype != VH_DTYPE_F16)) && !per_direction && sp.chunk[0] == W &&
         sp.chunk[1] == W && sp.chunk[2] == H && sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0 &&
         H * W * C < (int64_t(1) << 31) && sp.max_chunks * d * d < (int64_t(1) << 31)) {
-        const int64_t tiles_h = (H + 15) / 16, tiles_w = (W + 15) / 16;
+        // 8 x 8 tiles for maps of at most 8 x 8 (the Tiny 7 x 7 stage), else 16 x 16
+        const bool small = H <= 8 && W <= 8;
+        const int64_t tp = small ? 8 : 16;
+        const int64_t tiles_h = (H + tp - 1) / tp, tiles_w = (W + tp - 1) / tp;
         // one workgroup per tile and 16-channel half
         const int64_t n_tiles = sp.B * sp.heads * tiles_h * tiles_w * (d / 16);
         VH_REQUIRE(n_tiles <= 0x7fffffff, VH_ERR_SHAPE, "SRNL readout grid too large");
@@ -1441,12 +1447,17 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
             constexpr int DD = decltype(dc)::value;
             // bf16 maps always carry split states here (state_split_bf16)
             constexpr bool SPLIT = std::is_same<T, bf16_t>::value;
-            if (out_f32)
-                hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD, SPLIT>), dim3(static_cast<unsigned>(n_tiles)),
-                                   dim3(256), 0, stream, fp, tiles_h, tiles_w);
-            else
-                hipLaunchKernelGGL((srnl_readout_tile_kernel<T, T, DD, SPLIT>), dim3(static_cast<unsigned>(n_tiles)),
-                                   dim3(256), 0, stream, fp, tiles_h, tiles_w);
+            auto run = [&](auto tpc) {
+                constexpr int TPV = decltype(tpc)::value;
+                if (out_f32)
+                    hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD, SPLIT, TPV>),
+                                       dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0, stream, fp, tiles_h, tiles_w);
+                else
+                    hipLaunchKernelGGL((srnl_readout_tile_kernel<T, T, DD, SPLIT, TPV>),
+                                       dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0, stream, fp, tiles_h, tiles_w);
+            };
+            if (small) run(std::integral_constant<int, 8>{});
+            else run(std::integral_constant<int, 16>{});
         };
         int rc;
         if (d == 16) rc = dispatch_t(io_dtype, [&](auto tv) { go(tv, std::integral_constant<int, 16>{}); });
