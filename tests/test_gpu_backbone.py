@@ -123,14 +123,17 @@ def test_checkpoint_round_trip_prepared_gpu(tiny_case, device, tmp_path):
     assert err <= 1e-4
 
 
-def test_graph_replays_match_eager_forward(tiny_case, device):
-    """The prepared Tiny forward as the bench runs it (bf16 autocast, inference mode, every
-    block forking a side stream for the query projection and the position encoding and
-    joining it before the readout) captured in one HIP graph: three replays, with an eager
-    forward and a synchronisation between replays, give the eager logits bit for bit, and
-    the eager forwards agree with each other."""
+@pytest.mark.parametrize("overlap", [False, True])
+def test_graph_replays_match_eager_forward(tiny_case, device, monkeypatch, overlap):
+    """The prepared Tiny forward as the bench runs it (bf16 autocast, inference mode; every
+    block's scan, query projection and position encoding in order on one stream, or with
+    ``OVERLAP_SCAN`` the scan on a side stream joined before the readout) captured in one
+    HIP graph: three replays, with an eager forward and a synchronisation between replays,
+    give the eager logits bit for bit, and the eager forwards agree with each other."""
     from visionhope_amd.inference.prepare import prepare_for_inference
+    from visionhope_amd.models import block as block_mod
 
+    monkeypatch.setattr(block_mod, "OVERLAP_SCAN", overlap)
     model, images, _ = tiny_case
     gpu = copy.deepcopy(model).to(device).to(memory_format=torch.channels_last)
     prepare_for_inference(gpu)

@@ -64,19 +64,26 @@ def _chunk_array(chunks):
     return hip.int64_array([int(c) for c in chunks])
 
 
+def srnl_spatial_workspace(x_nhwc, head_dim, chunks):
+    """An uninitialised workspace for ``srnl_spatial_scan`` of x_nhwc ``[B, H, W, C]``."""
+    batch, height, width, channels = x_nhwc.shape
+    max_chunks = max(math.ceil(height * width / int(c)) for c in chunks)
+    lib = hip.load_library()
+    return hip.workspace(lib.vh_srnl_workspace_bytes(batch * 4 * (channels // head_dim), max_chunks, head_dim),
+                         x_nhwc.device)
+
+
 @on_tensor_device
-def srnl_spatial_scan(states, x_nhwc, chunks):
+def srnl_spatial_scan(states, x_nhwc, chunks, workspace=None):
     """First half of ``srnl_spatial_inference``: the four scans of x_nhwc ``[B, H, W, C]``.
-    Returns the workspace holding every chunk-start content memory, for
-    ``srnl_spatial_readout`` on the same stream."""
+    Returns the workspace holding every chunk-start content memory (``workspace`` when
+    given, from ``srnl_spatial_workspace``), for ``srnl_spatial_readout``."""
     batch, height, width, channels = x_nhwc.shape
     head_dim = states[0].shape[-1]
     mems = _fp32_states(states)
     x_c = x_nhwc.contiguous()
     lib = hip.load_library()
-    max_chunks = max(math.ceil(height * width / int(c)) for c in chunks)
-    ws = hip.workspace(lib.vh_srnl_workspace_bytes(batch * 4 * (channels // head_dim), max_chunks, head_dim),
-                       x_nhwc.device)
+    ws = srnl_spatial_workspace(x_nhwc, head_dim, chunks) if workspace is None else workspace
     chunk_ptr, _keep = _chunk_array(chunks)
     hip.check(lib.vh_srnl_spatial_scan(
         hip.ptr(x_c), hip.dtype_code(x_c.dtype), *[hip.ptr(m) for m in mems], batch, height, width, channels,
