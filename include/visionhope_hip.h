@@ -83,6 +83,8 @@ const char* vh_last_error(void);
  *   fusion_tile      "<a>x<b>x<h>"    direction fusion: 2^a x 2^b pixel tiles, h heads per
  *                                     workgroup
  *   grn_pieces       2 .. 64          one-pass GRN: pieces per image
+ *   readout_tile     "8" | "16"       SRNL tile readout: pixel tile edge (default 8 for maps
+ *                                     of at most 8 x 8, else 16)
  * Results stay within each kernel's stated tolerance under every override: an
  * override changes which kernel runs, never what it computes. */
 int vh_set_dispatch_override(const char* name, const char* value);

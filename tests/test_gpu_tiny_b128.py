@@ -99,6 +99,8 @@ def test_tiny_b128_scan_readout_bf16_aux(oracle, device, hw, heads, kind):
     (56, 2, {"scan_wide": 4, "scan_tb": 2}),       # wide scan, token blocks
     (14, 8, {"scan_ut": 0}),                       # stepped form, 2 x 2 packing, 4096 lines
     (14, 8, {"scan_pack": "4x4"}),                 # block form, 4 x 4 packing
+    (28, 4, {"readout_tile": 8}),                  # 8 x 8-pixel readout tiles on a larger map
+    (7, 16, {"readout_tile": 16}),                 # 16 x 16-pixel readout tiles on a 7 x 7 map
 ])
 def test_tiny_b128_forced_kernels_share_the_state_format(oracle, device, dispatch, hw, heads, forced):
     """Whichever scan kernel runs, the readout decodes the states it wrote: the fused entry

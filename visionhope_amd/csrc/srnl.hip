@@ -1435,8 +1435,10 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
     if ((d == 16 || (d == 32 && io_dtype != VH_DTYPE_F16)) && !per_direction && sp.chunk[0] == W &&
         sp.chunk[1] == W && sp.chunk[2] == H && sp.chunk[3] == H && align % 16 == 0 && C % 16 == 0 &&
         H * W * C < (int64_t(1) << 31) && sp.max_chunks * d * d < (int64_t(1) << 31)) {
-        // 8 x 8 tiles for maps of at most 8 x 8 (the Tiny 7 x 7 stage), else 16 x 16
-        const bool small = H <= 8 && W <= 8;
+        // 8 x 8 tiles for maps of at most 8 x 8 (the Tiny 7 x 7 stage), else 16 x 16; the
+        // readout_tile override forces either
+        const Override rt("readout_tile");
+        const bool small = rt.set() ? rt.value[0] == '8' : (H <= 8 && W <= 8);
         const int64_t tp = small ? 8 : 16;
         const int64_t tiles_h = (H + tp - 1) / tp, tiles_w = (W + tp - 1) / tp;
         // one workgroup per tile and 16-channel half

@@ -108,6 +108,7 @@ OverrideSlot g_overrides[] = {
     {"grn_spin_limit", [](const char* v) { return is_uint(v, 1, 1 << 20); }, ""},
     {"fusion_tile", fusion_tile_ok, ""},
     {"grn_pieces", [](const char* v) { return is_uint(v, 2, 64); }, ""},
+    {"readout_tile", [](const char* v) { return one_of(v, {"8", "16"}); }, ""},
 };
 std::mutex g_override_mutex;
 
