@@ -259,23 +259,21 @@ void srnl_scan16_ut_kernel(const ScanParams p) {
             }
             __syncthreads();
             // ---- L = diag(rho) K^T K diag(kappa), strict upper triangle (lane 16 q + t,
-            //      entry j: L[4q + j][t]), stored by columns: Lc[tc][t][s] = L[s][t] ----
+            //      entry j: L[4q + j][t]), stored by columns: Lc[tc][t][s] = L[s][t].  The
+            //      Gram tile K^T K takes the keys split once (the same registers are its A
+            //      and B operands); row and column factors scale it after the product
+            //      (rho_s P kappa_t <= 1 for s < t, each factor below 2^117) ----
 #pragma unroll
             for (int tc = 0; tc < TCW; ++tc) {
-                const float rho = tk[16 * tc + i16], kap = tk[TT + 16 * tc + i16];
-                float ka[4], kb[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    ka[j] = kn4[tc][j] * rho;
-                    kb[j] = kn4[tc][j] * kap;
-                }
-                v4s kah, kal, kbh, kbl;
-                split4(ka, kah, kal);
-                split4(kb, kbh, kbl);
-                const v4f P = mma3(kah, kal, kbh, kbl, v4f{0.f, 0.f, 0.f, 0.f});
+                const float kap = tk[TT + 16 * tc + i16];
+                const float4 r4 = ld4(tk + 16 * tc + 4 * q);   // rho of rows 4q..4q+3
+                const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+                v4s kh, kl;
+                split4(kn4[tc], kh, kl);
+                const v4f P = mma3(kh, kl, kh, kl, v4f{0.f, 0.f, 0.f, 0.f});
                 float lv[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) lv[j] = (4 * q + j < i16) ? P[j] : 0.f;
+                for (int j = 0; j < 4; ++j) lv[j] = (4 * q + j < i16) ? (P[j] * rr[j]) * kap : 0.f;
                 *reinterpret_cast<float4*>(Lc + (16 * tc + i16) * LS + 4 * q) = make_float4(lv[0], lv[1], lv[2], lv[3]);
             }
             __syncthreads();

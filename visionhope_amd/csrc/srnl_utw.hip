@@ -182,22 +182,18 @@ __global__ __launch_bounds__(64 * W) void srnl_scan16_utw_kernel(const ScanParam
                 tkw[48 + lane] = eh * __builtin_amdgcn_exp2f(tot - cl);   // w
             }
             wave_sync();
-            // ---- L = diag(rho) K^T K diag(kappa), strict upper triangle, by columns ----
+            // ---- L = diag(rho) K^T K diag(kappa), strict upper triangle, by columns (the
+            //      Gram tile from the keys split once, scaled after the product) ----
             {
-                const float rho = tkw[i16], kap = tkw[16 + i16];
-                float ka[4], kb[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    ka[j] = kn4[j] * rho;
-                    kb[j] = kn4[j] * kap;
-                }
-                v4s kah, kal, kbh, kbl;
-                split4(ka, kah, kal);
-                split4(kb, kbh, kbl);
-                const v4f P = mma3(kah, kal, kbh, kbl, v4f{0.f, 0.f, 0.f, 0.f});
+                const float kap = tkw[16 + i16];
+                const float4 r4 = ld4(tkw + 4 * q);   // rho of rows 4q..4q+3
+                const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+                v4s kh, kl;
+                split4(kn4, kh, kl);
+                const v4f P = mma3(kh, kl, kh, kl, v4f{0.f, 0.f, 0.f, 0.f});
                 float lv[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) lv[j] = (4 * q + j < i16) ? P[j] : 0.f;
+                for (int j = 0; j < 4; ++j) lv[j] = (4 * q + j < i16) ? (P[j] * rr[j]) * kap : 0.f;
                 *reinterpret_cast<float4*>(Lcw + i16 * TS + 4 * q) = make_float4(lv[0], lv[1], lv[2], lv[3]);
             }
             wave_sync();

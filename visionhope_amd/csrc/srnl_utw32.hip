@@ -212,23 +212,17 @@ __global__ __launch_bounds__(64 * W) void srnl_scan32_utw_kernel(const ScanParam
             // ---- L = diag(rho) K^T K diag(kappa) over 32 features, strict upper triangle,
             //      by columns ----
             {
-                const float rho = tkw[i16], kap = tkw[16 + i16];
-                v4s kah[2], kal[2], kbh[2], kbl[2];
+                // the Gram tile from the keys split once, scaled after the product
+                const float kap = tkw[16 + i16];
+                const float4 r4 = ld4(tkw + 4 * q);   // rho of rows 4q..4q+3
+                const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+                v4s kh[2], kl[2];
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    float ka[4], kb[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        ka[j] = kn4[kk][j] * rho;
-                        kb[j] = kn4[kk][j] * kap;
-                    }
-                    blockform::split4(ka, kah[kk], kal[kk]);
-                    blockform::split4(kb, kbh[kk], kbl[kk]);
-                }
-                const v4f P = mma3k2(kah, kal, kbh, kbl, v4f{0.f, 0.f, 0.f, 0.f});
+                for (int kk = 0; kk < 2; ++kk) blockform::split4(kn4[kk], kh[kk], kl[kk]);
+                const v4f P = mma3k2(kh, kl, kh, kl, v4f{0.f, 0.f, 0.f, 0.f});
                 float lv[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) lv[j] = (4 * q + j < i16) ? P[j] : 0.f;
+                for (int j = 0; j < 4; ++j) lv[j] = (4 * q + j < i16) ? (P[j] * rr[j]) * kap : 0.f;
                 *reinterpret_cast<float4*>(LZw + i16 * TS + 4 * q) = make_float4(lv[0], lv[1], lv[2], lv[3]);
             }
             wave_sync();
