@@ -37,7 +37,7 @@ TINY_STAGES = [  # (grid, mixer channels, depth), head_dim 16 (models/factory.py
 # HBM bytes per vh_srnl_spatial_forward launch (scan + readout) at B=128, bf16, from
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of `bench.py --stages-only`, calibrated against a
 # 512 MiB copy (profiles/srnl_stages_b128_traffic.md).  Valid for the kernels measured there.
-SRNL_TRAFFIC_BYTES_B128 = {56: 269.7e6, 28: 187.5e6, 14: 152.4e6, 7: 135.6e6}
+SRNL_TRAFFIC_BYTES_B128 = {56: 271.0e6, 28: 187.8e6, 14: 152.9e6, 7: 135.6e6}
 
 
 def srnl_flops(batch, height, width, channels, head_dim, chunks):
