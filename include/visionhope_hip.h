@@ -158,6 +158,19 @@ int vh_srnl_spatial_readout(
     const float* dir_weight, const void* aux, void* out, int32_t out_dtype, int64_t B, int64_t H,
     int64_t W, int64_t C, int32_t head_dim, const int64_t chunks[4], const void* workspace,
     size_t workspace_bytes, void* stream);
+/* vh_srnl_spatial_readout with the block's local position encoding computed in the same
+ * pass: out (io dtype) = the readout + io_dtype(conv5x5(x) + lepe_bias), conv5x5 the
+ * depthwise 5x5 convolution of x with zero padding, lepe_taps [25, C] FP32 taps-major
+ * (tap dy*5+dx of channel c at [dy*5+dx][c]) and lepe_bias [C] FP32 or NULL.  The same
+ * bits as vh_dwconv2d_nhwc_forward (ksize 5, plain epilogue) followed by
+ * vh_srnl_spatial_readout with that result as aux and out_dtype = io_dtype.  No
+ * counterpart in the reference, whose block adds local_position(x_local) to the operator
+ * output in a separate step (models/block.py:77-78). */
+int vh_srnl_spatial_readout_lepe(
+    const void* x, const void* q, int32_t io_dtype, const float* d_skip, int32_t skip_per_direction,
+    const float* dir_weight, const float* lepe_taps, const float* lepe_bias, void* out, int64_t B,
+    int64_t H, int64_t W, int64_t C, int32_t head_dim, const int64_t chunks[4], const void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /* Backward of the packed SRNL forward: vh_srnl_sequence_forward (q_raw = 1, q [B, R, N,
  * heads*d] in io_dtype) or vh_srnl_forward (q_raw = 0, pre-normalised fp32 q [B, R, heads,

@@ -962,14 +962,27 @@ __device__ __forceinline__ v4f readout_mfma(const float (&m)[D / 4], const XRaw<
 // 16-channel halves in two workgroups.  TP = 8 (maps of at most 8 x 8): 8 x 8-pixel tiles,
 // two rows and two columns per wave, so a 7 x 7 map issues half the loads of a 16 x 16
 // tile (the 16-pixel product still runs; the lanes past the tile store nothing).
+//
+// LEPE: the block's local position encoding, a 5x5 depthwise convolution of x (zero
+// padding) plus bias, rounded to T and added to the result, is computed here instead of
+// in a separate pass (models/block.py:77-78).  The tile's 16 channels of x with a
+// two-pixel halo are loaded at the start (held in registers over the column pass) and
+// staged raw in LDS; thread (channel, tile column) then convolves TP or TP / 2 rows with
+// its channel's 25 taps in registers, each output accumulated from the bias in tap-row
+// order, left to right (the order of the depthwise kernels, so the value is the one
+// they store), and hands the rounded results to the row pass through the same LDS.
 // ---------------------------------------------------------------------------
-template <typename T, typename TO, int D, bool SPLIT = false, int TP = 16>
+template <typename T, typename TO, int D, bool SPLIT = false, int TP = 16, bool LEPE = false>
 __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams p, const int64_t tiles_h,
                                                                 const int64_t tiles_w) {
     static_assert(TP == 16 || TP == 8, "tile size");
     constexpr int REC = 20, PER = TP / 4, KQ = D / 4;   // 16 channels + 4 padding floats per pixel record
     using Raw = typename Pix4<T>::Raw;
     __shared__ __align__(16) float col[256 * REC];
+    // LEPE: halo tile of HP x HP pixels x 16 channels (raw T), later the rounded results
+    constexpr int HP = TP + 4, HALO_Q = HP * HP * 4, HALO_IT = (HALO_Q + 255) / 256;
+    constexpr int LRP = TP * TP / 16;              // rows per thread in the convolution
+    __shared__ __align__(16) Raw halo[LEPE ? HALO_Q : 1];
     // Tile indices fit 32 bits (the host checks the grid size).  head_dim 32: two
     // workgroups per tile, one per 16-channel half (the halves' registers do not share a
     // wave, so more waves stay resident).
@@ -1012,6 +1025,18 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
         const T* xb = static_cast<const T*>(p.x) + img;
         const int mrow = 16 * half + n;                        // M row of this lane (A operand)
 
+        // LEPE halo: quad e % 4 of pixel e / 4 of the HP x HP tile, zeros outside the image.
+        [[maybe_unused]] Raw hraw[LEPE ? HALO_IT : 1];
+        if constexpr (LEPE) {
+#pragma unroll
+            for (int i = 0; i < HALO_IT; ++i) {
+                const int e = static_cast<int>(threadIdx.x) + 256 * i, px = e >> 2;
+                const int hy = h0 - 2 + px / HP, wx = w0 - 2 + px % HP;
+                hraw[i] = Raw{};
+                if (e < HALO_Q && hy >= 0 && hy < H && wx >= 0 && wx < W)
+                    hraw[i] = *reinterpret_cast<const Raw*>(xb + (pix(hy, wx) + 16 * half + 4 * (e & 3)));
+            }
+        }
         // Row pass operands (directions 0, 1): tile row hh = 4 wv + k, lane n holds pixel
         // (h0 + hh, w0 + n).  Issued first; consumed after the column pass.
         XRaw<T, D> rq[PER];
@@ -1025,7 +1050,7 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
             rx[k] = *reinterpret_cast<const Raw*>(xb + (pix(h, wr) + cl));
             load_m(st[0], h, mrow, m0[k]);
             load_m(st[1], H - 1 - h, mrow, m1[k]);
-            if (p.aux) ra[k] = *reinterpret_cast<const Raw*>(static_cast<const T*>(p.aux) + img + (pix(h, wr) + cl));
+            if (!LEPE && p.aux) ra[k] = *reinterpret_cast<const Raw*>(static_cast<const T*>(p.aux) + img + (pix(h, wr) + cl));
         }
 
         // Column pass (directions 2, 3): tile column ww = 4 wv + k, lane n holds pixel
@@ -1066,7 +1091,74 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
                     make_float4(c23[0], c23[1], c23[2], c23[3]);
             }
         }
+        if constexpr (LEPE) {
+#pragma unroll
+            for (int i = 0; i < HALO_IT; ++i) {
+                const int e = static_cast<int>(threadIdx.x) + 256 * i;
+                if (e < HALO_Q) halo[e] = hraw[i];
+            }
+        }
         __syncthreads();
+        [[maybe_unused]] float lepe[PER][4];
+        if constexpr (LEPE) {
+            // Thread t: channel c = t % 16 of the half, tile column x = (t / 16) % TP, rows
+            // LRP (t / 16 / TP) .. + LRP - 1.  Halo row r feeds output row k through tap
+            // row r - k, so visiting r in order adds each output's terms row by row.
+            const int c = static_cast<int>(threadIdx.x) & 15, rest = static_cast<int>(threadIdx.x) >> 4;
+            const int x = rest % TP, r0 = LRP * (rest / TP);
+            const int64_t cg = head * D + 16 * half + c;
+            float tap[25];
+#pragma unroll
+            for (int i = 0; i < 25; ++i) tap[i] = p.lepe_taps[i * C + cg];
+            const float bias = p.lepe_bias ? p.lepe_bias[cg] : 0.f;
+            float acc[LRP];
+#pragma unroll
+            for (int k = 0; k < LRP; ++k) acc[k] = bias;
+            const auto* hv = reinterpret_cast<const std::conditional_t<sizeof(T) == 4, float, uint16_t>*>(halo);
+#pragma unroll
+            for (int r = 0; r < LRP + 4; ++r) {
+                float v[5];
+#pragma unroll
+                for (int dx = 0; dx < 5; ++dx) {
+                    const auto u = hv[((r0 + r) * HP + x + dx) * 16 + c];
+                    if constexpr (sizeof(T) == 4) v[dx] = u;
+                    else v[dx] = to_f32(T{u});
+                }
+#pragma unroll
+                for (int k = 0; k < LRP; ++k) {
+                    const int dy = r - k;
+                    if (dy >= 0 && dy < 5) {
+#pragma unroll
+                        for (int dx = 0; dx < 5; ++dx) acc[k] = fmaf(v[dx], tap[dy * 5 + dx], acc[k]);
+                    }
+                }
+            }
+            __syncthreads();   // every halo read done: the results overwrite it
+            auto* res = reinterpret_cast<std::conditional_t<sizeof(T) == 4, float, uint16_t>*>(halo);
+#pragma unroll
+            for (int k = 0; k < LRP; ++k) {
+                const int at = ((r0 + k) * TP + x) * 16 + c;
+                if constexpr (sizeof(T) == 4) {
+                    res[at] = acc[k];
+                } else {
+                    // the FP32 sum first, then T (as the depthwise kernel stores it): the
+                    // empty asm keeps the last multiply-add from fusing with the conversion
+                    // into one multiply-add that rounds to fp16 directly
+                    float a = acc[k];
+                    asm volatile("" : "+v"(a));
+                    res[at] = from_f32<T>(a).bits;
+                }
+            }
+            __syncthreads();
+            // this lane's 4 channels of its row-pass pixels (lanes past an 8-wide tile read
+            // column TP - 1 and store nothing)
+            const int xn = min(n, TP - 1);
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const Raw rr = *reinterpret_cast<const Raw*>(res + ((PER * wv + k) * TP + xn) * 16 + 4 * g);
+                raw4_to_f32<T>(rr, lepe[k]);
+            }
+        }
 
         const int w = w0 + n;
 #pragma unroll
@@ -1084,7 +1176,10 @@ __global__ __launch_bounds__(256) void srnl_readout_tile_kernel(const FuseParams
             for (int j = 0; j < 4; ++j)
                 o[j] = (wt[0][j] * (y0[j] * inv + sk[0][j] * xv[j]) + wt[1][j] * (y1[j] * inv + sk[1][j] * xv[j])) +
                        c23v[j];
-            if (p.aux) {
+            if constexpr (LEPE) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] += lepe[k][j];
+            } else if (p.aux) {
                 float a[4];
                 raw4_to_f32<T>(ra[k], a);
 #pragma unroll
@@ -1414,14 +1509,18 @@ int run_scan(const LineInput& x, int io_dtype, const float* Mm, const float* Mv,
 int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_direction, int io_dtype,
              const float* skip, int skip_per_dir, const float* wgt, void* out, int64_t H,
              int64_t W, int64_t C, int d, hipStream_t stream, const void* aux = nullptr,
-             int out_dtype = VH_DTYPE_F32) {
+             int out_dtype = VH_DTYPE_F32, const float* lepe_taps = nullptr, const float* lepe_bias = nullptr) {
     VH_REQUIRE(skip && wgt && out && q, VH_ERR_ARG, "SRNL fusion arguments must not be null");
     VH_REQUIRE(out_dtype == VH_DTYPE_F32 || out_dtype == io_dtype, VH_ERR_DTYPE,
                "SRNL fused output must be fp32 or the io dtype");
+    const bool lepe = lepe_taps != nullptr;
+    VH_REQUIRE(!lepe || (out_dtype == io_dtype && !aux && !per_direction), VH_ERR_ARG,
+               "the position encoding is fused only into a spatial readout to the io dtype, without aux");
     FuseParams fp{};
     fp.x = x; fp.q = q; fp.per_direction = per_direction;
     fp.states = sp.states; fp.max_chunks = sp.max_chunks;
     fp.skip = skip; fp.skip_per_dir = skip_per_dir; fp.wgt = wgt; fp.out = out; fp.aux = aux;
+    fp.lepe_taps = lepe_taps; fp.lepe_bias = lepe_bias;
     fp.B = sp.B; fp.H = H; fp.W = W; fp.C = C; fp.heads = sp.heads;
     for (int r = 0; r < 4; ++r) fp.chunk[r] = sp.chunk[r];
     fp.split_states = sp.split_states;
@@ -1451,7 +1550,10 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
             constexpr bool SPLIT = std::is_same<T, bf16_t>::value;
             auto run = [&](auto tpc) {
                 constexpr int TPV = decltype(tpc)::value;
-                if (out_f32)
+                if (lepe)
+                    hipLaunchKernelGGL((srnl_readout_tile_kernel<T, T, DD, SPLIT, TPV, true>),
+                                       dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0, stream, fp, tiles_h, tiles_w);
+                else if (out_f32)
                     hipLaunchKernelGGL((srnl_readout_tile_kernel<T, float, DD, SPLIT, TPV>),
                                        dim3(static_cast<unsigned>(n_tiles)), dim3(256), 0, stream, fp, tiles_h, tiles_w);
                 else
@@ -1467,6 +1569,14 @@ int run_fuse(const ScanParams& sp, const void* x, const void* q, int per_directi
         else rc = (go(float{}, std::integral_constant<int, 32>{}), VH_OK);
         if (rc) return rc;
         return check_launch("srnl_readout_tile_kernel");
+    }
+    if (lepe) {
+        // The encoding goes to `out` first (the depthwise kernel, the same bits), and the
+        // per-element readout adds it in place (each thread reads its own element first).
+        const int rc = vh_dwconv2d_nhwc_forward(x, io_dtype, lepe_taps, lepe_bias, 5, 0, nullptr, out, sp.B, H, W, C,
+                                                stream);
+        if (rc) return rc;
+        fp.aux = out;
     }
     const int64_t total = sp.B * H * W * C;
     const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
@@ -1541,6 +1651,15 @@ int srnl_spatial_forward_ws(const void* x, const void* q, int32_t io_dtype, cons
 
 }  // namespace vh
 
+namespace vh {
+// vh_srnl_spatial_readout, with the position encoding fused when lepe_taps is not null
+int spatial_readout_impl(const void* x, const void* q, int32_t io_dtype, const float* d_skip,
+                         int32_t skip_per_direction, const float* dir_weight, const void* aux, void* out,
+                         int32_t out_dtype, int64_t B, int64_t H, int64_t W, int64_t C, int32_t head_dim,
+                         const int64_t chunks[4], const void* workspace, size_t workspace_bytes, void* stream,
+                         const float* lepe_taps, const float* lepe_bias);
+}  // namespace vh
+
 using namespace vh;
 
 extern "C" {
@@ -1585,6 +1704,18 @@ int vh_srnl_spatial_readout(const void* x, const void* q, int32_t io_dtype, cons
                             int32_t out_dtype, int64_t B, int64_t H, int64_t W, int64_t C, int32_t head_dim,
                             const int64_t chunks[4], const void* workspace, size_t workspace_bytes,
                             void* stream) {
+    return spatial_readout_impl(x, q, io_dtype, d_skip, skip_per_direction, dir_weight, aux, out, out_dtype, B, H, W,
+                                C, head_dim, chunks, workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+}  // extern "C"
+
+namespace vh {
+int spatial_readout_impl(const void* x, const void* q, int32_t io_dtype, const float* d_skip,
+                         int32_t skip_per_direction, const float* dir_weight, const void* aux, void* out,
+                         int32_t out_dtype, int64_t B, int64_t H, int64_t W, int64_t C, int32_t head_dim,
+                         const int64_t chunks[4], const void* workspace, size_t workspace_bytes, void* stream,
+                         const float* lepe_taps, const float* lepe_bias) {
     VH_REQUIRE(x && q && workspace && chunks, VH_ERR_ARG, "spatial SRNL readout pointers must not be null");
     VH_REQUIRE(H > 0 && W > 0 && C > 0 && B > 0, VH_ERR_SHAPE, "spatial SRNL needs nonempty [B,H,W,C]");
     VH_REQUIRE(valid_head_dim(head_dim), VH_ERR_HEAD_DIM,
@@ -1605,7 +1736,21 @@ int vh_srnl_spatial_readout(const void* x, const void* q, int32_t io_dtype, cons
     sp.states = const_cast<float*>(static_cast<const float*>(workspace));
     sp.split_states = state_split_bf16(io_dtype, head_dim, true) ? 1 : 0;
     return run_fuse(sp, x, q, 0, io_dtype, d_skip, skip_per_direction, dir_weight, out, H, W, C, head_dim,
-                    static_cast<hipStream_t>(stream), aux, out_dtype);
+                    static_cast<hipStream_t>(stream), aux, out_dtype, lepe_taps, lepe_bias);
+}
+}  // namespace vh
+
+extern "C" {
+
+int vh_srnl_spatial_readout_lepe(const void* x, const void* q, int32_t io_dtype, const float* d_skip,
+                                 int32_t skip_per_direction, const float* dir_weight, const float* lepe_taps,
+                                 const float* lepe_bias, void* out, int64_t B, int64_t H, int64_t W, int64_t C,
+                                 int32_t head_dim, const int64_t chunks[4], const void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    VH_REQUIRE(lepe_taps, VH_ERR_ARG, "position encoding taps must not be null");
+    VH_REQUIRE(H * W * C < (int64_t(1) << 31), VH_ERR_SHAPE, "position encoding: one image must be below 2^31 elements");
+    return spatial_readout_impl(x, q, io_dtype, d_skip, skip_per_direction, dir_weight, nullptr, out, io_dtype, B, H,
+                                W, C, head_dim, chunks, workspace, workspace_bytes, stream, lepe_taps, lepe_bias);
 }
 
 int vh_srnl_line_forward_seq_noatomic(const void* X, const void* Q_raw, int32_t io_dtype,

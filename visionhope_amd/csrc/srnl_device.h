@@ -321,6 +321,10 @@ struct FuseParams {
     const float* wgt;
     void* out;          // [B, H, W, C], fp32 or the io dtype (see the kernel's TO)
     const void* aux;    // optional [B, H, W, C] io-dtype addend of the fused result
+    // optional 5x5 depthwise convolution of x added to the fused result (the tiled
+    // readout only): taps [25, C] FP32 taps-major, bias [C] FP32 or null
+    const float* lepe_taps;
+    const float* lepe_bias;
     int64_t B, H, W, C, heads;
     int chunk[4];
     int split_states;   // states stored as bf16 hi + lo pairs (see state_split_bf16)

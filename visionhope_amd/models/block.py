@@ -33,6 +33,11 @@ FUSE_CPE_LAYERNORM = True
 # than the overlap saved; Tiny forward 9.52 -> 9.42 ms measured on MI355X).
 OVERLAP_SCAN = False
 
+# The local position encoding (5x5 depthwise of x_local) computed inside the operator's
+# readout (True: one pass, the same bits) or as a separate depthwise pass whose result the
+# readout adds (False, for measurements).
+FUSE_LEPE_READOUT = True
+
 
 def _side_stream(device):
     """One default-priority side stream per device for work overlapped with the scan."""
@@ -272,9 +277,9 @@ class VisionHOPEBlock(nn.Module):
     def _spatial_overlapped(self, x_local):
         """Operator output plus local position encoding, ``[B, H, W, C]`` in x_local's dtype.
 
-        The scan, then the query projection and the position encoding (which the readout
-        reads right after, while they are still cached); the readout fuses the four
-        directions, adds the encoding and rounds once (``operator.py:159-193`` +
+        The scan, then the query projection; the readout fuses the four directions,
+        computes and adds the position encoding (``FUSE_LEPE_READOUT``; otherwise a separate
+        depthwise pass ahead of it) and rounds once (``operator.py:159-193`` +
         ``block.py:77-78``).  With ``OVERLAP_SCAN`` the scan runs on a side stream
         instead, overlapping the other two; every tensor that both streams touch (the
         scan's workspace) is allocated on the caller's stream before the fork.
@@ -306,14 +311,18 @@ class VisionHOPEBlock(nn.Module):
             else:
                 weight, bias = linear_weights(op.W_q, x_local.dtype)
                 q = torch.addmm(bias, x_nhwc.reshape(-1, channels), weight.t()).view(x_nhwc.shape)
-            lepe = None
+            lepe = fused_lepe = None
             if self.local_position is not None:
-                lepe = dwconv.depthwise_conv(x_local, self.local_position, dwconv.EPI_PLAIN)
+                if FUSE_LEPE_READOUT and self.local_position.kernel_size == (5, 5) and dwconv.is_depthwise(
+                        self.local_position):
+                    fused_lepe = dwconv.depthwise_taps(self.local_position)
+                else:
+                    lepe = dwconv.depthwise_conv(x_local, self.local_position, dwconv.EPI_PLAIN)
         if OVERLAP_SCAN:
             main.wait_stream(side)
         return srnl_spatial_readout(ws, x_nhwc, q, op.d_skip, weights, chunks, op.head_dim,
                                     aux=None if lepe is None else lepe.permute(0, 2, 3, 1),
-                                    out_dtype=x_local.dtype)
+                                    out_dtype=x_local.dtype, lepe=fused_lepe)
 
     def _local_features(self, x):
         """``proj_in`` followed by the local mixing of ``local_mode``."""

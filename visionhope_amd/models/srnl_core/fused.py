@@ -94,9 +94,13 @@ def srnl_spatial_scan(states, x_nhwc, chunks, workspace=None):
 
 @on_tensor_device
 def srnl_spatial_readout(workspace, x_nhwc, q_nhwc, d_skip, weights, chunks, head_dim, *, aux=None,
-                         out_dtype=torch.float32):
+                         out_dtype=torch.float32, lepe=None):
     """Second half: sum_r w_r (y_r + skip_r x) (+ aux) as ``[B, H, W, C]`` ``out_dtype``
-    (FP32 or x's dtype); aux is an optional x-dtype ``[B, H, W, C]`` addend."""
+    (FP32 or x's dtype); aux is an optional x-dtype ``[B, H, W, C]`` addend.
+
+    ``lepe = (taps, bias)`` (FP32 ``[25, C]`` taps-major and ``[C]`` or None) adds the
+    block's 5x5 depthwise position encoding of x instead, computed in the same pass
+    (``vh_srnl_spatial_readout_lepe``; output in x's dtype, no aux)."""
     batch, height, width, channels = x_nhwc.shape
     if q_nhwc.shape != x_nhwc.shape or q_nhwc.dtype != x_nhwc.dtype:
         raise ValueError("Spatial SRNL expects x and queries with the same [B, H, W, C] shape and dtype")
@@ -105,6 +109,24 @@ def srnl_spatial_readout(workspace, x_nhwc, q_nhwc, d_skip, weights, chunks, hea
     skip = d_skip.detach().float().contiguous()
     wts = weights.detach().float().contiguous()
     x_c, q_c = x_nhwc.contiguous(), q_nhwc.contiguous()
+    if lepe is not None:
+        taps, bias = lepe
+        if aux is not None or out_dtype != x_nhwc.dtype:
+            raise ValueError("The fused position encoding writes x's dtype and takes no addend")
+        if taps.shape != (25, channels) or taps.dtype != torch.float32 or (
+                bias is not None and (bias.shape != (channels,) or bias.dtype != torch.float32)):
+            raise ValueError("Position encoding taps must be FP32 [25, C] and the bias FP32 [C]")
+        taps_c = taps.contiguous()
+        bias_c = None if bias is None else bias.contiguous()
+        out = torch.empty((batch, height, width, channels), device=x_nhwc.device, dtype=out_dtype)
+        lib = hip.load_library()
+        chunk_ptr, _keep = _chunk_array(chunks)
+        hip.check(lib.vh_srnl_spatial_readout_lepe(
+            hip.ptr(x_c), hip.ptr(q_c), hip.dtype_code(x_c.dtype), hip.ptr(skip), int(skip.numel() == 4 * channels),
+            hip.ptr(wts), hip.ptr(taps_c), hip.ptr(bias_c), hip.ptr(out), batch, height, width, channels, head_dim,
+            chunk_ptr, hip.ptr(workspace), workspace.numel() * 4, hip.stream_of(x_c)),
+            "vh_srnl_spatial_readout_lepe")
+        return out
     aux_c = None if aux is None else aux.contiguous()
     out = torch.empty((batch, height, width, channels), device=x_nhwc.device, dtype=out_dtype)
     lib = hip.load_library()

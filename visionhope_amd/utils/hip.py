@@ -28,7 +28,7 @@ EXPORTED_SYMBOLS = (
     "vh_abi_version", "vh_last_error", "vh_set_dispatch_override", "vh_clear_dispatch_overrides",
     "vh_grn_workspace_fallbacks", "vh_stream_capture_id", "vh_srnl_workspace_bytes", "vh_srnl_spatial_forward",
     "vh_srnl_spatial_forward_noalloc",
-    "vh_srnl_spatial_scan", "vh_srnl_spatial_readout",
+    "vh_srnl_spatial_scan", "vh_srnl_spatial_readout", "vh_srnl_spatial_readout_lepe",
     "vh_srnl_line_forward_seq_noatomic", "vh_srnl_sequence_forward", "vh_srnl_forward",
     "vh_postprocess_scale_forward", "vh_grn_workspace_bytes", "vh_grn_forward",
     "vh_layernorm2d_forward", "vh_add_layernorm2d_forward", "vh_qnorm_forward", "vh_residual_add_forward",
@@ -81,6 +81,8 @@ _SIGNATURES = {
         _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _I64P, _CP, _vp, _sz, _vp]),
     "vh_srnl_spatial_readout": (ctypes.c_int, [
         _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _I64P, _vp, _sz, _vp]),
+    "vh_srnl_spatial_readout_lepe": (ctypes.c_int, [
+        _vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _I64P, _vp, _sz, _vp]),
     "vh_srnl_backward_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i32, _I64P]),
     "vh_srnl_backward": (ctypes.c_int, [
         _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
