@@ -40,9 +40,11 @@ def _dw_reference(x, conv, epilogue, gate=None, acc=None):
 @pytest.mark.parametrize("epilogue", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
 @pytest.mark.parametrize("tile", ["0", "2"])
-def test_depthwise_epilogues(device, dispatch, ksize, epilogue, dtype, tol, tile):
+@pytest.mark.parametrize("hw", [(9, 13), (6, 14)])
+def test_depthwise_epilogues(device, dispatch, ksize, epilogue, dtype, tol, tile, hw):
     """Both kernels (the per-thread window one, dw_tile="0", and the LDS-tiled one
-    wherever it applies, dw_tile="2"; FP32 maps always take the first)."""
+    wherever it applies, dw_tile="2"; FP32 maps always take the first), on a ragged map
+    and on one whose width 7 divides (7 pixels per thread in the window kernel)."""
     from visionhope_amd.utils import dwconv
 
     dispatch(dw_tile=tile)
@@ -53,10 +55,10 @@ def test_depthwise_epilogues(device, dispatch, ksize, epilogue, dtype, tol, tile
         conv.weight.copy_(randn(*conv.weight.shape, seed=11, scale=0.3))
         conv.bias.copy_(randn(channels, seed=12, scale=0.1))
     conv = conv.to(device)
-    # Ragged spatial shape: odd height, width not a multiple of anything.
-    x = randn(2, channels, 9, 13, seed=13).to(dtype)
-    gate = randn(2, channels, 9, 13, seed=14).to(dtype)
-    acc = randn(2, 9, 13, channels, seed=15)
+    h, w = hw
+    x = randn(2, channels, h, w, seed=13).to(dtype)
+    gate = randn(2, channels, h, w, seed=14).to(dtype)
+    acc = randn(2, h, w, channels, seed=15)
     x_dev = x.to(device).contiguous(memory_format=torch.channels_last)
     gate_dev = gate.to(device).contiguous(memory_format=torch.channels_last)
     acc_dev = acc.to(device).contiguous()

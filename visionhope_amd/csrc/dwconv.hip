@@ -494,7 +494,9 @@ namespace {
 // MI355X at the Tiny shapes (B=128; W = 56, 14 and 7): 8 pixels for 3x3, 4 for 5x5,
 // 2 for 7x7 on wide maps and 8 on narrow ones.
 inline int dw_default_pixels(int K, int64_t W) {
-    if (K == 3) return 8;
+    // 3x3: 7 on widths that 7 divides and 8 does not (the Tiny 28, 14 and 7), so no
+    // thread computes pixels past the row end; the segment count is unchanged there.
+    if (K == 3) return (W % 8 != 0 && W % 7 == 0) ? 7 : 8;
     if (K == 5) return 4;
     return W >= 28 ? 2 : 8;
 }
@@ -646,7 +648,10 @@ void launch_dw(int epi, const DwParams& dp, hipStream_t s) {
             return;
         }
     }
-    if constexpr (K == 3) launch_dw_p<K, T, 8>(epi, dp, s);
+    if constexpr (K == 3) {
+        if (dw_pixels(K, dp.W) == 7) launch_dw_p<K, T, 7>(epi, dp, s);
+        else launch_dw_p<K, T, 8>(epi, dp, s);
+    }
     else if constexpr (K == 5) launch_dw_p<K, T, 4>(epi, dp, s);
     else if (dw_pixels(K, dp.W) == 2) launch_dw_p<K, T, 2>(epi, dp, s);
     else launch_dw_p<K, T, 8>(epi, dp, s);
