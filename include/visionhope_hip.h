@@ -392,6 +392,16 @@ int vh_pointwise_conv_nhwc_forward(
     const void* residual, const float* grn_scale, const float* grn_beta, int64_t pixels_per_image,
     void* out, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Two chained 1x1 convolutions of the same pixels, as two vh_pointwise_conv_nhwc_forward
+ * calls with the bias epilogue give them: out [M, N] = bf16(x @ weight^T + bias) and out2
+ * [M, N] = bf16(out @ weight2^T + bias2), bf16 operands (x [M, K], weight [N, K], weight2
+ * [N, N]), FP32 biases or NULL, N = 64 or 128, K % 64 == 0, 16-byte aligned.  One launch:
+ * each block keeps its rows of out in LDS for the second product.  No counterpart in the
+ * reference (its block runs proj_in, then local_gate on the result: models/block.py:63-66). */
+int vh_pointwise_chain_nhwc_forward(
+    const void* x, const void* weight, const float* bias, const void* weight2, const float* bias2,
+    void* out, void* out2, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* 3x3 convolution, padding 1, stride 1 or 2, on a channels-last map as an implicit GEMM
  * on the matrix cores: out [B, Ho, Wo, N] bf16 = act(bf16(conv(x, weight) + bias)),
  * rounded to bf16 after the sum and after the activation (act 0 = none, 1 = exact GELU).

@@ -175,3 +175,45 @@ def test_grn_scale_few_and_many_images(oracle, device, batch, channels, hw):
     y = x.float() * scale.cpu()[:, :, None, None] + beta[None, :, None, None]
     expected = oracle.grn(x.float().numpy(), gamma.numpy(), beta.numpy())
     assert_close(y.numpy(), expected, 2e-5, f"GRN scale B={batch} C={channels} {hw}x{hw}")
+
+
+@pytest.mark.parametrize("m,k,n", [(25088, 256, 128), (1000, 256, 128), (37, 128, 128), (1, 64, 128),
+                                   (100352, 128, 64), (1000, 64, 64), (300, 512, 64)])
+def test_pointwise_chain_matches_two_projections(device, m, k, n):
+    """``vh_pointwise_chain_nhwc_forward``: out = proj_in(x) and out2 = local_gate(out) in one
+    launch.  out has the bits of a separate projection (same tiles, same k order); at
+    N = 128 so does out2 (the separate launch of the N x N product takes the same 64 x 128
+    tiles), at N = 64 the separate launch takes the LDS-free kernel, so out2 is held to
+    the FP64 product of the bf16 operands (one bf16 rounding, 5e-3)."""
+    from visionhope_amd.utils import pointwise
+
+    first, second = nn.Linear(k, n), nn.Linear(n, n)
+    with torch.no_grad():
+        for lin, seed in ((first, 31), (second, 32)):
+            lin.weight.copy_(randn(*lin.weight.shape, seed=seed, scale=lin.weight.shape[1] ** -0.5))
+            lin.bias.copy_(randn(lin.bias.shape[0], seed=seed + 1, scale=0.1))
+    x = _bf16(randn(m, k, seed=33))
+    first_d, second_d = first.to(device), second.to(device)
+    print(f"\n[case] chain M={m} K={k} N={n}", flush=True)
+    xd = x.to(device)
+    out, out2 = pointwise.pointwise_chain(xd, first_d, second_d)
+    ref1 = pointwise.pointwise_conv(xd, first_d)
+    ref2 = pointwise.pointwise_conv(ref1, second_d)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref1), "first product differs from the separate projection"
+    if n == 128:
+        assert torch.equal(out2, ref2), "second product differs from the separate projection"
+    expected = _linear_ref(out.cpu(), second)
+    assert_close(out2.double().cpu().numpy(), expected.double().numpy(), 5e-3, "chained second product")
+
+
+def test_pointwise_chain_declines_other_widths(device):
+    from visionhope_amd.utils import pointwise
+
+    assert not pointwise.chain_supported(nn.Linear(256, 256), nn.Linear(256, 256))   # N = 256
+    assert not pointwise.chain_supported(nn.Linear(96, 128), nn.Linear(128, 128))    # K % 64
+    assert not pointwise.chain_supported(nn.Linear(256, 128), nn.Linear(128, 64))    # second not N x N
+    assert pointwise.chain_supported(nn.Linear(256, 128), nn.Linear(128, 128))
+    with pytest.raises(ValueError):
+        pointwise.pointwise_chain(torch.zeros(4, 96, device=device, dtype=torch.bfloat16), nn.Linear(96, 128).to(device),
+                                  nn.Linear(128, 128).to(device))

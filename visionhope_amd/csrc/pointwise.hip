@@ -212,11 +212,16 @@ __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "
 
 // NI > 0: GRN prologue, the k tile's scale rows of the NI images a block can span (at least
 // BM / (NI - 1) pixels per image) and beta staged in LDS with the operand tiles.
-template <int BM, int BN, int WGM, int EPI, int NI, int OCC>
+// CHAIN (N = BN, bias epilogue): the block's output rows, rounded to bf16 and stored, are
+// also written to LDS in the operand layout and multiplied by w2 (N x N, its k tiles
+// copied into the ring meanwhile) for out2, the next 1x1 projection of the same pixels,
+// with the k order and tile layout of a separate launch of this kernel (the same bits).
+template <int BM, int BN, int WGM, int EPI, int NI, int OCC, bool CHAIN = false>
 __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams p) {
     constexpr int BK = 64, WGN = 4 / WGM, WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
     constexpr bool PRO = NI > 0;
     static_assert(TN % 2 == 0 && BM % 32 == 0 && BN % 32 == 0 && NI >= 0 && NI <= 3, "tile shape");
+    static_assert(!CHAIN || (NI == 0 && EPI == PW_BIAS && BN % 64 == 0 && BN / 64 <= 3), "chained product");
     constexpr int A_INS = BM / 32, B_INS = BN / 32;             // wave instructions per operand and stage
     constexpr int D = A_INS + B_INS + (PRO ? 1 : 0);            // copies per wave and stage
     constexpr int GRN_CPW = (NI + 1) * BK / 16;                 // 16-byte GRN chunks per wave and stage
@@ -323,6 +328,83 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
 #pragma unroll
                 for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = mfma_16x16x32(af[tn], bfr[tm], acc[tn][tm]);
         }
+    }
+
+    if constexpr (CHAIN) {
+        constexpr int NT2 = BN / 64;   // k tiles of the second product
+        // Every wave has consumed its last operand reads (their values fed the products
+        // above), so after the barrier the ring is free: w2's k tiles go to the B areas of
+        // stages 0 .. NT2 - 1 while this block's output rows go to their A areas.
+        block_barrier();
+        const int K2 = BN;
+#pragma unroll
+        for (int kt = 0; kt < NT2; ++kt) {
+#pragma unroll
+            for (int i = 0; i < B_INS; ++i) {
+                const int R = (wv * B_INS + i) * 8 + lrow, rn = R / WN, rr = R % WN;
+                const bf16_t* src = p.w2 + static_cast<int64_t>(rn * WN + pw_wrow(rr / 16, rr % 16)) * K2 + 8 * lchunk +
+                                    kt * BK;
+                lds_dma16(src, __builtin_amdgcn_readfirstlane(lds0 + kt * STAGE + BM * BK * 2 + (wv * B_INS + i) * 1024));
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < TN / 2; ++q) {
+            const int nl = wn * WN + 32 * q + 8 * kg;   // n0 = 0: the block covers all N = BN outputs
+            float bv[8];
+            pw_bias8(p, nl, bv);
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const int r = wm * WM + 16 * tm + i16;
+                const int64_t m = m0 + r;
+                const v4f_pw& a0 = acc[2 * q][tm];
+                const v4f_pw& a1 = acc[2 * q + 1][tm];
+                // bf16(acc + bias) as pw_store8 rounds it (two values per conversion)
+                const uint4 w = make_uint4(pack_bf16x2(a0[0] + bv[0], a0[1] + bv[1]), pack_bf16x2(a0[2] + bv[2], a0[3] + bv[3]),
+                                           pack_bf16x2(a1[0] + bv[4], a1[1] + bv[5]), pack_bf16x2(a1[2] + bv[6], a1[3] + bv[7]));
+                if (m < p.M) *reinterpret_cast<uint4*>(p.out + m * p.N + nl) = w;
+                *reinterpret_cast<uint4*>(lds + (nl / BK) * STAGE + slot(r, (nl % BK) / 8)) = w;
+            }
+        }
+        wait_vmem<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        block_barrier();
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = v4f_pw{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kt = 0; kt < NT2; ++kt) {
+            const unsigned char* sa = lds + kt * STAGE;
+            const unsigned char* sbp = sa + BM * BK * 2;
+#pragma unroll
+            for (int ks = 0; ks < BK / 32; ++ks) {
+                const int c = 4 * ks + kg;
+                uint4 af[TN], bfr[TM];
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) af[tn] = *reinterpret_cast<const uint4*>(sbp + slot(brow[tn], c));
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) bfr[tm] = *reinterpret_cast<const uint4*>(sa + slot(wm * WM + 16 * tm + i16, c));
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = mfma_16x16x32(af[tn], bfr[tm], acc[tn][tm]);
+            }
+        }
+        PwParams p2 = p;
+        p2.bias = p.bias2;
+        p2.out = p.out2;
+#pragma unroll
+        for (int q = 0; q < TN / 2; ++q) {
+            const int n = wn * WN + 32 * q + 8 * kg;
+            float bv[8];
+            pw_bias8(p2, n, bv);
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const int64_t m = m0 + wm * WM + 16 * tm + i16;
+                if (m < p.M) pw_store8<PW_BIAS>(p2, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm]);
+            }
+        }
+        return;
     }
 
 #pragma unroll
@@ -743,4 +825,41 @@ extern "C" int vh_pointwise_conv_nhwc_forward(const void* x, int32_t io_dtype, c
         case PW_SILU: return pro ? launch_pw<PW_SILU, true>(p, s) : launch_pw<PW_SILU, false>(p, s);
         default: return pro ? launch_pw<PW_ADD, true>(p, s) : launch_pw<PW_ADD, false>(p, s);
     }
+}
+
+extern "C" int vh_pointwise_chain_nhwc_forward(const void* x, const void* weight, const float* bias,
+                                               const void* weight2, const float* bias2, void* out, void* out2,
+                                               int64_t M, int64_t N, int64_t K, void* stream) {
+    VH_REQUIRE(x && weight && weight2 && out && out2, VH_ERR_ARG, "chained pointwise conv pointers must not be null");
+    VH_REQUIRE(M > 0 && M < (int64_t(1) << 31), VH_ERR_SHAPE, "chained pointwise conv expects 0 < M < 2^31");
+    VH_REQUIRE(N == 64 || N == 128, VH_ERR_SHAPE, "chained pointwise conv takes N = 64 or 128, got %lld", (long long)N);
+    VH_REQUIRE(K % 64 == 0 && K >= 64 && K <= 65536, VH_ERR_SHAPE,
+               "chained pointwise conv needs K %% 64 == 0 (64 .. 65536), got %lld", (long long)K);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+                            reinterpret_cast<uintptr_t>(weight2) | reinterpret_cast<uintptr_t>(out) |
+                            reinterpret_cast<uintptr_t>(out2) | reinterpret_cast<uintptr_t>(bias) |
+                            reinterpret_cast<uintptr_t>(bias2);
+    VH_REQUIRE(align % 16 == 0, VH_ERR_ARG, "chained pointwise conv tensors must be 16-byte aligned");
+    PwParams p{};
+    p.x = static_cast<const bf16_t*>(x);
+    p.w = static_cast<const bf16_t*>(weight);
+    p.bias = bias;
+    p.out = static_cast<bf16_t*>(out);
+    p.M = M;
+    p.N = static_cast<int>(N);
+    p.K = static_cast<int>(K);
+    p.rows_per_image = make_fastdiv(1u);
+    p.w2 = static_cast<const bf16_t*>(weight2);
+    p.bias2 = bias2;
+    p.out2 = static_cast<bf16_t*>(out2);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // The tiles of the separate launches at these widths (64 x 128, and 128 x 64 for N = 64).
+    if (N == 128) {
+        hipLaunchKernelGGL((pointwise_dma_kernel<64, 128, 2, PW_BIAS, 0, 3, true>),
+                           dim3(static_cast<unsigned>((M + 63) / 64)), dim3(256), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((pointwise_dma_kernel<128, 64, 2, PW_BIAS, 0, 3, true>),
+                           dim3(static_cast<unsigned>((M + 127) / 128)), dim3(256), 0, s, p);
+    }
+    return check_launch("pointwise_dma_kernel (chained)");
 }

@@ -24,6 +24,11 @@ struct PwParams {
     int64_t M;
     int N, K;
     FastDiv rows_per_image; // pixels per image (prologue)
+    // chained product (pointwise_dma_kernel CHAIN): out2 [M, N] = bf16(out @ w2^T + bias2),
+    // w2 [N, N] bf16, bias2 [N] fp32 or null
+    const bf16_t* w2;
+    const float* bias2;
+    bf16_t* out2;
 };
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));

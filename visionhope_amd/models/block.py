@@ -33,6 +33,10 @@ FUSE_CPE_LAYERNORM = True
 # than the overlap saved; Tiny forward 9.52 -> 9.42 ms measured on MI355X).
 OVERLAP_SCAN = False
 
+# proj_in and local_gate (gated local mixing) as one chained launch where the widths allow
+# (True), or as two projections (False, for measurements); the same bits either way.
+FUSE_GATE_CHAIN = True
+
 # The local position encoding (5x5 depthwise of x_local) computed inside the operator's
 # readout (True: one pass, the same bits) or as a separate depthwise pass whose result the
 # readout adds (False, for measurements).
@@ -71,7 +75,12 @@ def _matrix_core_ok(t_nhwc, module, grn_prologue=False):
     pixels = t_nhwc.numel() // max(t_nhwc.shape[-1], 1)
     return (t_nhwc.is_contiguous() and t_nhwc.data_ptr() % 16 == 0 and module.bias is not None
             and pointwise.supported(k, n) and t_nhwc.shape[-1] == k
-            and (grn_prologue or pixels >= _LIBRARY_MAX_PIXELS or k * n < _LIBRARY_MIN_KN))
+            and (grn_prologue or _native_size(pixels, k, n)))
+
+
+def _native_size(pixels, k, n):
+    """The size rule of ``_matrix_core_ok``: the library GEMM keeps deep, short products."""
+    return pixels >= _LIBRARY_MAX_PIXELS or k * n < _LIBRARY_MIN_KN
 
 
 def _grn_beta(grn):
@@ -212,9 +221,19 @@ class VisionHOPEBlock(nn.Module):
         if h is None:
             h = visionhope_layernorm2d(x, self.norm1.weight, self.norm1.bias, self.norm1.eps,
                                        force_channels_last=True, out_dtype=act)
-        inner = project(h.permute(0, 2, 3, 1), self.proj_in)
+        h_nhwc = h.permute(0, 2, 3, 1)
+        gate = None
+        if (self.local_mode == "gated_dwconv7" and FUSE_GATE_CHAIN and act == torch.bfloat16
+                and pointwise.chain_supported(self.proj_in, self.local_gate) and _matrix_core_ok(h_nhwc, self.proj_in)
+                and _native_size(h_nhwc.numel() // h_nhwc.shape[-1], self.local_gate.weight.shape[1],
+                                 self.local_gate.weight.shape[0])):
+            # proj_in and local_gate in one launch (the same bits as the two projections)
+            inner, gate = pointwise.pointwise_chain(h_nhwc, self.proj_in, self.local_gate)
+        else:
+            inner = project(h_nhwc, self.proj_in)
         if self.local_mode == "gated_dwconv7":
-            gate = project(inner, self.local_gate)
+            if gate is None:
+                gate = project(inner, self.local_gate)
             x_local = dwconv.depthwise_conv(nchw(inner), self.local_conv, dwconv.EPI_GATE, aux=nchw(gate))
         elif self.local_mode == "residual_dwconv":
             x_local = dwconv.depthwise_conv(nchw(inner), self.local_conv, dwconv.EPI_ADD_INPUT)

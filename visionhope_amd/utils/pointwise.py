@@ -107,3 +107,37 @@ def pointwise_gemm(x, weight, bias, epilogue=EPI_BIAS, residual=None, grn=None, 
         hip.ptr(scale), hip.ptr(beta), per_image, hip.ptr(out), m, n, k, hip.stream_of(x)),
         "vh_pointwise_conv_nhwc_forward")
     return out
+
+
+def chain_supported(first, second):
+    """Whether ``pointwise_chain`` covers ``second(first(x))``: two 1x1 projections with
+    biases, ``first`` K -> N (K % 64 == 0) and ``second`` N -> N, N = 64 or 128."""
+    if not (is_pointwise(first) and is_pointwise(second)) or first.bias is None or second.bias is None:
+        return False
+    n, k = first.weight.shape[0], first.weight.shape[1]
+    return n in (64, 128) and k % 64 == 0 and tuple(second.weight.shape[:2]) == (n, n)
+
+
+@on_tensor_device
+def pointwise_chain(x, first, second):
+    """``(first(x), second(first(x)))`` for ``x [..., K]`` contiguous bf16, both rounded to
+    bf16 as two ``pointwise_conv`` calls give them, in one launch
+    (``vh_pointwise_chain_nhwc_forward``); ``chain_supported`` must hold."""
+    if not chain_supported(first, second):
+        raise ValueError("pointwise_chain covers K -> N -> N projections with N = 64 or 128 and K % 64 == 0")
+    if not x.is_cuda or x.dtype != torch.bfloat16 or not x.is_contiguous() or x.data_ptr() % 16:
+        raise ValueError("pointwise_chain expects a contiguous 16-byte aligned CUDA bf16 tensor")
+    w1, b1 = pointwise_operands(first)
+    w2, b2 = pointwise_operands(second)
+    n, k = w1.shape
+    if x.shape[-1] != k:
+        raise ValueError(f"pointwise_chain expects {k} input channels, got {x.shape[-1]}")
+    m = x.numel() // k
+    shape = (*x.shape[:-1], n)
+    out = torch.empty(shape, device=x.device, dtype=torch.bfloat16)
+    out2 = torch.empty(shape, device=x.device, dtype=torch.bfloat16)
+    lib = hip.load_library()
+    hip.check(lib.vh_pointwise_chain_nhwc_forward(
+        hip.ptr(x), hip.ptr(w1), hip.ptr(b1), hip.ptr(w2), hip.ptr(b2), hip.ptr(out), hip.ptr(out2), m, n, k,
+        hip.stream_of(x)), "vh_pointwise_chain_nhwc_forward")
+    return out, out2
