@@ -395,7 +395,8 @@ int vh_pointwise_conv_nhwc_forward(
 /* Two chained 1x1 convolutions of the same pixels, as two vh_pointwise_conv_nhwc_forward
  * calls with the bias epilogue give them: out [M, N] = bf16(x @ weight^T + bias) and out2
  * [M, N] = bf16(out @ weight2^T + bias2), bf16 operands (x [M, K], weight [N, K], weight2
- * [N, N]), FP32 biases or NULL, N = 64 or 128, K % 64 == 0, 16-byte aligned.  One launch:
+ * [N, N]), FP32 biases or NULL, N = 64 or 128 with K % 64 == 0, or N = 32 with K = 32 or 64,
+ * 16-byte aligned.  One launch:
  * each block keeps its rows of out in LDS for the second product.  No counterpart in the
  * reference (its block runs proj_in, then local_gate on the result: models/block.py:63-66). */
 int vh_pointwise_chain_nhwc_forward(

@@ -178,13 +178,15 @@ def test_grn_scale_few_and_many_images(oracle, device, batch, channels, hw):
 
 
 @pytest.mark.parametrize("m,k,n", [(25088, 256, 128), (1000, 256, 128), (37, 128, 128), (1, 64, 128),
-                                   (100352, 128, 64), (1000, 64, 64), (300, 512, 64)])
+                                   (100352, 128, 64), (1000, 64, 64), (300, 512, 64),
+                                   (401408, 64, 32), (1000, 64, 32), (37, 32, 32), (1, 32, 32)])
 def test_pointwise_chain_matches_two_projections(device, m, k, n):
     """``vh_pointwise_chain_nhwc_forward``: out = proj_in(x) and out2 = local_gate(out) in one
     launch.  out has the bits of a separate projection (same tiles, same k order); at
-    N = 128 so does out2 (the separate launch of the N x N product takes the same 64 x 128
-    tiles), at N = 64 the separate launch takes the LDS-free kernel, so out2 is held to
-    the FP64 product of the bf16 operands (one bf16 rounding, 5e-3)."""
+    N = 128 and 32 so does out2 (the separate launch of the N x N product takes the same
+    64 x 128 tiles, or the same LDS-free kernel), at N = 64 the separate launch takes the
+    LDS-free kernel and the chain 128 x 64 tiles, so out2 is also held to the FP64 product
+    of the bf16 operands (one bf16 rounding, 5e-3)."""
     from visionhope_amd.utils import pointwise
 
     first, second = nn.Linear(k, n), nn.Linear(n, n)
@@ -201,7 +203,7 @@ def test_pointwise_chain_matches_two_projections(device, m, k, n):
     ref2 = pointwise.pointwise_conv(ref1, second_d)
     torch.cuda.synchronize()
     assert torch.equal(out, ref1), "first product differs from the separate projection"
-    if n == 128:
+    if n in (32, 128):
         assert torch.equal(out2, ref2), "second product differs from the separate projection"
     expected = _linear_ref(out.cpu(), second)
     assert_close(out2.double().cpu().numpy(), expected.double().numpy(), 5e-3, "chained second product")
@@ -212,6 +214,7 @@ def test_pointwise_chain_declines_other_widths(device):
 
     assert not pointwise.chain_supported(nn.Linear(256, 256), nn.Linear(256, 256))   # N = 256
     assert not pointwise.chain_supported(nn.Linear(96, 128), nn.Linear(128, 128))    # K % 64
+    assert not pointwise.chain_supported(nn.Linear(128, 32), nn.Linear(32, 32))      # N = 32 needs K <= 64
     assert not pointwise.chain_supported(nn.Linear(256, 128), nn.Linear(128, 64))    # second not N x N
     assert pointwise.chain_supported(nn.Linear(256, 128), nn.Linear(128, 128))
     with pytest.raises(ValueError):

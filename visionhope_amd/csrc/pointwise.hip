@@ -557,9 +557,14 @@ __global__ __launch_bounds__(256, 2) void pointwise_resident_kernel(const PwPara
 // every output channel; it issues all loads of its x rows at once (TM * KS 16-byte
 // fragments), reads the small weight fragments through L1 and writes each pixel's
 // channels once.
-template <int KS, int TN, int TM, int EPI, bool PRO>
+// CHAIN (bias epilogue): out2 = bf16(out @ w2^T + bias2) too, w2 N x N.  A lane ends the
+// first product with 8 consecutive channels of one pixel, 32 q + 8 kg .. + 7, which is
+// the operand fragment of k step q of the second product for that pixel, so the packed
+// bf16 output feeds it directly (the bits a separate launch would load).
+template <int KS, int TN, int TM, int EPI, bool PRO, bool CHAIN = false>
 __global__ __launch_bounds__(256) void pointwise_narrow_kernel(const PwParams p) {
     static_assert(TN % 2 == 0, "n tiles come in pairs");
+    static_assert(!CHAIN || (EPI == PW_BIAS && !PRO), "chained product: bias epilogue, no prologue");
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, i16 = lane & 15, kg = lane >> 4;
     const int64_t m_wave = (static_cast<int64_t>(xcd_remap_any(blockIdx.x, gridDim.x)) * 4 + wv) * (16 * TM);
     if (m_wave >= p.M) return;
@@ -593,6 +598,56 @@ __global__ __launch_bounds__(256) void pointwise_narrow_kernel(const PwParams p)
         for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = mfma_16x16x32(wf[tn], xf[tm][ks], acc[tn][tm]);
+    }
+    if constexpr (CHAIN) {
+        constexpr int K2 = 16 * TN;   // = N
+        uint4 yf[TN / 2][TM];         // bf16 output fragments: k step q of the second product
+#pragma unroll
+        for (int q = 0; q < TN / 2; ++q) {
+            const int n = 32 * q + 8 * kg;
+            float bv[8];
+            pw_bias8(p, n, bv);
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const v4f_pw& a0 = acc[2 * q][tm];
+                const v4f_pw& a1 = acc[2 * q + 1][tm];
+                // bf16(acc + bias) as pw_store8 rounds it (two values per conversion)
+                yf[q][tm] = make_uint4(pack_bf16x2(a0[0] + bv[0], a0[1] + bv[1]), pack_bf16x2(a0[2] + bv[2], a0[3] + bv[3]),
+                                       pack_bf16x2(a1[0] + bv[4], a1[1] + bv[5]), pack_bf16x2(a1[2] + bv[6], a1[3] + bv[7]));
+                const int64_t m = m_wave + 16 * tm + i16;
+                if (m < p.M) *reinterpret_cast<uint4*>(p.out + m * p.N + n) = yf[q][tm];
+            }
+        }
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = v4f_pw{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < TN / 2; ++ks) {
+            uint4 wf[TN];
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn)
+                wf[tn] = *reinterpret_cast<const uint4*>(p.w2 + pw_wrow(tn, i16) * K2 + 32 * ks + 8 * kg);
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = mfma_16x16x32(wf[tn], yf[ks][tm], acc[tn][tm]);
+        }
+        PwParams p2 = p;
+        p2.bias = p.bias2;
+        p2.out = p.out2;
+#pragma unroll
+        for (int q = 0; q < TN / 2; ++q) {
+            const int n = 32 * q + 8 * kg;
+            float bv[8];
+            pw_bias8(p2, n, bv);
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const int64_t m = m_wave + 16 * tm + i16;
+                if (m < p.M) pw_store8<PW_BIAS>(p2, m, n, bv, acc[2 * q][tm], acc[2 * q + 1][tm]);
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int q = 0; q < TN / 2; ++q) {
@@ -832,9 +887,9 @@ extern "C" int vh_pointwise_chain_nhwc_forward(const void* x, const void* weight
                                                int64_t M, int64_t N, int64_t K, void* stream) {
     VH_REQUIRE(x && weight && weight2 && out && out2, VH_ERR_ARG, "chained pointwise conv pointers must not be null");
     VH_REQUIRE(M > 0 && M < (int64_t(1) << 31), VH_ERR_SHAPE, "chained pointwise conv expects 0 < M < 2^31");
-    VH_REQUIRE(N == 64 || N == 128, VH_ERR_SHAPE, "chained pointwise conv takes N = 64 or 128, got %lld", (long long)N);
-    VH_REQUIRE(K % 64 == 0 && K >= 64 && K <= 65536, VH_ERR_SHAPE,
-               "chained pointwise conv needs K %% 64 == 0 (64 .. 65536), got %lld", (long long)K);
+    VH_REQUIRE(((N == 64 || N == 128) && K % 64 == 0 && K >= 64 && K <= 65536) || (N == 32 && (K == 32 || K == 64)),
+               VH_ERR_SHAPE, "chained pointwise conv takes N = 64 or 128 with K %% 64 == 0, or N = 32 with K = 32 or 64; "
+               "got N = %lld, K = %lld", (long long)N, (long long)K);
     const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
                             reinterpret_cast<uintptr_t>(weight2) | reinterpret_cast<uintptr_t>(out) |
                             reinterpret_cast<uintptr_t>(out2) | reinterpret_cast<uintptr_t>(bias) |
@@ -853,8 +908,13 @@ extern "C" int vh_pointwise_chain_nhwc_forward(const void* x, const void* weight
     p.bias2 = bias2;
     p.out2 = static_cast<bf16_t*>(out2);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // The tiles of the separate launches at these widths (64 x 128, and 128 x 64 for N = 64).
-    if (N == 128) {
+    // The tiles of the separate launches at these widths (64 x 128, 128 x 64 for N = 64, and
+    // the LDS-free kernel with 64 pixels per wave for N = 32).
+    if (N == 32) {
+        const dim3 grid(static_cast<unsigned>((M + 255) / 256));
+        if (K == 32) hipLaunchKernelGGL((pointwise_narrow_kernel<1, 2, 4, PW_BIAS, false, true>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((pointwise_narrow_kernel<2, 2, 4, PW_BIAS, false, true>), grid, dim3(256), 0, s, p);
+    } else if (N == 128) {
         hipLaunchKernelGGL((pointwise_dma_kernel<64, 128, 2, PW_BIAS, 0, 3, true>),
                            dim3(static_cast<unsigned>((M + 63) / 64)), dim3(256), 0, s, p);
     } else {

@@ -111,11 +111,13 @@ def pointwise_gemm(x, weight, bias, epilogue=EPI_BIAS, residual=None, grn=None, 
 
 def chain_supported(first, second):
     """Whether ``pointwise_chain`` covers ``second(first(x))``: two 1x1 projections with
-    biases, ``first`` K -> N (K % 64 == 0) and ``second`` N -> N, N = 64 or 128."""
+    biases, ``first`` K -> N and ``second`` N -> N, with N = 64 or 128 and K % 64 == 0, or
+    N = 32 and K = 32 or 64."""
     if not (is_pointwise(first) and is_pointwise(second)) or first.bias is None or second.bias is None:
         return False
     n, k = first.weight.shape[0], first.weight.shape[1]
-    return n in (64, 128) and k % 64 == 0 and tuple(second.weight.shape[:2]) == (n, n)
+    widths = (n in (64, 128) and k % 64 == 0) or (n == 32 and k in (32, 64))
+    return widths and tuple(second.weight.shape[:2]) == (n, n)
 
 
 @on_tensor_device
@@ -124,7 +126,8 @@ def pointwise_chain(x, first, second):
     bf16 as two ``pointwise_conv`` calls give them, in one launch
     (``vh_pointwise_chain_nhwc_forward``); ``chain_supported`` must hold."""
     if not chain_supported(first, second):
-        raise ValueError("pointwise_chain covers K -> N -> N projections with N = 64 or 128 and K % 64 == 0")
+        raise ValueError("pointwise_chain covers K -> N -> N projections with N = 64 or 128 and K % 64 == 0, "
+                         "or N = 32 and K = 32 or 64")
     if not x.is_cuda or x.dtype != torch.bfloat16 or not x.is_contiguous() or x.data_ptr() % 16:
         raise ValueError("pointwise_chain expects a contiguous 16-byte aligned CUDA bf16 tensor")
     w1, b1 = pointwise_operands(first)
