@@ -403,6 +403,19 @@ int vh_pointwise_chain_nhwc_forward(
     const void* x, const void* weight, const float* bias, const void* weight2, const float* bias2,
     void* out, void* out2, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* A 1x1 convolution with the residual add and the LayerNorm that follow it in the block
+ * (proj_out, then norm2 of the sum), in one launch: out_sum [M, N] = bf16(residual +
+ * bf16(x @ weight^T + bias)) and out_norm [M, N] = bf16(LayerNorm(out_sum)) over the N
+ * channels of each pixel (ln_weight, ln_bias [N] fp32, eps), all bf16 but the affine and
+ * bias; N = 64 with K = 32 or 64, or N = 128 or 256 with K = 64 or 128; 16-byte aligned.
+ * The bits of vh_pointwise_conv_nhwc_forward (bias epilogue) followed by
+ * vh_add_layernorm2d_forward: the LayerNorm sums run in that kernel's order.  No
+ * counterpart in the reference (its block adds the branch and applies norm2 in separate
+ * steps: models/block.py:104-106). */
+int vh_pointwise_add_layernorm_nhwc_forward(
+    const void* x, const void* weight, const float* bias, const void* residual, const float* ln_weight,
+    const float* ln_bias, float eps, void* out_sum, void* out_norm, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* 3x3 convolution, padding 1, stride 1 or 2, on a channels-last map as an implicit GEMM
  * on the matrix cores: out [B, Ho, Wo, N] bf16 = act(bf16(conv(x, weight) + bias)),
  * rounded to bf16 after the sum and after the activation (act 0 = none, 1 = exact GELU).

@@ -220,3 +220,42 @@ def test_pointwise_chain_declines_other_widths(device):
     with pytest.raises(ValueError):
         pointwise.pointwise_chain(torch.zeros(4, 96, device=device, dtype=torch.bfloat16), nn.Linear(96, 128).to(device),
                                   nn.Linear(128, 128).to(device))
+
+
+@pytest.mark.parametrize("m,k,n", [(401408, 32, 64), (1000, 64, 64), (100352, 64, 128), (37, 128, 128),
+                                   (25088, 128, 256), (1000, 64, 256), (1, 128, 256)])
+def test_pointwise_add_layernorm_matches_separate_kernels(device, m, k, n):
+    """``vh_pointwise_add_layernorm_nhwc_forward`` (proj_out + residual add + norm2) against
+    the projection followed by the channels-last add + LayerNorm kernel: the same bits,
+    the LayerNorm sums running in that kernel's order; and against FP64 (two bf16
+    roundings of the sum and of the output)."""
+    from visionhope_amd.utils import pointwise
+    from visionhope_amd.utils.layer_norm_cuda import visionhope_add_layernorm2d
+
+    lin = nn.Linear(k, n)
+    with torch.no_grad():
+        lin.weight.copy_(randn(n, k, seed=41, scale=k ** -0.5))
+        lin.bias.copy_(randn(n, seed=42, scale=0.1))
+    x = _bf16(randn(m, k, seed=43))
+    res = _bf16(randn(m, n, seed=44))
+    lw = 1 + randn(n, seed=45, scale=0.2)
+    lb = randn(n, seed=46, scale=0.2)
+    lin_d = lin.to(device)
+    print(f"\n[case] proj + add + LayerNorm M={m} K={k} N={n}", flush=True)
+    xd, rd, lwd, lbd = x.to(device), res.to(device), lw.to(device), lb.to(device)
+    s, h = pointwise.pointwise_add_layernorm(xd, lin_d, rd, lwd, lbd, 1e-6)
+    branch = pointwise.pointwise_conv(xd, lin_d)
+    # the add + LayerNorm kernel on [1, N, 1, M] channels-last views of the same rows
+    as_map = lambda t: t.reshape(1, 1, m, n).permute(0, 3, 1, 2)
+    s_ref, h_ref = visionhope_add_layernorm2d(as_map(rd), as_map(branch), lwd, lbd, 1e-6, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    s_ref = s_ref.permute(0, 2, 3, 1).reshape(m, n)
+    h_ref = h_ref.permute(0, 2, 3, 1).reshape(m, n)
+    ds, dh = (s != s_ref).sum().item(), (h != h_ref).sum().item()
+    print(f"[bits] sum differs in {ds}, norm in {dh} of {m * n}", flush=True)
+    assert ds == 0 and dh == 0
+    s64 = (res.double() + _linear_ref(x, lin).double()).to(torch.bfloat16).double()
+    mu = s64.mean(-1, keepdim=True)
+    var = ((s64 - mu) ** 2).mean(-1, keepdim=True)
+    expected = (s64 - mu) / torch.sqrt(var + 1e-6) * lw.double() + lb.double()
+    assert_close(h.double().cpu().numpy(), expected.numpy(), 1e-2, "fused add + LayerNorm")

@@ -222,12 +222,15 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
     constexpr bool PRO = NI > 0;
     static_assert(TN % 2 == 0 && BM % 32 == 0 && BN % 32 == 0 && NI >= 0 && NI <= 3, "tile shape");
     static_assert(!CHAIN || (NI == 0 && EPI == PW_BIAS && BN % 64 == 0 && BN / 64 <= 3), "chained product");
+    static_assert(EPI != PW_ADD_LN || (WGM == 4 && NI == 0 && !CHAIN), "add + LayerNorm: whole pixel rows per wave");
     constexpr int A_INS = BM / 32, B_INS = BN / 32;             // wave instructions per operand and stage
     constexpr int D = A_INS + B_INS + (PRO ? 1 : 0);            // copies per wave and stage
     constexpr int GRN_CPW = (NI + 1) * BK / 16;                 // 16-byte GRN chunks per wave and stage
     constexpr int GRN_BYTES = PRO ? (NI + 1) * BK * 4 : 0;
     constexpr int STAGE = (BM + BN) * BK * 2 + GRN_BYTES;
-    __shared__ __align__(16) unsigned char lds[3 * STAGE];
+    // PW_ADD_LN launches have at most two k tiles (K <= 128, checked on the host): two stages
+    constexpr int NSTAGE = EPI == PW_ADD_LN ? 2 : 3;
+    __shared__ __align__(16) unsigned char lds[NSTAGE * STAGE];
     __shared__ float gtab[EPI == PW_GELU ? GELU_TAB_N : 1];
     if constexpr (EPI == PW_GELU) {
         gelu_tab_fill(gtab, static_cast<int>(threadIdx.x), 256);
@@ -330,6 +333,15 @@ __global__ __launch_bounds__(256, OCC) void pointwise_dma_kernel(const PwParams 
         }
     }
 
+    if constexpr (EPI == PW_ADD_LN) {
+        // one tile across all N = BN channels (n0 = 0): the pixel's LayerNorm in the epilogue
+        v4f_pw a[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) a[tn] = acc[tn][0];
+        const int64_t m = m0 + wm * WM + i16;
+        pw_add_ln_store<TN / 2>(p, m, m < p.M, kg, a);
+        return;
+    }
     if constexpr (CHAIN) {
         constexpr int NT2 = BN / 64;   // k tiles of the second product
         // Every wave has consumed its last operand reads (their values fed the products
@@ -598,6 +610,17 @@ __global__ __launch_bounds__(256) void pointwise_narrow_kernel(const PwParams p)
         for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = mfma_16x16x32(wf[tn], xf[tm][ks], acc[tn][tm]);
+    }
+    if constexpr (EPI == PW_ADD_LN) {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            v4f_pw a[TN];
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) a[tn] = acc[tn][tm];
+            const int64_t m = m_wave + 16 * tm + i16;
+            pw_add_ln_store<TN / 2>(p, m, m < p.M, kg, a);
+        }
+        return;
     }
     if constexpr (CHAIN) {
         constexpr int K2 = 16 * TN;   // = N
@@ -922,4 +945,50 @@ extern "C" int vh_pointwise_chain_nhwc_forward(const void* x, const void* weight
                            dim3(static_cast<unsigned>((M + 127) / 128)), dim3(256), 0, s, p);
     }
     return check_launch("pointwise_dma_kernel (chained)");
+}
+
+extern "C" int vh_pointwise_add_layernorm_nhwc_forward(const void* x, const void* weight, const float* bias,
+                                                       const void* residual, const float* ln_weight,
+                                                       const float* ln_bias, float eps, void* out_sum, void* out_norm,
+                                                       int64_t M, int64_t N, int64_t K, void* stream) {
+    VH_REQUIRE(x && weight && residual && ln_weight && ln_bias && out_sum && out_norm, VH_ERR_ARG,
+               "pointwise conv + add + LayerNorm pointers must not be null");
+    VH_REQUIRE(M > 0 && M < (int64_t(1) << 31), VH_ERR_SHAPE, "pointwise conv + add + LayerNorm expects 0 < M < 2^31");
+    VH_REQUIRE((N == 64 && (K == 32 || K == 64)) || ((N == 128 || N == 256) && (K == 64 || K == 128)), VH_ERR_SHAPE,
+               "pointwise conv + add + LayerNorm takes N = 64 with K = 32 or 64, or N = 128 or 256 with K = 64 or 128; "
+               "got N = %lld, K = %lld", (long long)N, (long long)K);
+    VH_REQUIRE(eps > 0.f, VH_ERR_ARG, "LayerNorm eps must be positive");
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+                            reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(residual) |
+                            reinterpret_cast<uintptr_t>(ln_weight) | reinterpret_cast<uintptr_t>(ln_bias) |
+                            reinterpret_cast<uintptr_t>(out_sum) | reinterpret_cast<uintptr_t>(out_norm);
+    VH_REQUIRE(align % 16 == 0, VH_ERR_ARG, "pointwise conv + add + LayerNorm tensors must be 16-byte aligned");
+    PwParams p{};
+    p.x = static_cast<const bf16_t*>(x);
+    p.w = static_cast<const bf16_t*>(weight);
+    p.bias = bias;
+    p.res = static_cast<const bf16_t*>(residual);
+    p.out = static_cast<bf16_t*>(out_sum);
+    p.M = M;
+    p.N = static_cast<int>(N);
+    p.K = static_cast<int>(K);
+    p.rows_per_image = make_fastdiv(1u);
+    p.ln_w = ln_weight;
+    p.ln_b = ln_bias;
+    p.ln_eps = eps;
+    p.ln_out = static_cast<bf16_t*>(out_norm);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (N == 64) {
+        // the LDS-free kernel, 64 pixels per wave: all 64 channels of a pixel in four lanes
+        const dim3 grid(static_cast<unsigned>((M + 255) / 256));
+        if (K == 32) hipLaunchKernelGGL((pointwise_narrow_kernel<1, 4, 4, PW_ADD_LN, false>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((pointwise_narrow_kernel<2, 4, 4, PW_ADD_LN, false>), grid, dim3(256), 0, s, p);
+    } else if (N == 128) {
+        hipLaunchKernelGGL((pointwise_dma_kernel<64, 128, 4, PW_ADD_LN, 0, 3>), dim3(static_cast<unsigned>((M + 63) / 64)),
+                           dim3(256), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((pointwise_dma_kernel<64, 256, 4, PW_ADD_LN, 0, 2>), dim3(static_cast<unsigned>((M + 63) / 64)),
+                           dim3(256), 0, s, p);
+    }
+    return check_launch("pointwise conv + add + LayerNorm");
 }

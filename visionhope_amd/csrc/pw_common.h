@@ -11,7 +11,8 @@
 
 namespace vh {
 
-enum PwEpilogue { PW_BIAS = 0, PW_GELU = 1, PW_ADD = 2, PW_SILU = 3 };
+enum PwEpilogue { PW_BIAS = 0, PW_GELU = 1, PW_ADD = 2, PW_SILU = 3,
+                  PW_ADD_LN = 4 };   // internal: residual add + LayerNorm of the sum (vh_pointwise_add_layernorm_nhwc_forward)
 
 struct PwParams {
     const bf16_t* x;        // [M, K]
@@ -29,6 +30,12 @@ struct PwParams {
     const bf16_t* w2;
     const float* bias2;
     bf16_t* out2;
+    // PW_ADD_LN: out = bf16(res + bf16(x @ w^T + bias)) and ln_out = bf16(LayerNorm(out))
+    // over the N channels of each pixel, affine ln_w / ln_b [N] fp32
+    const float* ln_w;
+    const float* ln_b;
+    float ln_eps;
+    bf16_t* ln_out;
 };
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -93,6 +100,82 @@ __device__ __forceinline__ void pw_bias8(const PwParams& p, int n, float (&bv)[8
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) bv[j] = 0.f;
+    }
+}
+
+// PW_ADD_LN epilogue of pixel m from the 2Q accumulator tiles of a lane (all N = 32 Q
+// channels of the pixel over the four lanes kg = 0..3 of row i16: channels 32 q + 8 kg + j).
+// The sums of the LayerNorm run in the order of layernorm_nhwc8_kernel<..., ADD> over the
+// same map (8-channel groups g = 4 q + kg, each summed in channel order from zero, then a
+// balanced tree over the groups in index order: kg pairs by lane exchanges, then q pairs in
+// the lane), so both outputs carry the bits of that kernel after a bias-epilogue product.
+// Every lane takes part in the exchanges; `valid` gates the stores.
+template <int Q>
+__device__ __forceinline__ void pw_add_ln_store(const PwParams& p, int64_t m, bool valid, int kg, const v4f_pw (&a)[2 * Q]) {
+    const int64_t mm = valid ? m : 0;
+    float v[Q][8], s[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int n = 32 * q + 8 * kg;
+        float bv[8];
+        pw_bias8(p, n, bv);
+        uint32_t bw[4];   // bf16(acc + bias): the product's output
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+            bw[j / 2] = pack_bf16x2(a[2 * q][j] + bv[j], a[2 * q][j + 1] + bv[j + 1]);
+            bw[2 + j / 2] = pack_bf16x2(a[2 * q + 1][j] + bv[4 + j], a[2 * q + 1][j + 1] + bv[5 + j]);
+        }
+        const uint4 r = *reinterpret_cast<const uint4*>(p.res + mm * p.N + n);
+        const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+        uint32_t sw[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+            sw[h] = pack_bf16x2(bf16_lo(rw[h]) + bf16_lo(bw[h]), bf16_hi(rw[h]) + bf16_hi(bw[h]));
+        if (valid) *reinterpret_cast<uint4*>(p.out + m * p.N + n) = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+        s[q] = 0.f;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            v[q][2 * h] = bf16_lo(sw[h]);
+            v[q][2 * h + 1] = bf16_hi(sw[h]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s[q] += v[q][j];
+    }
+    auto tree = [&](float (&t)[Q]) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            t[q] += __shfl_xor(t[q], 16);
+            t[q] += __shfl_xor(t[q], 32);
+        }
+#pragma unroll
+        for (int w = 1; w < Q; w *= 2)
+#pragma unroll
+            for (int q = 0; q < Q; q += 2 * w) t[q] += t[q + w];
+        return t[0];
+    };
+    const float inv_c = 1.f / static_cast<float>(p.N);   // exact for power-of-two N
+    const float mean = tree(s) * inv_c;
+    float sq[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        sq[q] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[q][j] -= mean;
+            sq[q] += v[q][j] * v[q][j];
+        }
+    }
+    const float rstd = __builtin_amdgcn_rsqf(tree(sq) * inv_c + p.ln_eps);
+    if (!valid) return;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int n = 32 * q + 8 * kg;
+        float wv[8], bv[8], o[8];
+        load8<float>(p.ln_w + n, wv);
+        load8<float>(p.ln_b + n, bv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = v[q][j] * rstd * wv[j] + bv[j];
+        store8<bf16_t>(p.ln_out + m * p.N + n, o);
     }
 }
 

@@ -37,6 +37,11 @@ OVERLAP_SCAN = False
 # (True), or as two projections (False, for measurements); the same bits either way.
 FUSE_GATE_CHAIN = True
 
+# proj_out with the residual add and norm2 in its epilogue where the block width allows
+# (True), or the projection followed by the add + LayerNorm kernel (False, for
+# measurements); the same bits either way.
+FUSE_OUT_NORM = True
+
 # The local position encoding (5x5 depthwise of x_local) computed inside the operator's
 # readout (True: one pass, the same bits) or as a separate depthwise pass whose result the
 # readout adds (False, for measurements).
@@ -240,10 +245,23 @@ class VisionHOPEBlock(nn.Module):
         else:
             x_local = F.silu(dwconv.depthwise_conv(nchw(inner), self.local_conv))
         path, _ = self.operator._inference_path(x_local)
+        x_h = None   # (x + branch, norm2 of it) when proj_out's launch produced them
         if path == "ordinary":
             branch = self._spatial_tail(x_local, True)
         elif path == "spatial" and x_local.dtype == act:
-            branch = nchw(project(self._spatial_overlapped(x_local), self.proj_out))
+            op_out = self._spatial_overlapped(x_local)
+            x_nhwc = x.permute(0, 2, 3, 1)
+            if (FUSE_OUT_NORM and self.gamma1 is None and act == torch.bfloat16
+                    and pointwise.add_layernorm_supported(self.proj_out) and _matrix_core_ok(op_out, self.proj_out)
+                    and x.dtype == act and x_nhwc.is_contiguous() and x_nhwc.data_ptr() % 16 == 0
+                    and isinstance(self.norm2, LayerNorm2d)):
+                # proj_out, the residual add and norm2 in one launch (the same bits)
+                s_nhwc, h_nhwc = pointwise.pointwise_add_layernorm(op_out, self.proj_out, x_nhwc, self.norm2.weight,
+                                                                   self.norm2.bias, self.norm2.eps)
+                x_h = (nchw(s_nhwc), nchw(h_nhwc))
+                branch = None
+            else:
+                branch = nchw(project(op_out, self.proj_out))
         else:
             out = self.operator._forward_fast(x_local, path)
             if self.local_position is not None:
@@ -254,7 +272,9 @@ class VisionHOPEBlock(nn.Module):
             branch = nchw(project(out, self.proj_out))
         # Feed-forward branch (the residual add fused into norm2 when LayerScale is folded).
         ffn = self.ffn
-        if self.gamma1 is None and can_fuse_add_layernorm2d(x, branch, self.norm2.weight, self.norm2.bias):
+        if x_h is not None:
+            x, h = x_h
+        elif self.gamma1 is None and can_fuse_add_layernorm2d(x, branch, self.norm2.weight, self.norm2.bias):
             x, h = visionhope_add_layernorm2d(x, branch, self.norm2.weight, self.norm2.bias, self.norm2.eps,
                                               out_dtype=act)
         else:

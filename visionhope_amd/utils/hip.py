@@ -32,7 +32,7 @@ EXPORTED_SYMBOLS = (
     "vh_srnl_line_forward_seq_noatomic", "vh_srnl_sequence_forward", "vh_srnl_forward",
     "vh_postprocess_scale_forward", "vh_grn_workspace_bytes", "vh_grn_forward",
     "vh_layernorm2d_forward", "vh_add_layernorm2d_forward", "vh_qnorm_forward", "vh_residual_add_forward",
-    "vh_dwconv2d_nhwc_forward", "vh_dwconv2d_add_layernorm2d_forward", "vh_grn_scale_forward", "vh_pointwise_chain_nhwc_forward", "vh_pointwise_conv_nhwc_forward",
+    "vh_dwconv2d_nhwc_forward", "vh_dwconv2d_add_layernorm2d_forward", "vh_grn_scale_forward", "vh_pointwise_add_layernorm_nhwc_forward", "vh_pointwise_chain_nhwc_forward", "vh_pointwise_conv_nhwc_forward",
     "vh_bias_act_nhwc_forward", "vh_dwconv2d_gelu_grn_workspace_bytes", "vh_dwconv2d_gelu_grn_forward",
     "vh_conv3x3_nhwc_forward", "vh_srnl_backward_workspace_bytes", "vh_srnl_backward",
     "vh_postprocess_scale_backward_workspace_bytes", "vh_postprocess_scale_backward",
@@ -127,6 +127,8 @@ _SIGNATURES = {
     "vh_pointwise_conv_nhwc_forward": (ctypes.c_int, [
         _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "vh_pointwise_chain_nhwc_forward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "vh_pointwise_add_layernorm_nhwc_forward": (ctypes.c_int, [
+        _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64, _i64, _vp]),
     "vh_bias_act_nhwc_forward": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _i64, _i64, _vp]),
     "vh_conv3x3_nhwc_forward": (ctypes.c_int, [
         _vp, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _vp]),

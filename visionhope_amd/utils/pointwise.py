@@ -144,3 +144,42 @@ def pointwise_chain(x, first, second):
         hip.ptr(x), hip.ptr(w1), hip.ptr(b1), hip.ptr(w2), hip.ptr(b2), hip.ptr(out), hip.ptr(out2), m, n, k,
         hip.stream_of(x)), "vh_pointwise_chain_nhwc_forward")
     return out, out2
+
+
+def add_layernorm_supported(module):
+    """Whether ``pointwise_add_layernorm`` covers ``module`` (K -> N with bias): N = 64 with
+    K = 32 or 64, or N = 128 or 256 with K = 64 or 128."""
+    if not is_pointwise(module) or module.bias is None:
+        return False
+    n, k = module.weight.shape[0], module.weight.shape[1]
+    return (n == 64 and k in (32, 64)) or (n in (128, 256) and k in (64, 128))
+
+
+@on_tensor_device
+def pointwise_add_layernorm(x, module, residual, ln_weight, ln_bias, eps):
+    """``s = bf16(residual + module(x))`` and ``bf16(LayerNorm(s))`` over the channels, both
+    ``[..., N]`` bf16, in the product's launch (``vh_pointwise_add_layernorm_nhwc_forward``):
+    the bits of ``pointwise_conv`` followed by the channels-last residual add + LayerNorm
+    (``visionhope_add_layernorm2d``).  ``add_layernorm_supported(module)`` must hold."""
+    if not add_layernorm_supported(module):
+        raise ValueError("pointwise_add_layernorm covers N = 64 (K = 32, 64) and N = 128, 256 (K = 64, 128)")
+    if not x.is_cuda or x.dtype != torch.bfloat16 or not x.is_contiguous() or x.data_ptr() % 16:
+        raise ValueError("pointwise_add_layernorm expects a contiguous 16-byte aligned CUDA bf16 tensor")
+    weight, bias = pointwise_operands(module)
+    n, k = weight.shape
+    shape = (*x.shape[:-1], n)
+    if (x.shape[-1] != k or residual.shape != shape or residual.dtype != torch.bfloat16
+            or not residual.is_contiguous() or residual.data_ptr() % 16):
+        raise ValueError("pointwise_add_layernorm needs x [..., K] and a contiguous bf16 residual [..., N]")
+    lw = ln_weight.detach().float().contiguous()
+    lb = ln_bias.detach().float().contiguous()
+    if lw.numel() != n or lb.numel() != n:
+        raise ValueError("LayerNorm weight and bias must have N entries")
+    m = x.numel() // k
+    out_sum = torch.empty(shape, device=x.device, dtype=torch.bfloat16)
+    out_norm = torch.empty(shape, device=x.device, dtype=torch.bfloat16)
+    lib = hip.load_library()
+    hip.check(lib.vh_pointwise_add_layernorm_nhwc_forward(
+        hip.ptr(x), hip.ptr(weight), hip.ptr(bias), hip.ptr(residual), hip.ptr(lw), hip.ptr(lb), float(eps),
+        hip.ptr(out_sum), hip.ptr(out_norm), m, n, k, hip.stream_of(x)), "vh_pointwise_add_layernorm_nhwc_forward")
+    return out_sum, out_norm
