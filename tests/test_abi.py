@@ -163,6 +163,45 @@ def test_pointwise_conv_rejects_bad_arguments(lib):
     assert b"aligned" in lib.vh_last_error()
 
 
+def test_pointwise_chain_and_add_layernorm_reject_bad_arguments(lib):
+    """The chained proj_in + local_gate and the proj_out + add + norm2 entries validate their
+    shapes, pointers and alignment before launching anything."""
+    p = ctypes.c_void_p(0x1000)
+
+    def chain(m=64, n=128, k=256, x=p, w2=p):
+        return lib.vh_pointwise_chain_nhwc_forward(x, p, p, w2, p, p, p, m, n, k, None)
+
+    assert chain(n=256) == hip.VH_ERR_SHAPE              # N = 32, 64 or 128 only
+    assert chain(k=96) == hip.VH_ERR_SHAPE               # K % 64 for N = 64, 128
+    assert chain(n=32, k=128) == hip.VH_ERR_SHAPE        # N = 32 takes K = 32 or 64
+    assert chain(m=0) == hip.VH_ERR_SHAPE
+    assert chain(w2=None) == hip.VH_ERR_ARG
+    assert chain(x=ctypes.c_void_p(0x1008)) == hip.VH_ERR_ARG
+
+    def addln(m=64, n=256, k=128, eps=1e-6, res=p, x=p):
+        return lib.vh_pointwise_add_layernorm_nhwc_forward(x, p, p, res, p, p, eps, p, p, m, n, k, None)
+
+    assert addln(n=512) == hip.VH_ERR_SHAPE
+    assert addln(n=64, k=128) == hip.VH_ERR_SHAPE
+    assert addln(k=256) == hip.VH_ERR_SHAPE
+    assert addln(m=0) == hip.VH_ERR_SHAPE
+    assert addln(eps=0.0) == hip.VH_ERR_ARG
+    assert addln(res=None) == hip.VH_ERR_ARG
+    assert addln(x=ctypes.c_void_p(0x1008)) == hip.VH_ERR_ARG
+
+
+def test_readout_lepe_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(0x1000)
+    arr, keep = hip.int64_array((4, 4, 4, 4))
+
+    def call(taps=p, h=4, w=4):
+        return lib.vh_srnl_spatial_readout_lepe(p, p, hip.VH_DTYPE_BF16, p, 0, p, taps, None, p, 2, h, w, 32, 16,
+                                                arr, p, 1 << 20, None)
+
+    assert call(taps=None) == hip.VH_ERR_ARG
+    assert call(h=0) == hip.VH_ERR_SHAPE
+
+
 def test_grn_scale_rejects_bad_arguments(lib):
     p = ctypes.c_void_p(0x1000)
 
