@@ -246,11 +246,13 @@ def test_conv3x3_rejects_bad_arguments(lib):
 
 
 def test_dwconv_grn_workspace_query(lib):
-    # Covered: C/8 divides 256 and the 256-thread blocks tile whole images.
+    # Covered: blocks of G * (256 / G) threads (G = C / 8 channel groups) tile whole images.
     assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(2, 56, 56, 256, 3) == 2 * 49 * 256 * 4
     assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(128, 14, 14, 1024, 3) == 128 * 14 * 1024 * 4
+    # Base stage 2: 96 groups, blocks of 192 threads, 64 rows x 8 segments -> 256 per image
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(8, 64, 64, 768, 3) == 8 * 256 * 768 * 4
     assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 14, 14, 256, 3) == 0     # 896 threads per image
-    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 8, 8, 96, 3) == 0        # C/8 = 12 does not divide 256
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 8, 8, 96, 3) == 0        # 96 threads, blocks of 252
     p = ctypes.c_void_p(0x1000)
     rc = lib.vh_dwconv2d_gelu_grn_forward(p, hip.VH_DTYPE_BF16, p, p, 3, p, ctypes.c_float(1e-6), p, p, p, p,
                                           1, 14, 14, 256, p, 1 << 20, None)

@@ -263,6 +263,33 @@ def test_depthwise_gelu_grn_statistics(device, dispatch, dtype, shape, ksize, ti
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(2, 768, 16, 16), (2, 1792, 8, 8), (2, 768, 64, 64), (3, 384, 10, 16)])
+def test_depthwise_gelu_grn_statistics_whole_group_blocks(device, dtype, shape):
+    """Channel counts whose 8-channel groups do not divide 256 (Base: 768 and 1792 FFN
+    channels, blocks of 192 and 224 threads), and few images with many slabs (the spread
+    statistics: 256 slabs per image at 64 x 64): the map equals the plain fused depthwise +
+    GELU and the scale matches the separate GRN statistics pass."""
+    from visionhope_amd.utils import dwconv
+    from visionhope_amd.utils.grn_cuda import grn_scale
+
+    b, c, h, w = shape
+    conv = torch.nn.Conv2d(c, c, 3, padding=1, groups=c)
+    with torch.no_grad():
+        conv.weight.copy_(randn(*conv.weight.shape, seed=61, scale=0.3))
+        conv.bias.copy_(randn(c, seed=62, scale=0.1))
+    conv = conv.to(device)
+    gamma = randn(c, seed=63, scale=0.3).to(device)
+    x = randn(b, c, h, w, seed=64).to(dtype).to(device).contiguous(memory_format=torch.channels_last)
+    print(f"\n[case] dwconv + GRN sums {dtype} {shape}", flush=True)
+    fused = dwconv.depthwise_conv_gelu_grn(x, conv, gamma, 1e-6)
+    assert fused is not None
+    out, scale = fused
+    plain = dwconv.depthwise_conv(x, conv, dwconv.EPI_ADD_GELU)
+    assert torch.equal(out, plain)
+    assert_close(scale.cpu().numpy(), grn_scale(plain, gamma, 1e-6).cpu().numpy(), 1e-5, "fused GRN scale")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape", [(2, 64, 56, 56), (3, 128, 28, 28), (2, 256, 14, 14), (4, 256, 7, 7),
                                    (2, 128, 9, 13), (2, 8, 5, 6), (1, 32, 1, 17)])
 def test_depthwise_add_layernorm_matches_separate_kernels(device, dtype, shape):

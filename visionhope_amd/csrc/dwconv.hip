@@ -140,12 +140,13 @@ template <int K, int EPI, typename T, int P>
 __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, const DwGrid g, const uint32_t x_bytes) {
     constexpr int R = K / 2, NI = P + K - 1;
     constexpr uint32_t OUTSIDE = 0x80000000u;
-    const uint32_t idx = xcd_remap_any(blockIdx.x, gridDim.x) * 256u + threadIdx.x;
+    // 256 threads per block, or G * (256 / G) (whole channel groups) for the GRN sums
+    const uint32_t idx = xcd_remap_any(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x;
     // GELU table of 2-byte outputs, copied to LDS by every thread before any returns
     [[maybe_unused]] const float2* gq = nullptr;
     if constexpr ((EPI == DW_ADD_GELU || EPI == DW_ADD_GELU_SUMSQ) && sizeof(T) == 2) {
         __shared__ float4 gq4[GELU_QI_N / 2];
-        gelu_qi_fill(gq4, static_cast<int>(threadIdx.x), 256);
+        gelu_qi_fill(gq4, static_cast<int>(threadIdx.x), static_cast<int>(blockDim.x));
         __syncthreads();
         gq = reinterpret_cast<const float2*>(gq4);
     }
@@ -294,9 +295,10 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
         }
     }
     if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
-        // GRN partial sums: this block's threads cover whole channel groups of one image
-        // (the host checks 256 % G == 0 and whole blocks per image), 256 / G threads per
-        // group; the first G threads add their group's rows in order (deterministic).
+        // GRN partial sums: this block's G * (256 / G) threads cover whole channel groups
+        // of one image (the host launches that block size and checks whole blocks per
+        // image), blockDim / G threads per group; the first G threads add their group's
+        // rows in order (deterministic).
         __shared__ float red[256 * 8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) red[threadIdx.x * 8 + j] = sumsq[j];
@@ -304,12 +306,12 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
         const int G = static_cast<int>(g.G.d);
         if (static_cast<int>(threadIdx.x) < G) {
             float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            for (int r = 0; r < 256 / G; ++r)
+            for (int r = 0; r < static_cast<int>(blockDim.x) / G; ++r)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) tot[j] += red[(r * G + threadIdx.x) * 8 + j];
             // Blocks of one image are consecutive logical blocks: partial [b][slab] is
-            // row idx / 256 of [B * blocks per image, C].
-            float* dst = p.partial + static_cast<int64_t>(idx / 256u) * C + 8 * threadIdx.x;
+            // row idx / blockDim of [B * blocks per image, C].
+            float* dst = p.partial + static_cast<int64_t>(idx / blockDim.x) * C + 8 * threadIdx.x;
 #pragma unroll
             for (int j = 0; j < 8; ++j) dst[j] = tot[j];
         }
@@ -513,6 +515,9 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
     const int64_t image_elems = dp.H * dp.W * dp.C;
     const int64_t per_launch = std::max<int64_t>(1, limit / (image_elems * int64_t(sizeof(T))));
     const int64_t segs = (dp.W + P - 1) / P;
+    // block size: 256 threads, or whole channel groups (G * (256 / G)) for the GRN sums
+    const int64_t G = dp.C / 8;
+    const uint32_t bd = epi == DW_ADD_GELU_SUMSQ && G <= 256 ? static_cast<uint32_t>(G * (256 / G)) : 256u;
     const size_t out_size = epi == DW_ACCUM_F32 ? sizeof(float) : sizeof(T);
     const size_t aux_size = epi == DW_ADD_F32_AUX ? sizeof(float) : sizeof(T);
     for (int64_t b0 = 0; b0 < dp.B; b0 += per_launch) {
@@ -522,7 +527,7 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
         q.x = static_cast<const char*>(dp.x) + skip * sizeof(T);
         q.out = static_cast<char*>(dp.out) + skip * out_size;
         if (dp.aux) q.aux = static_cast<const char*>(dp.aux) + skip * aux_size;
-        if (dp.partial) q.partial = dp.partial + b0 * (dp.H * segs * (dp.C / 8) / 256) * dp.C;
+        if (dp.partial) q.partial = dp.partial + b0 * (dp.H * segs * (dp.C / 8) / bd) * dp.C;
         if (dp.out_norm) q.out_norm = static_cast<char*>(dp.out_norm) + skip * sizeof(T);
         DwGrid g;
         g.total = static_cast<uint32_t>(q.B * q.H * segs * (q.C / 8));
@@ -530,10 +535,10 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
         g.segs = make_fastdiv(static_cast<uint32_t>(segs));
         g.H = make_fastdiv(static_cast<uint32_t>(q.H));
         const uint32_t x_bytes = static_cast<uint32_t>(q.B * image_elems * int64_t(sizeof(T)));
-        const dim3 grid((g.total + 255) / 256);
+        const dim3 grid((g.total + bd - 1) / bd);
         switch (epi) {
 #define VH_DW(E)                                                                                         \
-    case E: hipLaunchKernelGGL((dwconv_nhwc_kernel<K, E, T, P>), grid, dim3(256), 0, s, q, g, x_bytes); \
+    case E: hipLaunchKernelGGL((dwconv_nhwc_kernel<K, E, T, P>), grid, dim3(bd), 0, s, q, g, x_bytes); \
         break;
             VH_DW(DW_PLAIN) VH_DW(DW_ADD_INPUT) VH_DW(DW_GATE) VH_DW(DW_ADD_GELU) VH_DW(DW_ACCUM_F32)
             VH_DW(DW_ADD_F32_AUX) VH_DW(DW_ADD_GELU_SUMSQ)
@@ -548,12 +553,14 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
 
 inline int dw_pixels(int K, int64_t W) { return dw_default_pixels(K, W); }
 
-// Blocks per image of the depthwise grid, or 0 when blocks do not tile whole images
-// and whole channel groups (the condition of the GRN partial-sum epilogue).
+// Blocks per image of the depthwise grid with the GRN partial-sum epilogue (blocks of
+// G * (256 / G) threads: whole channel groups), or 0 when blocks do not tile whole images.
 inline int64_t dw_blocks_per_image(int K, int64_t H, int64_t W, int64_t C) {
     const int64_t G = C / 8, segs = (W + dw_pixels(K, W) - 1) / dw_pixels(K, W);
-    if (C % 8 != 0 || G > 256 || 256 % G != 0 || (H * segs * G) % 256 != 0) return 0;
-    return H * segs * G / 256;
+    if (C % 8 != 0 || G > 256) return 0;
+    const int64_t bd = G * (256 / G);
+    if ((H * segs * G) % bd != 0) return 0;
+    return H * segs * G / bd;
 }
 
 // Plan of dwconv_tile_kernel for a map of `es`-byte elements (2-byte maps: bf16 and

@@ -1237,9 +1237,17 @@ __global__ __launch_bounds__(256) void bias_act8_kernel(const T* __restrict__ x,
 // depthwise kernel that produces the partial sums in its epilogue.
 int launch_grn_finalize(const float* partial, float* gx, float* inv_den, int64_t B, int64_t C, int64_t nslab,
                         float eps, const float* gamma, float* scale, hipStream_t s) {
-    hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s, partial, gx, inv_den,
-                       C, nslab, eps, gamma, scale);
-    return check_launch("grn_finalize_kernel");
+    if (B >= 64 || nslab < 64 || C > (int64_t(1) << 30) || nslab > (int64_t(1) << 30)) {
+        hipLaunchKernelGGL(grn_finalize_kernel, dim3(static_cast<unsigned>(B)), dim3(kGrnFinalizeThreads), 0, s, partial, gx,
+                           inv_den, C, nslab, eps, gamma, scale);
+        return check_launch("grn_finalize_kernel");
+    }
+    // few images with many slabs: the slab sums spread over channel blocks x images
+    hipLaunchKernelGGL(grn_gx8_kernel, dim3(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>(B)), dim3(256), 0, s,
+                       partial, gx, static_cast<int>(C), static_cast<int>(nslab));
+    hipLaunchKernelGGL(grn_image_scale_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, s, gx, inv_den, C, eps, gamma,
+                       scale);
+    return check_launch("grn statistics kernels");
 }
 
 }  // namespace vh
