@@ -246,16 +246,21 @@ def test_conv3x3_rejects_bad_arguments(lib):
 
 
 def test_dwconv_grn_workspace_query(lib):
-    # Covered: blocks of G * (256 / G) threads (G = C / 8 channel groups) tile whole images.
+    # Blocks of G x r threads (G = C / 8 channel groups, r <= 256 / G pixel segments, the
+    # largest r dividing an image's rows x segments) tile whole images.
     assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(2, 56, 56, 256, 3) == 2 * 49 * 256 * 4
     assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(128, 14, 14, 1024, 3) == 128 * 14 * 1024 * 4
-    # Base stage 2: 96 groups, blocks of 192 threads, 64 rows x 8 segments -> 256 per image
+    # Base stage 2: 96 groups x 2 segments (192 threads), 64 rows x 8 segments -> 256 per image
     assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(8, 64, 64, 768, 3) == 8 * 256 * 768 * 4
-    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 14, 14, 256, 3) == 0     # 896 threads per image
-    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 8, 8, 96, 3) == 0        # 96 threads, blocks of 252
+    # Base stage 1: 48 groups x 4 segments (5 do not divide 128 rows x 16 segments)
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(8, 128, 128, 384, 3) == 8 * 512 * 384 * 4
+    # 14 rows x 2 segments: 32 groups x 7 segments, 4 blocks per image
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 14, 14, 256, 3) == 4 * 256 * 4
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 7, 7, 2560, 3) == 0      # 320 groups > 256
+    assert lib.vh_dwconv2d_gelu_grn_workspace_bytes(1, 8, 8, 100, 3) == 0       # C % 8
     p = ctypes.c_void_p(0x1000)
     rc = lib.vh_dwconv2d_gelu_grn_forward(p, hip.VH_DTYPE_BF16, p, p, 3, p, ctypes.c_float(1e-6), p, p, p, p,
-                                          1, 14, 14, 256, p, 1 << 20, None)
+                                          1, 7, 7, 2560, p, 1 << 20, None)
     assert rc == hip.VH_ERR_SHAPE
 
 

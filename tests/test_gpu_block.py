@@ -263,12 +263,14 @@ def test_depthwise_gelu_grn_statistics(device, dispatch, dtype, shape, ksize, ti
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("shape", [(2, 768, 16, 16), (2, 1792, 8, 8), (2, 768, 64, 64), (3, 384, 10, 16)])
+@pytest.mark.parametrize("shape", [(2, 768, 16, 16), (2, 1792, 8, 8), (2, 768, 64, 64), (3, 384, 10, 16),
+                                   (2, 384, 128, 128), (1, 256, 14, 14), (2, 96, 8, 8)])
 def test_depthwise_gelu_grn_statistics_whole_group_blocks(device, dtype, shape):
-    """Channel counts whose 8-channel groups do not divide 256 (Base: 768 and 1792 FFN
-    channels, blocks of 192 and 224 threads), and few images with many slabs (the spread
-    statistics: 256 slabs per image at 64 x 64): the map equals the plain fused depthwise +
-    GELU and the scale matches the separate GRN statistics pass."""
+    """Blocks of whole channel groups other than 256 threads (Base: 768, 1792 and 384 FFN
+    channels in blocks of 192, 224 and 192 threads; 256 channels on 14 x 14 in blocks of 7
+    segments; 96 channels), and few images with many slabs (the spread statistics: 256 and
+    512 slabs per image): the map equals the plain fused depthwise + GELU and the scale
+    matches the separate GRN statistics pass."""
     from visionhope_amd.utils import dwconv
     from visionhope_amd.utils.grn_cuda import grn_scale
 
@@ -331,6 +333,7 @@ def test_depthwise_add_layernorm_declines_uncovered_shapes(device):
 def test_depthwise_gelu_grn_declines_uncovered_shapes(device):
     from visionhope_amd.utils import dwconv
 
-    conv = torch.nn.Conv2d(256, 256, 3, padding=1, groups=256).to(device)
-    x = torch.randn(1, 256, 14, 14, device=device).contiguous(memory_format=torch.channels_last)
-    assert dwconv.depthwise_conv_gelu_grn(x, conv, torch.ones(256, device=device), 1e-6) is None
+    # 2,560 channels: 320 groups of 8, more than one block of 256 threads holds
+    conv = torch.nn.Conv2d(2560, 2560, 3, padding=1, groups=2560).to(device)
+    x = torch.randn(1, 2560, 7, 7, device=device).contiguous(memory_format=torch.channels_last)
+    assert dwconv.depthwise_conv_gelu_grn(x, conv, torch.ones(2560, device=device), 1e-6) is None

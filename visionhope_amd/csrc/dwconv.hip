@@ -140,7 +140,7 @@ template <int K, int EPI, typename T, int P>
 __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, const DwGrid g, const uint32_t x_bytes) {
     constexpr int R = K / 2, NI = P + K - 1;
     constexpr uint32_t OUTSIDE = 0x80000000u;
-    // 256 threads per block, or G * (256 / G) (whole channel groups) for the GRN sums
+    // 256 threads per block, or whole channel groups (G * r threads) for the GRN sums
     const uint32_t idx = xcd_remap_any(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x;
     // GELU table of 2-byte outputs, copied to LDS by every thread before any returns
     [[maybe_unused]] const float2* gq = nullptr;
@@ -295,10 +295,10 @@ __global__ __launch_bounds__(256) void dwconv_nhwc_kernel(const DwParams p, cons
         }
     }
     if constexpr (EPI == DW_ADD_GELU_SUMSQ) {
-        // GRN partial sums: this block's G * (256 / G) threads cover whole channel groups
-        // of one image (the host launches that block size and checks whole blocks per
-        // image), blockDim / G threads per group; the first G threads add their group's
-        // rows in order (deterministic).
+        // GRN partial sums: this block's threads cover whole channel groups of one image
+        // (the host launches G * r threads, r pixel segments, and whole blocks per image),
+        // blockDim / G threads per group; the first G threads add their group's rows in
+        // order (deterministic).
         __shared__ float red[256 * 8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) red[threadIdx.x * 8 + j] = sumsq[j];
@@ -503,6 +503,15 @@ inline int dw_default_pixels(int K, int64_t W) {
     return W >= 28 ? 2 : 8;
 }
 
+// Threads per block of the GRN partial-sum launch: G channel groups times the most
+// pixel segments per block (at most 256 / G) that divide an image's rows x segments, so
+// blocks hold whole channel groups and tile whole images.
+inline int64_t dw_sumsq_block(int64_t G, int64_t rowsegs) {
+    for (int64_t r = 256 / G; r > 1; --r)
+        if (rowsegs % r == 0) return G * r;
+    return G;
+}
+
 template <int K, typename T, int P>
 void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
     // The input of one launch is addressed as one buffer below 2^31 bytes: large batches
@@ -515,9 +524,9 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
     const int64_t image_elems = dp.H * dp.W * dp.C;
     const int64_t per_launch = std::max<int64_t>(1, limit / (image_elems * int64_t(sizeof(T))));
     const int64_t segs = (dp.W + P - 1) / P;
-    // block size: 256 threads, or whole channel groups (G * (256 / G)) for the GRN sums
+    // block size: 256 threads, or whole channel groups tiling whole images for the GRN sums
     const int64_t G = dp.C / 8;
-    const uint32_t bd = epi == DW_ADD_GELU_SUMSQ && G <= 256 ? static_cast<uint32_t>(G * (256 / G)) : 256u;
+    const uint32_t bd = epi == DW_ADD_GELU_SUMSQ && G <= 256 ? static_cast<uint32_t>(dw_sumsq_block(G, dp.H * segs)) : 256u;
     const size_t out_size = epi == DW_ACCUM_F32 ? sizeof(float) : sizeof(T);
     const size_t aux_size = epi == DW_ADD_F32_AUX ? sizeof(float) : sizeof(T);
     for (int64_t b0 = 0; b0 < dp.B; b0 += per_launch) {
@@ -553,14 +562,12 @@ void launch_dw_p(int epi, const DwParams& dp, hipStream_t s) {
 
 inline int dw_pixels(int K, int64_t W) { return dw_default_pixels(K, W); }
 
-// Blocks per image of the depthwise grid with the GRN partial-sum epilogue (blocks of
-// G * (256 / G) threads: whole channel groups), or 0 when blocks do not tile whole images.
+// Blocks per image of the depthwise grid with the GRN partial-sum epilogue, or 0 when the
+// channels do not form at most 256 groups of 8.
 inline int64_t dw_blocks_per_image(int K, int64_t H, int64_t W, int64_t C) {
     const int64_t G = C / 8, segs = (W + dw_pixels(K, W) - 1) / dw_pixels(K, W);
-    if (C % 8 != 0 || G > 256) return 0;
-    const int64_t bd = G * (256 / G);
-    if ((H * segs * G) % bd != 0) return 0;
-    return H * segs * G / bd;
+    if (C % 8 != 0 || G > 256 || G < 1) return 0;
+    return H * segs * G / dw_sumsq_block(G, H * segs);
 }
 
 // Plan of dwconv_tile_kernel for a map of `es`-byte elements (2-byte maps: bf16 and
