@@ -206,3 +206,5 @@ def test_query_once_and_launch_audit(tiny_case, device, autocast):
     assert evidence["fused_operators"] == 29 and evidence["fused_srnl_calls"] == 29
     assert evidence["scan_kernels"] == 29 and evidence["readout_kernels"] == 29
     assert evidence["query_once"] is True
+    # every block's position encoding is computed inside its readout
+    assert evidence["separate_lepe_kernels"] == 0

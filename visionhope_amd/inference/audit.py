@@ -140,7 +140,10 @@ def audit_fast_path(model, forward):
                    for record in evidence[key].values())
     if scans != expected or readouts != expected:
         raise RuntimeError(f"Expected {expected} SRNL scans and readouts, observed {scans} and {readouts}")
+    # separate 5x5 depthwise launches (the position encoding when the readout does not
+    # compute it)
+    lepe_passes = sum(1 for n in names if "dwconv_nhwc_kernel<5" in n or "dwconv_tile_kernel<5" in n)
     return output, {"fused_blocks": audit.block_count, "fused_operators": len(evidence["query_audit"]),
                     "fused_srnl_calls": expected, "query_once": True if evidence["query_audit"] else None,
                     "scan_kernels": scans, "readout_kernels": readouts, "gpu_kernels": len(names),
-                    "grn_modules_fp32": len(evidence["grn_audit"])}
+                    "separate_lepe_kernels": lepe_passes, "grn_modules_fp32": len(evidence["grn_audit"])}
